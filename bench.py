@@ -1,0 +1,184 @@
+"""Benchmark of the STAR-KV fused decode-attention path on one MI355X.
+
+Workload ("cfg2"): Llama-2-7B-shaped layer, MHA
+32 heads x 128, fp16, batch 16, context 32768, head-wise K ranks from
+{16..96} (sum 1640, committed fixture), V rank 1640, one decode query token.
+Synthetic seeded data, inputs resident in HBM before timing.
+
+A "step" is one decode-attention pass of one layer over the whole batch:
+K-logits (latent K reconstruction + RoPE + q.K), softmax, P.V latent and the
+B_v up-projection -- the scope of the reference's "attention us/layer"
+(latency.py:262-268).
+
+Prints ONE JSON line.  value = algorithmic HBM bytes of the step / step time
+(GB/s); roofline = the dominant kernel against MI355X's 8 TB/s HBM;
+cpu_baseline = the reference's eager PyTorch decode path restated op for op
+(oracle/starkv_oracle.py), timed on this host's cores on batch 1 of the same
+workload.
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "star-kv_amd"), os.path.join(ROOT, "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+HEAD_DIM = 128
+
+
+def algorithmic_bytes(case):
+    """Per-step algorithmic bytes: latent caches + B_k + U_v + q + output."""
+    esz = 2
+    xk = sum(case.B * case.S * r for r in case.ranks) * esz
+    xv = case.B * case.S * case.Rv * esz
+    bk = sum(case.ranks) * HEAD_DIM * esz
+    uv = case.Hkv * HEAD_DIM * case.Rv * esz
+    q = case.B * case.Hq * HEAD_DIM * esz
+    out = case.B * case.Hq * HEAD_DIM * esz
+    return {"k_logits": xk + bk + q, "pv_latent": xv, "up_proj": uv + out, "total": xk + xv + bk + uv + q + out}
+
+
+def cpu_baseline(case_cpu_fn, reps):
+    """Time the oracle's eager restatement of the reference decode path."""
+    import torch
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    fn = case_cpu_fn()
+    for _ in range(2):
+        fn()
+    ts = []
+    t_end = time.perf_counter() + 25.0
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end:
+            break
+    return statistics.median(ts), threads, torch.get_num_threads(), len(ts)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=7)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from _util import cfg2_ranks, make_case
+    from starkv import RopeConfig, decode_attention
+    from starkv.ops import _workspace  # noqa: F401  (workspace is allocated on first call, outside timing)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ranks = cfg2_ranks()
+    B, H, S, Rv = 16, 32, 32768, 1640
+    case = make_case(B, H, H, S, ranks, Rv, dtype=torch.float16, device=dev, seed=0)
+    rope = RopeConfig()
+    out = torch.empty(B, H, HEAD_DIM, dtype=torch.float16, device=dev)
+    nbytes = algorithmic_bytes(case)
+
+    def step(ev=None):
+        decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, out=out, events=ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for e4 in evs:
+        for e in e4:
+            e.record()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    k1 = [e[0].elapsed_time(e[1]) for e in evs]
+    k2 = [e[1].elapsed_time(e[2]) for e in evs]
+    k3 = [e[2].elapsed_time(e[3]) for e in evs]
+    gpu_ms = statistics.mean([e[0].elapsed_time(e[3]) for e in evs])
+    wall_ms = wall * 1e3 / args.steps
+    ms = max(gpu_ms, 1e-9)
+    k1m, k2m, k3m = statistics.mean(k1), statistics.mean(k2), statistics.mean(k3)
+    gbs = nbytes["total"] / (ms * 1e-3) / 1e9
+
+    dom = "k_logits" if k1m >= k2m else "pv_latent"
+    dom_ms = k1m if dom == "k_logits" else k2m
+    dom_gbs = nbytes[dom] / (dom_ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_cfg2.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dom)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import starkv_oracle as o
+
+        def make_fn():
+            c = {
+                "q": case.q[:1].float().cpu(),
+                "bk": [b.float().cpu() for b in case.bk_heads],
+                "xk": [x[:1].float().cpu() for x in case.xk_heads],
+                "xv": case.xv[:1].float().cpu(),
+                "uv": case.uv.float().cpu(),
+            }
+            cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), 1.0)
+
+            def fn():
+                with torch.no_grad():
+                    o.decode_attention(c["q"], c["bk"], c["xk"], c["xv"], c["uv"], cos, sin, dtype=torch.float32)
+            return fn
+
+        med, cores, nthreads, n = cpu_baseline(make_fn, args.cpu_reps)
+        cpu_bytes = nbytes["total"] / B
+        cpu = {"value": round(cpu_bytes / med / 1e9, 3), "unit": "GB/s", "cores": nthreads,
+               "kind": "port", "host_cpus": cores, "us_per_layer_b1": round(med * 1e6, 1),
+               "sample": f"cfg2 workload batch 1 of {B} (S={S}), fp32 torch eager restatement of the reference "
+                         f"decode path (oracle.starkv_oracle.decode_attention), median of {n} reps"}
+
+    rec = {
+        "metric": "decode attn us/layer + HBM GB/s (% peak) at B16 S32K; e2e decode tok/s",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: Llama-2-7B-shaped decode attention layer, MHA 32x128, fp16, "
+                               "batch 16, context 32768, ragged K ranks (sum 1640), V rank 1640",
+                   "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": H},
+        "us_per_layer": round(ms * 1e3, 1),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 1),
+        "attn_layer_tokens_per_s": round(B / (ms * 1e-3), 1),
+        "kernels_us": {"k_logits": round(k1m * 1e3, 1), "pv_latent": round(k2m * 1e3, 1), "up_proj": round(k3m * 1e3, 1)},
+        "algorithmic_bytes": nbytes,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

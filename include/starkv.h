@@ -1,0 +1,202 @@
+/*
+ * starkv.h — C ABI of the MI355X (gfx950) STAR-KV decode-attention library
+ * (libstarkv.so, built from star-kv_amd/csrc/).
+ *
+ * Every entry point takes plain pointers and sizes, returns an int status
+ * (0 = OK, negative = argument validation error, positive = HIP error code)
+ * and never throws.  Device pointers are HIP device addresses; "host" arrays
+ * are read during the call only.  Work is enqueued asynchronously on the
+ * given hipStream_t (pass torch.cuda.current_stream().cuda_stream).  No entry
+ * point allocates device memory: scratch comes from a caller-owned workspace
+ * sized by the matching *_workspace_bytes query.  Calls are re-entrant (no
+ * mutable global state); two calls that share one workspace must be ordered
+ * on one stream.
+ */
+#ifndef STARKV_H_
+#define STARKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STARKV_ABI_VERSION 1
+
+/* element types */
+enum {
+  STARKV_F16 = 1,
+  STARKV_BF16 = 2,
+  STARKV_F32 = 3,
+  STARKV_I8 = 4,
+  STARKV_U8 = 5
+};
+
+/* status codes */
+enum {
+  STARKV_OK = 0,
+  STARKV_ERR_NULL = -1,       /* a required pointer is NULL */
+  STARKV_ERR_SHAPE = -2,      /* inconsistent or unsupported sizes */
+  STARKV_ERR_DTYPE = -3,      /* unsupported element type */
+  STARKV_ERR_ALIGN = -4,      /* pointer / stride alignment */
+  STARKV_ERR_RANK = -5,       /* latent rank outside 1..128 (K) or 1..8192 (V) */
+  STARKV_ERR_WORKSPACE = -6,  /* workspace NULL or smaller than required */
+  STARKV_ERR_LIMIT = -7,      /* exceeds a compiled limit (heads, items, positions) */
+  STARKV_ERR_FORMAT = -8      /* unknown quantisation format */
+};
+
+/* quantised latent formats */
+enum {
+  STARKV_FMT_DENSE = 0,      /* fp16 / bf16 latent, reference layout */
+  STARKV_FMT_INT4_REF = 1,   /* reference nibbles: rank j in byte j>>1 (lo = even),
+                                value (nib-8)*s, one fp16 scale per token
+                                (bx_quant.py:75-86) */
+  STARKV_FMT_INT8_SYM = 2,   /* int8 q*s, one fp16 scale per token (per (b,h,s) for K) */
+  STARKV_FMT_INT4_G64 = 3    /* int4 asymmetric, groups of 64 ranks, fp16 scale+zero
+                                per (b,s,group), build-defined MFMA-blocked layout */
+};
+
+int starkv_abi_version(void);
+const char* starkv_status_string(int status);
+
+/* ---------------------------------------------------------------------
+ * RoPE tables.  Replaces the per-program cos/sin recomputation of
+ * get_freq_multi_tokens (abx_rope_batched.py:40-48) and the theta=10000
+ * constant of the Triton launch (abx_rope_batched.py:184).  inv_freq is the
+ * host array of D/2 = 64 inverse frequencies as HF computes them
+ * (default or llama3); attention_scaling multiplies cos and sin
+ * (HF:models/llama/modeling_llama.py:125-126).
+ * ------------------------------------------------------------------- */
+size_t starkv_rope_table_bytes(int max_positions);
+int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int max_positions,
+                      void* table, size_t table_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
+ * K-latent description shared by the K-logit and decode entry points.
+ * KV head h has rank r_h = rank[h] (1..128); element (b, h, s, j) of the
+ * latent lives at  base + b*stride_b + head_offset[h] + s*pos_stride[h] + j.
+ * The reference cache [B, Hkv, S, r] (LlamaLoRaAttention_headwise.py:88-102)
+ * is head_offset[h] = h*stride(1), pos_stride[h] = stride(2).
+ * B_k (k_u^T, model.py:455) row j of head h lives at
+ * bk + bk_head_offset[h] + j*bk_row_stride, 128 contiguous elements.
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int n_kv_heads;
+  const int* rank;                 /* host [Hkv] */
+  const int64_t* head_offset;      /* host [Hkv], elements */
+  const int64_t* pos_stride;       /* host [Hkv], elements */
+  int64_t stride_b;                /* elements */
+  int format;                      /* STARKV_FMT_DENSE or STARKV_FMT_INT8_SYM */
+  const void* data;                /* device */
+  /* INT8_SYM: fp16 scale of (b,h,s) at scale + b*scale_stride_b + h*scale_stride_h + s */
+  const void* scale;
+  int64_t scale_stride_b, scale_stride_h;
+  const void* bk;                  /* device, act dtype */
+  const int64_t* bk_head_offset;   /* host [Hkv], elements */
+  int64_t bk_row_stride;           /* elements */
+} starkv_klatent;
+
+/* ---------------------------------------------------------------------
+ * starkv_k_logits — replaces abx(a, b, x, dtype) (abx_rope_batched.py:135-186)
+ * and the Triton _abx_fwd kernel (55-132):
+ *   out[b, q, s] = scale * q_rot[b,q] . RoPE_s(X_k[b, q//gs, s] @ B_k[q//gs])  (+ mask)
+ * q: [B, Hq, 128] act dtype (already rotated), element (b,q,d) at
+ * q + b*q_stride_b + q*q_stride_h + d.  out: out_dtype (act dtype or F32),
+ * element (b,q,s) at out + b*out_stride_b + q*out_stride_h + s.
+ * Position s uses the angle of position s (the Triton kernel's semantics).
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int batch, n_q_heads, head_dim, seq_len;
+  int dtype;                        /* act dtype of q, X_k (dense), B_k */
+  const void* q; int64_t q_stride_b, q_stride_h;
+  starkv_klatent k;
+  const void* rope_table; int rope_max_positions;
+  float scale;
+  const void* mask; int mask_dtype; int64_t mask_stride_b, mask_stride_h;   /* optional */
+  void* out; int out_dtype; int64_t out_stride_b, out_stride_h;
+} starkv_klogits_desc;
+
+size_t starkv_k_logits_workspace_bytes(const starkv_klogits_desc* d);
+int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
+ * V-latent description.  Dense: element (b, s, j) at
+ * data + b*stride_b + s*stride_s + j (reference cache [B, S, Rv],
+ * LlamaLoRaAttention_headwise.py:96-102).  INT4_REF (bx_quant.py:117-166
+ * x1/x2): ranks [0, split) in data (bytes, (b,s,byte) at data + b*stride_b +
+ * s*stride_s + byte) with fp16 per-token scale `scale`; ranks [split, rank)
+ * in data2/scale2 likewise; split_format says whether the upper block is
+ * INT4_REF (split/2 bytes per token) or INT8_SYM (split bytes per token).
+ * INT4_G64: the build's blocked layout written by starkv_quant_v_g64.
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int rank;
+  int format;
+  const void* data; int64_t stride_b, stride_s;
+  const void* scale; int64_t scale_stride_b, scale_stride_s;
+  int split; int split_format;
+  const void* data2; int64_t stride2_b, stride2_s;
+  const void* scale2; int64_t scale2_stride_b, scale2_stride_s;
+  const void* zero;   /* INT4_G64 zero points */
+  int capacity;       /* INT4_G64: positions allocated (multiple of 16) */
+} starkv_vlatent;
+
+/* ---------------------------------------------------------------------
+ * starkv_pv_latent — replaces bx(b, x1, x2, scale_v_upper, scale_v_lower,
+ * original_rank, upper_rank) (bx_quant.py:117-166) and the reference decode
+ * line prob_v = P @ X_v (model.py:484):  out[b, h, j] = sum_s P[b,h,s] V[b,s,j].
+ * p: act dtype, element (b,h,s) at p + b*p_stride_b + h*p_stride_h + s.
+ * out: act dtype, element (b,h,j) at out + b*out_stride_b + h*out_stride_h + j.
+ * Deterministic (fixed-order split-S reduction; no float atomics, unlike
+ * bx_quant.py:113-114).
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int batch, n_heads, seq_len;
+  int dtype;
+  const void* p; int64_t p_stride_b, p_stride_h;
+  starkv_vlatent v;
+  void* out; int64_t out_stride_b, out_stride_h;
+} starkv_pv_desc;
+
+size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d);
+int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
+ * starkv_decode_attention — the fused decode step that replaces the
+ * reference decode branch model.py:450-487 (abx -> /sqrt(D) -> +mask ->
+ * softmax(fp32) -> P @ X_v -> per-head up-projection), i.e. the scope of the
+ * reference's "attention us/layer" (latency.py:262-268):
+ *   out[b, q, :] = U_v[q//gs] @ sum_s softmax_s(logit[b,q,s]) X_v[b, s, :]
+ * uv: v_proj.U.weight [Hkv*128, Rv] act dtype, row i at uv + i*uv_row_stride.
+ * out: [B, Hq, 128], element (b,q,d) at out + b*out_stride_b + q*out_stride_h
+ * + d, of type out_dtype (0 = the act dtype, or STARKV_F32).
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int batch, n_q_heads, head_dim, seq_len;
+  int dtype;
+  const void* q; int64_t q_stride_b, q_stride_h;
+  starkv_klatent k;
+  starkv_vlatent v;
+  const void* uv; int64_t uv_row_stride;
+  const void* rope_table; int rope_max_positions;
+  float scale;
+  const void* mask; int mask_dtype; int64_t mask_stride_b, mask_stride_h;   /* optional */
+  void* out; int out_dtype; int64_t out_stride_b, out_stride_h;
+} starkv_decode_desc;
+
+size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d);
+int starkv_decode_attention(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Same as starkv_decode_attention, and records events[0..3] (hipEvent_t) on
+ * the stream before the K-logit kernel, after it, after the P.V kernel and
+ * after the up-projection, so a caller can time each kernel on the stream it
+ * runs on (the reference times with triton.testing.do_bench,
+ * latency.py:221-223). */
+int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes,
+                                  void* stream, void* const* events);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* STARKV_H_ */

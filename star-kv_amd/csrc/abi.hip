@@ -1,0 +1,390 @@
+// C ABI of libstarkv: argument validation, launch planning, workspace layout.
+//
+// Nothing here allocates device memory or synchronises; validation runs
+// before any HIP call so that every argument error is reported without a GPU.
+#include <algorithm>
+#include <vector>
+
+#include "common.hpp"
+
+using namespace starkv;
+
+namespace {
+
+constexpr int MI355X_CUS = 256;     // launch geometry is planned for one MI355X
+constexpr int K1_WG_PER_CU = 1;     // k_logits_kernel: __launch_bounds__(256, 1)
+constexpr int K2_WG_PER_CU = 2;     // pv_kernel: __launch_bounds__(256, 2)
+constexpr int PV_NT_HOST = 8;       // N-tiles (of 32 ranks) per P.V workgroup
+constexpr int MAX_S = 1 << 24;
+constexpr int MAX_RV = 8192;
+constexpr int K2_MAX_H = 32;
+
+int esize(int dt) {
+  switch (dt) {
+    case STARKV_F16: case STARKV_BF16: return 2;
+    case STARKV_F32: return 4;
+    case STARKV_I8: case STARKV_U8: return 1;
+    default: return 0;
+  }
+}
+bool al(const void* p, int n) { return ((uintptr_t)p % (uintptr_t)n) == 0; }
+bool al64(int64_t v, int n) { return v % n == 0; }
+
+size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Choose how many position splits give the best whole-GPU fill for
+// `groups` independent (batch, plan) groups; `penalty` prices extra splits.
+int choose_splits(int64_t groups, int slots, int n_units, int max_n, double penalty_per_split) {
+  int best = 1;
+  double best_score = -1.0;
+  for (int n = 1; n <= std::max(1, std::min(max_n, n_units)); ++n) {
+    const int len = (int)ceil_div(n_units, n);
+    const int ne = (int)ceil_div(n_units, len);
+    const int64_t W = groups * ne;
+    const int64_t rounds = ceil_div(W, slots);
+    const double fill = (double)W / (double)(rounds * slots);
+    const double bal = (double)n_units / (double)((int64_t)ne * len);
+    const double score = fill * bal / (1.0 + penalty_per_split * ne);
+    if (score > best_score * 1.0001) { best_score = score; best = n; }
+  }
+  return best;
+}
+
+struct KPlan {
+  int n_wg = 0;
+  bool fast = false;
+};
+
+int validate_klatent(const starkv_klatent& k, int Hq, int dtype, int* gs_out) {
+  if (k.n_kv_heads < 1 || k.n_kv_heads > K_MAX_KV) return k.n_kv_heads < 1 ? STARKV_ERR_SHAPE : STARKV_ERR_LIMIT;
+  if (Hq < 1 || Hq % k.n_kv_heads) return STARKV_ERR_SHAPE;
+  if (Hq > K_MAX_QH) return STARKV_ERR_LIMIT;
+  if (!k.rank || !k.head_offset || !k.pos_stride || !k.bk_head_offset) return STARKV_ERR_NULL;
+  if (!k.data || !k.bk) return STARKV_ERR_NULL;
+  if (k.format != STARKV_FMT_DENSE && k.format != STARKV_FMT_INT8_SYM) return STARKV_ERR_FORMAT;
+  if (k.format == STARKV_FMT_INT8_SYM && !k.scale) return STARKV_ERR_NULL;
+  if (dtype != STARKV_F16 && dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    if (k.rank[h] < 1 || k.rank[h] > 128) return STARKV_ERR_RANK;
+    if (k.pos_stride[h] < k.rank[h] || k.head_offset[h] < 0) return STARKV_ERR_SHAPE;
+  }
+  if (k.stride_b < 0 || k.bk_row_stride < HEAD_DIM) return STARKV_ERR_SHAPE;
+  *gs_out = Hq / k.n_kv_heads;
+  return STARKV_OK;
+}
+
+// Pack (query head, 32-rank M-tile) items into waves of K_MAXI items (first
+// fit decreasing, whole heads per wave) and waves into 4-wave workgroups.
+int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan) {
+  struct QH { int qh, kv, ni; };
+  std::vector<QH> heads;
+  for (int qh = 0; qh < Hq; ++qh) {
+    const int kv = qh / gs;
+    heads.push_back({qh, kv, (int)ceil_div(k.rank[kv], 32)});
+  }
+  std::stable_sort(heads.begin(), heads.end(), [](const QH& x, const QH& y) { return x.ni > y.ni; });
+  std::vector<std::vector<QH>> bins;
+  std::vector<int> load;
+  for (const QH& h : heads) {
+    size_t i = 0;
+    for (; i < bins.size(); ++i) if (load[i] + h.ni <= K_MAXI) break;
+    if (i == bins.size()) { bins.emplace_back(); load.push_back(0); }
+    bins[i].push_back(h);
+    load[i] += h.ni;
+  }
+  const int n_waves = (int)bins.size();
+  plan.n_wg = (int)ceil_div(n_waves, K_WAVES);
+  if (plan.n_wg > K_MAX_WG) return STARKV_ERR_LIMIT;
+  for (int g = 0; g < K_MAX_WG; ++g)
+    for (int w = 0; w < K_WAVES; ++w)
+      for (int i = 0; i < K_MAXI; ++i) a.items[g][w][i] = 0;
+  // deal bins round-robin so that workgroups get similar loads
+  for (int bi = 0; bi < n_waves; ++bi) {
+    std::vector<QH> v = bins[bi];
+    std::sort(v.begin(), v.end(), [](const QH& x, const QH& y) { return x.qh < y.qh; });
+    const int g = bi % plan.n_wg, w = bi / plan.n_wg;
+    int i = 0;
+    for (const QH& h : v) {
+      const int r = k.rank[h.kv];
+      for (int mt = 0; mt < h.ni; ++mt) {
+        const int nv = std::min(32, r - 32 * mt);
+        a.items[g][w][i++] = item_pack(h.qh, h.kv, mt, nv, mt == h.ni - 1);
+      }
+    }
+  }
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    a.xoff[h] = k.head_offset[h];
+    a.xpitch[h] = (int)k.pos_stride[h];
+    a.bkoff[h] = k.bk_head_offset[h];
+  }
+  a.n_wg = plan.n_wg;
+  return STARKV_OK;
+}
+
+bool k_fast(const starkv_klatent& k, int dtype, const void* q, int64_t q_sb, int64_t q_sh) {
+  const int xe = k.format == STARKV_FMT_INT8_SYM ? 1 : esize(dtype);
+  if (!al(k.data, 16) || !al64(k.stride_b * xe, 16)) return false;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    if (k.rank[h] % (xe == 1 ? 16 : 8)) return false;
+    if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
+    if (!al64(k.bk_head_offset[h] * 2, 8)) return false;
+  }
+  if (!al(k.bk, 8) || !al64(k.bk_row_stride * 2, 8)) return false;
+  if (!al(q, 8) || !al64(q_sb * 2, 8) || !al64(q_sh * 2, 8)) return false;
+  return true;
+}
+
+int check_mask(const void* mask, int mask_dtype) {
+  if (!mask) return STARKV_OK;
+  if (mask_dtype != STARKV_F32 && mask_dtype != STARKV_F16 && mask_dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  return STARKV_OK;
+}
+
+int rope_tiles(int max_positions) { return (int)ceil_div(max_positions, TILE) + 2; }
+
+// ---- decode workspace layout (shared by the size query and the call)
+struct DecodeLayout {
+  int S_pad, n_c1, tiles_per_chunk, n_cb, n_c2, c2_len, Rvp;
+  size_t off_logits, off_cmax, off_part, off_psum, off_olat, off_lsum, off_cnt, total;
+};
+
+DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg) {
+  DecodeLayout L;
+  L.S_pad = (int)round_up(S, 64);
+  const int n_tiles = (int)ceil_div(S, TILE);
+  L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
+  L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
+  L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
+  L.Rvp = (int)round_up(Rv, 32);
+  L.n_cb = (int)ceil_div(L.Rvp / 32, PV_NT_HOST);
+  const int n_ks = (int)ceil_div(S, KSTEP);
+  L.n_c2 = choose_splits((int64_t)B * L.n_cb, MI355X_CUS * K2_WG_PER_CU, n_ks, 64, 128.0 / std::max(S, 1));
+  L.c2_len = (int)ceil_div(n_ks, L.n_c2) * KSTEP;
+  L.n_c2 = (int)ceil_div(S, L.c2_len);
+  size_t o = 0;
+  L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
+  L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
+  L.off_part = o; o = a256(o + (size_t)B * L.n_c2 * 32 * L.Rvp * 4);
+  L.off_psum = o; o = a256(o + (size_t)B * L.n_c2 * 32 * 4);
+  L.off_olat = o; o = a256(o + (size_t)B * 32 * L.Rvp * 4);
+  L.off_lsum = o; o = a256(o + (size_t)B * 32 * 4);
+  L.off_cnt = o; o = a256(o + (size_t)B * L.n_cb * 4);
+  L.total = o;
+  return L;
+}
+
+int validate_vdense(const starkv_vlatent& v, int S) {
+  if (v.format != STARKV_FMT_DENSE) return STARKV_ERR_FORMAT;
+  if (!v.data) return STARKV_ERR_NULL;
+  if (v.rank < 1 || v.rank > MAX_RV) return STARKV_ERR_RANK;
+  if (v.stride_s < v.rank || v.stride_b < 0) return STARKV_ERR_SHAPE;
+  (void)S;
+  return STARKV_OK;
+}
+
+bool v_fast(const starkv_vlatent& v) {
+  return al(v.data, 16) && al64(v.stride_s * 2, 16) && al64(v.stride_b * 2, 16) && v.rank % 8 == 0;
+}
+
+int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S) return STARKV_ERR_SHAPE;
+  if (d->head_dim != HEAD_DIM) return STARKV_ERR_SHAPE;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  if (d->n_q_heads > K2_MAX_H) return STARKV_ERR_LIMIT;
+  int st = validate_klatent(d->k, d->n_q_heads, d->dtype, gs);
+  if (st) return st;
+  if ((st = validate_vdense(d->v, d->seq_len))) return st;
+  if (!d->q || !d->uv || !d->out || !d->rope_table) return STARKV_ERR_NULL;
+  if (d->seq_len > d->rope_max_positions) return STARKV_ERR_SHAPE;
+  if (d->uv_row_stride < d->v.rank) return STARKV_ERR_SHAPE;
+  if ((st = check_mask(d->mask, d->mask_dtype))) return st;
+  if (d->out_dtype != 0 && d->out_dtype != d->dtype && d->out_dtype != STARKV_F32) return STARKV_ERR_DTYPE;
+  KArgs tmp;
+  KPlan plan;
+  if ((st = build_k_plan(d->k, d->n_q_heads, *gs, tmp, plan))) return st;
+  *n_wg = plan.n_wg;
+  return STARKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int starkv_abi_version(void) { return STARKV_ABI_VERSION; }
+
+const char* starkv_status_string(int s) {
+  switch (s) {
+    case STARKV_OK: return "ok";
+    case STARKV_ERR_NULL: return "a required pointer is NULL";
+    case STARKV_ERR_SHAPE: return "inconsistent or unsupported sizes";
+    case STARKV_ERR_DTYPE: return "unsupported element type";
+    case STARKV_ERR_ALIGN: return "pointer or stride misaligned";
+    case STARKV_ERR_RANK: return "latent rank out of range";
+    case STARKV_ERR_WORKSPACE: return "workspace missing or too small";
+    case STARKV_ERR_LIMIT: return "exceeds a compiled limit";
+    case STARKV_ERR_FORMAT: return "unknown quantisation format";
+    default: return s > 0 ? hipGetErrorString((hipError_t)s) : "unknown error";
+  }
+}
+
+size_t starkv_rope_table_bytes(int max_positions) {
+  if (max_positions < 1) return 0;
+  return (size_t)(TILE + rope_tiles(max_positions)) * 64 * 2 * sizeof(float);
+}
+
+int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int max_positions,
+                      void* table, size_t table_bytes, void* stream) {
+  if (!inv_freq_host || !table) return STARKV_ERR_NULL;
+  if (max_positions < 1 || max_positions > MAX_S) return STARKV_ERR_SHAPE;
+  if (table_bytes < starkv_rope_table_bytes(max_positions)) return STARKV_ERR_WORKSPACE;
+  if (!al(table, 16)) return STARKV_ERR_ALIGN;
+  float f[64];
+  for (int i = 0; i < 64; ++i) f[i] = inv_freq_host[i];
+  return launch_rope_tables(f, max_positions, attention_scaling, (float*)table, (hipStream_t)stream);
+}
+
+size_t starkv_k_logits_workspace_bytes(const starkv_klogits_desc*) { return 0; }
+
+int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace; (void)workspace_bytes;
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S || d->head_dim != HEAD_DIM) return STARKV_ERR_SHAPE;
+  int gs = 0, st;
+  if ((st = validate_klatent(d->k, d->n_q_heads, d->dtype, &gs))) return st;
+  if (!d->q || !d->out || !d->rope_table) return STARKV_ERR_NULL;
+  if (d->seq_len > d->rope_max_positions) return STARKV_ERR_SHAPE;
+  if (d->out_dtype != STARKV_F32 && d->out_dtype != STARKV_F16 && d->out_dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  if ((st = check_mask(d->mask, d->mask_dtype))) return st;
+  KArgs a;
+  KPlan plan;
+  if ((st = build_k_plan(d->k, d->n_q_heads, gs, a, plan))) return st;
+  a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h;
+  a.x = d->k.data; a.x_sb = d->k.stride_b;
+  a.xscale = d->k.scale; a.xs_sb = d->k.scale_stride_b; a.xs_sh = d->k.scale_stride_h;
+  a.bk = d->k.bk; a.bk_rs = d->k.bk_row_stride;
+  a.rope = (const float*)d->rope_table;
+  a.mask = d->mask; a.m_sb = d->mask_stride_b; a.m_sh = d->mask_stride_h; a.mask_dtype = d->mask_dtype;
+  a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
+  a.chunkmax = nullptr; a.zero_ptr = nullptr; a.zero_count = 0;
+  a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
+  const int n_tiles = (int)ceil_div(d->seq_len, TILE);
+  int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
+  a.tiles_per_chunk = (int)ceil_div(n_tiles, nc);
+  a.n_chunks = (int)ceil_div(n_tiles, a.tiles_per_chunk);
+  const bool fast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
+  return launch_k_logits(a, d->dtype, d->k.format, d->out_dtype == STARKV_F32, d->out_dtype, fast, d->batch, (hipStream_t)stream);
+}
+
+size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {
+  if (!d || d->batch < 1 || d->seq_len < 1 || d->v.rank < 1) return 0;
+  const int Rvp = (int)round_up(d->v.rank, 32);
+  const int n_cb = (int)ceil_div(Rvp / 32, PV_NT_HOST);
+  const int n_ks = (int)ceil_div(d->seq_len, KSTEP);
+  int n_c2 = choose_splits((int64_t)d->batch * n_cb, MI355X_CUS * K2_WG_PER_CU, n_ks, 64, 128.0 / d->seq_len);
+  const int c2_len = (int)ceil_div(n_ks, n_c2) * KSTEP;
+  n_c2 = (int)ceil_div(d->seq_len, c2_len);
+  return a256((size_t)d->batch * n_c2 * 32 * Rvp * 4) + a256((size_t)d->batch * n_cb * 4);
+}
+
+int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S || d->n_heads < 1) return STARKV_ERR_SHAPE;
+  if (d->n_heads > K2_MAX_H) return STARKV_ERR_LIMIT;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  int st;
+  if ((st = validate_vdense(d->v, d->seq_len))) return st;
+  if (!d->p || !d->out) return STARKV_ERR_NULL;
+  const size_t need = starkv_pv_latent_workspace_bytes(d);
+  if (!workspace || workspace_bytes < need) return STARKV_ERR_WORKSPACE;
+  if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
+  PVArgs a = {};
+  a.Rv = d->v.rank; a.Rvp = (int)round_up(a.Rv, 32);
+  a.n_cb = (int)ceil_div(a.Rvp / 32, PV_NT_HOST);
+  const int n_ks = (int)ceil_div(d->seq_len, KSTEP);
+  int n_c2 = choose_splits((int64_t)d->batch * a.n_cb, MI355X_CUS * K2_WG_PER_CU, n_ks, 64, 128.0 / d->seq_len);
+  a.c2_len = (int)ceil_div(n_ks, n_c2) * KSTEP;
+  a.n_c2 = (int)ceil_div(d->seq_len, a.c2_len);
+  a.x = d->v.data; a.x_sb = d->v.stride_b; a.x_ss = d->v.stride_s;
+  a.p = d->p; a.p_sb = d->p_stride_b; a.p_sh = d->p_stride_h;
+  char* ws = (char*)workspace;
+  a.part = (float*)ws;
+  a.counters = (int*)(ws + a256((size_t)d->batch * a.n_c2 * 32 * a.Rvp * 4));
+  a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
+  a.S = d->seq_len; a.H = d->n_heads;
+  hipStream_t s = (hipStream_t)stream;
+  if ((st = launch_fill_i32(a.counters, d->batch * a.n_cb, 0, s))) return st;
+  return launch_pv(a, d->dtype, false, v_fast(d->v), d->batch, s);
+}
+
+size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
+  int gs = 0, n_wg = 0;
+  if (validate_decode(d, &gs, &n_wg)) return 0;
+  return decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg).total;
+}
+
+static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream,
+                       void* const* events) {
+  int gs = 0, n_wg = 0, st;
+  if ((st = validate_decode(d, &gs, &n_wg))) return st;
+  const DecodeLayout L = decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg);
+  if (!workspace || workspace_bytes < L.total) return STARKV_ERR_WORKSPACE;
+  if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
+  char* ws = (char*)workspace;
+  hipStream_t s = (hipStream_t)stream;
+  const int B = d->batch, Hq = d->n_q_heads;
+
+  KArgs ka;
+  KPlan plan;
+  if ((st = build_k_plan(d->k, Hq, gs, ka, plan))) return st;
+  ka.q = d->q; ka.q_sb = d->q_stride_b; ka.q_sh = d->q_stride_h;
+  ka.x = d->k.data; ka.x_sb = d->k.stride_b;
+  ka.xscale = d->k.scale; ka.xs_sb = d->k.scale_stride_b; ka.xs_sh = d->k.scale_stride_h;
+  ka.bk = d->k.bk; ka.bk_rs = d->k.bk_row_stride;
+  ka.rope = (const float*)d->rope_table;
+  ka.mask = d->mask; ka.m_sb = d->mask_stride_b; ka.m_sh = d->mask_stride_h; ka.mask_dtype = d->mask_dtype;
+  ka.out = ws + L.off_logits; ka.o_sb = (int64_t)Hq * L.S_pad; ka.o_sh = L.S_pad;
+  ka.chunkmax = (float*)(ws + L.off_cmax);
+  ka.zero_ptr = (int*)(ws + L.off_cnt); ka.zero_count = B * L.n_cb;
+  ka.S = d->seq_len; ka.Hq = Hq; ka.n_chunks = L.n_c1; ka.tiles_per_chunk = L.tiles_per_chunk;
+  ka.wscale = d->scale;
+  const bool kfast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
+  if (events && (st = (int)hipEventRecord((hipEvent_t)events[0], s))) return st;
+  if ((st = launch_k_logits(ka, d->dtype, d->k.format, true, STARKV_F32, kfast, B, s))) return st;
+  if (events && (st = (int)hipEventRecord((hipEvent_t)events[1], s))) return st;
+
+  PVArgs pa = {};
+  pa.x = d->v.data; pa.x_sb = d->v.stride_b; pa.x_ss = d->v.stride_s;
+  pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = (int64_t)Hq * L.S_pad; pa.l_sh = L.S_pad;
+  pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
+  pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
+  pa.olat = (float*)(ws + L.off_olat); pa.lsum = (float*)(ws + L.off_lsum);
+  pa.counters = (int*)(ws + L.off_cnt);
+  pa.S = d->seq_len; pa.H = Hq; pa.Rv = d->v.rank; pa.Rvp = L.Rvp;
+  pa.n_cb = L.n_cb; pa.n_c2 = L.n_c2; pa.c2_len = L.c2_len;
+  if ((st = launch_pv(pa, d->dtype, true, v_fast(d->v), B, s))) return st;
+  if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
+
+  UPArgs ua;
+  ua.olat = pa.olat; ua.Rvp = L.Rvp; ua.lsum = pa.lsum;
+  ua.uv = d->uv; ua.uv_rs = d->uv_row_stride;
+  ua.out = d->out; ua.o_sb = d->out_stride_b; ua.o_sh = d->out_stride_h;
+  ua.B = B; ua.Hq = Hq; ua.gs = gs; ua.Rv = d->v.rank;
+  ua.out_f32 = d->out_dtype == STARKV_F32;
+  const bool ufast = al(d->uv, 16) && al64(d->uv_row_stride * 2, 16);
+  if ((st = launch_up_proj(ua, d->dtype, ufast, s))) return st;
+  if (events && (st = (int)hipEventRecord((hipEvent_t)events[3], s))) return st;
+  return STARKV_OK;
+}
+
+int starkv_decode_attention(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_impl(d, workspace, workspace_bytes, stream, nullptr);
+}
+
+int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes,
+                                  void* stream, void* const* events) {
+  if (!events || !events[0] || !events[1] || !events[2] || !events[3]) return STARKV_ERR_NULL;
+  return decode_impl(d, workspace, workspace_bytes, stream, events);
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+// Shared device/host definitions of libstarkv (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/starkv.h"
+
+namespace starkv {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int HEAD_DIM = 128;
+constexpr int TILE = 32;            // positions per K-logit tile (the MFMA N dimension)
+constexpr int KSTEP = 16;           // positions per P.V MFMA K-step
+
+// ---------------------------------------------------------------------------
+// K-logit launch plan (passed by value as a kernel argument, read with
+// scalar loads).  A workgroup runs 4 waves; wave w of workgroup-plan g owns
+// up to K_MAXI "items"; an item is one 32-rank M-tile of one query head.
+// ---------------------------------------------------------------------------
+constexpr int K_WAVES = 4;
+constexpr int K_MAXI = 4;
+constexpr int K_MAX_WG = 16;
+constexpr int K_MAX_KV = 64;
+constexpr int K_MAX_QH = 64;
+
+// item word: qhead[0:8) kv[8:16) mtile[16:20) nvalid[20:26) last_of_q[26] valid[27]
+__host__ __device__ inline uint32_t item_pack(int qh, int kv, int mt, int nv, int last) {
+  return (uint32_t)qh | ((uint32_t)kv << 8) | ((uint32_t)mt << 16) | ((uint32_t)nv << 20) |
+         ((uint32_t)(last ? 1 : 0) << 26) | (1u << 27);
+}
+__device__ inline int item_qh(uint32_t w) { return w & 0xff; }
+__device__ inline int item_kv(uint32_t w) { return (w >> 8) & 0xff; }
+__device__ inline int item_mt(uint32_t w) { return (w >> 16) & 0xf; }
+__device__ inline int item_nv(uint32_t w) { return (w >> 20) & 0x3f; }
+__device__ inline bool item_last(uint32_t w) { return (w >> 26) & 1; }
+__device__ inline bool item_valid(uint32_t w) { return (w >> 27) & 1; }
+
+struct KArgs {
+  const void* q; int64_t q_sb, q_sh;
+  const void* x; int64_t x_sb;
+  const void* xscale; int64_t xs_sb, xs_sh;       // int8 K scales (fp16)
+  const void* bk; int64_t bk_rs;
+  const float* rope;                               // T0 [32][64][2] then RT [tiles][64][2]
+  const void* mask; int64_t m_sb, m_sh; int mask_dtype;
+  void* out; int64_t o_sb, o_sh;
+  float* chunkmax;                                 // [B][Hq][n_chunks] (optional)
+  int* zero_ptr; int zero_count;                   // counters to clear (optional)
+  int S, Hq, n_chunks, tiles_per_chunk, n_wg;
+  float wscale;                                    // softmax scale * rope attention scaling
+  int64_t xoff[K_MAX_KV];
+  int xpitch[K_MAX_KV];
+  int64_t bkoff[K_MAX_KV];
+  uint32_t items[K_MAX_WG][K_WAVES][K_MAXI];
+};
+
+// ---------------------------------------------------------------------------
+// P.V launch arguments.
+// ---------------------------------------------------------------------------
+struct PVArgs {
+  const void* x; int64_t x_sb, x_ss;               // dense V latent
+  const float* logits; int64_t l_sb, l_sh;         // fused path: fp32 logits
+  const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
+  const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
+  float* part;                                     // [B][n_c2][32][Rvp] fp32
+  float* psum;                                     // [B][n_c2][32]
+  float* olat;                                     // [B][32][Rvp] fp32 (fused) ...
+  void* out; int64_t o_sb, o_sh;                   // ... or act-dtype [B][H][Rv] (drop-in)
+  float* lsum;                                     // [B][32] softmax denominators (fused)
+  int* counters;                                   // [B][n_cb]
+  int S, H, Rv, Rvp, n_cb, n_c2, c2_len;
+};
+
+// ---------------------------------------------------------------------------
+// Up-projection arguments.
+// ---------------------------------------------------------------------------
+struct UPArgs {
+  const float* olat; int Rvp;                      // [B][32][Rvp]
+  const float* lsum;                               // [B][32]
+  const void* uv; int64_t uv_rs;                   // [Hkv*128][Rv]
+  void* out; int64_t o_sb, o_sh;                   // [B][Hq][128]
+  int B, Hq, gs, Rv;
+  int out_f32;                                     // 1: fp32 output, 0: weight dtype
+};
+
+// ---------------------------------------------------------------------------
+// small helpers
+// ---------------------------------------------------------------------------
+template <typename T> struct ElemTraits;
+template <> struct ElemTraits<_Float16> { static constexpr int code = STARKV_F16; };
+template <> struct ElemTraits<__bf16> { static constexpr int code = STARKV_BF16; };
+
+__device__ inline float bf16_bits_to_float(uint32_t lo16) { return __uint_as_float(lo16 << 16); }
+
+__device__ inline float to_f32(_Float16 h) { return (float)h; }
+__device__ inline float to_f32(__bf16 h) { return (float)h; }
+
+template <typename T> __device__ inline T from_f32(float f);
+template <> __device__ inline _Float16 from_f32<_Float16>(float f) { return (_Float16)f; }
+template <> __device__ inline __bf16 from_f32<__bf16>(float f) { return (__bf16)f; }
+template <> __device__ inline float from_f32<float>(float f) { return f; }
+
+__device__ inline float load_elem_f32(const void* p, int dtype, int64_t idx) {
+  if (dtype == STARKV_F32) return ((const float*)p)[idx];
+  if (dtype == STARKV_F16) return (float)((const _Float16*)p)[idx];
+  return (float)((const __bf16*)p)[idx];
+}
+
+__device__ inline floatx16 mfma_f16(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ inline floatx16 mfma_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// value of lane (l ^ 32): sum of the two halves of a wave64
+__device__ inline float add_halves(float v) {
+  auto x = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(x[0]) + __int_as_float(x[1]);
+}
+
+__device__ inline float wave_max32(float v) {   // max over the 32 lanes of a half wave
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// launchers (return hipError_t as int; 0 on success)
+int launch_rope_tables(const float* inv_freq_host, int max_positions, float scaling, float* table, hipStream_t st);
+int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
+int launch_pv(const PVArgs& a, int dtype, bool fused, bool fast, int B, hipStream_t st);
+int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
+int launch_fill_i32(int* p, int n, int v, hipStream_t st);
+
+}  // namespace starkv

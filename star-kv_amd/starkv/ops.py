@@ -1,0 +1,257 @@
+"""Torch-facing operators over the libstarkv C ABI.
+
+Tensors stay where they are (borrowed device pointers, arbitrary strides with
+a contiguous last dimension); outputs and workspaces are allocated through
+torch's caching allocator; work is enqueued on torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT8_SYM, DecodeDesc, KLatent, KLogitsDesc, PVDesc,
+                   StarKVError, VLatent, check, i64_array, int_array)
+from .rope import RopeConfig, rope_table
+
+HEAD_DIM = 128
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.float16:
+        return F16
+    if t.dtype == torch.bfloat16:
+        return BF16
+    if t.dtype == torch.float32:
+        return F32
+    raise StarKVError(f"unsupported dtype {t.dtype}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise StarKVError("libstarkv operators take device tensors (there is no CPU path)")
+
+
+_WS: dict = {}
+
+
+def _workspace(device, nbytes: int) -> torch.Tensor:
+    """Per-device scratch reused across calls (ordered on one stream)."""
+    key = torch.device(device)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+class KLatentSpec:
+    """Where the key latent of every KV head lives (see include/starkv.h,
+    starkv_klatent).  Element (b, h, s, j) is at
+    data[b*stride_b + head_offset[h] + s*pos_stride[h] + j]; B_k (k_u^T) row j
+    of head h at bk[bk_head_offset[h] + j*bk_row_stride]."""
+
+    def __init__(self, data: torch.Tensor, ranks: Sequence[int], head_offset: Sequence[int],
+                 pos_stride: Sequence[int], stride_b: int, bk: torch.Tensor, bk_head_offset: Sequence[int],
+                 bk_row_stride: int, fmt: int = FMT_DENSE, scale: Optional[torch.Tensor] = None,
+                 scale_stride_b: int = 0, scale_stride_h: int = 0):
+        self.data, self.bk, self.scale = data, bk, scale
+        self.ranks = [int(r) for r in ranks]
+        self.head_offset = [int(v) for v in head_offset]
+        self.pos_stride = [int(v) for v in pos_stride]
+        self.stride_b = int(stride_b)
+        self.bk_head_offset = [int(v) for v in bk_head_offset]
+        self.bk_row_stride = int(bk_row_stride)
+        self.fmt = fmt
+        self.scale_stride_b, self.scale_stride_h = int(scale_stride_b), int(scale_stride_h)
+
+    @property
+    def n_kv_heads(self) -> int:
+        return len(self.ranks)
+
+    @classmethod
+    def from_reference(cls, x: torch.Tensor, b: torch.Tensor) -> "KLatentSpec":
+        """The reference layouts: x = K latent cache [B, Hkv, S, r]
+        (LlamaLoRaAttention_headwise.py:88-102), b = k_u^T [Hkv, r, 128]
+        (model.py:455)."""
+        if x.dim() != 4 or b.dim() != 3:
+            raise StarKVError("expected x [B, Hkv, S, r] and b [Hkv, r, 128]")
+        B, H, S, r = x.shape
+        if b.shape[0] != H or b.shape[1] != r or b.shape[2] != HEAD_DIM:
+            raise StarKVError(f"b shape {tuple(b.shape)} does not match x {tuple(x.shape)}")
+        if x.stride(3) != 1 or b.stride(2) != 1:
+            raise StarKVError("the last dimension of x and b must be contiguous")
+        return cls(x, [r] * H, [h * x.stride(1) for h in range(H)], [x.stride(2)] * H, x.stride(0),
+                   b, [h * b.stride(0) for h in range(H)], b.stride(1))
+
+    def c_struct(self, keep: list) -> KLatent:
+        arrs = (int_array(self.ranks), i64_array(self.head_offset), i64_array(self.pos_stride),
+                i64_array(self.bk_head_offset))
+        keep.extend(arrs)
+        k = KLatent()
+        k.n_kv_heads = self.n_kv_heads
+        k.rank, k.head_offset, k.pos_stride, k.bk_head_offset = arrs
+        k.stride_b = self.stride_b
+        k.format = self.fmt
+        k.data = self.data.data_ptr()
+        k.scale = self.scale.data_ptr() if self.scale is not None else None
+        k.scale_stride_b, k.scale_stride_h = self.scale_stride_b, self.scale_stride_h
+        k.bk = self.bk.data_ptr()
+        k.bk_row_stride = self.bk_row_stride
+        return k
+
+
+def _q3(q: torch.Tensor) -> torch.Tensor:
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise StarKVError("decode takes one query token per sequence")
+        q = q[:, :, 0, :]
+    if q.dim() != 3 or q.shape[-1] != HEAD_DIM or q.stride(-1) != 1:
+        raise StarKVError("q must be [B, Hq, 128] (or [B, Hq, 1, 128]) with a contiguous last dim")
+    return q
+
+
+def _mask_args(mask: Optional[torch.Tensor], B: int, S: int):
+    """Accept an additive mask broadcastable to [B, Hq, S] (HF's [B, 1, 1, S>=S] included)."""
+    if mask is None:
+        return None, 0, 0, 0
+    m = mask
+    while m.dim() > 3:
+        if m.shape[-2] != 1:
+            raise StarKVError("decode masks must have one query row")
+        m = m.select(-2, 0)
+    if m.dim() == 2:
+        m = m[:, None, :]
+    if m.shape[-1] < S or m.stride(-1) != 1:
+        raise StarKVError("mask must cover S positions with a contiguous last dim")
+    sb = m.stride(0) if m.shape[0] == B else 0
+    sh = m.stride(1) if m.shape[1] != 1 else 0
+    return m, _dt(m), sb, sh
+
+
+def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = RopeConfig(),
+             scale: float = 1.0, mask: Optional[torch.Tensor] = None,
+             out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """logits[b, q, s] = scale * q_rot[b,q] . RoPE_s(X_k[b, q//gs, s] @ B_k[q//gs]) (+ mask), [B, Hq, S]."""
+    q = _q3(q)
+    _require_cuda(q, k.data, k.bk, mask)
+    B, Hq, _ = q.shape
+    S = int(seq_len)
+    out_dtype = out_dtype or torch.float32
+    out = torch.empty(B, Hq, S, dtype=out_dtype, device=q.device)
+    table, cap = rope_table(rope, S, q.device)
+    m, mdt, msb, msh = _mask_args(mask, B, S)
+    keep: list = []
+    d = KLogitsDesc()
+    d.batch, d.n_q_heads, d.head_dim, d.seq_len = B, Hq, HEAD_DIM, S
+    d.dtype = _dt(q)
+    d.q, d.q_stride_b, d.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    d.k = k.c_struct(keep)
+    d.rope_table, d.rope_max_positions = table.data_ptr(), cap
+    d.scale = float(scale) * rope.attention_scaling
+    d.mask = m.data_ptr() if m is not None else None
+    d.mask_dtype, d.mask_stride_b, d.mask_stride_h = mdt, msb, msh
+    d.out, d.out_dtype, d.out_stride_b, d.out_stride_h = out.data_ptr(), _dt(out), out.stride(0), out.stride(1)
+    check(_lib.lib().starkv_k_logits(ctypes.byref(d), None, 0, _stream(q.device)), "starkv_k_logits")
+    return out
+
+
+def _vdense(xv: torch.Tensor) -> VLatent:
+    if xv.dim() != 3 or xv.stride(2) != 1:
+        raise StarKVError("V latent must be [B, S, Rv] with a contiguous last dim")
+    v = VLatent()
+    v.rank, v.format = xv.shape[2], FMT_DENSE
+    v.data, v.stride_b, v.stride_s = xv.data_ptr(), xv.stride(0), xv.stride(1)
+    return v
+
+
+def pv_latent(p: torch.Tensor, xv: torch.Tensor) -> torch.Tensor:
+    """out[b, h, j] = sum_s p[b, h, s] * xv[b, s, j]  (model.py:484), [B, H, Rv] in p's dtype."""
+    _require_cuda(p, xv)
+    if p.dim() != 3 or p.stride(2) != 1:
+        raise StarKVError("p must be [B, H, S] with a contiguous last dim")
+    B, H, S = p.shape
+    if xv.shape[0] != B or xv.shape[1] < S:
+        raise StarKVError("xv must be [B, >=S, Rv]")
+    out = torch.empty(B, H, xv.shape[2], dtype=p.dtype, device=p.device)
+    d = PVDesc()
+    d.batch, d.n_heads, d.seq_len, d.dtype = B, H, S, _dt(p)
+    d.p, d.p_stride_b, d.p_stride_h = p.data_ptr(), p.stride(0), p.stride(1)
+    d.v = _vdense(xv)
+    d.out, d.out_stride_b, d.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    L = _lib.lib()
+    nb = L.starkv_pv_latent_workspace_bytes(ctypes.byref(d))
+    ws = _workspace(p.device, nb)
+    check(L.starkv_pv_latent(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(p.device)),
+          "starkv_pv_latent")
+    return out
+
+
+def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weight: torch.Tensor,
+                     rope: RopeConfig = RopeConfig(), seq_len: Optional[int] = None,
+                     mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                     out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+                     events: Optional[Sequence] = None) -> torch.Tensor:
+    """Fused decode attention core (model.py:450-487): [B, Hq, 128] in q's dtype
+    (or float32 with out_dtype=torch.float32).  ``events``: four
+    torch.cuda.Event recorded around the three kernels (timing).
+
+    q: rotated query [B, Hq, 128]; k: key-latent spec; xv: V latent [B, S, Rv];
+    uv_weight: v_proj.U.weight [Hkv*128, Rv]; seq_len defaults to xv.shape[1]."""
+    q = _q3(q)
+    _require_cuda(q, k.data, k.bk, xv, uv_weight, mask)
+    B, Hq, _ = q.shape
+    S = int(seq_len if seq_len is not None else xv.shape[1])
+    if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape[1] != xv.shape[2]:
+        raise StarKVError("uv_weight must be [Hkv*128, Rv] with a contiguous last dim")
+    if uv_weight.shape[0] != k.n_kv_heads * HEAD_DIM:
+        raise StarKVError("uv_weight rows must be Hkv*128")
+    if out is None:
+        out = torch.empty(B, Hq, HEAD_DIM, dtype=out_dtype or q.dtype, device=q.device)
+    if out.dtype not in (q.dtype, torch.float32) or out.stride(-1) != 1:
+        raise StarKVError("out must be [B, Hq, 128] of q's dtype or float32")
+    table, cap = rope_table(rope, S, q.device)
+    m, mdt, msb, msh = _mask_args(mask, B, S)
+    keep: list = []
+    d = DecodeDesc()
+    d.batch, d.n_q_heads, d.head_dim, d.seq_len = B, Hq, HEAD_DIM, S
+    d.dtype = _dt(q)
+    d.q, d.q_stride_b, d.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    d.k = k.c_struct(keep)
+    d.v = _vdense(xv)
+    d.uv, d.uv_row_stride = uv_weight.data_ptr(), uv_weight.stride(0)
+    d.rope_table, d.rope_max_positions = table.data_ptr(), cap
+    d.scale = float(scale if scale is not None else 1.0 / math.sqrt(HEAD_DIM)) * rope.attention_scaling
+    d.mask = m.data_ptr() if m is not None else None
+    d.mask_dtype, d.mask_stride_b, d.mask_stride_h = mdt, msb, msh
+    d.out, d.out_stride_b, d.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    d.out_dtype = F32 if out.dtype == torch.float32 else 0
+    L = _lib.lib()
+    nb = L.starkv_decode_workspace_bytes(ctypes.byref(d))
+    if nb == 0:
+        # re-run validation through the call itself to surface the status code
+        check(L.starkv_decode_attention(ctypes.byref(d), None, 0, _stream(q.device)), "starkv_decode_attention")
+    ws = _workspace(q.device, nb)
+    if events is None:
+        check(L.starkv_decode_attention(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                        _stream(q.device)), "starkv_decode_attention")
+    else:
+        for e in events:
+            if e.cuda_event == 0:
+                e.record()   # creates the underlying hipEvent
+        handles = (ctypes.c_void_p * 4)(*[e.cuda_event for e in events])
+        check(L.starkv_decode_attention_timed(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                              _stream(q.device), handles), "starkv_decode_attention_timed")
+    return out

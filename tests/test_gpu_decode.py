@@ -1,0 +1,132 @@
+"""GPU parity of the fused decode path and the K-logit / P.V entry points
+against the CPU oracle (oracle/starkv_oracle.py), same seeded inputs.
+
+Gates: attention outputs within max-abs 2e-2 and
+mean-rel 1e-3 of the fp32/fp64 eager oracle."""
+import math
+
+import pytest
+import torch
+
+from _util import cfg2_ranks, cfg4_ranks, errors, make_case, oracle_decode, oracle_logits
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_REL = 1e-3
+
+
+def _flush(msg):
+    print(msg, flush=True)
+
+
+def _run_decode(case, rope=None, mask=None, out_dtype=None):
+    from starkv import RopeConfig, decode_attention
+    rope = rope or RopeConfig()
+    return decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, mask=mask, out_dtype=out_dtype)
+
+
+def _check(case, ref, rope=None, mask=None):
+    """fp16 cases gate the stored output; bf16 cases gate the fp32 output
+    (bf16 storage alone costs ~1.4e-3 mean-rel) and check the stored bf16
+    output against the oracle rounded to bf16."""
+    if case.dtype == torch.bfloat16:
+        out32 = _run_decode(case, rope, mask, out_dtype=torch.float32)
+        outbf = _run_decode(case, rope, mask)
+        mx, mr = errors(out32, ref)
+        d = (outbf.float().cpu().double() - ref.to(torch.bfloat16).double()).abs()
+        mr_bf = float(d.mean() / ref.abs().mean())
+        _flush(f"   fp32-out max_abs={mx:.3e} mean_rel={mr:.3e}; bf16-out vs bf16(ref) mean_rel={mr_bf:.3e}")
+        assert mr_bf <= MEAN_REL, mr_bf
+    else:
+        out = _run_decode(case, rope, mask)
+        assert torch.isfinite(out).all()
+        mx, mr = errors(out, ref)
+        _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
+
+
+CASES = [
+    # name, B, Hq, Hkv, S, ranks, Rv, dtype, layout
+    ("mha_uniform_ref", 2, 32, 32, 1000, [32] * 32, 256, torch.float16, "reference"),
+    ("mha_ragged_cfg2ranks", 2, 32, 32, 777, None, 1640, torch.float16, "ragged"),
+    ("gqa4_ragged", 2, 32, 8, 1500, [32, 128, 32, 80, 32, 64, 80, 64], 512, torch.float16, "ragged"),
+    ("bf16_ragged", 2, 32, 32, 600, None, 1640, torch.bfloat16, "ragged"),
+    ("s1", 3, 32, 32, 1, [16] * 32, 64, torch.float16, "reference"),
+    ("s33_rv40", 1, 32, 32, 33, [24] * 32, 40, torch.float16, "reference"),
+    ("unaligned_r_rv", 2, 32, 32, 129, [20] * 32, 50, torch.float16, "reference"),
+    ("mqa_hq8", 2, 8, 1, 300, [128], 128, torch.float16, "ragged"),
+]
+
+
+@pytest.mark.parametrize("name,B,Hq,Hkv,S,ranks,Rv,dtype,layout", CASES, ids=[c[0] for c in CASES])
+def test_decode_matches_oracle(name, B, Hq, Hkv, S, ranks, Rv, dtype, layout):
+    ranks = ranks or cfg2_ranks()
+    _flush(f"[decode] {name} B={B} Hq={Hq} Hkv={Hkv} S={S} Rv={Rv} {dtype}")
+    case = make_case(B, Hq, Hkv, S, ranks, Rv, dtype=dtype, seed=1, layout=layout)
+    ref, _, _ = oracle_decode(case)
+    _check(case, ref)
+
+
+def test_decode_llama3_rope_gqa_bf16():
+    from starkv import RopeConfig
+    rope = RopeConfig(theta=500000.0, rope_type="llama3", factor=8.0, low_freq_factor=1.0,
+                      high_freq_factor=4.0, original_max_position_embeddings=8192)
+    case = make_case(1, 32, 8, 9000, cfg4_ranks(), 512, dtype=torch.bfloat16, seed=2)
+    _flush("[decode] llama3 gqa bf16 S=9000")
+    ref, _, _ = oracle_decode(case, rope=rope)
+    _check(case, ref, rope=rope)
+
+
+def test_decode_with_mask():
+    case = make_case(2, 32, 32, 500, [32] * 32, 256, seed=3, layout="reference")
+    mask = torch.zeros(2, 1, 1, 500, device="cuda", dtype=torch.float16)
+    mask[0, ..., :100] = torch.finfo(torch.float16).min     # left padding of sequence 0
+    mask[1, ..., 450:] = -5.0
+    out = _run_decode(case, mask=mask)
+    ref, _, _ = oracle_decode(case, mask=mask.float().view(2, 1, 500))
+    mx, mr = errors(out, ref)
+    assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
+
+
+def test_decode_deterministic():
+    case = make_case(4, 32, 32, 3000, cfg2_ranks(), 1640, seed=4)
+    a = _run_decode(case).clone()
+    b = _run_decode(case).clone()
+    assert torch.equal(a, b)
+
+
+def test_k_logits_matches_oracle():
+    from starkv import RopeConfig, k_logits
+    case = make_case(2, 32, 32, 1234, cfg2_ranks(), 64, seed=5)
+    out = k_logits(case.q, case.kspec, case.S, RopeConfig(), scale=1.0)
+    ref = oracle_logits(case)
+    mx, mr = errors(out, ref)
+    _flush(f"[k_logits] max_abs={mx:.3e} mean_rel={mr:.3e} ref_rms={ref.pow(2).mean().sqrt():.3f}")
+    assert mr <= 1e-3 and mx <= 2e-2 * float(ref.abs().max()), (mx, mr)
+
+
+def test_pv_latent_matches_oracle():
+    from starkv import pv_latent
+    g = torch.Generator(device="cuda").manual_seed(6)
+    B, H, S, Rv = 3, 32, 2000, 1640
+    p = torch.softmax(torch.randn(B, H, S, device="cuda", generator=g), -1).half()
+    xv = torch.randn(B, S, Rv, device="cuda", generator=g).half()
+    out = pv_latent(p, xv)
+    ref = p.double().cpu() @ xv.double().cpu()
+    mx, mr = errors(out, ref)
+    assert mr <= 1e-3 and mx <= 2e-2, (mx, mr)
+
+
+@pytest.mark.parametrize("batch_sel", [[0], [15]])
+def test_decode_cfg2_full_shape(batch_sel):
+    """The benchmark workload itself (B16, S32768, ragged ranks sum 1640,
+    Rv 1640, fp16): all 16 batches run on the GPU; the oracle (fp32 on the CPU)
+    checks the selected batch."""
+    case = make_case(16, 32, 32, 32768, cfg2_ranks(), 1640, seed=0)
+    _flush(f"[decode] cfg2 full shape, checking batch {batch_sel}")
+    out = _run_decode(case)
+    ref, _, _ = oracle_decode(case, batches=batch_sel, dtype=torch.float32)
+    mx, mr = errors(out[batch_sel], ref)
+    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
