@@ -12,9 +12,7 @@ using namespace starkv;
 namespace {
 
 constexpr int MI355X_CUS = 256;     // launch geometry is planned for one MI355X
-constexpr int K1_WG_PER_CU = 1;     // k_logits_kernel: __launch_bounds__(256, 1)
-constexpr int K2_WG_PER_CU = 2;     // pv_kernel: __launch_bounds__(256, 2)
-constexpr int PV_NT_HOST = 8;       // N-tiles (of 32 ranks) per P.V workgroup
+constexpr int K1_WG_PER_CU = 1;     // k_logits_kernel: one 8-wave (or 4-wave) workgroup per CU
 constexpr int MAX_S = 1 << 24;
 constexpr int MAX_RV = 8192;
 constexpr int K2_MAX_H = 32;
@@ -73,32 +71,37 @@ int validate_klatent(const starkv_klatent& k, int Hq, int dtype, int* gs_out) {
   return STARKV_OK;
 }
 
-// Pack (query head, 32-rank M-tile) items into waves of K_MAXI items (first
-// fit decreasing, whole heads per wave) and waves into 4-wave workgroups.
+// Pack (query head, 32-rank M-tile) items into waves of up to 2 or 4 items
+// (first fit decreasing, whole heads per wave; 4 once any head has rank > 64)
+// and deal the waves round-robin over workgroups of 8 waves (2-item waves) or
+// 4 waves (4-item waves).
 int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan) {
   struct QH { int qh, kv, ni; };
   std::vector<QH> heads;
+  int max_ni = 1;
   for (int qh = 0; qh < Hq; ++qh) {
     const int kv = qh / gs;
-    heads.push_back({qh, kv, (int)ceil_div(k.rank[kv], 32)});
+    const int ni = (int)ceil_div(k.rank[kv], 32);
+    max_ni = std::max(max_ni, ni);
+    heads.push_back({qh, kv, ni});
   }
+  const int maxi = max_ni <= 2 ? 2 : 4;   // whole heads per wave
+  const int nw = maxi == 2 ? 8 : 4;
   std::stable_sort(heads.begin(), heads.end(), [](const QH& x, const QH& y) { return x.ni > y.ni; });
   std::vector<std::vector<QH>> bins;
   std::vector<int> load;
   for (const QH& h : heads) {
     size_t i = 0;
-    for (; i < bins.size(); ++i) if (load[i] + h.ni <= K_MAXI) break;
+    for (; i < bins.size(); ++i) if (load[i] + h.ni <= maxi) break;
     if (i == bins.size()) { bins.emplace_back(); load.push_back(0); }
     bins[i].push_back(h);
     load[i] += h.ni;
   }
   const int n_waves = (int)bins.size();
-  plan.n_wg = (int)ceil_div(n_waves, K_WAVES);
-  if (plan.n_wg > K_MAX_WG) return STARKV_ERR_LIMIT;
-  for (int g = 0; g < K_MAX_WG; ++g)
-    for (int w = 0; w < K_WAVES; ++w)
-      for (int i = 0; i < K_MAXI; ++i) a.items[g][w][i] = 0;
-  // deal bins round-robin so that workgroups get similar loads
+  plan.n_wg = (int)ceil_div(n_waves, nw);
+  if (plan.n_wg * nw > K_MAX_WAVES) return STARKV_ERR_LIMIT;
+  for (int w = 0; w < K_MAX_WAVES; ++w)
+    for (int i = 0; i < K_MAXI; ++i) a.items[w][i] = 0;
   for (int bi = 0; bi < n_waves; ++bi) {
     std::vector<QH> v = bins[bi];
     std::sort(v.begin(), v.end(), [](const QH& x, const QH& y) { return x.qh < y.qh; });
@@ -108,7 +111,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan)
       const int r = k.rank[h.kv];
       for (int mt = 0; mt < h.ni; ++mt) {
         const int nv = std::min(32, r - 32 * mt);
-        a.items[g][w][i++] = item_pack(h.qh, h.kv, mt, nv, mt == h.ni - 1);
+        a.items[g * nw + w][i++] = item_pack(h.qh, h.kv, mt, nv, mt == h.ni - 1);
       }
     }
   }
@@ -118,6 +121,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan)
     a.bkoff[h] = k.bk_head_offset[h];
   }
   a.n_wg = plan.n_wg;
+  a.maxi = maxi;
   return STARKV_OK;
 }
 
@@ -140,12 +144,31 @@ int check_mask(const void* mask, int mask_dtype) {
   return STARKV_OK;
 }
 
-int rope_tiles(int max_positions) { return (int)ceil_div(max_positions, TILE) + 2; }
+
+// ---- P.V geometry: workgroup = 4 waves x NTW column tiles of one position chunk
+struct PVGeom {
+  int Rvp, n_cb, n_c2, c2_len;
+};
+
+PVGeom pv_geometry(int B, int S, int Rv, bool fused) {
+  PVGeom g;
+  g.Rvp = (int)round_up(Rv, 32);
+  const int ntw = pv_tiles_per_wave(g.Rvp, fused);
+  g.n_cb = (int)ceil_div(g.Rvp / 32, 4 * ntw);
+  const int wg_per_cu = ntw >= 8 ? 1 : 2;    // registers / LDS staging allow one workgroup per CU from NTW 8
+  const int n_ks = (int)ceil_div(S, KSTEP);
+  // each extra split writes and re-reads one fp32 partial (~128/S of the X_v stream)
+  int n = choose_splits((int64_t)B * g.n_cb, MI355X_CUS * wg_per_cu, n_ks, 64, 128.0 / std::max(S, 1));
+  g.c2_len = (int)ceil_div(n_ks, n) * KSTEP;
+  g.n_c2 = (int)ceil_div(S, g.c2_len);
+  return g;
+}
 
 // ---- decode workspace layout (shared by the size query and the call)
 struct DecodeLayout {
-  int S_pad, n_c1, tiles_per_chunk, n_cb, n_c2, c2_len, Rvp;
-  size_t off_logits, off_cmax, off_part, off_psum, off_olat, off_lsum, off_cnt, total;
+  int S_pad, n_c1, tiles_per_chunk;
+  PVGeom pv;
+  size_t off_logits, off_cmax, off_part, off_psum, off_olat, off_lsum, total;
 };
 
 DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg) {
@@ -155,20 +178,15 @@ DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg) {
   L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
-  L.Rvp = (int)round_up(Rv, 32);
-  L.n_cb = (int)ceil_div(L.Rvp / 32, PV_NT_HOST);
-  const int n_ks = (int)ceil_div(S, KSTEP);
-  L.n_c2 = choose_splits((int64_t)B * L.n_cb, MI355X_CUS * K2_WG_PER_CU, n_ks, 64, 128.0 / std::max(S, 1));
-  L.c2_len = (int)ceil_div(n_ks, L.n_c2) * KSTEP;
-  L.n_c2 = (int)ceil_div(S, L.c2_len);
+  L.pv = pv_geometry(B, S, Rv, true);
+  const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
-  L.off_part = o; o = a256(o + (size_t)B * L.n_c2 * 32 * L.Rvp * 4);
-  L.off_psum = o; o = a256(o + (size_t)B * L.n_c2 * 32 * 4);
-  L.off_olat = o; o = a256(o + (size_t)B * 32 * L.Rvp * 4);
+  L.off_part = o; o = a256(o + (size_t)B * n_c2 * 32 * Rvp * 4);
+  L.off_psum = o; o = a256(o + (size_t)B * n_c2 * 32 * 4);
+  L.off_olat = o; o = a256(o + (size_t)B * 32 * Rvp * 4);
   L.off_lsum = o; o = a256(o + (size_t)B * 32 * 4);
-  L.off_cnt = o; o = a256(o + (size_t)B * L.n_cb * 4);
   L.total = o;
   return L;
 }
@@ -230,7 +248,7 @@ const char* starkv_status_string(int s) {
 
 size_t starkv_rope_table_bytes(int max_positions) {
   if (max_positions < 1) return 0;
-  return (size_t)(TILE + rope_tiles(max_positions)) * 64 * 2 * sizeof(float);
+  return (size_t)rope_table_tiles(max_positions) * 512 * 16;
 }
 
 int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int max_positions,
@@ -241,7 +259,7 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
   if (!al(table, 16)) return STARKV_ERR_ALIGN;
   float f[64];
   for (int i = 0; i < 64; ++i) f[i] = inv_freq_host[i];
-  return launch_rope_tables(f, max_positions, attention_scaling, (float*)table, (hipStream_t)stream);
+  return launch_rope_table(f, max_positions, attention_scaling, table, (hipStream_t)stream);
 }
 
 size_t starkv_k_logits_workspace_bytes(const starkv_klogits_desc*) { return 0; }
@@ -263,10 +281,10 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.x = d->k.data; a.x_sb = d->k.stride_b;
   a.xscale = d->k.scale; a.xs_sb = d->k.scale_stride_b; a.xs_sh = d->k.scale_stride_h;
   a.bk = d->k.bk; a.bk_rs = d->k.bk_row_stride;
-  a.rope = (const float*)d->rope_table;
+  a.rope = (const uint4*)d->rope_table;
   a.mask = d->mask; a.m_sb = d->mask_stride_b; a.m_sh = d->mask_stride_h; a.mask_dtype = d->mask_dtype;
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
-  a.chunkmax = nullptr; a.zero_ptr = nullptr; a.zero_count = 0;
+  a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
   const int n_tiles = (int)ceil_div(d->seq_len, TILE);
   int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
@@ -278,13 +296,8 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
 
 size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {
   if (!d || d->batch < 1 || d->seq_len < 1 || d->v.rank < 1) return 0;
-  const int Rvp = (int)round_up(d->v.rank, 32);
-  const int n_cb = (int)ceil_div(Rvp / 32, PV_NT_HOST);
-  const int n_ks = (int)ceil_div(d->seq_len, KSTEP);
-  int n_c2 = choose_splits((int64_t)d->batch * n_cb, MI355X_CUS * K2_WG_PER_CU, n_ks, 64, 128.0 / d->seq_len);
-  const int c2_len = (int)ceil_div(n_ks, n_c2) * KSTEP;
-  n_c2 = (int)ceil_div(d->seq_len, c2_len);
-  return a256((size_t)d->batch * n_c2 * 32 * Rvp * 4) + a256((size_t)d->batch * n_cb * 4);
+  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false);
+  return a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4);
 }
 
 int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
@@ -299,22 +312,15 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
   if (!workspace || workspace_bytes < need) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   PVArgs a = {};
-  a.Rv = d->v.rank; a.Rvp = (int)round_up(a.Rv, 32);
-  a.n_cb = (int)ceil_div(a.Rvp / 32, PV_NT_HOST);
-  const int n_ks = (int)ceil_div(d->seq_len, KSTEP);
-  int n_c2 = choose_splits((int64_t)d->batch * a.n_cb, MI355X_CUS * K2_WG_PER_CU, n_ks, 64, 128.0 / d->seq_len);
-  a.c2_len = (int)ceil_div(n_ks, n_c2) * KSTEP;
-  a.n_c2 = (int)ceil_div(d->seq_len, a.c2_len);
+  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false);
+  a.Rv = d->v.rank; a.Rvp = g.Rvp; a.n_cb = g.n_cb; a.n_c2 = g.n_c2; a.c2_len = g.c2_len;
   a.x = d->v.data; a.x_sb = d->v.stride_b; a.x_ss = d->v.stride_s;
   a.p = d->p; a.p_sb = d->p_stride_b; a.p_sh = d->p_stride_h;
-  char* ws = (char*)workspace;
-  a.part = (float*)ws;
-  a.counters = (int*)(ws + a256((size_t)d->batch * a.n_c2 * 32 * a.Rvp * 4));
+  a.p_vec = al(d->p, 16) && al64(d->p_stride_b * 2, 16) && al64(d->p_stride_h * 2, 16);
+  a.part = (float*)workspace;
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
   a.S = d->seq_len; a.H = d->n_heads;
-  hipStream_t s = (hipStream_t)stream;
-  if ((st = launch_fill_i32(a.counters, d->batch * a.n_cb, 0, s))) return st;
-  return launch_pv(a, d->dtype, false, v_fast(d->v), d->batch, s);
+  return launch_pv(a, d->dtype, false, v_fast(d->v), d->batch, (hipStream_t)stream);
 }
 
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
@@ -341,11 +347,10 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   ka.x = d->k.data; ka.x_sb = d->k.stride_b;
   ka.xscale = d->k.scale; ka.xs_sb = d->k.scale_stride_b; ka.xs_sh = d->k.scale_stride_h;
   ka.bk = d->k.bk; ka.bk_rs = d->k.bk_row_stride;
-  ka.rope = (const float*)d->rope_table;
+  ka.rope = (const uint4*)d->rope_table;
   ka.mask = d->mask; ka.m_sb = d->mask_stride_b; ka.m_sh = d->mask_stride_h; ka.mask_dtype = d->mask_dtype;
   ka.out = ws + L.off_logits; ka.o_sb = (int64_t)Hq * L.S_pad; ka.o_sh = L.S_pad;
   ka.chunkmax = (float*)(ws + L.off_cmax);
-  ka.zero_ptr = (int*)(ws + L.off_cnt); ka.zero_count = B * L.n_cb;
   ka.S = d->seq_len; ka.Hq = Hq; ka.n_chunks = L.n_c1; ka.tiles_per_chunk = L.tiles_per_chunk;
   ka.wscale = d->scale;
   const bool kfast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
@@ -359,14 +364,13 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
   pa.olat = (float*)(ws + L.off_olat); pa.lsum = (float*)(ws + L.off_lsum);
-  pa.counters = (int*)(ws + L.off_cnt);
-  pa.S = d->seq_len; pa.H = Hq; pa.Rv = d->v.rank; pa.Rvp = L.Rvp;
-  pa.n_cb = L.n_cb; pa.n_c2 = L.n_c2; pa.c2_len = L.c2_len;
+  pa.S = d->seq_len; pa.H = Hq; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
+  pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;
   if ((st = launch_pv(pa, d->dtype, true, v_fast(d->v), B, s))) return st;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
 
   UPArgs ua;
-  ua.olat = pa.olat; ua.Rvp = L.Rvp; ua.lsum = pa.lsum;
+  ua.olat = pa.olat; ua.Rvp = L.pv.Rvp; ua.lsum = pa.lsum;
   ua.uv = d->uv; ua.uv_rs = d->uv_row_stride;
   ua.out = d->out; ua.o_sb = d->out_stride_b; ua.o_sh = d->out_stride_h;
   ua.B = B; ua.Hq = Hq; ua.gs = gs; ua.Rv = d->v.rank;

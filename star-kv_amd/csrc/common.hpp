@@ -21,12 +21,11 @@ constexpr int KSTEP = 16;           // positions per P.V MFMA K-step
 
 // ---------------------------------------------------------------------------
 // K-logit launch plan (passed by value as a kernel argument, read with
-// scalar loads).  A workgroup runs 4 waves; wave w of workgroup-plan g owns
-// up to K_MAXI "items"; an item is one 32-rank M-tile of one query head.
+// scalar loads).  Wave w of workgroup-plan g owns up to `maxi` "items"; an
+// item is one 32-rank M-tile of one query head.
 // ---------------------------------------------------------------------------
-constexpr int K_WAVES = 4;
-constexpr int K_MAXI = 4;
-constexpr int K_MAX_WG = 16;
+constexpr int K_MAXI = 4;          // items per wave (upper bound over kernel variants)
+constexpr int K_MAX_WAVES = 64;    // waves in one batch's plan
 constexpr int K_MAX_KV = 64;
 constexpr int K_MAX_QH = 64;
 
@@ -47,17 +46,17 @@ struct KArgs {
   const void* x; int64_t x_sb;
   const void* xscale; int64_t xs_sb, xs_sh;       // int8 K scales (fp16)
   const void* bk; int64_t bk_rs;
-  const float* rope;                               // T0 [32][64][2] then RT [tiles][64][2]
+  const uint4* rope;                               // RoPE operand table [tile][8][64] x 16 B
   const void* mask; int64_t m_sb, m_sh; int mask_dtype;
   void* out; int64_t o_sb, o_sh;
   float* chunkmax;                                 // [B][Hq][n_chunks] (optional)
-  int* zero_ptr; int zero_count;                   // counters to clear (optional)
   int S, Hq, n_chunks, tiles_per_chunk, n_wg;
+  int maxi;                                        // items per wave of the launched variant (3 or 4)
   float wscale;                                    // softmax scale * rope attention scaling
   int64_t xoff[K_MAX_KV];
   int xpitch[K_MAX_KV];
   int64_t bkoff[K_MAX_KV];
-  uint32_t items[K_MAX_WG][K_WAVES][K_MAXI];
+  uint32_t items[K_MAX_WAVES][K_MAXI];             // [workgroup plan * waves + wave][item]
 };
 
 // ---------------------------------------------------------------------------
@@ -68,12 +67,12 @@ struct PVArgs {
   const float* logits; int64_t l_sb, l_sh;         // fused path: fp32 logits
   const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
+  int p_vec;                                       // drop-in: P rows allow 16-byte loads
   float* part;                                     // [B][n_c2][32][Rvp] fp32
   float* psum;                                     // [B][n_c2][32]
   float* olat;                                     // [B][32][Rvp] fp32 (fused) ...
   void* out; int64_t o_sb, o_sh;                   // ... or act-dtype [B][H][Rv] (drop-in)
   float* lsum;                                     // [B][32] softmax denominators (fused)
-  int* counters;                                   // [B][n_cb]
   int S, H, Rv, Rvp, n_cb, n_c2, c2_len;
 };
 
@@ -135,9 +134,11 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
 // launchers (return hipError_t as int; 0 on success)
-int launch_rope_tables(const float* inv_freq_host, int max_positions, float scaling, float* table, hipStream_t st);
+int rope_table_tiles(int max_positions);
+int launch_rope_table(const float* inv_freq_host, int max_positions, float scaling, void* table, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
 int launch_pv(const PVArgs& a, int dtype, bool fused, bool fast, int B, hipStream_t st);
+int pv_tiles_per_wave(int Rvp, bool fused);   // column tiles (of 32 ranks) per P.V wave
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 

@@ -10,35 +10,30 @@
 //     W[j][2i]   = scale * (B_k[j][i] q[i]    + B_k[j][i+64] q[i+64])
 //     W[j][2i+1] = scale * (B_k[j][i] q[i+64] - B_k[j][i+64] q[i])
 //     logit[s]   = sum_j X_k[s][j] * V[j][s],   V = W . T,  T[c][s] = (cos|sin)(s*theta_i)
-// V for a 32-position tile is one 32x32x16 f16 MFMA chain per 32 ranks
-// (K = the 128 rotation coefficients), with the position-dependent rotation
-// table T as the B operand shared by every head and batch, and the latent X
-// enters only through one FMA per element in the epilogue.  The MFMA output
-// rows are permuted so that each lane holds 16 consecutive ranks of one
-// position: the epilogue reads X with two 16-byte loads per lane and needs no
-// shuffles except one half-wave swap per head.
+// V for a 32-position tile is one chain of eight 32x32x16 f16 MFMAs per 32
+// ranks (K = the 128 rotation coefficients).  The rotation operand T comes
+// from a table already laid out as the MFMA B operand (rope.hip), shared by
+// every head and batch through L2 and by the waves of a workgroup through LDS.
+// The MFMA output rows are permuted so that each lane holds 16 consecutive
+// ranks of one position: the latent X enters only through one fused
+// multiply-add per element, read with two 16-byte loads per lane, and a
+// head's logit needs one half-wave swap.
 //
-// Work decomposition: grid (chunk of positions, workgroup plan, batch); the
-// 4 waves of a workgroup each own up to K_MAXI items (query head, 32-rank
-// M-tile) packed by the host so that ragged head-wise ranks are balanced.
-// The T tile (32 positions x 128 coefficients, fp16, 8 KB) is produced once
-// per workgroup and tile into LDS by a per-thread rotation recurrence seeded
-// from the RoPE tables.
+// Work decomposition: grid (chunk of positions, workgroup plan, batch).
+// Each wave owns whole query heads: up to 2 items (query head, 32-rank
+// M-tile) in 8-wave workgroups, or up to 4 in 4-wave workgroups when a head
+// has rank > 64, packed on the host so ragged head-wise ranks are balanced.
+// A wave streams its latent rows two tiles ahead in registers; the MFMA
+// result of each item is consumed before the next item's MFMAs.
 #include "common.hpp"
 
 namespace starkv {
-
-template <typename XT, int XFMT>
-struct XBuf {
-  uint4 v[K_MAXI][2];
-  float sc[K_MAXI];
-};
 
 template <typename XT>
 __device__ inline void load4(const XT* p, float* out) {
   // four consecutive elements (8 bytes, 8-byte aligned)
   uint2 u = *(const uint2*)p;
-  if constexpr (sizeof(XT) == 2 && __is_same(XT, _Float16)) {
+  if constexpr (__is_same(XT, _Float16)) {
     half4 h = __builtin_bit_cast(half4, u);
     out[0] = (float)h[0]; out[1] = (float)h[1]; out[2] = (float)h[2]; out[3] = (float)h[3];
   } else {
@@ -52,37 +47,69 @@ __device__ inline void load4_any(const XT* p, float* out) {
   for (int e = 0; e < 4; ++e) out[e] = to_f32(p[e]);
 }
 
-// dot of 8 packed 16-bit elements with 8 accumulators
+// dot of 8 packed 16-bit latent elements with 8 fp32 accumulators
 template <typename XT>
-__device__ inline float dot8(uint4 u, const float* acc, float part) {
+__device__ inline float dot8(uint4 u, const floatx16& acc, int v0, float part) {
   if constexpr (__is_same(XT, _Float16)) {
-    half8 h = __builtin_bit_cast(half8, u);
+    const half8 h = __builtin_bit_cast(half8, u);
 #pragma unroll
-    for (int v = 0; v < 8; ++v) part = fmaf((float)h[v], acc[v], part);
+    for (int v = 0; v < 8; ++v) part = fmaf((float)h[v], acc[v0 + v], part);
   } else {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      part = fmaf(__uint_as_float(w[v] << 16), acc[2 * v], part);
-      part = fmaf(__uint_as_float(w[v] & 0xffff0000u), acc[2 * v + 1], part);
+      part = fmaf(__uint_as_float(w[v] << 16), acc[v0 + 2 * v], part);
+      part = fmaf(__uint_as_float(w[v] & 0xffff0000u), acc[v0 + 2 * v + 1], part);
     }
   }
   return part;
 }
 
-__device__ inline float dot_i8x4(uint32_t w, const float* acc, float part) {
-  part = fmaf((float)(int)(int8_t)(w & 0xff), acc[0], part);
-  part = fmaf((float)(int)(int8_t)((w >> 8) & 0xff), acc[1], part);
-  part = fmaf((float)(int)(int8_t)((w >> 16) & 0xff), acc[2], part);
-  part = fmaf((float)(int)(int8_t)(w >> 24), acc[3], part);
+__device__ inline float dot_i8x4(uint32_t w, const floatx16& acc, int v0, float part) {
+  part = fmaf((float)(int)(int8_t)(w & 0xff), acc[v0], part);
+  part = fmaf((float)(int)(int8_t)((w >> 8) & 0xff), acc[v0 + 1], part);
+  part = fmaf((float)(int)(int8_t)((w >> 16) & 0xff), acc[v0 + 2], part);
+  part = fmaf((float)(int)(int8_t)(w >> 24), acc[v0 + 3], part);
   return part;
 }
 
+// Latent loads are cached: one instruction reads 16 bytes of each of 32
+// position rows, so the other pieces of each cache line are picked up by the
+// item's next load from L1/L2 (non-temporal loads would refetch the line).
+__device__ inline uint4 ld_stream(const void* p) { return *(const uint4*)p; }
+__device__ inline uint2 ld_stream8(const void* p) { return *(const uint2*)p; }
+
+// native vector type: a HIP uint4 assignment between address spaces lowers to
+// a memcpy that keeps the staging registers in scratch memory
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int G, int TPT>
+struct TStage {
+  u32x4 v[G][TPT];       // rotation pieces of one staging group (this thread's share)
+};
+
+template <int XFMT, int MAXI>
+struct KBuf {
+  uint4 x[MAXI][2];      // latent: 16 ranks of one position per lane
+  float sc[MAXI];        // int8 format: per-position scale
+};
+
 // XFMT: 0 = dense act dtype, 2 = int8 symmetric with per-(b,kv,s) fp16 scale
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
-template <typename XT, int XFMT, int OUTK, bool FAST>
-__global__ __launch_bounds__(256, 1) void k_logits_kernel(const KArgs a) {
-  __shared__ half8 Tl[2][8][64];
+// NW waves x MAXI items.  The folded query matrices W stay in registers (the
+// MFMA A operand, 32 VGPRs per item).  The rotation operand (8 KB per
+// 32-position tile) is staged once per workgroup, three tiles at a time, into
+// a two-slot LDS ring and read by every wave from there: read per wave from
+// global memory it triples the L2 traffic of the latent stream and caps the
+// kernel near 3.5 TB/s.
+template <typename XT, int XFMT, int OUTK, bool FAST, int MAXI, int NW, int G>
+__global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
+  constexpr int XE = XFMT == 2 ? 1 : 2;
+  constexpr int NT = NW * 64;
+  constexpr int TPT = 512 / NT;   // 16-byte rotation pieces staged per thread per tile
+  static_assert(512 % NT == 0, "workgroup must divide the rotation tile");
+  static_assert(G % 3 == 0, "groups are whole cycles of the 3-tile latent ring");
+  __shared__ u32x4 Ts[2][G][512];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -90,200 +117,214 @@ __global__ __launch_bounds__(256, 1) void k_logits_kernel(const KArgs a) {
   const int t = lane & 31, hh = lane >> 5;
   const int chunk = blockIdx.x, wgp = blockIdx.y, b = blockIdx.z;
 
-  if (a.zero_ptr != nullptr && chunk == 0 && wgp == 0 && b == 0)
-    for (int i = tid; i < a.zero_count; i += 256) a.zero_ptr[i] = 0;
-
   const int S = a.S;
   const int n_tiles = (S + TILE - 1) / TILE;
   const int tile0 = chunk * a.tiles_per_chunk;
   const int tile1 = min(tile0 + a.tiles_per_chunk, n_tiles);
-  if (tile0 >= tile1) return;   // uniform over the workgroup
+  if (tile0 >= tile1) return;
 
-  // ---- RoPE recurrence state: thread -> frequency quad fq, positions tt0, tt0+16
-  const int fq = tid & 15, tt0 = tid >> 4;
-  const int ti0 = 8 * (fq >> 1) + 4 * (fq & 1);
-  const float* T0 = a.rope;
-  const float* RT = a.rope + TILE * 128;
-  float rc[2][4], rs[2][4], stc[4], sts[4];
+  uint32_t it[MAXI];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int i = ti0 + e;
-    stc[e] = RT[128 + 2 * i];
-    sts[e] = RT[128 + 2 * i + 1];
-    const float c0 = RT[(int64_t)tile0 * 128 + 2 * i], s0 = RT[(int64_t)tile0 * 128 + 2 * i + 1];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float ct = T0[(tt0 + 16 * u) * 128 + 2 * i], st = T0[(tt0 + 16 * u) * 128 + 2 * i + 1];
-      rc[u][e] = c0 * ct - s0 * st;
-      rs[u][e] = s0 * ct + c0 * st;
-    }
-  }
+  for (int i = 0; i < MAXI; ++i) it[i] = a.items[wgp * NW + wave][i];
 
-  // ---- items of this wave and their folded query matrices W (MFMA A operand)
-  uint32_t it[K_MAXI];
-#pragma unroll
-  for (int i = 0; i < K_MAXI; ++i) it[i] = a.items[wgp][wave][i];
-
-  half8 W[K_MAXI][8];
+  // ---- W of this wave's items (rows at or beyond the valid ranks are zero)
   const int rho = lane & 31;
-  const int jrow = 16 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);   // rank of A-row rho within the M-tile
+  const int jrow = 16 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);
+  half8 wr[MAXI][8];
 #pragma unroll
-  for (int i = 0; i < K_MAXI; ++i) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) W[i][k] = half8{};
-    if (!item_valid(it[i])) continue;
-    const int qh = item_qh(it[i]), kv = item_kv(it[i]), mt = item_mt(it[i]), nv = item_nv(it[i]);
-    if (jrow >= nv) continue;
+  for (int i = 0; i < MAXI; ++i) {
+    const bool ok = item_valid(it[i]) && jrow < item_nv(it[i]);
+    const int qh = item_qh(it[i]), kv = item_kv(it[i]), mt = item_mt(it[i]);
     const XT* qrow = (const XT*)a.q + b * a.q_sb + qh * a.q_sh;
     const XT* brow = (const XT*)a.bk + a.bkoff[kv] + (int64_t)(mt * 32 + jrow) * a.bk_rs;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int i0 = 8 * k + 4 * hh;
-      float ql[4], qu[4], bl[4], bu[4];
-      if (FAST) {
-        load4<XT>(qrow + i0, ql); load4<XT>(qrow + i0 + 64, qu);
-        load4<XT>(brow + i0, bl); load4<XT>(brow + i0 + 64, bu);
-      } else {
-        load4_any<XT>(qrow + i0, ql); load4_any<XT>(qrow + i0 + 64, qu);
-        load4_any<XT>(brow + i0, bl); load4_any<XT>(brow + i0 + 64, bu);
-      }
-      half8 w;
+      half8 w = half8{};
+      if (ok) {
+        const int i0 = 8 * k + 4 * hh;
+        float ql[4], qu[4], bl[4], bu[4];
+        if (FAST) {
+          load4<XT>(qrow + i0, ql); load4<XT>(qrow + i0 + 64, qu);
+          load4<XT>(brow + i0, bl); load4<XT>(brow + i0 + 64, bu);
+        } else {
+          load4_any<XT>(qrow + i0, ql); load4_any<XT>(qrow + i0 + 64, qu);
+          load4_any<XT>(brow + i0, bl); load4_any<XT>(brow + i0 + 64, bu);
+        }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[2 * e] = (_Float16)(a.wscale * (bl[e] * ql[e] + bu[e] * qu[e]));
-        w[2 * e + 1] = (_Float16)(a.wscale * (bl[e] * qu[e] - bu[e] * ql[e]));
+        for (int e = 0; e < 4; ++e) {
+          w[2 * e] = (_Float16)(a.wscale * (bl[e] * ql[e] + bu[e] * qu[e]));
+          w[2 * e + 1] = (_Float16)(a.wscale * (bl[e] * qu[e] - bu[e] * ql[e]));
+        }
       }
-      W[i][k] = w;
+      wr[i][k] = w;
     }
   }
+  // idle waves (plan padding) load and compute nothing but take part in the
+  // rotation staging and its barriers
+  const bool active = item_valid(it[0]);
 
-  float mx[K_MAXI];
+  // ---- per-item latent row bases (bytes).  Lanes whose ranks lie beyond the
+  // item's valid ranks re-read the item's first chunk of the same row (in
+  // bounds; multiplied by the zero rows of W).
+  const char* xb[MAXI];
+  int off1[MAXI], off2[MAXI];
+  int64_t xpitch[MAXI];
+  const _Float16* scb[MAXI];
 #pragma unroll
-  for (int i = 0; i < K_MAXI; ++i) mx[i] = -INFINITY;
+  for (int i = 0; i < MAXI; ++i) {
+    const int kv = item_kv(it[i]), mt = item_mt(it[i]);
+    const int nvh = item_valid(it[i]) ? item_nv(it[i]) - 16 * hh : 0;
+    xpitch[i] = (int64_t)a.xpitch[kv] * XE;
+    xb[i] = (const char*)a.x + (b * a.x_sb + a.xoff[kv] + mt * 32) * XE;
+    off1[i] = nvh > 0 ? 16 * hh * XE : 0;
+    off2[i] = nvh >= 16 ? (16 * hh + 8) * XE : off1[i];
+    scb[i] = nullptr;
+    if constexpr (XFMT == 2) scb[i] = (const _Float16*)a.xscale + b * a.xs_sb + (int64_t)kv * a.xs_sh;
+  }
 
-  // ---- latent loads for one tile
-  auto load_x = [&](XBuf<XT, XFMT>& xb, int tile) {
-    const int s = tile * TILE + t;
+  float mx[MAXI];
 #pragma unroll
-    for (int i = 0; i < K_MAXI; ++i) {
-      xb.v[i][0] = make_uint4(0, 0, 0, 0);
-      xb.v[i][1] = make_uint4(0, 0, 0, 0);
-      xb.sc[i] = 0.f;
+  for (int i = 0; i < MAXI; ++i) mx[i] = -INFINITY;
+
+  // Tiles are processed in groups of G (a multiple of the 3-tile latent
+  // register ring) per staging barrier.  Every
+  // index is clamped to the chunk's last tile, so a group past the end
+  // re-reads that tile (cached) and only its stores are predicated off: the
+  // group body has no data-dependent branches and the compiler keeps the
+  // latent loads two tiles ahead of their use.
+  const int last = tile1 - 1;
+  const int n_groups = (tile1 - tile0 + G - 1) / G;
+
+  auto load = [&](KBuf<XFMT, MAXI>& kb, int tile) __attribute__((always_inline)) {
+    const int pos = min(min(tile, last) * TILE + t, S - 1);
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
       if (!item_valid(it[i])) continue;
-      const int kv = item_kv(it[i]), mt = item_mt(it[i]);
-      const int nvh = item_nv(it[i]) - 16 * hh;
-      if (s >= S || nvh <= 0) continue;
-      const int64_t off = b * a.x_sb + a.xoff[kv] + (int64_t)s * a.xpitch[kv] + mt * 32 + 16 * hh;
+      const char* p = xb[i] + (int64_t)pos * xpitch[i];
       if constexpr (XFMT == 0) {
-        const XT* p = (const XT*)a.x + off;
         if (FAST) {
-          xb.v[i][0] = *(const uint4*)p;
-          if (nvh >= 16) xb.v[i][1] = *(const uint4*)(p + 8);
+          kb.x[i][0] = ld_stream(p + off1[i]);
+          kb.x[i][1] = ld_stream(p + off2[i]);
         } else {
+          const int nvh = item_nv(it[i]) - 16 * hh;
           uint16_t tmp[16];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) tmp[v] = v < nvh ? ((const uint16_t*)p)[v] : (uint16_t)0;
-          xb.v[i][0] = make_uint4(tmp[0] | (tmp[1] << 16), tmp[2] | (tmp[3] << 16), tmp[4] | (tmp[5] << 16), tmp[6] | (tmp[7] << 16));
-          xb.v[i][1] = make_uint4(tmp[8] | (tmp[9] << 16), tmp[10] | (tmp[11] << 16), tmp[12] | (tmp[13] << 16), tmp[14] | (tmp[15] << 16));
+          for (int v = 0; v < 16; ++v) tmp[v] = v < nvh ? ((const uint16_t*)(p + 16 * hh * XE))[v] : (uint16_t)0;
+          kb.x[i][0] = make_uint4(tmp[0] | (tmp[1] << 16), tmp[2] | (tmp[3] << 16), tmp[4] | (tmp[5] << 16), tmp[6] | (tmp[7] << 16));
+          kb.x[i][1] = make_uint4(tmp[8] | (tmp[9] << 16), tmp[10] | (tmp[11] << 16), tmp[12] | (tmp[13] << 16), tmp[14] | (tmp[15] << 16));
         }
       } else {
-        const uint8_t* p = (const uint8_t*)a.x + off;
         if (FAST) {
-          if (nvh >= 16) xb.v[i][0] = *(const uint4*)p;
-          else { uint2 u = *(const uint2*)p; xb.v[i][0] = make_uint4(u.x, u.y, 0, 0); }
+          const uint2 lo = ld_stream8(p + off1[i]);
+          const uint2 hi = ld_stream8(p + (item_nv(it[i]) - 16 * hh >= 16 ? off1[i] + 8 : off1[i]));
+          kb.x[i][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
         } else {
+          const int nvh = item_nv(it[i]) - 16 * hh;
           uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-          for (int v = 0; v < 16; ++v) if (v < nvh) w[v >> 2] |= (uint32_t)p[v] << (8 * (v & 3));
-          xb.v[i][0] = make_uint4(w[0], w[1], w[2], w[3]);
+          for (int v = 0; v < 16; ++v) if (v < nvh) w[v >> 2] |= (uint32_t)((const uint8_t*)(p + 16 * hh))[v] << (8 * (v & 3));
+          kb.x[i][0] = make_uint4(w[0], w[1], w[2], w[3]);
         }
-        if (item_last(it[i]))
-          xb.sc[i] = (float)((const _Float16*)a.xscale)[b * a.xs_sb + kv * a.xs_sh + s];
+        kb.sc[i] = 0.f;
+        if (item_last(it[i])) kb.sc[i] = (float)scb[i][pos];
       }
     }
   };
 
-  auto compute = [&](const XBuf<XT, XFMT>& xb, int tile, int buf) {
-    // produce this tile's rotation operand
+  // rotation operand of group g (tiles tile0 + G*g + j) -> Ts[slot][j]
+  const u32x4* rt = (const u32x4*)a.rope + tid;
+  TStage<G, TPT> tst;
+  auto tload = [&](TStage<G, TPT>& ts, int g) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      half8 h;
+    for (int j = 0; j < G; ++j) {
+      const u32x4* q = rt + (int64_t)min(tile0 + G * g + j, last) * 512;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { h[2 * e] = (_Float16)rc[u][e]; h[2 * e + 1] = (_Float16)rs[u][e]; }
-      Tl[buf][fq >> 1][(tt0 + 16 * u) * 2 + (fq & 1)] = h;
+      for (int p = 0; p < TPT; ++p) ts.v[j][p] = q[p * NT];
     }
+  };
+  auto twrite = [&](const TStage<G, TPT>& ts, int slot) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int j = 0; j < G; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float c = rc[u][e], s_ = rs[u][e];
-        rc[u][e] = c * stc[e] - s_ * sts[e];
-        rs[u][e] = s_ * stc[e] + c * sts[e];
-      }
-    __syncthreads();
+      for (int p = 0; p < TPT; ++p) Ts[slot][j][tid + p * NT] = ts.v[j][p];
+  };
+
+  auto compute = [&](const KBuf<XFMT, MAXI>& kb, int tile, int slot, int j) __attribute__((always_inline)) {
+    const int s = tile * TILE + t;
+    const bool store = tile < tile1 && s < S;
+    float part = 0.f;
     half8 T[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) T[k] = Tl[buf][k][t * 2 + hh];
-
-    floatx16 acc[K_MAXI];
+    for (int k = 0; k < 8; ++k) T[k] = __builtin_bit_cast(half8, Ts[slot][j][k * 64 + lane]);
 #pragma unroll
-    for (int i = 0; i < K_MAXI; ++i) acc[i] = floatx16{};
+    for (int i = 0; i < MAXI; ++i) {
+      if (!item_valid(it[i])) break;
+      floatx16 acc = mfma_f16(wr[i][0], T[0], floatx16{});
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-#pragma unroll
-      for (int i = 0; i < K_MAXI; ++i)
-        if (item_valid(it[i])) acc[i] = mfma_f16(W[i][k], T[k], acc[i]);
-
-    const int s = tile * TILE + t;
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < K_MAXI; ++i) {
-      if (!item_valid(it[i])) continue;
-      float av[16];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) av[v] = acc[i][v];
+      for (int k = 1; k < 8; ++k) acc = mfma_f16(wr[i][k], T[k], acc);
       if constexpr (XFMT == 0) {
-        part = dot8<XT>(xb.v[i][0], av, part);
-        part = dot8<XT>(xb.v[i][1], av + 8, part);
+        part = dot8<XT>(kb.x[i][0], acc, 0, part);
+        part = dot8<XT>(kb.x[i][1], acc, 8, part);
       } else {
-        part = dot_i8x4(xb.v[i][0].x, av, part);
-        part = dot_i8x4(xb.v[i][0].y, av + 4, part);
-        part = dot_i8x4(xb.v[i][0].z, av + 8, part);
-        part = dot_i8x4(xb.v[i][0].w, av + 12, part);
+        part = dot_i8x4(kb.x[i][0].x, acc, 0, part);
+        part = dot_i8x4(kb.x[i][0].y, acc, 4, part);
+        part = dot_i8x4(kb.x[i][0].z, acc, 8, part);
+        part = dot_i8x4(kb.x[i][0].w, acc, 12, part);
       }
       if (item_last(it[i])) {
         float tot = add_halves(part);
         part = 0.f;
-        if constexpr (XFMT == 2) tot *= xb.sc[i];
+        if constexpr (XFMT == 2) tot *= kb.sc[i];
         const int qh = item_qh(it[i]);
-        if (s < S) {
+        if (store) {
           if (a.mask != nullptr) tot += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
-          if (hh == 0) {
-            const int64_t o = b * a.o_sb + qh * a.o_sh + s;
-            if constexpr (OUTK == 0) ((float*)a.out)[o] = tot;
-            else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)tot;
-            else ((__bf16*)a.out)[o] = (__bf16)tot;
-          }
+          const int64_t o = b * a.o_sb + qh * a.o_sh + s;
+          if constexpr (OUTK == 0) ((float*)a.out)[o] = tot;
+          else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)tot;
+          else ((__bf16*)a.out)[o] = (__bf16)tot;
           mx[i] = fmaxf(mx[i], tot);
         }
       }
     }
   };
 
-  XBuf<XT, XFMT> xa, xn;
-  load_x(xa, tile0);
-  for (int tile = tile0; tile < tile1; tile += 2) {
-    if (tile + 1 < tile1) load_x(xn, tile + 1);
-    compute(xa, tile, 0);
-    if (tile + 1 >= tile1) break;
-    if (tile + 2 < tile1) load_x(xa, tile + 2);
-    compute(xn, tile + 1, 1);
+  // Staging: slot g&1 holds group g from the barrier at the start of group g;
+  // behind that barrier group g+1 is written into the other slot (last read
+  // in group g-1) and group g+2 is fetched into registers.
+  tload(tst, 0);
+  twrite(tst, 0);
+  tload(tst, 1);
+  if (!active) {
+    for (int g = 0; g < n_groups; ++g) {
+      __syncthreads();
+      twrite(tst, (g + 1) & 1);
+      tload(tst, g + 2);
+    }
+    return;
+  }
+  KBuf<XFMT, MAXI> b0, b1, b2;
+  load(b0, tile0);
+  load(b1, tile0 + 1);
+  for (int g = 0; g < n_groups; ++g) {
+    __syncthreads();
+    twrite(tst, (g + 1) & 1);
+    tload(tst, g + 2);
+    const int tb = tile0 + G * g, slot = g & 1;
+#pragma unroll
+    for (int j = 0; j < G; j += 3) {
+      load(b2, tb + j + 2);
+      compute(b0, tb + j, slot, j);
+      load(b0, tb + j + 3);
+      compute(b1, tb + j + 1, slot, j + 1);
+      load(b1, tb + j + 4);
+      compute(b2, tb + j + 2, slot, j + 2);
+    }
   }
 
   if constexpr (OUTK == 0) {
     if (a.chunkmax != nullptr) {
 #pragma unroll
-      for (int i = 0; i < K_MAXI; ++i) {
+      for (int i = 0; i < MAXI; ++i) {
         if (!item_valid(it[i]) || !item_last(it[i])) continue;
         const float m = wave_max32(mx[i]);
         if (lane == 0) a.chunkmax[((int64_t)b * a.Hq + item_qh(it[i])) * a.n_chunks + chunk] = m;
@@ -292,11 +333,21 @@ __global__ __launch_bounds__(256, 1) void k_logits_kernel(const KArgs a) {
   }
 }
 
+template <typename XT, int XFMT, int OUTK, int MAXI, int NW, int G>
+static void launch_v(const KArgs& a, bool fast, dim3 grid, hipStream_t st) {
+  if (fast) hipLaunchKernelGGL((k_logits_kernel<XT, XFMT, OUTK, true, MAXI, NW, G>), grid, dim3(NW * 64), 0, st, a);
+  else hipLaunchKernelGGL((k_logits_kernel<XT, XFMT, OUTK, false, MAXI, NW, G>), grid, dim3(NW * 64), 0, st, a);
+}
+
+// items per wave -> workgroup shape: up to 2 items in 8-wave workgroups (two
+// waves per SIMD), else up to 4 items in 4-wave workgroups.  (Measured on
+// MI355X with ragged ranks up to 96: four independent item chains per wave
+// beat a 3-item, 8-wave shape, which spills at 256 registers.)
 template <typename XT, int XFMT, int OUTK>
 static int launch_t(const KArgs& a, bool fast, int B, hipStream_t st) {
-  dim3 grid(a.n_chunks, a.n_wg, B), block(256);
-  if (fast) hipLaunchKernelGGL((k_logits_kernel<XT, XFMT, OUTK, true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((k_logits_kernel<XT, XFMT, OUTK, false>), grid, block, 0, st, a);
+  dim3 grid(a.n_chunks, a.n_wg, B);
+  if (a.maxi <= 2) launch_v<XT, XFMT, OUTK, 2, 8, 3>(a, fast, grid, st);
+  else launch_v<XT, XFMT, OUTK, 4, 4, 3>(a, fast, grid, st);
   return (int)hipGetLastError();
 }
 

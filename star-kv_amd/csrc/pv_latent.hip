@@ -6,23 +6,23 @@
 // X_v is one latent shared by every head, so a workgroup streams a
 // (position chunk x column block) slab of X_v once for all 32 heads: the MFMA
 // 32x32x16 A operand is P (32 heads x 16 positions), the B operand is X_v
-// (16 positions x 32 ranks).  X_v rows arrive with coalesced 16-byte loads,
-// are staged in LDS (wave-private, double buffered) and are read back
+// (16 positions x 32 ranks).  The four waves of a workgroup take the same
+// positions and split the column tiles, so every wave owns its accumulators.
+// X_v rows arrive with coalesced 16-byte non-temporal loads (two K-steps in
+// flight per wave), are staged in wave-private LDS and are read back
 // transposed with ds_read_b64_tr_b16, the gfx950 LDS transpose load: within
 // each 16-lane group, lane j receives column j%4 of the rows addressed by
 // lanes {j/4, 4+j/4, 8+j/4, 12+j/4}.
 //
 // Fused mode: P = exp(logit - M) is formed in registers from the fp32 logits
-// of K1 with M the global row max (from K1's chunk maxima), so no softmax
-// pass and no normalisation happen here; the denominators are summed on the
-// side.  Drop-in mode (bx): P is read as given.
+// of K1 with M the global row max (from K1's chunk maxima); the softmax
+// denominators are summed on the side and normalisation happens in K3.
+// Drop-in mode (bx): P is read as given.
 //
-// Split-S: the 4 waves of a workgroup take interleaved 16-position K-steps of
-// the chunk and are summed through LDS; the n_c2 chunk partials of each
-// (batch, column block) are summed in fixed chunk order by whichever
-// workgroup finishes last (atomic ticket), so the result is deterministic
-// (no float atomics; the reference accumulates fp16 atomics into an
-// uninitialised tensor, bx_quant.py:113-114, 147).
+// Split-S: each workgroup writes its chunk's partial sums; pv_reduce_kernel
+// adds the chunk partials in fixed chunk order (deterministic; no float
+// atomics, unlike the fp16 atomics into an uninitialised tensor of
+// bx_quant.py:113-114, 147).
 #include "common.hpp"
 
 namespace starkv {
@@ -34,27 +34,35 @@ __device__ inline uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
-template <typename VT>
-__device__ inline void load8_f32(const float* p, float* out) {
-  const float4 u = *(const float4*)p, v = *(const float4*)(p + 4);
-  out[0] = u.x; out[1] = u.y; out[2] = u.z; out[3] = u.w; out[4] = v.x; out[5] = v.y; out[6] = v.z; out[7] = v.w;
+__device__ inline uint4 ld_stream16(const void* p) {
+  typedef unsigned u4v __attribute__((ext_vector_type(4)));
+  const u4v t = __builtin_nontemporal_load((const u4v*)p);
+  return make_uint4(t.x, t.y, t.z, t.w);
 }
 
-template <typename VT, int NT, bool FUSED, bool FAST>
-__global__ __launch_bounds__(256, 2) void pv_kernel(const PVArgs a) {
-  constexpr int PITCH = NT * 32 + 8;            // elements per staged row (16-byte pad)
-  constexpr int STAGE = 16 * PITCH;             // elements per staged K-step
-  constexpr int NTP = 2;                        // N-tiles per LDS reduction pass
+template <int NTW>
+struct PVStage {
+  uint4 r[NTW];     // X_v chunks (16 B each) of this wave's slab
+  float p[8];       // fused: fp32 logits of the A operand
+  uint4 praw;       // drop-in: 8 probabilities of the A operand (act dtype)
+};
+
+template <typename VT, int NTW, bool FUSED, bool FAST>
+__global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
+  constexpr int PITCH = NTW * 32 + 8;            // elements per staged row (16-byte pad)
+  constexpr int STAGE = 16 * PITCH;              // elements per staged K-step
+  constexpr int CPR = NTW * 4;                   // 16-byte chunks per staged row
   __shared__ __attribute__((aligned(16))) uint16_t stage[4][2][STAGE];
   __shared__ float Ms[32];
   __shared__ float Ps[4][32];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
   const int cb = blockIdx.x % a.n_cb, c2 = blockIdx.x / a.n_cb, b = blockIdx.y;
-  const int col0 = cb * NT * 32;
+  const int tile0 = (cb * 4 + wave) * NTW;                    // first 32-column tile of this wave
+  const int nvt = max(0, min(NTW, a.Rvp / 32 - tile0));       // valid tiles (wave-uniform)
+  const int col0 = tile0 * 32;
   const int H = a.H;
 
   if constexpr (FUSED) {
@@ -73,78 +81,92 @@ __global__ __launch_bounds__(256, 2) void pv_kernel(const PVArgs a) {
 
   const int s_begin = c2 * a.c2_len;
   const int s_end = min(a.S, s_begin + a.c2_len);
-  const int nks = s_begin < s_end ? (s_end - s_begin + KSTEP - 1) / KSTEP : 0;
+  const int nks = (s_end - s_begin + KSTEP - 1) / KSTEP;
 
-  floatx16 acc[NT];
+  floatx16 acc[NTW];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = floatx16{};
+  for (int j = 0; j < NTW; ++j) acc[j] = floatx16{};
   float psum = 0.f;
 
-  // ---- staging map: lane, chunk c -> (row, 16-byte column chunk)
-  uint4 R[NT];
-  auto gload = [&](int ks) {
-    const int s0 = s_begin + ks * KSTEP;
+  // ---- per-lane staging map: chunk c -> (row, 16-byte column chunk) of the 16 x NTW*32 slab
+  int goff[NTW], soff[NTW], grow[NTW], gcol[NTW];
+  bool cok[NTW];
 #pragma unroll
-    for (int c = 0; c < NT; ++c) {
-      const int f = c * 64 + lane;
-      const int row = f / (NT * 4), c16 = f % (NT * 4);
-      const int s = s0 + row, col = col0 + c16 * 8;
-      R[c] = make_uint4(0, 0, 0, 0);
-      if (s < s_end && col < a.Rv) {
-        const VT* p = (const VT*)a.x + b * a.x_sb + (int64_t)s * a.x_ss + col;
+  for (int c = 0; c < NTW; ++c) {
+    const int f = c * 64 + lane;
+    const int row = f / CPR, c16 = f % CPR;
+    grow[c] = row;
+    gcol[c] = col0 + c16 * 8;
+    goff[c] = row * (int)a.x_ss + gcol[c];
+    soff[c] = row * PITCH + c16 * 8;
+    cok[c] = (c16 / 4 < nvt) && (gcol[c] < a.Rv);
+  }
+  const VT* xb = (const VT*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
+
+  auto load = [&](PVStage<NTW>& st, int ks) {
+    const int s0 = s_begin + ks * KSTEP;
+    const VT* base = xb + (int64_t)ks * KSTEP * a.x_ss;
+    const bool full = s0 + KSTEP <= s_end;
+#pragma unroll
+    for (int c = 0; c < NTW; ++c) {
+      st.r[c] = make_uint4(0, 0, 0, 0);
+      if (cok[c] && (full || s0 + grow[c] < s_end)) {
+        const VT* p = base + goff[c];
         if (FAST) {
-          R[c] = *(const uint4*)p;
+          st.r[c] = ld_stream16(p);
         } else {
           uint16_t tmp[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) tmp[e] = (col + e < a.Rv) ? ((const uint16_t*)p)[e] : (uint16_t)0;
-          R[c] = make_uint4(tmp[0] | (tmp[1] << 16), tmp[2] | (tmp[3] << 16), tmp[4] | (tmp[5] << 16), tmp[6] | (tmp[7] << 16));
+          for (int e = 0; e < 8; ++e) tmp[e] = (gcol[c] + e < a.Rv) ? ((const uint16_t*)p)[e] : (uint16_t)0;
+          st.r[c] = make_uint4(tmp[0] | (tmp[1] << 16), tmp[2] | (tmp[3] << 16), tmp[4] | (tmp[5] << 16), tmp[6] | (tmp[7] << 16));
+        }
+      }
+    }
+    const int sa = s0 + 8 * hh;
+    if constexpr (FUSED) {
+      if (qok) {
+        const float* lp = a.logits + b * a.l_sb + n * a.l_sh + sa;
+        const float4 u = *(const float4*)lp, v = *(const float4*)(lp + 4);
+        st.p[0] = u.x; st.p[1] = u.y; st.p[2] = u.z; st.p[3] = u.w;
+        st.p[4] = v.x; st.p[5] = v.y; st.p[6] = v.z; st.p[7] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st.p[e] = 0.f;
+      }
+    } else {
+      const VT* pp = (const VT*)a.p + b * a.p_sb + n * a.p_sh + sa;
+      st.praw = make_uint4(0, 0, 0, 0);
+      if (qok) {
+        if (a.p_vec && sa + 8 <= s_end) {
+          st.praw = *(const uint4*)pp;
+        } else {
+          uint16_t tmp[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) tmp[e] = sa + e < s_end ? ((const uint16_t*)pp)[e] : (uint16_t)0;
+          st.praw = make_uint4(tmp[0] | (tmp[1] << 16), tmp[2] | (tmp[3] << 16), tmp[4] | (tmp[5] << 16), tmp[6] | (tmp[7] << 16));
         }
       }
     }
   };
-  auto swrite = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < NT; ++c) {
-      const int f = c * 64 + lane;
-      const int row = f / (NT * 4), c16 = f % (NT * 4);
-      *(uint4*)&stage[wave][buf][row * PITCH + c16 * 8] = R[c];
-    }
-  };
 
-  // transposed-read addressing (see header): group g = lane/16, rho = lane%16
+  // transposed-read addressing: group g = lane/16, rho = lane%16
   const int g = lane >> 4, rho = lane & 15;
   const int tr_off = (8 * hh + (rho >> 2)) * PITCH + 16 * (g & 1) + 4 * (rho & 3);
 
-  // P-operand source for one K-step (prefetched together with the X_v rows)
-  float pn[8];
-  auto pload = [&](int ks) {
-    const int sa = s_begin + ks * KSTEP + 8 * hh;
-    if constexpr (FUSED) {
-      if (qok) {
-        load8_f32<VT>(a.logits + b * a.l_sb + n * a.l_sh + sa, pn);
-      } else {
+  auto compute = [&](PVStage<NTW>& st, int ks, int buf) {
+    uint16_t* sbuf = &stage[wave][buf][0];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pn[e] = 0.f;
-      }
-    } else {
-      const VT* pp = (const VT*)a.p + b * a.p_sb + n * a.p_sh;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pn[e] = (qok && sa + e < s_end) ? to_f32(pp[sa + e]) : 0.f;
-    }
-  };
-
-  int buf = 0;
-  int ks = wave;
-  if (ks < nks) { pload(ks); gload(ks); }
-  for (; ks < nks; ks += 4) {
-    swrite(buf);
+    for (int c = 0; c < NTW; ++c) *(uint4*)&sbuf[soff[c]] = st.r[c];
     float pc[8];
+    uint4 praw;
+    if constexpr (FUSED) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pc[e] = pn[e];
-    if (ks + 4 < nks) { pload(ks + 4); gload(ks + 4); }
+      for (int e = 0; e < 8; ++e) pc[e] = st.p[e];
+    } else {
+      praw = st.praw;
+    }
+    if (ks + 2 < nks) load(st, ks + 2);
 
-    // A operand: P[q = n][s0 + 8hh + e]
     const int sa = s_begin + ks * KSTEP + 8 * hh;
     float pv[8];
     if constexpr (FUSED) {
@@ -153,21 +175,26 @@ __global__ __launch_bounds__(256, 2) void pv_kernel(const PVArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) psum += pv[e];
     } else {
+      const uint32_t w[4] = {praw.x, praw.y, praw.z, praw.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = pc[e];
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t u = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        pv[e] = to_f32(__builtin_bit_cast(VT, u));
+      }
     }
 
-    const uint16_t* sb = &stage[wave][buf][tr_off];
+    const uint16_t* sb = sbuf + tr_off;
     if constexpr (__is_same(VT, _Float16)) {
       half8 A;
 #pragma unroll
       for (int e = 0; e < 8; ++e) A[e] = (_Float16)pv[e];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const uint2 lo = lds_read_tr16(sb + 32 * j);
-        const uint2 hi = lds_read_tr16(sb + 32 * j + 4 * PITCH);
-        const half8 Bv = __builtin_bit_cast(half8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-        acc[j] = mfma_f16(A, Bv, acc[j]);
+      for (int j = 0; j < NTW; ++j) {
+        if (j < nvt) {
+          const uint2 lo = lds_read_tr16(sb + 32 * j);
+          const uint2 hi = lds_read_tr16(sb + 32 * j + 4 * PITCH);
+          acc[j] = mfma_f16(A, __builtin_bit_cast(half8, make_uint4(lo.x, lo.y, hi.x, hi.y)), acc[j]);
+        }
       }
     } else {
       bf16x8 Ah, Al;
@@ -178,87 +205,99 @@ __global__ __launch_bounds__(256, 2) void pv_kernel(const PVArgs a) {
         Al[e] = (__bf16)(pv[e] - (float)h);
       }
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const uint2 lo = lds_read_tr16(sb + 32 * j);
-        const uint2 hi = lds_read_tr16(sb + 32 * j + 4 * PITCH);
-        const bf16x8 Bv = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-        acc[j] = mfma_bf16(Ah, Bv, acc[j]);
-        acc[j] = mfma_bf16(Al, Bv, acc[j]);
+      for (int j = 0; j < NTW; ++j) {
+        if (j < nvt) {
+          const uint2 lo = lds_read_tr16(sb + 32 * j);
+          const uint2 hi = lds_read_tr16(sb + 32 * j + 4 * PITCH);
+          const bf16x8 Bv = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          acc[j] = mfma_bf16(Ah, Bv, acc[j]);
+          acc[j] = mfma_bf16(Al, Bv, acc[j]);
+        }
       }
     }
-    buf ^= 1;
+  };
+
+  if (nvt > 0) {
+    PVStage<NTW> st0, st1;
+    if (nks > 0) load(st0, 0);
+    if (nks > 1) load(st1, 1);
+    for (int ks = 0; ks < nks; ks += 2) {
+      compute(st0, ks, 0);
+      if (ks + 1 >= nks) break;
+      compute(st1, ks + 1, 1);
+    }
   }
 
-  // ---- cross-wave reduction through LDS (reuses the staging buffers)
-  float* red = (float*)&stage[0][0][0];    // [4 waves][NTP][64 lanes][17]
-  static_assert(4 * NTP * 64 * 17 * 4 <= (int)sizeof(stage), "reduction buffer");
+  // ---- this chunk's partial sums: D[row q][col] -> part[b][c2][q][col]
   const int Rvp = a.Rvp;
   float* part = a.part + (((int64_t)b * a.n_c2 + c2) * 32) * Rvp;
 #pragma unroll
-  for (int p0 = 0; p0 < NT; p0 += NTP) {
-    __syncthreads();
+  for (int j = 0; j < NTW; ++j) {
+    if (j < nvt) {
 #pragma unroll
-    for (int jj = 0; jj < NTP; ++jj) {
-      if (p0 + jj < NT) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) red[((wave * NTP + jj) * 64 + lane) * 17 + v] = acc[p0 + jj][v];
+      for (int v = 0; v < 16; ++v) {
+        const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
+        part[(int64_t)q * Rvp + col0 + 32 * j + n] = acc[j][v];
       }
-    }
-    __syncthreads();
-    for (int e = tid; e < NTP * 1024; e += 256) {
-      const int jj = e >> 10, q = (e >> 5) & 31, nn = e & 31;
-      const int col = col0 + 32 * (p0 + jj) + nn;
-      if (p0 + jj >= NT || col >= Rvp) continue;
-      const int ln = nn + 32 * ((q >> 2) & 1), v = 4 * (q >> 3) + (q & 3);
-      float s = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) s += red[((w * NTP + jj) * 64 + ln) * 17 + v];
-      part[(int64_t)q * Rvp + col] = s;
     }
   }
   if constexpr (FUSED) {
     const float ps = add_halves(psum);
     if (hh == 0) Ps[wave][n] = ps;
     __syncthreads();
-    if (cb == 0 && tid < 32) a.psum[((int64_t)b * a.n_c2 + c2) * 32 + tid] = Ps[0][tid] + Ps[1][tid] + Ps[2][tid] + Ps[3][tid];
+    if (cb == 0 && tid < 32) a.psum[((int64_t)b * a.n_c2 + c2) * 32 + tid] = Ps[0][tid];
   }
+}
 
-  // ---- fixed-order reduction of the chunk partials by the last workgroup
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&a.counters[b * a.n_cb + cb], 1) == a.n_c2 - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+// Sum of the chunk partials in fixed chunk order.  Fused: o_lat (fp32, with
+// the denominators L); drop-in: the act-dtype output of bx.
+template <typename VT, bool FUSED>
+__global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
+  const int tile = blockIdx.x, b = blockIdx.y;
+  const int Rvp = a.Rvp;
   const float* pb = a.part + ((int64_t)b * a.n_c2 * 32) * Rvp;
-  for (int e = tid; e < 32 * NT * 32; e += 256) {
-    const int q = e / (NT * 32), col = col0 + e % (NT * 32);
-    if (col >= Rvp) continue;
+  for (int e = threadIdx.x; e < 32 * 32; e += 256) {
+    const int q = e >> 5, col = tile * 32 + (e & 31);
     float s = 0.f;
     for (int c = 0; c < a.n_c2; ++c) s += pb[((int64_t)c * 32 + q) * Rvp + col];
     if constexpr (FUSED) {
       a.olat[((int64_t)b * 32 + q) * Rvp + col] = s;
     } else {
-      if (q < H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + q * a.o_sh + col] = (VT)s;
+      if (q < a.H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + q * a.o_sh + col] = (VT)s;
     }
   }
   if constexpr (FUSED) {
-    if (cb == 0 && tid < 32) {
+    if (tile == 0 && threadIdx.x < 32) {
       float L = 0.f;
-      for (int c = 0; c < a.n_c2; ++c) L += a.psum[((int64_t)b * a.n_c2 + c) * 32 + tid];
-      a.lsum[b * 32 + tid] = L;
+      for (int c = 0; c < a.n_c2; ++c) L += a.psum[((int64_t)b * a.n_c2 + c) * 32 + threadIdx.x];
+      a.lsum[b * 32 + threadIdx.x] = L;
     }
   }
-  if (tid == 0) a.counters[b * a.n_cb + cb] = 0;
 }
 
-constexpr int PV_NT = 8;
+int pv_tiles_per_wave(int Rvp, bool fused) {
+  const int tiles = Rvp / 32;
+  if (tiles <= 16) return 4;
+  if (tiles <= 32 || !fused) return 8;   // the drop-in P-input variant stays at 8 (register budget)
+  return 13;
+}
+
+template <typename VT, bool FUSED, int NTW>
+static void launch_pv_n(const PVArgs& a, bool fast, int B, hipStream_t st) {
+  dim3 grid(a.n_cb * a.n_c2, B), block(256);
+  if (fast) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, false>), grid, block, 0, st, a);
+}
 
 template <typename VT, bool FUSED>
 static int launch_pv_t(const PVArgs& a, bool fast, int B, hipStream_t st) {
-  dim3 grid(a.n_cb * a.n_c2, B), block(256);
-  if (fast) hipLaunchKernelGGL((pv_kernel<VT, PV_NT, FUSED, true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((pv_kernel<VT, PV_NT, FUSED, false>), grid, block, 0, st, a);
+  const int ntw = pv_tiles_per_wave(a.Rvp, FUSED);
+  if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, fast, B, st);
+  else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, fast, B, st);
+  else if constexpr (FUSED) launch_pv_n<VT, FUSED, 13>(a, fast, B, st);
+  int e = (int)hipGetLastError();
+  if (e) return e;
+  hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 
