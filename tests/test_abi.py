@@ -1,0 +1,228 @@
+"""C-ABI checks of libstarkv.so that need no GPU.
+
+The library must load, export every function include/starkv.h declares, agree
+with the ctypes mirrors on struct layout, and reject bad arguments with the
+documented status codes.  Validation runs before any HIP call, so every call
+below returns before touching a device (device pointers are never
+dereferenced on the host; fake addresses are enough).
+"""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from starkv import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "starkv.h")
+
+OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_RANK, ERR_WORKSPACE, ERR_LIMIT, ERR_FORMAT = 0, -1, -2, -3, -4, -5, -6, -7, -8
+FAKE = 0x7F0000000000          # 256-byte aligned stand-in for a device address
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(starkv_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = L.lib()
+    decl = declared_functions()
+    assert len(decl) >= 11
+    missing = [n for n in decl if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(L.EXPORTS) == decl
+
+
+def test_version_and_status_strings():
+    lib = L.lib()
+    assert lib.starkv_abi_version() == 1
+    for code in (OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_RANK, ERR_WORKSPACE, ERR_LIMIT, ERR_FORMAT):
+        s = lib.starkv_status_string(code).decode()
+        assert s and s != "unknown error"
+    assert lib.starkv_status_string(-99).decode() == "unknown error"
+
+
+_C_LAYOUT = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "starkv.h"
+#define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
+#define S(T) printf(#T " sizeof %zu\n", sizeof(T));
+int main(void) {
+  S(starkv_klatent) F(starkv_klatent, rank) F(starkv_klatent, data) F(starkv_klatent, scale_stride_h) F(starkv_klatent, bk_row_stride)
+  S(starkv_klogits_desc) F(starkv_klogits_desc, q) F(starkv_klogits_desc, k) F(starkv_klogits_desc, rope_table)
+  F(starkv_klogits_desc, scale) F(starkv_klogits_desc, mask) F(starkv_klogits_desc, out) F(starkv_klogits_desc, out_stride_h)
+  S(starkv_vlatent) F(starkv_vlatent, data) F(starkv_vlatent, split) F(starkv_vlatent, data2) F(starkv_vlatent, zero) F(starkv_vlatent, capacity)
+  S(starkv_pv_desc) F(starkv_pv_desc, p) F(starkv_pv_desc, v) F(starkv_pv_desc, out_stride_h)
+  S(starkv_decode_desc) F(starkv_decode_desc, k) F(starkv_decode_desc, v) F(starkv_decode_desc, uv)
+  F(starkv_decode_desc, rope_table) F(starkv_decode_desc, scale) F(starkv_decode_desc, mask) F(starkv_decode_desc, out_dtype)
+  F(starkv_decode_desc, out_stride_h)
+  return 0;
+}
+"""
+
+_PY = {"starkv_klatent": L.KLatent, "starkv_klogits_desc": L.KLogitsDesc, "starkv_vlatent": L.VLatent,
+       "starkv_pv_desc": L.PVDesc, "starkv_decode_desc": L.DecodeDesc}
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_ctypes_struct_layout_matches_the_c_compiler(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(_C_LAYOUT)
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    n = 0
+    for line in filter(None, lines):
+        cname, field, val = line.split()
+        py = _PY[cname]
+        got = ctypes.sizeof(py) if field == "sizeof" else getattr(py, field).offset
+        assert got == int(val), (cname, field, got, val)
+        n += 1
+    assert n > 20
+
+
+# ---------------------------------------------------------------- validation
+
+def _klatent(ranks, keep):
+    Hkv = len(ranks)
+    keep += [L.int_array(ranks), L.i64_array([h * 4096 * 64 for h in range(Hkv)]),
+             L.i64_array([64] * Hkv), L.i64_array([sum(ranks[:h]) * 128 for h in range(Hkv)])]
+    return L.KLatent(n_kv_heads=Hkv, rank=keep[-4], head_offset=keep[-3], pos_stride=keep[-2],
+                     stride_b=Hkv * 4096 * 64, format=L.FMT_DENSE, data=FAKE, scale=None,
+                     scale_stride_b=0, scale_stride_h=0, bk=FAKE, bk_head_offset=keep[-1], bk_row_stride=128)
+
+
+def _decode_desc(keep, B=2, Hq=8, Hkv=8, S=1000, Rv=256, ranks=None):
+    ranks = ranks or [32] * Hkv
+    d = L.DecodeDesc()
+    d.batch, d.n_q_heads, d.head_dim, d.seq_len, d.dtype = B, Hq, 128, S, L.F16
+    d.q, d.q_stride_b, d.q_stride_h = FAKE, Hq * 128, 128
+    d.k = _klatent(ranks, keep)
+    d.v = L.VLatent(rank=Rv, format=L.FMT_DENSE, data=FAKE, stride_b=S * Rv, stride_s=Rv)
+    d.uv, d.uv_row_stride = FAKE, Rv
+    d.rope_table, d.rope_max_positions = FAKE, 4096
+    d.scale = 128 ** -0.5
+    d.out, d.out_dtype, d.out_stride_b, d.out_stride_h = FAKE, 0, Hq * 128, 128
+    return d
+
+
+def _call(d, ws=None, nbytes=0):
+    return L.lib().starkv_decode_attention(ctypes.byref(d), ws, nbytes, None)
+
+
+def test_valid_descriptor_sizes_a_workspace_and_asks_for_it():
+    keep = []
+    d = _decode_desc(keep)
+    need = L.lib().starkv_decode_workspace_bytes(ctypes.byref(d))
+    assert need > 0 and need % 256 == 0
+    assert _call(d) == ERR_WORKSPACE
+    assert _call(d, FAKE, need - 1) == ERR_WORKSPACE
+    assert _call(d, FAKE + 16, need) == ERR_ALIGN
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("batch", 0, ERR_SHAPE),
+    ("seq_len", 0, ERR_SHAPE),
+    ("seq_len", 5000, ERR_SHAPE),          # beyond rope_max_positions
+    ("head_dim", 64, ERR_SHAPE),
+    ("dtype", L.F32, ERR_DTYPE),
+    ("n_q_heads", 12, ERR_SHAPE),          # not a multiple of n_kv_heads
+    ("n_q_heads", 40, ERR_LIMIT),          # P.V kernel handles up to 32 query heads
+    ("q", None, ERR_NULL),
+    ("uv", None, ERR_NULL),
+    ("out", None, ERR_NULL),
+    ("rope_table", None, ERR_NULL),
+    ("out_dtype", L.I8, ERR_DTYPE),
+    ("uv_row_stride", 100, ERR_SHAPE),
+    ("mask_dtype", L.I8, ERR_DTYPE),
+])
+def test_decode_rejects(field, value, code):
+    keep = []
+    d = _decode_desc(keep)
+    setattr(d, field, value)
+    if field == "mask_dtype":
+        d.mask = FAKE
+    assert _call(d) == code
+    assert L.lib().starkv_decode_workspace_bytes(ctypes.byref(d)) == 0
+
+
+@pytest.mark.parametrize("what,code", [
+    ("rank0", ERR_RANK), ("rank129", ERR_RANK), ("format", ERR_FORMAT), ("pos_stride", ERR_SHAPE),
+    ("k_null", ERR_NULL), ("int8_noscale", ERR_NULL), ("v_rank", ERR_RANK), ("v_format", ERR_FORMAT),
+    ("v_stride", ERR_SHAPE), ("kv_heads", ERR_LIMIT),
+])
+def test_decode_rejects_latent_descriptions(what, code):
+    keep = []
+    d = _decode_desc(keep)
+    if what == "rank0":
+        d.k.rank[3] = 0
+    elif what == "rank129":
+        d.k.rank[0] = 129
+    elif what == "format":
+        d.k.format = 9
+    elif what == "pos_stride":
+        d.k.pos_stride[1] = 16
+    elif what == "k_null":
+        d.k.data = None
+    elif what == "int8_noscale":
+        d.k.format = L.FMT_INT8_SYM
+    elif what == "v_rank":
+        d.v.rank = 0
+    elif what == "v_format":
+        d.v.format = 7
+    elif what == "v_stride":
+        d.v.stride_s = 10
+    elif what == "kv_heads":
+        d = _decode_desc(keep, Hq=65 * 2, Hkv=65, ranks=[8] * 65)
+    assert _call(d) == code
+
+
+def test_rope_build_and_pv_validation():
+    lib = L.lib()
+    assert lib.starkv_rope_table_bytes(0) == 0
+    assert lib.starkv_rope_table_bytes(1) == lib.starkv_rope_table_bytes(32) == 8192     # one 32-position tile
+    assert lib.starkv_rope_table_bytes(33) == 2 * 8192
+    inv = (ctypes.c_float * 64)(*([1.0] * 64))
+    assert lib.starkv_rope_build(None, 1.0, 32, FAKE, 8192, None) == ERR_NULL
+    assert lib.starkv_rope_build(inv, 1.0, 64, FAKE, 8192, None) == ERR_WORKSPACE
+    assert lib.starkv_rope_build(inv, 1.0, 32, FAKE + 8, 8192, None) == ERR_ALIGN
+    assert lib.starkv_rope_build(inv, 1.0, 0, FAKE, 8192, None) == ERR_SHAPE
+    p = L.PVDesc(batch=2, n_heads=32, seq_len=100, dtype=L.F16, p=FAKE, p_stride_b=3200, p_stride_h=100,
+                 v=L.VLatent(rank=256, format=L.FMT_DENSE, data=FAKE, stride_b=25600, stride_s=256),
+                 out=FAKE, out_stride_b=8192, out_stride_h=256)
+    need = lib.starkv_pv_latent_workspace_bytes(ctypes.byref(p))
+    assert need > 0
+    assert lib.starkv_pv_latent(ctypes.byref(p), None, 0, None) == ERR_WORKSPACE
+    p.n_heads = 33
+    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_LIMIT
+    p.n_heads, p.p = 32, None
+    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_NULL
+
+
+def test_k_logits_validation():
+    lib = L.lib()
+    keep = []
+    d = L.KLogitsDesc(batch=1, n_q_heads=8, head_dim=128, seq_len=64, dtype=L.F16, q=FAKE,
+                      q_stride_b=1024, q_stride_h=128, k=_klatent([16] * 8, keep), rope_table=FAKE,
+                      rope_max_positions=64, scale=1.0, out=FAKE, out_dtype=L.F32, out_stride_b=512, out_stride_h=64)
+    assert lib.starkv_k_logits_workspace_bytes(ctypes.byref(d)) == 0
+    for field, value, code in [("out_dtype", L.I8, ERR_DTYPE), ("q", None, ERR_NULL), ("seq_len", 65, ERR_SHAPE),
+                               ("n_q_heads", 7, ERR_SHAPE), ("head_dim", 96, ERR_SHAPE)]:
+        old = getattr(d, field)
+        setattr(d, field, value)
+        assert lib.starkv_k_logits(ctypes.byref(d), None, 0, None) == code, field
+        setattr(d, field, old)
+    assert lib.starkv_k_logits(None, None, 0, None) == ERR_NULL
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setattr(L, "_lib", None)
+    monkeypatch.setattr(L, "LIB_PATH", os.path.join(ROOT, "no-such-dir", "libstarkv.so"))
+    with pytest.raises(L.StarKVError, match="no fallback"):
+        L.lib()
