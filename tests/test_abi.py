@@ -226,3 +226,17 @@ def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(L, "LIB_PATH", os.path.join(ROOT, "no-such-dir", "libstarkv.so"))
     with pytest.raises(L.StarKVError, match="no fallback"):
         L.lib()
+
+
+def test_dropins_refuse_cpu_tensors():
+    import torch
+    from starkv.abx_rope_batched import abx
+    a = torch.zeros(1, 2, 1, 128, dtype=torch.float16)
+    b = torch.zeros(2, 16, 128, dtype=torch.float16)
+    x = torch.zeros(1, 2, 10, 16, dtype=torch.float16)
+    with pytest.raises(L.StarKVError, match="no CPU path"):
+        abx(a, b, x)
+    with pytest.raises(L.StarKVError):
+        abx(a[0], b, x)                      # wrong rank
+    with pytest.raises(L.StarKVError):
+        abx(a, b.float(), x)                 # mixed dtypes
