@@ -150,10 +150,10 @@ struct PVGeom {
   int Rvp, n_cb, n_c2, c2_len;
 };
 
-PVGeom pv_geometry(int B, int S, int Rv, bool fused) {
+PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq) {
   PVGeom g;
   g.Rvp = (int)round_up(Rv, 32);
-  const int ntw = pv_tiles_per_wave(g.Rvp, fused);
+  const int ntw = pv_tiles_per_wave(g.Rvp, fused, vq);
   g.n_cb = (int)ceil_div(g.Rvp / 32, 4 * ntw);
   const int wg_per_cu = ntw >= 8 ? 1 : 2;    // registers / LDS staging allow one workgroup per CU from NTW 8
   const int n_ks = (int)ceil_div(S, KSTEP);
@@ -171,14 +171,14 @@ struct DecodeLayout {
   size_t off_logits, off_cmax, off_part, off_psum, off_olat, off_lsum, total;
 };
 
-DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg) {
+DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg, int vq) {
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
   L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
-  L.pv = pv_geometry(B, S, Rv, true);
+  L.pv = pv_geometry(B, S, Rv, true, vq);
   const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
@@ -191,20 +191,71 @@ DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg) {
   return L;
 }
 
-int validate_vdense(const starkv_vlatent& v, int S) {
-  if (v.format != STARKV_FMT_DENSE) return STARKV_ERR_FORMAT;
+// V latent: validate the description and fill the P.V kernel's storage
+// fields (x / x2 / scales / zero points, split); *vq = its storage kind.
+// Quantised formats need rank and split multiples of 8 and 4-byte (int4) or
+// 8-byte (int8) aligned rows: they always run the vector-load kernel.
+int validate_v(const starkv_vlatent& v, PVArgs& pa, int* vq) {
   if (!v.data) return STARKV_ERR_NULL;
   if (v.rank < 1 || v.rank > MAX_RV) return STARKV_ERR_RANK;
-  if (v.stride_s < v.rank || v.stride_b < 0) return STARKV_ERR_SHAPE;
-  (void)S;
-  return STARKV_OK;
+  if (v.stride_b < 0 || v.stride_s < 0) return STARKV_ERR_SHAPE;
+  pa.x = v.data; pa.x_sb = v.stride_b; pa.x_ss = v.stride_s;
+  switch (v.format) {
+    case STARKV_FMT_DENSE:
+      if (v.stride_s < v.rank) return STARKV_ERR_SHAPE;
+      *vq = VQ_DENSE;
+      return STARKV_OK;
+    case STARKV_FMT_INT4_REF:
+    case STARKV_FMT_INT8_SYM: {
+      if (v.rank % 8) return STARKV_ERR_SHAPE;
+      if (!v.scale) return STARKV_ERR_NULL;
+      const bool two = v.format == STARKV_FMT_INT4_REF && v.split > 0 && v.split < v.rank;
+      if (two && v.split_format != STARKV_FMT_INT4_REF && v.split_format != STARKV_FMT_INT8_SYM)
+        return STARKV_ERR_FORMAT;
+      const int split = two ? v.split : v.rank;
+      const bool a8 = two ? v.split_format == STARKV_FMT_INT8_SYM : v.format == STARKV_FMT_INT8_SYM;
+      if (split % 8) return STARKV_ERR_SHAPE;
+      const int al_a = a8 ? 8 : 4;
+      if (v.stride_s < (a8 ? split : split / 2)) return STARKV_ERR_SHAPE;
+      if (!al(v.data, al_a) || !al64(v.stride_s, al_a) || !al64(v.stride_b, al_a) || !al(v.scale, 2))
+        return STARKV_ERR_ALIGN;
+      if (v.scale_stride_b < 0 || v.scale_stride_s < 0) return STARKV_ERR_SHAPE;
+      pa.split = split; pa.a_int8 = a8;
+      pa.xs = v.scale; pa.xs_sb = v.scale_stride_b; pa.xs_ss = v.scale_stride_s;
+      if (two) {
+        if (!v.data2 || !v.scale2) return STARKV_ERR_NULL;
+        if (v.stride2_s < (v.rank - split) / 2 || v.stride2_b < 0 || v.scale2_stride_b < 0 || v.scale2_stride_s < 0)
+          return STARKV_ERR_SHAPE;
+        if (!al(v.data2, 4) || !al64(v.stride2_s, 4) || !al64(v.stride2_b, 4) || !al(v.scale2, 2))
+          return STARKV_ERR_ALIGN;
+        pa.x2 = v.data2; pa.x2_sb = v.stride2_b; pa.x2_ss = v.stride2_s;
+        pa.xs2 = v.scale2; pa.xs2_sb = v.scale2_stride_b; pa.xs2_ss = v.scale2_stride_s;
+      }
+      *vq = VQ_BLOCK;
+      return STARKV_OK;
+    }
+    case STARKV_FMT_INT4_G64: {
+      if (v.rank % 8) return STARKV_ERR_SHAPE;
+      if (!v.scale || !v.zero) return STARKV_ERR_NULL;
+      if (v.stride_s < v.rank / 2 || v.scale_stride_s < (v.rank + 63) / 64 || v.scale_stride_b < 0)
+        return STARKV_ERR_SHAPE;
+      if (!al(v.data, 4) || !al64(v.stride_s, 4) || !al64(v.stride_b, 4) || !al(v.scale, 2) || !al(v.zero, 2))
+        return STARKV_ERR_ALIGN;
+      pa.xs = v.scale; pa.xs_sb = v.scale_stride_b; pa.xs_ss = v.scale_stride_s;
+      pa.xz = v.zero;
+      *vq = VQ_G64;
+      return STARKV_OK;
+    }
+    default:
+      return STARKV_ERR_FORMAT;
+  }
 }
 
 bool v_fast(const starkv_vlatent& v) {
   return al(v.data, 16) && al64(v.stride_s * 2, 16) && al64(v.stride_b * 2, 16) && v.rank % 8 == 0;
 }
 
-int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg) {
+int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S) return STARKV_ERR_SHAPE;
   if (d->head_dim != HEAD_DIM) return STARKV_ERR_SHAPE;
@@ -212,7 +263,8 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg) {
   if (d->n_q_heads > K2_MAX_H) return STARKV_ERR_LIMIT;
   int st = validate_klatent(d->k, d->n_q_heads, d->dtype, gs);
   if (st) return st;
-  if ((st = validate_vdense(d->v, d->seq_len))) return st;
+  PVArgs vtmp = {};
+  if ((st = validate_v(d->v, vtmp, vq))) return st;
   if (!d->q || !d->uv || !d->out || !d->rope_table) return STARKV_ERR_NULL;
   if (d->seq_len > d->rope_max_positions) return STARKV_ERR_SHAPE;
   if (d->uv_row_stride < d->v.rank) return STARKV_ERR_SHAPE;
@@ -296,7 +348,10 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
 
 size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {
   if (!d || d->batch < 1 || d->seq_len < 1 || d->v.rank < 1) return 0;
-  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false);
+  PVArgs tmp = {};
+  int vq = 0;
+  if (validate_v(d->v, tmp, &vq)) return 0;
+  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq);
   return a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4);
 }
 
@@ -305,35 +360,34 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
   if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S || d->n_heads < 1) return STARKV_ERR_SHAPE;
   if (d->n_heads > K2_MAX_H) return STARKV_ERR_LIMIT;
   if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
-  int st;
-  if ((st = validate_vdense(d->v, d->seq_len))) return st;
+  int st, vq = 0;
+  PVArgs a = {};
+  if ((st = validate_v(d->v, a, &vq))) return st;
   if (!d->p || !d->out) return STARKV_ERR_NULL;
   const size_t need = starkv_pv_latent_workspace_bytes(d);
   if (!workspace || workspace_bytes < need) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
-  PVArgs a = {};
-  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false);
+  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq);
   a.Rv = d->v.rank; a.Rvp = g.Rvp; a.n_cb = g.n_cb; a.n_c2 = g.n_c2; a.c2_len = g.c2_len;
-  a.x = d->v.data; a.x_sb = d->v.stride_b; a.x_ss = d->v.stride_s;
   a.p = d->p; a.p_sb = d->p_stride_b; a.p_sh = d->p_stride_h;
   a.p_vec = al(d->p, 16) && al64(d->p_stride_b * 2, 16) && al64(d->p_stride_h * 2, 16);
   a.part = (float*)workspace;
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
   a.S = d->seq_len; a.H = d->n_heads;
-  return launch_pv(a, d->dtype, false, v_fast(d->v), d->batch, (hipStream_t)stream);
+  return launch_pv(a, d->dtype, vq, false, v_fast(d->v), d->batch, (hipStream_t)stream);
 }
 
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
-  int gs = 0, n_wg = 0;
-  if (validate_decode(d, &gs, &n_wg)) return 0;
-  return decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg).total;
+  int gs = 0, n_wg = 0, vq = 0;
+  if (validate_decode(d, &gs, &n_wg, &vq)) return 0;
+  return decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq).total;
 }
 
 static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream,
                        void* const* events) {
-  int gs = 0, n_wg = 0, st;
-  if ((st = validate_decode(d, &gs, &n_wg))) return st;
-  const DecodeLayout L = decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg);
+  int gs = 0, n_wg = 0, vq = 0, st;
+  if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
+  const DecodeLayout L = decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq);
   if (!workspace || workspace_bytes < L.total) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   char* ws = (char*)workspace;
@@ -359,14 +413,14 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[1], s))) return st;
 
   PVArgs pa = {};
-  pa.x = d->v.data; pa.x_sb = d->v.stride_b; pa.x_ss = d->v.stride_s;
+  if ((st = validate_v(d->v, pa, &vq))) return st;
   pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = (int64_t)Hq * L.S_pad; pa.l_sh = L.S_pad;
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
   pa.olat = (float*)(ws + L.off_olat); pa.lsum = (float*)(ws + L.off_lsum);
   pa.S = d->seq_len; pa.H = Hq; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
   pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;
-  if ((st = launch_pv(pa, d->dtype, true, v_fast(d->v), B, s))) return st;
+  if ((st = launch_pv(pa, d->dtype, vq, true, v_fast(d->v), B, s))) return st;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
 
   UPArgs ua;

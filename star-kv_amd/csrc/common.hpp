@@ -62,8 +62,19 @@ struct KArgs {
 // ---------------------------------------------------------------------------
 // P.V launch arguments.
 // ---------------------------------------------------------------------------
+// V-latent storage of the P.V kernel (template parameter VQ)
+constexpr int VQ_DENSE = 0;    // act-dtype rows; x strides in elements
+constexpr int VQ_BLOCK = 1;    // per-token fp16 scale: ranks [0, split) in x (int4 nibbles, or int8 when
+                               // a_int8), ranks [split, Rv) in x2 (int4 nibbles); x strides in bytes
+constexpr int VQ_G64 = 2;      // int4 asymmetric: fp16 scale and zero per (b, s, 64-rank group)
+
 struct PVArgs {
-  const void* x; int64_t x_sb, x_ss;               // dense V latent
+  const void* x; int64_t x_sb, x_ss;               // V latent (VQ_DENSE: elements; else bytes)
+  const void* x2; int64_t x2_sb, x2_ss;            // VQ_BLOCK lower block (bytes)
+  const void* xs; int64_t xs_sb, xs_ss;            // fp16 scales of x: (b, s[, g]) in elements
+  const void* xs2; int64_t xs2_sb, xs2_ss;         // fp16 scales of x2
+  const void* xz;                                  // VQ_G64 fp16 zero points (strides of xs)
+  int split, a_int8;                               // VQ_BLOCK: first rank of x2; x holds int8
   const float* logits; int64_t l_sb, l_sh;         // fused path: fp32 logits
   const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
@@ -137,8 +148,8 @@ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 int rope_table_tiles(int max_positions);
 int launch_rope_table(const float* inv_freq_host, int max_positions, float scaling, void* table, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
-int launch_pv(const PVArgs& a, int dtype, bool fused, bool fast, int B, hipStream_t st);
-int pv_tiles_per_wave(int Rvp, bool fused);   // column tiles (of 32 ranks) per P.V wave
+int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st);
+int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ranks) per P.V wave
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 

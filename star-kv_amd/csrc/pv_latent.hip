@@ -14,6 +14,16 @@
 // each 16-lane group, lane j receives column j%4 of the rows addressed by
 // lanes {j/4, 4+j/4, 8+j/4, 12+j/4}.
 //
+// Quantised latents are fetched as packed bytes (int4 nibbles or int8) with
+// their fp16 scales, carried through the prefetch registers, and dequantised
+// just before the LDS write with packed-fp16 arithmetic: an integer n is
+// biased into the fp16 bit pattern 1024 + n (exact), the bias removed (exact),
+// then one correctly rounded multiply by the scale (reference int4 / int8:
+// fp16((n - 8) * s), bx_quant.py:83-86) or fused multiply-add with the zero
+// point (group-64 int4: fp16(n * s + z), one rounding).  bf16 activations
+// round that fp16 value once more to bf16, as torch_bx's .to(b.dtype) does
+// (bx_quant.py:171-172).
+//
 // Fused mode: P = exp(logit - M) is formed in registers from the fp32 logits
 // of K1 with M the global row max (from K1's chunk maxima); the softmax
 // denominators are summed on the side and normalisation happens in K3.
@@ -40,14 +50,69 @@ __device__ inline uint4 ld_stream16(const void* p) {
   return make_uint4(t.x, t.y, t.z, t.w);
 }
 
-template <int NTW>
+template <int NTW, int VQ>
 struct PVStage {
-  uint4 r[NTW];     // X_v chunks (16 B each) of this wave's slab
-  float p[8];       // fused: fp32 logits of the A operand
-  uint4 praw;       // drop-in: 8 probabilities of the A operand (act dtype)
+  uint4 r[VQ == VQ_DENSE ? NTW : 1];   // dense: X_v chunks (16 B = 8 ranks) of this wave's slab
+  uint2 q[VQ == VQ_DENSE ? 1 : NTW];   // quantised: the chunk's packed bytes (int4: .x)
+  uint16_t s[VQ == VQ_DENSE ? 1 : NTW];  // fp16 scale bits of the chunk's row (and group)
+  uint16_t z[VQ == VQ_G64 ? NTW : 1];  // fp16 zero-point bits (group-64 int4)
+  float p[8];                          // fused: fp32 logits of the A operand
+  uint4 praw;                          // drop-in: 8 probabilities of the A operand (act dtype)
 };
 
-template <typename VT, int NTW, bool FUSED, bool FAST>
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+__device__ inline h2v as_h2(uint32_t u) { return __builtin_bit_cast(h2v, u); }
+__device__ inline uint32_t as_u32(h2v h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Eight dequantised fp16 values of one chunk, packed two per dword (even rank
+// in the low half).  kind8: the bytes are int8 (x, y), else eight int4
+// nibbles in x, rank 2k in the low nibble of byte k.
+template <int VQ>
+__device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16) {
+  const h2v s = as_h2((uint32_t)s16 * 0x10001u);
+  uint32_t pr[4];
+  _Float16 bias;
+  if (VQ == VQ_BLOCK && kind8) {
+    const uint32_t x = q.x ^ 0x80808080u, y = q.y ^ 0x80808080u;      // n + 128, unsigned
+    pr[0] = (x & 0xFFu) | ((x << 8) & 0xFF0000u);
+    pr[1] = ((x >> 16) & 0xFFu) | ((x >> 8) & 0xFF0000u);
+    pr[2] = (y & 0xFFu) | ((y << 8) & 0xFF0000u);
+    pr[3] = ((y >> 16) & 0xFFu) | ((y >> 8) & 0xFF0000u);
+    bias = (_Float16)-1152.0f;                                       // 1024 + 128
+  } else {
+    const uint32_t w = q.x;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pr[k] = ((w >> (8 * k)) & 0xFu) | (((w >> (8 * k + 4)) & 0xFu) << 16);
+    bias = VQ == VQ_BLOCK ? (_Float16)-1032.0f : (_Float16)-1024.0f;  // nibble - 8 | nibble
+  }
+  const h2v b2 = {bias, bias};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const h2v n = as_h2(pr[k] | 0x64006400u) + b2;                     // exact small integers
+    if constexpr (VQ == VQ_G64) {
+      const h2v zz = as_h2((uint32_t)z16 * 0x10001u);
+      o[k] = as_u32(__builtin_elementwise_fma(n, s, zz));
+    } else {
+      o[k] = as_u32(n * s);
+    }
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
+  const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const h2v v = as_h2(w[k]);
+    const __bf16 lo = (__bf16)(float)v[0], hi = (__bf16)(float)v[1];
+    o[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <typename VT, int NTW, bool FUSED, bool FAST, int VQ>
 __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
   constexpr int PITCH = NTW * 32 + 8;            // elements per staged row (16-byte pad)
   constexpr int STAGE = 16 * PITCH;              // elements per staged K-step
@@ -102,13 +167,50 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     cok[c] = (c16 / 4 < nvt) && (gcol[c] < a.Rv);
   }
   const VT* xb = (const VT*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
+  // quantised: byte offset of the chunk in its row, its block, int8 or int4, its group
+  int qoff[NTW], qg[NTW];
+  bool qlo[NTW], q8[NTW];
+  const uint8_t* xq = (const uint8_t*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
+  const uint8_t* xq2 = (const uint8_t*)a.x2 + b * a.x2_sb + (int64_t)s_begin * a.x2_ss;
+  const uint16_t* sq = (const uint16_t*)a.xs + b * a.xs_sb + (int64_t)s_begin * a.xs_ss;
+  const uint16_t* sq2 = (const uint16_t*)a.xs2 + b * a.xs2_sb + (int64_t)s_begin * a.xs2_ss;
+  const uint16_t* zq = (const uint16_t*)a.xz + b * a.xs_sb + (int64_t)s_begin * a.xs_ss;
+#pragma unroll
+  for (int c = 0; c < NTW; ++c) {
+    qlo[c] = VQ == VQ_BLOCK && gcol[c] >= a.split;
+    q8[c] = VQ == VQ_BLOCK && !qlo[c] && a.a_int8;
+    qoff[c] = qlo[c] ? (gcol[c] - a.split) / 2 : (q8[c] ? gcol[c] : gcol[c] / 2);
+    qg[c] = gcol[c] / 64;
+  }
 
-  auto load = [&](PVStage<NTW>& st, int ks) {
+  auto load = [&](PVStage<NTW, VQ>& st, int ks) {
     const int s0 = s_begin + ks * KSTEP;
     const VT* base = xb + (int64_t)ks * KSTEP * a.x_ss;
     const bool full = s0 + KSTEP <= s_end;
+    if constexpr (VQ != VQ_DENSE) {
+#pragma unroll
+      for (int c = 0; c < NTW; ++c) {
+        st.q[c] = make_uint2(0, 0);
+        st.s[c] = 0;
+        if constexpr (VQ == VQ_G64) st.z[c] = 0;
+        if (cok[c] && (full || s0 + grow[c] < s_end)) {
+          const int64_t r = (int64_t)ks * KSTEP + grow[c];
+          if constexpr (VQ == VQ_BLOCK) {
+            const uint8_t* p = (qlo[c] ? xq2 + r * a.x2_ss : xq + r * a.x_ss) + qoff[c];
+            if (q8[c]) st.q[c] = *(const uint2*)p;
+            else st.q[c].x = *(const uint32_t*)p;
+            st.s[c] = qlo[c] ? sq2[r * a.xs2_ss] : sq[r * a.xs_ss];
+          } else {
+            st.q[c].x = *(const uint32_t*)(xq + r * a.x_ss + qoff[c]);
+            st.s[c] = sq[r * a.xs_ss + qg[c]];
+            st.z[c] = zq[r * a.xs_ss + qg[c]];
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int c = 0; c < NTW; ++c) {
+      if constexpr (VQ != VQ_DENSE) break;
       st.r[c] = make_uint4(0, 0, 0, 0);
       if (cok[c] && (full || s0 + grow[c] < s_end)) {
         const VT* p = base + goff[c];
@@ -153,10 +255,18 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
   const int g = lane >> 4, rho = lane & 15;
   const int tr_off = (8 * hh + (rho >> 2)) * PITCH + 16 * (g & 1) + 4 * (rho & 3);
 
-  auto compute = [&](PVStage<NTW>& st, int ks, int buf) {
+  auto compute = [&](PVStage<NTW, VQ>& st, int ks, int buf) {
     uint16_t* sbuf = &stage[wave][buf][0];
 #pragma unroll
-    for (int c = 0; c < NTW; ++c) *(uint4*)&sbuf[soff[c]] = st.r[c];
+    for (int c = 0; c < NTW; ++c) {
+      if constexpr (VQ == VQ_DENSE) {
+        *(uint4*)&sbuf[soff[c]] = st.r[c];
+      } else {
+        uint4 h = dequant8<VQ>(st.q[c], q8[c], st.s[c], VQ == VQ_G64 ? st.z[VQ == VQ_G64 ? c : 0] : (uint16_t)0);
+        if constexpr (__is_same(VT, __bf16)) h = f16x8_to_bf16x8(h);
+        *(uint4*)&sbuf[soff[c]] = h;
+      }
+    }
     float pc[8];
     uint4 praw;
     if constexpr (FUSED) {
@@ -218,7 +328,7 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
   };
 
   if (nvt > 0) {
-    PVStage<NTW> st0, st1;
+    PVStage<NTW, VQ> st0, st1;
     if (nks > 0) load(st0, 0);
     if (nks > 1) load(st1, 1);
     for (int ks = 0; ks < nks; ks += 2) {
@@ -275,35 +385,48 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
   }
 }
 
-int pv_tiles_per_wave(int Rvp, bool fused) {
+int pv_tiles_per_wave(int Rvp, bool fused, int vq) {
   const int tiles = Rvp / 32;
   if (tiles <= 16) return 4;
-  if (tiles <= 32 || !fused) return 8;   // the drop-in P-input variant stays at 8 (register budget)
+  // the drop-in P-input variant and the quantised formats stay at 8 (register budget)
+  if (tiles <= 32 || !fused || vq != VQ_DENSE) return 8;
   return 13;
 }
 
 template <typename VT, bool FUSED, int NTW>
-static void launch_pv_n(const PVArgs& a, bool fast, int B, hipStream_t st) {
+static void launch_pv_n(const PVArgs& a, int vq, bool fast, int B, hipStream_t st) {
   dim3 grid(a.n_cb * a.n_c2, B), block(256);
-  if (fast) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, false>), grid, block, 0, st, a);
+  if (vq == VQ_BLOCK) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_BLOCK>), grid, block, 0, st, a);
+  else if (vq == VQ_G64) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_G64>), grid, block, 0, st, a);
+  else if (fast) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_DENSE>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, false, VQ_DENSE>), grid, block, 0, st, a);
+}
+
+template <typename VT>
+static void launch_pv_n13(const PVArgs& a, bool fast, int B, hipStream_t st) {
+  dim3 grid(a.n_cb * a.n_c2, B), block(256);
+  if (fast) hipLaunchKernelGGL((pv_kernel<VT, 13, true, true, VQ_DENSE>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((pv_kernel<VT, 13, true, false, VQ_DENSE>), grid, block, 0, st, a);
 }
 
 template <typename VT, bool FUSED>
-static int launch_pv_t(const PVArgs& a, bool fast, int B, hipStream_t st) {
-  const int ntw = pv_tiles_per_wave(a.Rvp, FUSED);
-  if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, fast, B, st);
-  else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, fast, B, st);
-  else if constexpr (FUSED) launch_pv_n<VT, FUSED, 13>(a, fast, B, st);
+static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st) {
+  const int ntw = pv_tiles_per_wave(a.Rvp, FUSED, vq);
+  if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, vq, fast, B, st);
+  else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, vq, fast, B, st);
+  else if constexpr (FUSED) launch_pv_n13<VT>(a, fast, B, st);
   int e = (int)hipGetLastError();
   if (e) return e;
   hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 
-int launch_pv(const PVArgs& a, int dtype, bool fused, bool fast, int B, hipStream_t st) {
-  if (dtype == STARKV_F16) return fused ? launch_pv_t<_Float16, true>(a, fast, B, st) : launch_pv_t<_Float16, false>(a, fast, B, st);
-  return fused ? launch_pv_t<__bf16, true>(a, fast, B, st) : launch_pv_t<__bf16, false>(a, fast, B, st);
+// Quantised formats always take the vector-load variant (the C ABI checks the
+// alignment they need).
+int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st) {
+  if (dtype == STARKV_F16)
+    return fused ? launch_pv_t<_Float16, true>(a, vq, fast, B, st) : launch_pv_t<_Float16, false>(a, vq, fast, B, st);
+  return fused ? launch_pv_t<__bf16, true>(a, vq, fast, B, st) : launch_pv_t<__bf16, false>(a, vq, fast, B, st);
 }
 
 __global__ void fill_i32_kernel(int* p, int n, int v) {

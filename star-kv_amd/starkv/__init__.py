@@ -4,8 +4,8 @@ The compute lives in libstarkv.so (HIP kernels behind the C ABI of
 include/starkv.h); this package binds it to torch tensors.
 """
 from ._lib import StarKVError, lib
-from .ops import KLatentSpec, decode_attention, k_logits, pv_latent
+from .ops import KLatentSpec, VLatentSpec, decode_attention, k_logits, pv_latent
 from .rope import RopeConfig, rope_table
 
-__all__ = ["StarKVError", "lib", "KLatentSpec", "decode_attention", "k_logits", "pv_latent",
+__all__ = ["StarKVError", "lib", "KLatentSpec", "VLatentSpec", "decode_attention", "k_logits", "pv_latent",
            "RopeConfig", "rope_table"]

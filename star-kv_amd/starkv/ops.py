@@ -13,8 +13,8 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT8_SYM, DecodeDesc, KLatent, KLogitsDesc, PVDesc,
-                   StarKVError, VLatent, check, i64_array, int_array)
+from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KLatent,
+                   KLogitsDesc, PVDesc, StarKVError, VLatent, check, i64_array, int_array)
 from .rope import RopeConfig, rope_table
 
 HEAD_DIM = 128
@@ -168,28 +168,105 @@ def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = R
     return out
 
 
-def _vdense(xv: torch.Tensor) -> VLatent:
-    if xv.dim() != 3 or xv.stride(2) != 1:
-        raise StarKVError("V latent must be [B, S, Rv] with a contiguous last dim")
-    v = VLatent()
-    v.rank, v.format = xv.shape[2], FMT_DENSE
-    v.data, v.stride_b, v.stride_s = xv.data_ptr(), xv.stride(0), xv.stride(1)
-    return v
+class VLatentSpec:
+    """Where the value latent lives and how it is stored (include/starkv.h,
+    starkv_vlatent).  Build one with ``dense``, ``int4_ref``, ``int8`` or
+    ``int4_g64``; strides are in elements of the stored type (bytes for the
+    packed formats, fp16 elements for scales and zero points)."""
+
+    def __init__(self, rank: int, fmt: int, data: torch.Tensor, scale: Optional[torch.Tensor] = None,
+                 split: int = 0, split_fmt: int = FMT_INT4_REF, data2: Optional[torch.Tensor] = None,
+                 scale2: Optional[torch.Tensor] = None, zero: Optional[torch.Tensor] = None):
+        self.rank, self.fmt, self.data, self.scale = int(rank), fmt, data, scale
+        self.split, self.split_fmt, self.data2, self.scale2, self.zero = int(split), split_fmt, data2, scale2, zero
+
+    @property
+    def tensors(self):
+        return [t for t in (self.data, self.scale, self.data2, self.scale2, self.zero) if t is not None]
+
+    @classmethod
+    def dense(cls, xv: torch.Tensor) -> "VLatentSpec":
+        """[B, S, Rv] act dtype (the reference cache, LlamaLoRaAttention_headwise.py:96-102)."""
+        if xv.dim() != 3 or xv.stride(2) != 1:
+            raise StarKVError("V latent must be [B, S, Rv] with a contiguous last dim")
+        return cls(xv.shape[2], FMT_DENSE, xv)
+
+    @classmethod
+    def int4_ref(cls, x1: torch.Tensor, scale1: torch.Tensor, rank: int, split: Optional[int] = None,
+                 x2: Optional[torch.Tensor] = None, scale2: Optional[torch.Tensor] = None) -> "VLatentSpec":
+        """The reference's quantised V cache (bx_quant.py:117-166): ranks
+        [0, split) in ``x1`` with one fp16 scale per token ``scale1`` [B, S, 1],
+        ranks [split, rank) in ``x2`` / ``scale2``; ``x2`` holds int4 nibbles
+        [B, S, (rank - split)/2] (rank 2k in the low nibble of byte k, value
+        nibble - 8).  ``x1`` holds int4 nibbles [B, S, split/2] (the Triton
+        kernel's reading, bx_quant.py:75-86) or int8 values [B, S, split] (the
+        reading of LlamaLoRaAttention_headwise_quant.py:138, 164); the last
+        dimension tells which."""
+        split = int(rank if split is None else split)
+        if x1.dim() != 3 or scale1.dim() != 3 or x1.stride(2) != 1:
+            raise StarKVError("x1 must be [B, S, bytes] and its scale [B, S, 1]")
+        if x1.shape[2] == split // 2:
+            upper = FMT_INT4_REF
+        elif x1.shape[2] == split and x1.dtype == torch.int8:
+            upper = FMT_INT8_SYM
+        else:
+            raise StarKVError(f"x1 last dim {x1.shape[2]} matches neither int4 ({split // 2}) nor int8 ({split}) storage")
+        if split < rank:
+            if x2 is None or scale2 is None or x2.shape[2] != (rank - split) // 2:
+                raise StarKVError("the lower block needs x2 [B, S, (rank - split)/2] and its scales")
+            return cls(rank, FMT_INT4_REF, x1, scale1, split, upper, x2, scale2)
+        return cls(rank, FMT_INT4_REF if upper == FMT_INT4_REF else FMT_INT8_SYM, x1, scale1)
+
+    @classmethod
+    def int8(cls, q: torch.Tensor, scale: torch.Tensor) -> "VLatentSpec":
+        """int8 [B, S, Rv] with one fp16 scale per token [B, S, 1]: x = q * s."""
+        return cls(q.shape[2], FMT_INT8_SYM, q, scale)
+
+    @classmethod
+    def int4_g64(cls, packed: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor, rank: int) -> "VLatentSpec":
+        """int4 asymmetric, groups of 64 ranks: packed nibbles [B, S, rank/2]
+        (rank 2k low nibble of byte k), fp16 scale and zero [B, S, ceil(rank/64)]
+        with one set of strides: x = n * s + z rounded once to fp16."""
+        if scale.stride() != zero.stride():
+            raise StarKVError("scale and zero must share strides")
+        return cls(rank, FMT_INT4_G64, packed, scale, zero=zero)
+
+    def c_struct(self) -> VLatent:
+        v = VLatent()
+        v.rank, v.format = self.rank, self.fmt
+        d = self.data
+        v.data, v.stride_b, v.stride_s = d.data_ptr(), d.stride(0), d.stride(1)
+        if self.scale is not None:
+            v.scale, v.scale_stride_b, v.scale_stride_s = self.scale.data_ptr(), self.scale.stride(0), self.scale.stride(1)
+        if self.data2 is not None:
+            v.split, v.split_format = self.split, self.split_fmt
+            v.data2, v.stride2_b, v.stride2_s = self.data2.data_ptr(), self.data2.stride(0), self.data2.stride(1)
+            v.scale2, v.scale2_stride_b, v.scale2_stride_s = (self.scale2.data_ptr(), self.scale2.stride(0),
+                                                              self.scale2.stride(1))
+        if self.zero is not None:
+            v.zero = self.zero.data_ptr()
+        return v
 
 
-def pv_latent(p: torch.Tensor, xv: torch.Tensor) -> torch.Tensor:
-    """out[b, h, j] = sum_s p[b, h, s] * xv[b, s, j]  (model.py:484), [B, H, Rv] in p's dtype."""
-    _require_cuda(p, xv)
+def _vspec(xv) -> VLatentSpec:
+    return xv if isinstance(xv, VLatentSpec) else VLatentSpec.dense(xv)
+
+
+def pv_latent(p: torch.Tensor, xv) -> torch.Tensor:
+    """out[b, h, j] = sum_s p[b, h, s] * V[b, s, j]  (model.py:484; bx_quant.py:117-166),
+    [B, H, Rv] in p's dtype.  ``xv``: dense [B, S, Rv] tensor or a VLatentSpec."""
+    v = _vspec(xv)
+    _require_cuda(p, *v.tensors)
     if p.dim() != 3 or p.stride(2) != 1:
         raise StarKVError("p must be [B, H, S] with a contiguous last dim")
     B, H, S = p.shape
-    if xv.shape[0] != B or xv.shape[1] < S:
-        raise StarKVError("xv must be [B, >=S, Rv]")
-    out = torch.empty(B, H, xv.shape[2], dtype=p.dtype, device=p.device)
+    if v.data.shape[0] != B or v.data.shape[1] < S:
+        raise StarKVError("the V latent must be [B, >=S, ...]")
+    out = torch.empty(B, H, v.rank, dtype=p.dtype, device=p.device)
     d = PVDesc()
     d.batch, d.n_heads, d.seq_len, d.dtype = B, H, S, _dt(p)
     d.p, d.p_stride_b, d.p_stride_h = p.data_ptr(), p.stride(0), p.stride(1)
-    d.v = _vdense(xv)
+    d.v = v.c_struct()
     d.out, d.out_stride_b, d.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
     L = _lib.lib()
     nb = L.starkv_pv_latent_workspace_bytes(ctypes.byref(d))
@@ -208,13 +285,15 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     (or float32 with out_dtype=torch.float32).  ``events``: four
     torch.cuda.Event recorded around the three kernels (timing).
 
-    q: rotated query [B, Hq, 128]; k: key-latent spec; xv: V latent [B, S, Rv];
-    uv_weight: v_proj.U.weight [Hkv*128, Rv]; seq_len defaults to xv.shape[1]."""
+    q: rotated query [B, Hq, 128]; k: key-latent spec; xv: V latent [B, S, Rv]
+    (dense tensor) or a VLatentSpec; uv_weight: v_proj.U.weight [Hkv*128, Rv];
+    seq_len defaults to the V latent's position count."""
     q = _q3(q)
-    _require_cuda(q, k.data, k.bk, xv, uv_weight, mask)
+    v = _vspec(xv)
+    _require_cuda(q, k.data, k.bk, uv_weight, mask, *v.tensors)
     B, Hq, _ = q.shape
-    S = int(seq_len if seq_len is not None else xv.shape[1])
-    if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape[1] != xv.shape[2]:
+    S = int(seq_len if seq_len is not None else v.data.shape[1])
+    if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape[1] != v.rank:
         raise StarKVError("uv_weight must be [Hkv*128, Rv] with a contiguous last dim")
     if uv_weight.shape[0] != k.n_kv_heads * HEAD_DIM:
         raise StarKVError("uv_weight rows must be Hkv*128")
@@ -230,7 +309,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     d.dtype = _dt(q)
     d.q, d.q_stride_b, d.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
     d.k = k.c_struct(keep)
-    d.v = _vdense(xv)
+    d.v = v.c_struct()
     d.uv, d.uv_row_stride = uv_weight.data_ptr(), uv_weight.stride(0)
     d.rope_table, d.rope_max_positions = table.data_ptr(), cap
     d.scale = float(scale if scale is not None else 1.0 / math.sqrt(HEAD_DIM)) * rope.attention_scaling
