@@ -54,7 +54,7 @@ def cpu_baseline(case_cpu_fn, reps):
     for _ in range(2):
         fn()
     ts = []
-    t_end = time.perf_counter() + 25.0
+    t_end = time.perf_counter() + 15.0
     for _ in range(reps):
         t0 = time.perf_counter()
         fn()
@@ -70,7 +70,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-reps", type=int, default=7)
+    ap.add_argument("--cpu-reps", type=int, default=100)
+    ap.add_argument("--pmc-calibrate", action="store_true",
+                    help="only run three 1 GiB device-to-device copies (the known-size reference for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE per dispatch) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -84,6 +87,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_calibrate:
+        n = 1 << 30
+        src = torch.full((n // 4,), 7, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration_copy_bytes_read": n, "calibration_copy_bytes_written": n, "copies": 3}))
+        return
     ranks = cfg2_ranks()
     B, H, S, Rv = 16, 32, 32768, 1640
     case = make_case(B, H, H, S, ranks, Rv, dtype=torch.float16, device=dev, seed=0)
