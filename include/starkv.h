@@ -54,7 +54,7 @@ enum {
                                 (bx_quant.py:75-86) */
   STARKV_FMT_INT8_SYM = 2,   /* int8 q*s, one fp16 scale per token (per (b,h,s) for K) */
   STARKV_FMT_INT4_G64 = 3    /* int4 asymmetric, groups of 64 ranks, fp16 scale+zero
-                                per (b,s,group), build-defined MFMA-blocked layout */
+                                per (b,s,group), x = n*s + z rounded once to fp16 */
 };
 
 int starkv_abi_version(void);
@@ -80,21 +80,43 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
  * is head_offset[h] = h*stride(1), pos_stride[h] = stride(2).
  * B_k (k_u^T, model.py:455) row j of head h lives at
  * bk + bk_head_offset[h] + j*bk_row_stride, 128 contiguous elements.
+ *
+ * Quantised K (offsets and strides of data/data2 in bytes; ranks multiples
+ * of 8; every value dequantised to fp16 before use, as the reference's
+ * dequantise-then-multiply path does, LlamaLoRaAttention_headwise_quant.py:
+ * 137-144):
+ *   INT8_SYM  all ranks int8 in data, x = q * s, fp16 scale per (b,h,s) at
+ *             scale + b*scale_stride_b + h*scale_stride_h + s;
+ *   INT4_REF  split == 0: all ranks int4 nibbles in data (rank 2k low nibble
+ *             of byte k, x = (nibble - 8) * s), scale as above;
+ *             split > 0 (multiple of 16): ranks [0, split) in data (int8 when
+ *             split_format is STARKV_FMT_INT8_SYM, else int4 nibbles) with
+ *             scale, ranks [split, rank[h]) as int4 nibbles in data2 at
+ *             data2 + b*stride2_b + head_offset2[h] + s*pos_stride2[h] + byte
+ *             with fp16 scales scale2 (b,h,s) at scale2 + b*scale2_stride_b +
+ *             h*scale2_stride_h + s -- the split cache of
+ *             LlamaLoRaAttention_headwise_quant.py:107-127 (upper 16 ranks).
  * ------------------------------------------------------------------- */
 typedef struct {
   int n_kv_heads;
   const int* rank;                 /* host [Hkv] */
-  const int64_t* head_offset;      /* host [Hkv], elements */
-  const int64_t* pos_stride;       /* host [Hkv], elements */
-  int64_t stride_b;                /* elements */
-  int format;                      /* STARKV_FMT_DENSE or STARKV_FMT_INT8_SYM */
+  const int64_t* head_offset;      /* host [Hkv], elements (bytes when quantised) */
+  const int64_t* pos_stride;       /* host [Hkv], elements (bytes when quantised) */
+  int64_t stride_b;                /* elements (bytes when quantised) */
+  int format;                      /* STARKV_FMT_DENSE, STARKV_FMT_INT8_SYM or STARKV_FMT_INT4_REF */
   const void* data;                /* device */
-  /* INT8_SYM: fp16 scale of (b,h,s) at scale + b*scale_stride_b + h*scale_stride_h + s */
-  const void* scale;
+  const void* scale;               /* quantised: fp16 scales of data */
   int64_t scale_stride_b, scale_stride_h;
   const void* bk;                  /* device, act dtype */
   const int64_t* bk_head_offset;   /* host [Hkv], elements */
   int64_t bk_row_stride;           /* elements */
+  int split, split_format;         /* INT4_REF two-block cache (see above) */
+  const void* data2;
+  const int64_t* head_offset2;     /* host [Hkv], bytes */
+  const int64_t* pos_stride2;      /* host [Hkv], bytes */
+  int64_t stride2_b;               /* bytes */
+  const void* scale2;
+  int64_t scale2_stride_b, scale2_stride_h;
 } starkv_klatent;
 
 /* ---------------------------------------------------------------------
@@ -123,12 +145,22 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
 /* ---------------------------------------------------------------------
  * V-latent description.  Dense: element (b, s, j) at
  * data + b*stride_b + s*stride_s + j (reference cache [B, S, Rv],
- * LlamaLoRaAttention_headwise.py:96-102).  INT4_REF (bx_quant.py:117-166
- * x1/x2): ranks [0, split) in data (bytes, (b,s,byte) at data + b*stride_b +
- * s*stride_s + byte) with fp16 per-token scale `scale`; ranks [split, rank)
- * in data2/scale2 likewise; split_format says whether the upper block is
- * INT4_REF (split/2 bytes per token) or INT8_SYM (split bytes per token).
- * INT4_G64: the build's blocked layout written by starkv_quant_v_g64.
+ * LlamaLoRaAttention_headwise.py:96-102).  Quantised formats (rank and split
+ * multiples of 8; strides of data/data2 in bytes, of scales in fp16
+ * elements; every value dequantised to fp16 exactly as the reference kernel
+ * does, then rounded to bf16 for bf16 activations):
+ *   INT4_REF (bx_quant.py:117-166 x1/x2): with 0 < split < rank, ranks
+ *     [0, split) in data ((b,s,byte) at data + b*stride_b + s*stride_s +
+ *     byte) with the fp16 per-token scale (b,s) at scale + b*scale_stride_b +
+ *     s*scale_stride_s, ranks [split, rank) as int4 in data2/scale2 likewise;
+ *     split_format says whether the upper block holds int4 nibbles
+ *     (STARKV_FMT_INT4_REF, split/2 bytes per token) or int8
+ *     (STARKV_FMT_INT8_SYM, split bytes per token).  Otherwise all ranks are
+ *     int4 nibbles in data.
+ *   INT8_SYM: all ranks int8 in data, per-token scale.
+ *   INT4_G64: nibbles n (rank 2k low nibble of byte k) in data; fp16 scale
+ *     and zero of (b, s, group g = rank/64) at scale / zero + b*scale_stride_b
+ *     + s*scale_stride_s + g; x = n*s + z.
  * ------------------------------------------------------------------- */
 typedef struct {
   int rank;
@@ -139,7 +171,7 @@ typedef struct {
   const void* data2; int64_t stride2_b, stride2_s;
   const void* scale2; int64_t scale2_stride_b, scale2_stride_s;
   const void* zero;   /* INT4_G64 zero points */
-  int capacity;       /* INT4_G64: positions allocated (multiple of 16) */
+  int capacity;       /* reserved (0) */
 } starkv_vlatent;
 
 /* ---------------------------------------------------------------------

@@ -59,14 +59,46 @@ int validate_klatent(const starkv_klatent& k, int Hq, int dtype, int* gs_out) {
   if (Hq > K_MAX_QH) return STARKV_ERR_LIMIT;
   if (!k.rank || !k.head_offset || !k.pos_stride || !k.bk_head_offset) return STARKV_ERR_NULL;
   if (!k.data || !k.bk) return STARKV_ERR_NULL;
-  if (k.format != STARKV_FMT_DENSE && k.format != STARKV_FMT_INT8_SYM) return STARKV_ERR_FORMAT;
-  if (k.format == STARKV_FMT_INT8_SYM && !k.scale) return STARKV_ERR_NULL;
+  if (k.format != STARKV_FMT_DENSE && k.format != STARKV_FMT_INT8_SYM && k.format != STARKV_FMT_INT4_REF)
+    return STARKV_ERR_FORMAT;
   if (dtype != STARKV_F16 && dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
-  for (int h = 0; h < k.n_kv_heads; ++h) {
+  for (int h = 0; h < k.n_kv_heads; ++h)
     if (k.rank[h] < 1 || k.rank[h] > 128) return STARKV_ERR_RANK;
-    if (k.pos_stride[h] < k.rank[h] || k.head_offset[h] < 0) return STARKV_ERR_SHAPE;
-  }
   if (k.stride_b < 0 || k.bk_row_stride < HEAD_DIM) return STARKV_ERR_SHAPE;
+  if (k.format == STARKV_FMT_DENSE) {
+    for (int h = 0; h < k.n_kv_heads; ++h)
+      if (k.pos_stride[h] < k.rank[h] || k.head_offset[h] < 0) return STARKV_ERR_SHAPE;
+  } else {
+    // quantised: ranks multiples of 8, rows aligned for 8-byte (int8) / 4-byte (int4) loads
+    if (!k.scale) return STARKV_ERR_NULL;
+    const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+    if (two && (k.split % 16 || k.split > 128)) return STARKV_ERR_SHAPE;
+    if (two && k.split_format != STARKV_FMT_INT4_REF && k.split_format != STARKV_FMT_INT8_SYM) return STARKV_ERR_FORMAT;
+    const int split = two ? k.split : 128;
+    const bool a8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
+    const int al_a = a8 ? 8 : 4;
+    if (!al(k.data, al_a) || !al64(k.stride_b, al_a) || !al(k.scale, 2)) return STARKV_ERR_ALIGN;
+    if (k.scale_stride_b < 0 || k.scale_stride_h < 0) return STARKV_ERR_SHAPE;
+    bool any_lo = false;
+    for (int h = 0; h < k.n_kv_heads; ++h) {
+      const int r = k.rank[h];
+      if (r % 8) return STARKV_ERR_SHAPE;
+      const int ra = std::min(r, split);
+      if (k.head_offset[h] < 0 || k.pos_stride[h] < (a8 ? ra : ra / 2)) return STARKV_ERR_SHAPE;
+      if (!al64(k.head_offset[h], al_a) || !al64(k.pos_stride[h], al_a)) return STARKV_ERR_ALIGN;
+      any_lo |= r > split;
+    }
+    if (any_lo) {
+      if (!k.data2 || !k.scale2 || !k.head_offset2 || !k.pos_stride2) return STARKV_ERR_NULL;
+      if (!al(k.data2, 4) || !al64(k.stride2_b, 4) || !al(k.scale2, 2)) return STARKV_ERR_ALIGN;
+      if (k.stride2_b < 0 || k.scale2_stride_b < 0 || k.scale2_stride_h < 0) return STARKV_ERR_SHAPE;
+      for (int h = 0; h < k.n_kv_heads; ++h) {
+        if (k.rank[h] <= split) continue;
+        if (k.head_offset2[h] < 0 || k.pos_stride2[h] < (k.rank[h] - split) / 2) return STARKV_ERR_SHAPE;
+        if (!al64(k.head_offset2[h], 4) || !al64(k.pos_stride2[h], 4)) return STARKV_ERR_ALIGN;
+      }
+    }
+  }
   *gs_out = Hq / k.n_kv_heads;
   return STARKV_OK;
 }
@@ -115,22 +147,34 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan)
       }
     }
   }
+  const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+  a.ksplit = two ? k.split : 128;
+  a.k_a_int8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
+  a.x2 = k.data2; a.x2_sb = k.stride2_b;
+  a.xscale2 = k.scale2; a.xs2_sb = k.scale2_stride_b; a.xs2_sh = k.scale2_stride_h;
   for (int h = 0; h < k.n_kv_heads; ++h) {
     a.xoff[h] = k.head_offset[h];
     a.xpitch[h] = (int)k.pos_stride[h];
     a.bkoff[h] = k.bk_head_offset[h];
+    const bool lo = two && k.rank[h] > k.split;
+    a.xoff2[h] = lo ? k.head_offset2[h] : 0;
+    a.xpitch2[h] = lo ? (int)k.pos_stride2[h] : 0;
   }
   a.n_wg = plan.n_wg;
   a.maxi = maxi;
   return STARKV_OK;
 }
 
+// Vector-load variant: B_k and q rows 8-byte aligned, and (dense) latent rows
+// 16-byte aligned with ranks a multiple of 8.  Quantised latents are always
+// read with vector loads (their alignment is validated).
 bool k_fast(const starkv_klatent& k, int dtype, const void* q, int64_t q_sb, int64_t q_sh) {
-  const int xe = k.format == STARKV_FMT_INT8_SYM ? 1 : esize(dtype);
-  if (!al(k.data, 16) || !al64(k.stride_b * xe, 16)) return false;
+  const bool dense = k.format == STARKV_FMT_DENSE;
+  const int xe = esize(dtype);
+  if (dense && (!al(k.data, 16) || !al64(k.stride_b * xe, 16))) return false;
   for (int h = 0; h < k.n_kv_heads; ++h) {
-    if (k.rank[h] % (xe == 1 ? 16 : 8)) return false;
-    if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
+    if (dense && k.rank[h] % 8) return false;
+    if (dense && (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16))) return false;
     if (!al64(k.bk_head_offset[h] * 2, 8)) return false;
   }
   if (!al(k.bk, 8) || !al64(k.bk_row_stride * 2, 8)) return false;

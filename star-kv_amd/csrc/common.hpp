@@ -44,17 +44,22 @@ __device__ inline bool item_valid(uint32_t w) { return (w >> 27) & 1; }
 struct KArgs {
   const void* q; int64_t q_sb, q_sh;
   const void* x; int64_t x_sb;
-  const void* xscale; int64_t xs_sb, xs_sh;       // int8 K scales (fp16)
+  const void* xscale; int64_t xs_sb, xs_sh;       // quantised K: fp16 scales of x per (b, h, s)
+  const void* x2; int64_t x2_sb;                   // quantised K lower block (int4 nibbles, bytes)
+  const void* xscale2; int64_t xs2_sb, xs2_sh;     // its fp16 scales
+  int ksplit, k_a_int8;                            // ranks [0, ksplit) in x (int8 if k_a_int8, else int4)
   const void* bk; int64_t bk_rs;
   const uint4* rope;                               // RoPE operand table [tile][8][64] x 16 B
   const void* mask; int64_t m_sb, m_sh; int mask_dtype;
   void* out; int64_t o_sb, o_sh;
   float* chunkmax;                                 // [B][Hq][n_chunks] (optional)
   int S, Hq, n_chunks, tiles_per_chunk, n_wg;
-  int maxi;                                        // items per wave of the launched variant (3 or 4)
+  int maxi;                                        // items per wave of the launched variant (2 or 4)
   float wscale;                                    // softmax scale * rope attention scaling
-  int64_t xoff[K_MAX_KV];
+  int64_t xoff[K_MAX_KV];                          // per KV head: elements (dense) or bytes (quantised)
   int xpitch[K_MAX_KV];
+  int64_t xoff2[K_MAX_KV];                         // lower block (bytes)
+  int xpitch2[K_MAX_KV];
   int64_t bkoff[K_MAX_KV];
   uint32_t items[K_MAX_WAVES][K_MAXI];             // [workgroup plan * waves + wave][item]
 };

@@ -65,14 +65,6 @@ __device__ inline float dot8(uint4 u, const floatx16& acc, int v0, float part) {
   return part;
 }
 
-__device__ inline float dot_i8x4(uint32_t w, const floatx16& acc, int v0, float part) {
-  part = fmaf((float)(int)(int8_t)(w & 0xff), acc[v0], part);
-  part = fmaf((float)(int)(int8_t)((w >> 8) & 0xff), acc[v0 + 1], part);
-  part = fmaf((float)(int)(int8_t)((w >> 16) & 0xff), acc[v0 + 2], part);
-  part = fmaf((float)(int)(int8_t)(w >> 24), acc[v0 + 3], part);
-  return part;
-}
-
 // Latent loads are cached: one instruction reads 16 bytes of each of 32
 // position rows, so the other pieces of each cache line are picked up by the
 // item's next load from L1/L2 (non-temporal loads would refetch the line).
@@ -90,11 +82,47 @@ struct TStage {
 
 template <int XFMT, int MAXI>
 struct KBuf {
-  uint4 x[MAXI][2];      // latent: 16 ranks of one position per lane
-  float sc[MAXI];        // int8 format: per-position scale
+  uint4 x[MAXI][XFMT == 0 ? 2 : 1];   // latent: 16 ranks of one position per lane (quantised: packed)
+  uint16_t sq[XFMT == 0 ? 1 : MAXI];  // quantised: fp16 scale bits of the lane's block at that position
 };
 
-// XFMT: 0 = dense act dtype, 2 = int8 symmetric with per-(b,kv,s) fp16 scale
+typedef _Float16 kh2 __attribute__((ext_vector_type(2)));
+
+// 16 quantised ranks -> 16 fp16 values, bit-exact fp16(n * s): the integer is
+// biased into the fp16 pattern 1024 + n (exact), the bias removed (exact) and
+// one correctly rounded packed-fp16 multiply by the scale.  int8: 16 bytes;
+// int4: 8 bytes (rank 2k in the low nibble of byte k, value nibble - 8).
+__device__ inline void dequant16(uint4 r, bool k8, uint16_t s16, uint4& lo, uint4& hi) {
+  uint32_t pr[8];
+  _Float16 bias;
+  if (k8) {
+    const uint32_t w[4] = {r.x ^ 0x80808080u, r.y ^ 0x80808080u, r.z ^ 0x80808080u, r.w ^ 0x80808080u};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      pr[2 * k] = (w[k] & 0xFFu) | ((w[k] << 8) & 0xFF0000u);
+      pr[2 * k + 1] = ((w[k] >> 16) & 0xFFu) | ((w[k] >> 8) & 0xFF0000u);
+    }
+    bias = (_Float16)-1152.0f;
+  } else {
+    const uint32_t w[2] = {r.x, r.y};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t u = w[k >> 2] >> (8 * (k & 3));
+      pr[k] = (u & 0xFu) | (((u >> 4) & 0xFu) << 16);
+    }
+    bias = (_Float16)-1032.0f;
+  }
+  const kh2 s = __builtin_bit_cast(kh2, (uint32_t)s16 * 0x10001u), b2 = {bias, bias};
+  uint32_t o[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    o[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(kh2, pr[k] | 0x64006400u) + b2) * s);
+  lo = make_uint4(o[0], o[1], o[2], o[3]);
+  hi = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// XFMT: 0 = dense act dtype, 1 = quantised blocks (int8 / int4 with per-(b,kv,s)
+//       fp16 scales, dequantised to fp16 before the dot)
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
 // NW waves x MAXI items.  The folded query matrices W stay in registers (the
 // MFMA A operand, 32 VGPRs per item).  The rotation operand (8 KB per
@@ -104,7 +132,7 @@ struct KBuf {
 // kernel near 3.5 TB/s.
 template <typename XT, int XFMT, int OUTK, bool FAST, int MAXI, int NW, int G>
 __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
-  constexpr int XE = XFMT == 2 ? 1 : 2;
+  constexpr int XE = 2;   // dense latent element size
   constexpr int NT = NW * 64;
   constexpr int TPT = 512 / NT;   // 16-byte rotation pieces staged per thread per tile
   static_assert(512 % NT == 0, "workgroup must divide the rotation tile");
@@ -169,7 +197,6 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
   const char* xb[MAXI];
   int off1[MAXI], off2[MAXI];
   int64_t xpitch[MAXI];
-  const _Float16* scb[MAXI];
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     const int kv = item_kv(it[i]), mt = item_mt(it[i]);
@@ -178,8 +205,28 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
     xb[i] = (const char*)a.x + (b * a.x_sb + a.xoff[kv] + mt * 32) * XE;
     off1[i] = nvh > 0 ? 16 * hh * XE : 0;
     off2[i] = nvh >= 16 ? (16 * hh + 8) * XE : off1[i];
-    scb[i] = nullptr;
-    if constexpr (XFMT == 2) scb[i] = (const _Float16*)a.xscale + b * a.xs_sb + (int64_t)kv * a.xs_sh;
+  }
+  // quantised: each lane's 16 ranks sit in one block (split is a multiple of 16)
+  const uint8_t* qb[MAXI];
+  const uint16_t* qs[MAXI];
+  int64_t qpitch[MAXI];
+  int qoff[MAXI];
+  bool qk8[MAXI], q16[MAXI];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    if constexpr (XFMT != 1) break;
+    const int kv = item_kv(it[i]), mt = item_mt(it[i]);
+    const int nv = item_valid(it[i]) ? item_nv(it[i]) : 0;
+    const int nvh = nv - 16 * hh;
+    const int jl = nvh > 0 ? mt * 32 + 16 * hh : mt * 32;     // lanes past the valid ranks re-read the first 16
+    const bool inA = jl < a.ksplit;
+    qk8[i] = inA && a.k_a_int8;
+    q16[i] = (nvh > 0 ? nvh : nv) >= 16;
+    qb[i] = inA ? (const uint8_t*)a.x + b * a.x_sb + a.xoff[kv] : (const uint8_t*)a.x2 + b * a.x2_sb + a.xoff2[kv];
+    qpitch[i] = inA ? a.xpitch[kv] : a.xpitch2[kv];
+    qoff[i] = qk8[i] ? jl : (inA ? jl / 2 : (jl - a.ksplit) / 2);
+    qs[i] = inA ? (const uint16_t*)a.xscale + b * a.xs_sb + (int64_t)kv * a.xs_sh
+                : (const uint16_t*)a.xscale2 + b * a.xs2_sb + (int64_t)kv * a.xs2_sh;
   }
 
   float mx[MAXI];
@@ -200,8 +247,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
 #pragma unroll
     for (int i = 0; i < MAXI; ++i) {
       if (!item_valid(it[i])) continue;
-      const char* p = xb[i] + (int64_t)pos * xpitch[i];
       if constexpr (XFMT == 0) {
+        const char* p = xb[i] + (int64_t)pos * xpitch[i];
         if (FAST) {
           kb.x[i][0] = ld_stream(p + off1[i]);
           kb.x[i][1] = ld_stream(p + off2[i]);
@@ -214,19 +261,21 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
           kb.x[i][1] = make_uint4(tmp[8] | (tmp[9] << 16), tmp[10] | (tmp[11] << 16), tmp[12] | (tmp[13] << 16), tmp[14] | (tmp[15] << 16));
         }
       } else {
-        if (FAST) {
-          const uint2 lo = ld_stream8(p + off1[i]);
-          const uint2 hi = ld_stream8(p + (item_nv(it[i]) - 16 * hh >= 16 ? off1[i] + 8 : off1[i]));
-          kb.x[i][0] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        const uint8_t* q = qb[i] + (int64_t)pos * qpitch[i] + qoff[i];
+        uint4 r = make_uint4(0, 0, 0, 0);
+        if (qk8[i]) {
+          const uint2 lo = *(const uint2*)q;
+          r.x = lo.x; r.y = lo.y;
+          if (q16[i]) {
+            const uint2 hi = *(const uint2*)(q + 8);
+            r.z = hi.x; r.w = hi.y;
+          }
         } else {
-          const int nvh = item_nv(it[i]) - 16 * hh;
-          uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-          for (int v = 0; v < 16; ++v) if (v < nvh) w[v >> 2] |= (uint32_t)((const uint8_t*)(p + 16 * hh))[v] << (8 * (v & 3));
-          kb.x[i][0] = make_uint4(w[0], w[1], w[2], w[3]);
+          r.x = *(const uint32_t*)q;
+          if (q16[i]) r.y = *(const uint32_t*)(q + 4);
         }
-        kb.sc[i] = 0.f;
-        if (item_last(it[i])) kb.sc[i] = (float)scb[i][pos];
+        kb.x[i][0] = r;
+        kb.sq[i] = qs[i][pos];
       }
     }
   };
@@ -266,15 +315,14 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
         part = dot8<XT>(kb.x[i][0], acc, 0, part);
         part = dot8<XT>(kb.x[i][1], acc, 8, part);
       } else {
-        part = dot_i8x4(kb.x[i][0].x, acc, 0, part);
-        part = dot_i8x4(kb.x[i][0].y, acc, 4, part);
-        part = dot_i8x4(kb.x[i][0].z, acc, 8, part);
-        part = dot_i8x4(kb.x[i][0].w, acc, 12, part);
+        uint4 h0, h1;
+        dequant16(kb.x[i][0], qk8[i], kb.sq[i], h0, h1);
+        part = dot8<_Float16>(h0, acc, 0, part);
+        part = dot8<_Float16>(h1, acc, 8, part);
       }
       if (item_last(it[i])) {
         float tot = add_halves(part);
         part = 0.f;
-        if constexpr (XFMT == 2) tot *= kb.sc[i];
         const int qh = item_qh(it[i]);
         if (store) {
           if (a.mask != nullptr) tot += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
@@ -360,9 +408,9 @@ static int launch_o(const KArgs& a, int outk, bool fast, int B, hipStream_t st) 
 
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st) {
   const int outk = out_f32 ? 0 : (out_dtype == STARKV_F16 ? 1 : 2);
-  const bool i8 = fmt == STARKV_FMT_INT8_SYM;
-  if (dtype == STARKV_F16) return i8 ? launch_o<_Float16, 2>(a, outk, fast, B, st) : launch_o<_Float16, 0>(a, outk, fast, B, st);
-  return i8 ? launch_o<__bf16, 2>(a, outk, fast, B, st) : launch_o<__bf16, 0>(a, outk, fast, B, st);
+  const bool q = fmt != STARKV_FMT_DENSE;
+  if (dtype == STARKV_F16) return q ? launch_o<_Float16, 1>(a, outk, fast, B, st) : launch_o<_Float16, 0>(a, outk, fast, B, st);
+  return q ? launch_o<__bf16, 1>(a, outk, fast, B, st) : launch_o<__bf16, 0>(a, outk, fast, B, st);
 }
 
 }  // namespace starkv

@@ -37,6 +37,14 @@ class KLatent(ctypes.Structure):
         ("bk", ctypes.c_void_p),
         ("bk_head_offset", c_i64p),
         ("bk_row_stride", ctypes.c_int64),
+        ("split", ctypes.c_int), ("split_format", ctypes.c_int),
+        ("data2", ctypes.c_void_p),
+        ("head_offset2", c_i64p),
+        ("pos_stride2", c_i64p),
+        ("stride2_b", ctypes.c_int64),
+        ("scale2", ctypes.c_void_p),
+        ("scale2_stride_b", ctypes.c_int64),
+        ("scale2_stride_h", ctypes.c_int64),
     ]
 
 

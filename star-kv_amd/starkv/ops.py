@@ -66,7 +66,10 @@ class KLatentSpec:
     def __init__(self, data: torch.Tensor, ranks: Sequence[int], head_offset: Sequence[int],
                  pos_stride: Sequence[int], stride_b: int, bk: torch.Tensor, bk_head_offset: Sequence[int],
                  bk_row_stride: int, fmt: int = FMT_DENSE, scale: Optional[torch.Tensor] = None,
-                 scale_stride_b: int = 0, scale_stride_h: int = 0):
+                 scale_stride_b: int = 0, scale_stride_h: int = 0, split: int = 0, split_fmt: int = FMT_INT4_REF,
+                 data2: Optional[torch.Tensor] = None, head_offset2: Optional[Sequence[int]] = None,
+                 pos_stride2: Optional[Sequence[int]] = None, stride2_b: int = 0,
+                 scale2: Optional[torch.Tensor] = None, scale2_stride_b: int = 0, scale2_stride_h: int = 0):
         self.data, self.bk, self.scale = data, bk, scale
         self.ranks = [int(r) for r in ranks]
         self.head_offset = [int(v) for v in head_offset]
@@ -76,6 +79,17 @@ class KLatentSpec:
         self.bk_row_stride = int(bk_row_stride)
         self.fmt = fmt
         self.scale_stride_b, self.scale_stride_h = int(scale_stride_b), int(scale_stride_h)
+        self.split, self.split_fmt = int(split), split_fmt
+        self.data2, self.scale2 = data2, scale2
+        n = len(self.ranks)
+        self.head_offset2 = [int(v) for v in (head_offset2 or [0] * n)]
+        self.pos_stride2 = [int(v) for v in (pos_stride2 or [0] * n)]
+        self.stride2_b = int(stride2_b)
+        self.scale2_stride_b, self.scale2_stride_h = int(scale2_stride_b), int(scale2_stride_h)
+
+    @property
+    def tensors(self):
+        return [t for t in (self.data, self.bk, self.scale, self.data2, self.scale2) if t is not None]
 
     @property
     def n_kv_heads(self) -> int:
@@ -96,13 +110,58 @@ class KLatentSpec:
         return cls(x, [r] * H, [h * x.stride(1) for h in range(H)], [x.stride(2)] * H, x.stride(0),
                    b, [h * b.stride(0) for h in range(H)], b.stride(1))
 
+    @staticmethod
+    def _bk_args(b: torch.Tensor, n_heads: int):
+        """B_k [Hkv_b, r, 128]; with n_heads = a multiple of Hkv_b (a latent
+        cache repeated per query head, LlamaLoRaAttention_headwise_quant.py:
+        146-147), latent head h uses B_k of head h // (n_heads // Hkv_b)."""
+        if b.dim() != 3 or b.shape[2] != HEAD_DIM or b.stride(2) != 1 or n_heads % b.shape[0]:
+            raise StarKVError("b must be [Hkv, r, 128] with a contiguous last dim")
+        rep = n_heads // b.shape[0]
+        return [(h // rep) * b.stride(0) for h in range(n_heads)], b.stride(1)
+
+    @classmethod
+    def from_reference_quant(cls, x1: torch.Tensor, s1: torch.Tensor, b: torch.Tensor, rank: int,
+                             x2: Optional[torch.Tensor] = None, s2: Optional[torch.Tensor] = None,
+                             split: Optional[int] = None) -> "KLatentSpec":
+        """The quantised K cache of LlamaLoRaAttention_headwise_quant.py:107-127:
+        x1 [B, H, S, split] int8 (or [B, H, S, split/2] uint8 int4 nibbles),
+        s1 [B, H, S, 1] fp16, x2 [B, H, S, (rank - split)/2] uint8 int4 nibbles,
+        s2 [B, H, S, 1] fp16; b = k_u^T [Hkv, rank, 128] with H = Hkv or a
+        multiple of it.  With x2 None, x1 holds all ranks (int8: INT8_SYM,
+        uint8 nibbles: INT4_REF)."""
+        if x1.dim() != 4 or s1.dim() != 4 or x1.stride(3) != 1:
+            raise StarKVError("x1 must be [B, H, S, bytes] and s1 [B, H, S, 1]")
+        B, H, S, w1 = x1.shape
+        rank = int(rank)
+        bko, bkr = cls._bk_args(b, H)
+        ho, ps = [h * x1.stride(1) for h in range(H)], [x1.stride(2)] * H
+        if x2 is None:
+            if x1.dtype == torch.int8 and w1 == rank:
+                fmt = FMT_INT8_SYM
+            elif w1 * 2 == rank:
+                fmt = FMT_INT4_REF
+            else:
+                raise StarKVError(f"x1 last dim {w1} matches neither int8 nor int4 storage of rank {rank}")
+            return cls(x1, [rank] * H, ho, ps, x1.stride(0), b, bko, bkr, fmt, s1, s1.stride(0), s1.stride(1))
+        split = int(split if split is not None else (w1 if x1.dtype == torch.int8 else 2 * w1))
+        upper = FMT_INT8_SYM if (x1.dtype == torch.int8 and w1 == split) else FMT_INT4_REF
+        if upper == FMT_INT4_REF and w1 * 2 != split:
+            raise StarKVError("x1 does not hold `split` ranks")
+        if x2.dim() != 4 or x2.shape[3] * 2 != rank - split or x2.stride(3) != 1:
+            raise StarKVError("x2 must be [B, H, S, (rank - split)/2]")
+        return cls(x1, [rank] * H, ho, ps, x1.stride(0), b, bko, bkr, FMT_INT4_REF, s1, s1.stride(0), s1.stride(1),
+                   split=split, split_fmt=upper, data2=x2, head_offset2=[h * x2.stride(1) for h in range(H)],
+                   pos_stride2=[x2.stride(2)] * H, stride2_b=x2.stride(0), scale2=s2,
+                   scale2_stride_b=s2.stride(0), scale2_stride_h=s2.stride(1))
+
     def c_struct(self, keep: list) -> KLatent:
         arrs = (int_array(self.ranks), i64_array(self.head_offset), i64_array(self.pos_stride),
-                i64_array(self.bk_head_offset))
+                i64_array(self.bk_head_offset), i64_array(self.head_offset2), i64_array(self.pos_stride2))
         keep.extend(arrs)
         k = KLatent()
         k.n_kv_heads = self.n_kv_heads
-        k.rank, k.head_offset, k.pos_stride, k.bk_head_offset = arrs
+        k.rank, k.head_offset, k.pos_stride, k.bk_head_offset = arrs[:4]
         k.stride_b = self.stride_b
         k.format = self.fmt
         k.data = self.data.data_ptr()
@@ -110,6 +169,13 @@ class KLatentSpec:
         k.scale_stride_b, k.scale_stride_h = self.scale_stride_b, self.scale_stride_h
         k.bk = self.bk.data_ptr()
         k.bk_row_stride = self.bk_row_stride
+        k.split, k.split_format = self.split, self.split_fmt
+        k.head_offset2, k.pos_stride2 = arrs[4], arrs[5]
+        if self.data2 is not None:
+            k.data2, k.stride2_b = self.data2.data_ptr(), self.stride2_b
+        if self.scale2 is not None:
+            k.scale2, k.scale2_stride_b, k.scale2_stride_h = (self.scale2.data_ptr(), self.scale2_stride_b,
+                                                              self.scale2_stride_h)
         return k
 
 
@@ -146,7 +212,7 @@ def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = R
              out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """logits[b, q, s] = scale * q_rot[b,q] . RoPE_s(X_k[b, q//gs, s] @ B_k[q//gs]) (+ mask), [B, Hq, S]."""
     q = _q3(q)
-    _require_cuda(q, k.data, k.bk, mask)
+    _require_cuda(q, mask, *k.tensors)
     B, Hq, _ = q.shape
     S = int(seq_len)
     out_dtype = out_dtype or torch.float32
@@ -290,7 +356,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     seq_len defaults to the V latent's position count."""
     q = _q3(q)
     v = _vspec(xv)
-    _require_cuda(q, k.data, k.bk, uv_weight, mask, *v.tensors)
+    _require_cuda(q, uv_weight, mask, *k.tensors, *v.tensors)
     B, Hq, _ = q.shape
     S = int(seq_len if seq_len is not None else v.data.shape[1])
     if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape[1] != v.rank:

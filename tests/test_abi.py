@@ -55,6 +55,7 @@ _C_LAYOUT = r"""
 #define S(T) printf(#T " sizeof %zu\n", sizeof(T));
 int main(void) {
   S(starkv_klatent) F(starkv_klatent, rank) F(starkv_klatent, data) F(starkv_klatent, scale_stride_h) F(starkv_klatent, bk_row_stride)
+  F(starkv_klatent, split) F(starkv_klatent, data2) F(starkv_klatent, pos_stride2) F(starkv_klatent, scale2_stride_h)
   S(starkv_klogits_desc) F(starkv_klogits_desc, q) F(starkv_klogits_desc, k) F(starkv_klogits_desc, rope_table)
   F(starkv_klogits_desc, scale) F(starkv_klogits_desc, mask) F(starkv_klogits_desc, out) F(starkv_klogits_desc, out_stride_h)
   S(starkv_vlatent) F(starkv_vlatent, data) F(starkv_vlatent, split) F(starkv_vlatent, data2) F(starkv_vlatent, zero) F(starkv_vlatent, capacity)
