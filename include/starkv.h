@@ -228,6 +228,40 @@ int starkv_decode_attention(const starkv_decode_desc* d, void* workspace, size_t
 int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes,
                                   void* stream, void* const* events);
 
+/* ---------------------------------------------------------------------
+ * Latent-cache writers.  Quantise (or copy) n_tokens new latent rows into a
+ * preallocated cache at positions [pos0, pos0 + n_tokens), in place.
+ * Replaces the per-step torch.cat of HF DynamicLayer.update
+ * (HF:cache_utils.py:127-146, via model.py:411-419) and the quantise-on-write
+ * of LlamaLoRaAttention_headwise_quant.py:107-127 (quantize_r_split_int8_
+ * int4_packed, absent from the reference): int8 blocks s = fp16(amax/127),
+ * q = clip(rint(x/s), -127, 127); int4 blocks s = fp16(amax/7),
+ * n = clip(rint(x/s), -8, 7) stored as nibble n+8; group-64 asymmetric
+ * z = fp16(min), s = fp16((max-z)/15), n = clip(rint((x-z)/s), 0, 15); a zero
+ * scale becomes 1; divisions correctly rounded, rint half to even.
+ * The cache is the same description the attention entry points read (for K
+ * the B_k fields are ignored); capacity is the number of positions it holds.
+ * src: act dtype; K row (b, h, t) of rank[h] elements at src +
+ * b*src_stride_b + h*src_stride_h + t*src_stride_t, V row (b, t) of rank
+ * elements at src + b*src_stride_b + t*src_stride_t.
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int batch, n_tokens, pos0, capacity;
+  int dtype;
+  const void* src; int64_t src_stride_b, src_stride_h, src_stride_t;
+  starkv_klatent k;
+} starkv_k_append_desc;
+
+typedef struct {
+  int batch, n_tokens, pos0, capacity;
+  int dtype;
+  const void* src; int64_t src_stride_b, src_stride_t;
+  starkv_vlatent v;
+} starkv_v_append_desc;
+
+int starkv_k_append(const starkv_k_append_desc* d, void* stream);
+int starkv_v_append(const starkv_v_append_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

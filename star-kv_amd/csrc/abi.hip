@@ -53,18 +53,32 @@ struct KPlan {
   bool fast = false;
 };
 
+int validate_klayout(const starkv_klatent& k, int dtype);
+
 int validate_klatent(const starkv_klatent& k, int Hq, int dtype, int* gs_out) {
   if (k.n_kv_heads < 1 || k.n_kv_heads > K_MAX_KV) return k.n_kv_heads < 1 ? STARKV_ERR_SHAPE : STARKV_ERR_LIMIT;
   if (Hq < 1 || Hq % k.n_kv_heads) return STARKV_ERR_SHAPE;
   if (Hq > K_MAX_QH) return STARKV_ERR_LIMIT;
-  if (!k.rank || !k.head_offset || !k.pos_stride || !k.bk_head_offset) return STARKV_ERR_NULL;
-  if (!k.data || !k.bk) return STARKV_ERR_NULL;
+  if (!k.bk_head_offset || !k.bk) return STARKV_ERR_NULL;
+  if (k.bk_row_stride < HEAD_DIM) return STARKV_ERR_SHAPE;
+  const int st = validate_klayout(k, dtype);
+  if (st) return st;
+  *gs_out = Hq / k.n_kv_heads;
+  return STARKV_OK;
+}
+
+// Where the K latent lives and how it is stored (shared by the attention
+// entry points and the cache writer).
+int validate_klayout(const starkv_klatent& k, int dtype) {
+  if (k.n_kv_heads < 1 || k.n_kv_heads > K_MAX_KV) return k.n_kv_heads < 1 ? STARKV_ERR_SHAPE : STARKV_ERR_LIMIT;
+  if (!k.rank || !k.head_offset || !k.pos_stride) return STARKV_ERR_NULL;
+  if (!k.data) return STARKV_ERR_NULL;
   if (k.format != STARKV_FMT_DENSE && k.format != STARKV_FMT_INT8_SYM && k.format != STARKV_FMT_INT4_REF)
     return STARKV_ERR_FORMAT;
   if (dtype != STARKV_F16 && dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
   for (int h = 0; h < k.n_kv_heads; ++h)
     if (k.rank[h] < 1 || k.rank[h] > 128) return STARKV_ERR_RANK;
-  if (k.stride_b < 0 || k.bk_row_stride < HEAD_DIM) return STARKV_ERR_SHAPE;
+  if (k.stride_b < 0) return STARKV_ERR_SHAPE;
   if (k.format == STARKV_FMT_DENSE) {
     for (int h = 0; h < k.n_kv_heads; ++h)
       if (k.pos_stride[h] < k.rank[h] || k.head_offset[h] < 0) return STARKV_ERR_SHAPE;
@@ -99,7 +113,6 @@ int validate_klatent(const starkv_klatent& k, int Hq, int dtype, int* gs_out) {
       }
     }
   }
-  *gs_out = Hq / k.n_kv_heads;
   return STARKV_OK;
 }
 
@@ -487,6 +500,58 @@ int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, 
                                   void* stream, void* const* events) {
   if (!events || !events[0] || !events[1] || !events[2] || !events[3]) return STARKV_ERR_NULL;
   return decode_impl(d, workspace, workspace_bytes, stream, events);
+}
+
+int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;
+  if ((int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  const starkv_klatent& k = d->k;
+  int st = validate_klayout(k, d->dtype);
+  if (st) return st;
+  if (!d->src) return STARKV_ERR_NULL;
+  if (d->src_stride_b < 0 || d->src_stride_h < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
+  KAppendArgs a = {};
+  a.src = d->src; a.src_sb = d->src_stride_b; a.src_sh = d->src_stride_h; a.src_st = d->src_stride_t;
+  a.B = d->batch; a.H = k.n_kv_heads; a.T = d->n_tokens; a.pos0 = d->pos0;
+  a.fmt = k.format;
+  a.data = (void*)k.data; a.stride_b = k.stride_b;
+  a.scale = (void*)k.scale; a.sc_sb = k.scale_stride_b; a.sc_sh = k.scale_stride_h;
+  const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+  a.split = two ? k.split : 128;
+  a.a_int8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
+  a.data2 = (void*)k.data2; a.stride2_b = k.stride2_b;
+  a.scale2 = (void*)k.scale2; a.sc2_sb = k.scale2_stride_b; a.sc2_sh = k.scale2_stride_h;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    a.rank[h] = k.rank[h];
+    a.off[h] = k.head_offset[h]; a.pitch[h] = k.pos_stride[h];
+    const bool lo = two && k.rank[h] > k.split;
+    a.off2[h] = lo ? k.head_offset2[h] : 0; a.pitch2[h] = lo ? k.pos_stride2[h] : 0;
+  }
+  return launch_k_append(a, d->dtype, (hipStream_t)stream);
+}
+
+int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;
+  if ((int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  PVArgs pa = {};
+  int vq = 0, st;
+  if ((st = validate_v(d->v, pa, &vq))) return st;
+  if (!d->src) return STARKV_ERR_NULL;
+  if (d->src_stride_b < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
+  VAppendArgs a = {};
+  a.src = d->src; a.src_sb = d->src_stride_b; a.src_st = d->src_stride_t;
+  a.B = d->batch; a.T = d->n_tokens; a.pos0 = d->pos0; a.R = d->v.rank; a.vq = vq;
+  a.data = (void*)pa.x; a.stride_b = pa.x_sb; a.stride_s = pa.x_ss;
+  a.scale = (void*)pa.xs; a.sc_sb = pa.xs_sb; a.sc_ss = pa.xs_ss;
+  a.zero = (void*)pa.xz;
+  a.split = pa.split; a.a_int8 = pa.a_int8;
+  a.data2 = (void*)pa.x2; a.stride2_b = pa.x2_sb; a.stride2_s = pa.x2_ss;
+  a.scale2 = (void*)pa.xs2; a.sc2_sb = pa.xs2_sb; a.sc2_ss = pa.xs2_ss;
+  return launch_v_append(a, d->dtype, (hipStream_t)stream);
 }
 
 }  // extern "C"

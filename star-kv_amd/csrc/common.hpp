@@ -93,6 +93,34 @@ struct PVArgs {
 };
 
 // ---------------------------------------------------------------------------
+// Latent-cache writer arguments (quant.hip).
+// ---------------------------------------------------------------------------
+struct KAppendArgs {
+  const void* src; int64_t src_sb, src_sh, src_st;   // new rows (b, h, t), act dtype, elements
+  int B, H, T, pos0;
+  int fmt;                                          // STARKV_FMT_DENSE or a quantised format
+  void* data; int64_t stride_b;                     // dense: elements; quantised: bytes
+  void* scale; int64_t sc_sb, sc_sh;
+  int split, a_int8;                                // ranks [0, split) in data (int8 if a_int8)
+  void* data2; int64_t stride2_b;                   // ranks [split, r) as int4
+  void* scale2; int64_t sc2_sb, sc2_sh;
+  int rank[K_MAX_KV];
+  int64_t off[K_MAX_KV], pitch[K_MAX_KV];
+  int64_t off2[K_MAX_KV], pitch2[K_MAX_KV];
+};
+
+struct VAppendArgs {
+  const void* src; int64_t src_sb, src_st;          // new rows (b, t), act dtype, elements
+  int B, T, pos0, R, vq;
+  void* data; int64_t stride_b, stride_s;
+  void* scale; int64_t sc_sb, sc_ss;
+  void* zero;                                       // VQ_G64 (strides of scale)
+  int split, a_int8;
+  void* data2; int64_t stride2_b, stride2_s;
+  void* scale2; int64_t sc2_sb, sc2_ss;
+};
+
+// ---------------------------------------------------------------------------
 // Up-projection arguments.
 // ---------------------------------------------------------------------------
 struct UPArgs {
@@ -157,5 +185,7 @@ int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, 
 int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ranks) per P.V wave
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
+int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
+int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);
 
 }  // namespace starkv

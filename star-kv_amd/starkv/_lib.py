@@ -100,12 +100,32 @@ class DecodeDesc(ctypes.Structure):
     ]
 
 
+class KAppendDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int), ("n_tokens", ctypes.c_int), ("pos0", ctypes.c_int), ("capacity", ctypes.c_int),
+        ("dtype", ctypes.c_int),
+        ("src", ctypes.c_void_p), ("src_stride_b", ctypes.c_int64), ("src_stride_h", ctypes.c_int64),
+        ("src_stride_t", ctypes.c_int64),
+        ("k", KLatent),
+    ]
+
+
+class VAppendDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int), ("n_tokens", ctypes.c_int), ("pos0", ctypes.c_int), ("capacity", ctypes.c_int),
+        ("dtype", ctypes.c_int),
+        ("src", ctypes.c_void_p), ("src_stride_b", ctypes.c_int64), ("src_stride_t", ctypes.c_int64),
+        ("v", VLatent),
+    ]
+
+
 EXPORTS = (
     "starkv_abi_version", "starkv_status_string",
     "starkv_rope_table_bytes", "starkv_rope_build",
     "starkv_k_logits_workspace_bytes", "starkv_k_logits",
     "starkv_pv_latent_workspace_bytes", "starkv_pv_latent",
     "starkv_decode_workspace_bytes", "starkv_decode_attention", "starkv_decode_attention_timed",
+    "starkv_k_append", "starkv_v_append",
 )
 
 _lib = None
@@ -139,6 +159,10 @@ def lib() -> ctypes.CDLL:
     L.starkv_decode_attention_timed.restype = ctypes.c_int
     L.starkv_decode_attention_timed.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.c_void_p, ctypes.c_size_t,
                                                 ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    L.starkv_k_append.restype = ctypes.c_int
+    L.starkv_k_append.argtypes = [ctypes.POINTER(KAppendDesc), ctypes.c_void_p]
+    L.starkv_v_append.restype = ctypes.c_int
+    L.starkv_v_append.argtypes = [ctypes.POINTER(VAppendDesc), ctypes.c_void_p]
     if L.starkv_abi_version() != 1:
         raise StarKVError("libstarkv ABI version mismatch")
     _lib = L

@@ -1,0 +1,131 @@
+"""Static latent KV caches with in-place append.
+
+The reference grows its latent caches by ``torch.cat`` every decode step (HF
+``DynamicLayer.update``, HF:cache_utils.py:127-146, reached from
+model.py:411-419), re-copying the whole cache per token.  ``LatentCache``
+preallocates one layer's caches for ``capacity`` positions and writes each new
+token in place with the HIP cache writer (``starkv_k_append`` /
+``starkv_v_append``), quantising on the fly when the format asks for it.
+
+Formats (K / V):
+  "dense"       act dtype / act dtype
+  "int8_g64"    int8 per (b, h, s) / int4 asymmetric groups of 64 per (b, s, g)
+                (the quantised workload of the benchmark configurations)
+  "reference"   the reference quantised module's split caches
+                (LlamaLoRaAttention_headwise_quant.py:22-25, 107-127):
+                K ranks [0, 16) int8 + the rest int4, V ranks [0, 256) int8 +
+                the rest int4, one fp16 scale per block and token.
+
+K is stored head-major per batch ([S_cap, r_h] per head, back to back), so
+head-wise ranks may differ and each head's 32-position tile is one contiguous
+run -- the layout the K-logit kernel streams best.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence
+
+import torch
+
+from ._lib import FMT_DENSE, FMT_INT4_REF, FMT_INT8_SYM, StarKVError
+from .ops import KLatentSpec, VLatentSpec, k_append, v_append
+
+__all__ = ["LatentCache"]
+
+HEAD_DIM = 128
+
+
+def _round(n: int, m: int) -> int:
+    return (n + m - 1) // m * m
+
+
+class LatentCache:
+    """One layer's latent caches: K [B, Hkv, capacity, r_h], V [B, capacity, Rv]."""
+
+    def __init__(self, batch: int, ranks: Sequence[int], v_rank: int, capacity: int, dtype: torch.dtype,
+                 device, fmt: str = "dense", k_split: int = 16, v_split: int = 256):
+        self.B, self.ranks, self.Rv, self.cap = int(batch), [int(r) for r in ranks], int(v_rank), int(capacity)
+        self.dtype, self.device, self.fmt = dtype, torch.device(device), fmt
+        self.length = 0
+        Hkv, B, C = len(self.ranks), self.B, self.cap
+        dev = self.device
+        self._bk = None
+        if fmt == "dense":
+            offs = [C * sum(self.ranks[:h]) for h in range(Hkv)]
+            self.k_data = torch.zeros(B, C * sum(self.ranks), dtype=dtype, device=dev)
+            self._k = dict(data=self.k_data, head_offset=offs, pos_stride=self.ranks, stride_b=self.k_data.stride(0),
+                           fmt=FMT_DENSE)
+            self.v_data = torch.zeros(B, C, self.Rv, dtype=dtype, device=dev)
+            self.v_spec = VLatentSpec.dense(self.v_data)
+            return
+        if any(r % 8 for r in self.ranks) or self.Rv % 8:
+            raise StarKVError("quantised caches need ranks that are multiples of 8")
+        self.k_scale = torch.ones(B, Hkv, C, dtype=torch.float16, device=dev)
+        if fmt == "int8_g64":
+            offs = [C * sum(self.ranks[:h]) for h in range(Hkv)]
+            self.k_data = torch.zeros(B, C * sum(self.ranks), dtype=torch.int8, device=dev)
+            self._k = dict(data=self.k_data, head_offset=offs, pos_stride=self.ranks, stride_b=self.k_data.stride(0),
+                           fmt=FMT_INT8_SYM, scale=self.k_scale)
+            G = (self.Rv + 63) // 64
+            self.v_data = torch.zeros(B, C, self.Rv // 2, dtype=torch.uint8, device=dev)
+            self.v_scale = torch.ones(B, C, G, dtype=torch.float16, device=dev)
+            self.v_zero = torch.zeros(B, C, G, dtype=torch.float16, device=dev)
+            self.v_spec = VLatentSpec.int4_g64(self.v_data, self.v_scale, self.v_zero, self.Rv)
+            return
+        if fmt != "reference":
+            raise StarKVError(f"unknown cache format {fmt!r}")
+        # K: upper k_split ranks int8 (16 bytes per row), the rest int4 nibbles
+        up = [min(r, k_split) for r in self.ranks]
+        lo = [max(r - k_split, 0) for r in self.ranks]
+        pitch1 = [_round(u, 8) for u in up]
+        pitch2 = [_round(l // 2, 4) for l in lo]
+        self.k_data = torch.zeros(B, C * sum(pitch1), dtype=torch.int8, device=dev)
+        self.k_data2 = torch.zeros(B, max(1, C * sum(pitch2)), dtype=torch.uint8, device=dev)
+        self.k_scale2 = torch.ones(B, Hkv, C, dtype=torch.float16, device=dev)
+        self._k = dict(data=self.k_data, head_offset=[C * sum(pitch1[:h]) for h in range(Hkv)], pos_stride=pitch1,
+                       stride_b=self.k_data.stride(0), fmt=FMT_INT4_REF, scale=self.k_scale, split=k_split,
+                       split_fmt=FMT_INT8_SYM, data2=self.k_data2,
+                       head_offset2=[C * sum(pitch2[:h]) for h in range(Hkv)], pos_stride2=pitch2,
+                       stride2_b=self.k_data2.stride(0), scale2=self.k_scale2)
+        vu = min(self.Rv, v_split)
+        self.v_data = torch.zeros(B, C, vu, dtype=torch.int8, device=dev)
+        self.v_scale = torch.ones(B, C, 1, dtype=torch.float16, device=dev)
+        if self.Rv > vu:
+            self.v_data2 = torch.zeros(B, C, (self.Rv - vu) // 2, dtype=torch.uint8, device=dev)
+            self.v_scale2 = torch.ones(B, C, 1, dtype=torch.float16, device=dev)
+            self.v_spec = VLatentSpec.int4_ref(self.v_data, self.v_scale, self.Rv, split=vu, x2=self.v_data2,
+                                               scale2=self.v_scale2)
+        else:
+            self.v_spec = VLatentSpec.int8(self.v_data, self.v_scale)
+
+    def k_spec(self, bk: torch.Tensor) -> KLatentSpec:
+        """The K-latent description with B_k = k_u^T [Hkv, r_max, 128] (rows of
+        head h beyond r_h unused) or a list of per-head [r_h, 128] tensors in one
+        buffer."""
+        k = self._k
+        if bk.dim() != 3 or bk.stride(2) != 1:
+            raise StarKVError("bk must be [Hkv, r, 128] with a contiguous last dim")
+        sc = k.get("scale")
+        sc2 = k.get("scale2")
+        return KLatentSpec(k["data"], self.ranks, k["head_offset"], k["pos_stride"], k["stride_b"], bk,
+                           [h * bk.stride(0) for h in range(len(self.ranks))], bk.stride(1), fmt=k["fmt"],
+                           scale=sc, scale_stride_b=sc.stride(0) if sc is not None else 0,
+                           scale_stride_h=sc.stride(1) if sc is not None else 0,
+                           split=k.get("split", 0), split_fmt=k.get("split_fmt", FMT_INT4_REF),
+                           data2=k.get("data2"), head_offset2=k.get("head_offset2"), pos_stride2=k.get("pos_stride2"),
+                           stride2_b=k.get("stride2_b", 0), scale2=sc2,
+                           scale2_stride_b=sc2.stride(0) if sc2 is not None else 0,
+                           scale2_stride_h=sc2.stride(1) if sc2 is not None else 0)
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor):
+        """Write T new positions (k_new [B, Hkv, T, r_max], v_new [B, T, Rv]) in
+        place; returns (K spec, V spec, length) for the attention kernels."""
+        T = k_new.shape[2]
+        if v_new.shape[1] != T:
+            raise StarKVError("k_new and v_new must hold the same number of positions")
+        if self.length + T > self.cap:
+            raise StarKVError(f"cache full: {self.length} + {T} > capacity {self.cap}")
+        ks = self.k_spec(bk)
+        k_append(k_new.contiguous() if k_new.stride(3) != 1 else k_new, ks, self.length, self.cap)
+        v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, self.length, self.cap)
+        self.length += T
+        return ks, self.v_spec, self.length

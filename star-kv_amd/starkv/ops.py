@@ -13,8 +13,8 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KLatent,
-                   KLogitsDesc, PVDesc, StarKVError, VLatent, check, i64_array, int_array)
+from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KAppendDesc,
+                   KLatent, KLogitsDesc, PVDesc, StarKVError, VAppendDesc, VLatent, check, i64_array, int_array)
 from .rope import RopeConfig, rope_table
 
 HEAD_DIM = 128
@@ -400,3 +400,32 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
         check(L.starkv_decode_attention_timed(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                               _stream(q.device), handles), "starkv_decode_attention_timed")
     return out
+
+
+def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int) -> None:
+    """Write the new K latent rows src [B, Hkv, T, >= r_h] (act dtype, last dim
+    contiguous) into the cache described by ``k`` at positions
+    [pos0, pos0 + T), quantising to its format (starkv_k_append)."""
+    if src.dim() != 4 or src.stride(3) != 1:
+        raise StarKVError("src must be [B, Hkv, T, r] with a contiguous last dim")
+    _require_cuda(src, *[t for t in (k.data, k.scale, k.data2, k.scale2) if t is not None])
+    keep: list = []
+    d = KAppendDesc()
+    d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[2], int(pos0), int(capacity), _dt(src)
+    d.src, d.src_stride_b, d.src_stride_h, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1), src.stride(2)
+    d.k = k.c_struct(keep)
+    check(_lib.lib().starkv_k_append(ctypes.byref(d), _stream(src.device)), "starkv_k_append")
+
+
+def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int) -> None:
+    """Write the new V latent rows src [B, T, Rv] (act dtype, last dim
+    contiguous) into the cache described by ``v`` at positions
+    [pos0, pos0 + T), quantising to its format (starkv_v_append)."""
+    if src.dim() != 3 or src.stride(2) != 1:
+        raise StarKVError("src must be [B, T, Rv] with a contiguous last dim")
+    _require_cuda(src, *v.tensors)
+    d = VAppendDesc()
+    d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[1], int(pos0), int(capacity), _dt(src)
+    d.src, d.src_stride_b, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1)
+    d.v = v.c_struct()
+    check(_lib.lib().starkv_v_append(ctypes.byref(d), _stream(src.device)), "starkv_v_append")

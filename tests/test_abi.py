@@ -241,3 +241,28 @@ def test_dropins_refuse_cpu_tensors():
         abx(a[0], b, x)                      # wrong rank
     with pytest.raises(L.StarKVError):
         abx(a, b.float(), x)                 # mixed dtypes
+
+
+def test_cache_writer_validation():
+    lib = L.lib()
+    keep = []
+    d = L.KAppendDesc(batch=2, n_tokens=4, pos0=10, capacity=12, dtype=L.F16, src=FAKE,
+                      src_stride_b=8 * 4 * 32, src_stride_h=4 * 32, src_stride_t=32, k=_klatent([32] * 8, keep))
+    assert lib.starkv_k_append(ctypes.byref(d), None) == ERR_SHAPE          # 10 + 4 > 12
+    d.capacity = 14
+    d.dtype = L.F32
+    assert lib.starkv_k_append(ctypes.byref(d), None) == ERR_DTYPE
+    d.dtype, d.src = L.F16, None
+    assert lib.starkv_k_append(ctypes.byref(d), None) == ERR_NULL
+    d.src = FAKE
+    d.k.format = L.FMT_INT8_SYM                                            # quantised without scales
+    assert lib.starkv_k_append(ctypes.byref(d), None) == ERR_NULL
+    v = L.VAppendDesc(batch=1, n_tokens=1, pos0=0, capacity=8, dtype=L.F16, src=FAKE, src_stride_b=64,
+                      src_stride_t=64, v=L.VLatent(rank=64, format=L.FMT_INT4_G64, data=FAKE, stride_b=8 * 32,
+                                                    stride_s=32, scale=FAKE, scale_stride_b=8, scale_stride_s=1))
+    assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_NULL           # group-64 without zero points
+    v.v.zero, v.v.stride_s = FAKE, 30
+    assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_SHAPE          # row shorter than rank/2 bytes
+    v.v.stride_s, v.v.data = 32, FAKE + 2
+    assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_ALIGN
+    assert lib.starkv_v_append(None, None) == ERR_NULL

@@ -1,0 +1,192 @@
+"""GPU tests of the latent-cache writers (quantise / append in place) and the quantised module.
+
+The writer must reproduce the oracle's quantisers bit for bit (the same fp16
+input values, the same rounding steps); decode over a cache it filled must
+match the oracle on the oracle-quantised history.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from _util import cfg2_ranks, errors
+
+HEAD = 128
+
+
+def _flush(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(2, 8, 37, 128), (3, 50, 1640)])
+def test_quantize_r_split_bit_exact(shape):
+    from oracle import starkv_oracle as o
+    from starkv.quant_utils import quantize_r_split_int8_int4_packed, unpack_uint8_to_int4_signed
+    _flush(f"[quantize split] {shape}")
+    U = 16 if len(shape) == 4 else 256
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = (torch.randn(*shape, generator=g, device="cuda") * 3).half()
+    x[..., ::11] *= 20
+    x[0, 0] = 0                                               # an all-zero row: scale 1
+    up, s_up, lo, s_lo, r4 = quantize_r_split_int8_int4_packed(x, U)
+    torch.cuda.synchronize()
+    xn = x.float().cpu().numpy()
+    q8, s8 = o.quant_int8_sym(xn[..., :U])
+    p4, s4 = o.quant_int4_ref(xn[..., U:])
+    assert r4 == shape[-1] - U
+    assert np.array_equal(up.cpu().numpy(), q8)
+    assert np.array_equal(s_up.cpu().numpy().view(np.uint16), s8.view(np.uint16))
+    assert np.array_equal(lo.cpu().numpy(), p4)
+    assert np.array_equal(s_lo.cpu().numpy().view(np.uint16), s4.view(np.uint16))
+    assert np.array_equal(unpack_uint8_to_int4_signed(lo, r4).cpu().numpy(), o.unpack_int4_ref(p4, r4))
+
+
+def _oracle_history(fmt, kx, vx, ranks, Rv):
+    """Oracle-quantised (then dequantised) K per head [B, S, r_h] and V [B, S, Rv] from float histories."""
+    from oracle import starkv_oracle as o
+    if fmt == "dense":
+        return [torch.from_numpy(kx[h]).double() for h in range(len(ranks))], torch.from_numpy(vx).double()
+    ks = []
+    for h, r in enumerate(ranks):
+        x = kx[h]
+        if fmt == "int8_g64":
+            q, s = o.quant_int8_sym(x)
+            d = o.dequant_int8_sym(q, s)
+        else:
+            q, s = o.quant_int8_sym(x[..., :min(r, 16)])
+            parts = [o.dequant_int8_sym(q, s)]
+            if r > 16:
+                p, s2 = o.quant_int4_ref(x[..., 16:])
+                parts.append(o.dequant_int4_ref(p, s2, r - 16))
+            d = np.concatenate(parts, axis=-1)
+        ks.append(torch.from_numpy(d.astype(np.float64)))
+    if fmt == "int8_g64":
+        n, sc, zr = o.quant_int4_asym(vx, 64)
+        v = o.dequant_int4_asym(n, sc, zr, 64)
+    else:
+        U = min(Rv, 256)
+        q, s = o.quant_int8_sym(vx[..., :U])
+        parts = [o.dequant_int8_sym(q, s)]
+        if Rv > U:
+            p, s2 = o.quant_int4_ref(vx[..., U:])
+            parts.append(o.dequant_int4_ref(p, s2, Rv - U))
+        v = np.concatenate(parts, axis=-1)
+    return ks, torch.from_numpy(v.astype(np.float64))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["dense", "int8_g64", "reference"])
+def test_latent_cache_append_then_decode(fmt):
+    from oracle import starkv_oracle as o
+    from starkv import RopeConfig, decode_attention
+    from starkv.cache import LatentCache
+    _flush(f"[cache] {fmt}")
+    B, Rv, cap = 2, 1640, 96
+    ranks = cfg2_ranks()[:8]                                  # 8 heads, ragged 16..96
+    Hkv, Hq = len(ranks), 16
+    rmax = max(ranks)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    cache = LatentCache(B, ranks, Rv, cap, torch.float16, "cuda", fmt=fmt)
+    bk = torch.zeros(Hkv, rmax, HEAD, device="cuda")
+    for h, r in enumerate(ranks):
+        bk[h, :r] = torch.randn(r, HEAD, generator=g, device="cuda") / math.sqrt(r)
+    bk = bk.half()
+    uv = (torch.randn(Hkv * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).half()
+    steps = [40, 1, 1, 1]
+    kh, vh = [], []
+    rope = RopeConfig()
+    for T in steps:
+        k_new = torch.randn(B, Hkv, T, rmax, generator=g, device="cuda").half()
+        for h, r in enumerate(ranks):
+            k_new[:, h, :, r:] = 0
+        v_new = torch.randn(B, T, Rv, generator=g, device="cuda").half()
+        v_new[..., ::37] *= 10
+        kspec, vspec, S = cache.append(k_new, v_new, bk)
+        kh.append(k_new.float().cpu().numpy())
+        vh.append(v_new.float().cpu().numpy())
+        q = torch.randn(B, Hq, HEAD, generator=g, device="cuda").half()
+        out = decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=S, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        kx = np.concatenate(kh, axis=2)
+        kx = [kx[:, h, :, :r] for h, r in enumerate(ranks)]
+        ks, v = _oracle_history(fmt, kx, np.concatenate(vh, axis=1), ranks, Rv)
+        cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), rope.attention_scaling)
+        ref, _, _ = o.decode_attention(q.cpu(), [bk[h, :r].cpu() for h, r in enumerate(ranks)], ks, v, uv.cpu(), cos, sin)
+        mx, mr = errors(out, ref)
+        _flush(f"   S={S} max_abs={mx:.3e} mean_rel={mr:.3e}")
+        assert mr <= 1e-3 and mx <= 2e-2
+    if fmt == "int8_g64":
+        # stored bytes of head 0 equal the oracle's quantisation of its rows
+        q0, s0 = o.quant_int8_sym(np.concatenate(kh, axis=2)[:, 0, :, :ranks[0]])
+        stored = cache.k_data[:, :S * ranks[0]].cpu().numpy().reshape(B, S, ranks[0])
+        assert np.array_equal(stored, q0)
+        assert np.array_equal(cache.k_scale[:, 0, :S].cpu().numpy().view(np.uint16), s0[..., 0].view(np.uint16))
+
+
+class _KProj(torch.nn.Module):
+    def __init__(self, vs, u):
+        super().__init__()
+        self.VS = vs
+        self.register_buffer("U", u)
+
+
+class _VProj(torch.nn.Module):
+    def __init__(self, vs, u):
+        super().__init__()
+        self.VS = vs
+        self.U = u
+
+
+@pytest.mark.gpu
+def test_quant_module_decode_matches_dequantised_history():
+    from oracle import starkv_oracle as o
+    from transformers import LlamaConfig
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    from starkv.LlamaLoRaAttention_headwise_quant import LlamaCustomAttention
+    _flush("[quant module] Hq=8 Hkv=2 r=80 Rv=512, prefill 33 + 3 decode steps")
+    Hq, Hkv, r, Rv = 8, 2, 80, 512
+    torch.manual_seed(0)
+    cfg = LlamaConfig(hidden_size=Hq * HEAD, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                      intermediate_size=256, num_hidden_layers=1, max_position_embeddings=4096)
+    m = LlamaCustomAttention(cfg, layer_idx=0, decomp_goup_num=Hq)
+    m.k_proj = _KProj(torch.nn.Linear(cfg.hidden_size, Hkv * r, bias=False), torch.randn(Hkv, HEAD, r) / math.sqrt(r))
+    m.v_proj = _VProj(torch.nn.Linear(cfg.hidden_size, Rv, bias=False), torch.nn.Linear(Rv, Hkv * HEAD, bias=False))
+    m = m.to(device="cuda", dtype=torch.float16).eval()
+    rot = LlamaRotaryEmbedding(config=cfg).to("cuda")
+    B, P = 2, 33
+    g = torch.Generator(device="cuda").manual_seed(4)
+    hid = (torch.randn(B, P + 3, cfg.hidden_size, generator=g, device="cuda") * 0.5).half()
+    caches = [DynamicCache() for _ in range(4)]
+    with torch.no_grad():
+        pos = torch.arange(P, device="cuda")[None].expand(B, P)
+        m(hid[:, :P], rot(hid[:, :P], pos), None, pos, *caches)
+        for t in range(P, P + 3):
+            pos = torch.full((B, 1), t, device="cuda")
+            out, _ = m(hid[:, t:t + 1], rot(hid[:, t:t + 1], pos), None, pos, *caches)
+            torch.cuda.synchronize()
+            # fp64 attention over the module's own (dequantised) caches
+            ku, vu = caches[0].layers[0].keys, caches[0].layers[0].values
+            kl, vl = caches[1].layers[0].keys, caches[1].layers[0].values
+            sku, svu = caches[2].layers[0].keys, caches[2].layers[0].values
+            skl, svl = caches[3].layers[0].keys, caches[3].layers[0].values
+            kx = np.concatenate([o.dequant_int8_sym(ku.cpu().numpy(), sku.cpu().numpy()),
+                                 o.dequant_int4_ref(kl.cpu().numpy(), skl.cpu().numpy(), r - 16)], -1)
+            vx = np.concatenate([o.dequant_int8_sym(vu.cpu().numpy(), svu.cpu().numpy()),
+                                 o.dequant_int4_ref(vl.cpu().numpy(), svl.cpu().numpy(), Rv - 256)], -1)
+            S = kx.shape[2]
+            q = (hid[:, t:t + 1].double().cpu() @ m.q_proj.weight.double().cpu().T).view(B, 1, Hq, HEAD).transpose(1, 2)
+            cos, sin = o.rope_cos_sin(m.rope.inv_freq(), torch.arange(t, t + 1))
+            q = o.apply_rope(q[:, :, 0], cos.double(), sin.double())
+            cos, sin = o.rope_cos_sin(m.rope.inv_freq(), torch.arange(S))
+            bk = m.k_proj.U.double().cpu().transpose(-1, -2)
+            core, _, _ = o.decode_attention(q, [bk[h] for h in range(Hkv)], [torch.from_numpy(kx[:, h]).double() for h in range(Hkv)],
+                                            torch.from_numpy(vx).double(), m.v_proj.U.weight.double().cpu(), cos.double(), sin.double())
+            ref = core.reshape(B, 1, -1) @ m.o_proj.weight.double().cpu().T
+            mx, mr = errors(out.float(), ref)
+            _flush(f"   decode t={t} S={S} max_abs={mx:.3e} mean_rel={mr:.3e}")
+            assert mr <= 1e-2
