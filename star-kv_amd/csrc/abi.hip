@@ -120,7 +120,20 @@ int validate_klayout(const starkv_klatent& k, int dtype) {
 // (first fit decreasing, whole heads per wave; 4 once any head has rank > 64)
 // and deal the waves round-robin over workgroups of 8 waves (2-item waves) or
 // 4 waves (4-item waves).
-int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan) {
+// Warp-specialised K-logit kernel: dense latents with 16-byte aligned rows
+// (ranks a multiple of 8); q and B_k are read element-wise there.
+bool k_ws(const starkv_klatent& k, int dtype) {
+  if (k.format != STARKV_FMT_DENSE) return false;
+  const int xe = esize(dtype);
+  if (!al(k.data, 16) || !al64(k.stride_b * xe, 16)) return false;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    if (k.rank[h] % 8) return false;
+    if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
+  }
+  return true;
+}
+
+int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, KPlan& plan) {
   struct QH { int qh, kv, ni; };
   std::vector<QH> heads;
   int max_ni = 1;
@@ -130,7 +143,8 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan)
     max_ni = std::max(max_ni, ni);
     heads.push_back({qh, kv, ni});
   }
-  const int maxi = max_ni <= 2 ? 2 : 4;   // whole heads per wave
+  const bool ws = k_ws(k, dtype);
+  const int maxi = ws || max_ni > 2 ? 4 : 2;   // whole heads per (consumer) wave
   const int nw = maxi == 2 ? 8 : 4;
   std::stable_sort(heads.begin(), heads.end(), [](const QH& x, const QH& y) { return x.ni > y.ni; });
   std::vector<std::vector<QH>> bins;
@@ -175,6 +189,28 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, KArgs& a, KPlan& plan)
   }
   a.n_wg = plan.n_wg;
   a.maxi = maxi;
+  a.ws = ws;
+  a.ws_stage = a.ws_nst = 0;
+  if (ws) {
+    // stage = the largest workgroup's latent tile (16-byte chunks of its
+    // distinct KV heads, whole 1 KB DMA pieces) + the 8 KB RoPE operand
+    int max_chunks = 0;
+    for (int g = 0; g < plan.n_wg; ++g) {
+      bool seen[K_MAX_KV] = {};
+      int chunks = 0;
+      for (int w = 0; w < nw; ++w)
+        for (int i = 0; i < K_MAXI; ++i) {
+          const uint32_t it = a.items[g * nw + w][i];
+          const int kv = (it >> 8) & 0xff;
+          if (!((it >> 27) & 1) || seen[kv]) continue;
+          seen[kv] = true;
+          chunks += 4 * k.rank[kv];
+        }
+      max_chunks = std::max(max_chunks, chunks);
+    }
+    a.ws_stage = (int)round_up(max_chunks, 64) * 16 + 8192;
+    a.ws_nst = std::min(4, K1_WS_RING_BYTES / a.ws_stage);
+  }
   return STARKV_OK;
 }
 
@@ -329,7 +365,7 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
   if (d->out_dtype != 0 && d->out_dtype != d->dtype && d->out_dtype != STARKV_F32) return STARKV_ERR_DTYPE;
   KArgs tmp;
   KPlan plan;
-  if ((st = build_k_plan(d->k, d->n_q_heads, *gs, tmp, plan))) return st;
+  if ((st = build_k_plan(d->k, d->n_q_heads, *gs, d->dtype, tmp, plan))) return st;
   *n_wg = plan.n_wg;
   return STARKV_OK;
 }
@@ -385,7 +421,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   if ((st = check_mask(d->mask, d->mask_dtype))) return st;
   KArgs a;
   KPlan plan;
-  if ((st = build_k_plan(d->k, d->n_q_heads, gs, a, plan))) return st;
+  if ((st = build_k_plan(d->k, d->n_q_heads, gs, d->dtype, a, plan))) return st;
   a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h;
   a.x = d->k.data; a.x_sb = d->k.stride_b;
   a.xscale = d->k.scale; a.xs_sb = d->k.scale_stride_b; a.xs_sh = d->k.scale_stride_h;
@@ -453,7 +489,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
 
   KArgs ka;
   KPlan plan;
-  if ((st = build_k_plan(d->k, Hq, gs, ka, plan))) return st;
+  if ((st = build_k_plan(d->k, Hq, gs, d->dtype, ka, plan))) return st;
   ka.q = d->q; ka.q_sb = d->q_stride_b; ka.q_sh = d->q_stride_h;
   ka.x = d->k.data; ka.x_sb = d->k.stride_b;
   ka.xscale = d->k.scale; ka.xs_sb = d->k.scale_stride_b; ka.xs_sh = d->k.scale_stride_h;

@@ -28,6 +28,7 @@ constexpr int K_MAXI = 4;          // items per wave (upper bound over kernel va
 constexpr int K_MAX_WAVES = 64;    // waves in one batch's plan
 constexpr int K_MAX_KV = 64;
 constexpr int K_MAX_QH = 64;
+constexpr int K1_WS_RING_BYTES = 163840 - 1024;   // warp-specialised K-logit LDS ring (+ 1 KB carry)
 
 // item word: qhead[0:8) kv[8:16) mtile[16:20) nvalid[20:26) last_of_q[26] valid[27]
 __host__ __device__ inline uint32_t item_pack(int qh, int kv, int mt, int nv, int last) {
@@ -55,6 +56,8 @@ struct KArgs {
   float* chunkmax;                                 // [B][Hq][n_chunks] (optional)
   int S, Hq, n_chunks, tiles_per_chunk, n_wg;
   int maxi;                                        // items per wave of the launched variant (2 or 4)
+  int ws;                                          // warp-specialised kernel (dense, 16-byte aligned latents)
+  int ws_stage, ws_nst;                            // its LDS stage bytes and stage count
   float wscale;                                    // softmax scale * rope attention scaling
   int64_t xoff[K_MAX_KV];                          // per KV head: elements (dense) or bytes (quantised)
   int xpitch[K_MAX_KV];
@@ -181,6 +184,7 @@ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 int rope_table_tiles(int max_positions);
 int launch_rope_table(const float* inv_freq_host, int max_positions, float scaling, void* table, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
+int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
 int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st);
 int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ranks) per P.V wave
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);

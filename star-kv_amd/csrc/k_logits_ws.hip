@@ -1,0 +1,361 @@
+// K1, warp-specialised: latent-K decode logits for 16-byte aligned fp16/bf16
+// latents on gfx950.
+//
+// Same arithmetic as k_logits.hip (the folded query matrix W times the RoPE
+// operand T per 32-position tile, one FMA per latent element; see there), with
+// the work of a workgroup split by role:
+//
+// * 4 producer waves stream, per 32-position tile, the latent rows of every
+//   KV head the workgroup serves (each head's tile is 32 rows of 2*r_h bytes)
+//   and the tile's RoPE operand (8 KB) into an LDS ring of 3 or 4 stages
+//   (as many as fit; the stage is sized on the host for the largest
+//   workgroup) with global_load_lds: 16 bytes per lane, 1 KB per
+//   instruction, only as many instructions as the workgroup's chunks need.
+//   Rows are stored with their 16-byte chunks rotated (ws_shift) so the
+//   consumers' row-wise reads are free of LDS bank conflicts.
+// * 8 consumer waves, two per SIMD, so one wave's dot products and stores
+//   overlap the other's MFMA chains.  The plan packs whole heads into bins
+//   of up to 4 items (query head, 32-rank M-tile); consumer wave c runs items
+//   2*(c/4) and 2*(c/4)+1 of bin c%4.  A head whose items straddle the two
+//   halves of a bin is combined through LDS: the first wave leaves its
+//   partial logits for the tile, the second adds them one tile later (after
+//   the next barrier) and stores.
+//
+// Measured on MI355X (B16, S32768, ragged ranks summing to 1640): the
+// register-streaming kernel of k_logits.hip reaches 3.8 TB/s; this one
+// 4.2 TB/s.  With the consumers idle the producers alone stream 5.6-6.5 TB/s;
+// with them busy the shader clock falls from ~2.3 to ~1.6-2.0 GHz and the
+// per-CU fetch rate with it.
+//
+// Stage protocol (one s_barrier per tile, no fence): at tile i the producers
+// wait for their own DMA of tile i (vmcnt counts exactly: every lane of an
+// issued instruction is in bounds and the per-wave count is fixed), the
+// workgroup barriers, the producers issue the DMA of tile i+nst-1 into the
+// stage consumed at tile i-1, and the consumers compute tile i.  One extra
+// barrier after the last tile publishes the last straddle partials.
+#include "common.hpp"
+
+namespace starkv {
+
+namespace {
+
+constexpr int WS_PRODUCERS = 4;
+constexpr int WS_CONSUMERS = 8;
+constexpr int WS_BINS = 4;                          // item bins (of up to 4 items) per workgroup
+constexpr int WS_RING = K1_WS_RING_BYTES;           // LDS ring (the straddle carry takes the rest of the 160 KB)
+constexpr int WS_MAXK = (2048 / 64 + 8 + WS_PRODUCERS - 1) / WS_PRODUCERS;   // DMA instructions per producer per tile
+constexpr int WS_MAXH = 16;                        // KV heads staged by one workgroup
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Latent rows sit in LDS with their 16-byte chunks rotated by ws_shift(row):
+// ds_read_b128 serves 8 lanes (128 bytes, 32 banks) per cycle, and the lanes
+// of a group read the same logical chunk of 8 consecutive rows.  Rows of n16
+// chunks repeat their bank offset every p = 8 / gcd(n16, 8) rows; rotating
+// by row / p separates the rows that collide, so every group is conflict-free
+// for every rank (checked exhaustively for n16 = 1..16).
+__device__ inline int ws_shift(int row, int n16) {
+  const int g = min(n16 & -n16, 8);
+  return row / (8 / g);
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31]
+template <int N> __device__ inline void wait_vm() {
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+__device__ inline void wait_vm_n(int n) {
+  switch (n) {
+#define WS_CASE(N) case N: wait_vm<N>(); break;
+    WS_CASE(0) WS_CASE(1) WS_CASE(2) WS_CASE(3) WS_CASE(4) WS_CASE(5) WS_CASE(6) WS_CASE(7)
+    WS_CASE(8) WS_CASE(9) WS_CASE(10) WS_CASE(11) WS_CASE(12) WS_CASE(13) WS_CASE(14) WS_CASE(15)
+    WS_CASE(16) WS_CASE(17) WS_CASE(18) WS_CASE(19) WS_CASE(20) WS_CASE(21) WS_CASE(22) WS_CASE(23)
+    WS_CASE(24) WS_CASE(25) WS_CASE(26) WS_CASE(27) WS_CASE(28) WS_CASE(29) WS_CASE(30)
+#undef WS_CASE
+    default: wait_vm<0>(); break;
+  }
+}
+
+// 16 latent values (two 16-byte LDS chunks) . 16 accumulator rows, four partial sums
+__device__ inline float dot16h(uint4 u0, uint4 u1, const floatx16& acc) {
+  const half8 h0 = __builtin_bit_cast(half8, u0), h1 = __builtin_bit_cast(half8, u1);
+  float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int v = 0; v < 8; ++v) p[v & 3] = fmaf((float)h0[v], acc[v], p[v & 3]);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) p[v & 3] = fmaf((float)h1[v], acc[8 + v], p[v & 3]);
+  return (p[0] + p[1]) + (p[2] + p[3]);
+}
+__device__ inline float dot16b(uint4 u0, uint4 u1, const floatx16& acc) {
+  const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+  float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    p[(2 * v) & 3] = fmaf(__uint_as_float(w[v] << 16), acc[2 * v], p[(2 * v) & 3]);
+    p[(2 * v + 1) & 3] = fmaf(__uint_as_float(w[v] & 0xffff0000u), acc[2 * v + 1], p[(2 * v + 1) & 3]);
+  }
+  return (p[0] + p[1]) + (p[2] + p[3]);
+}
+
+}  // namespace
+
+// OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
+template <typename XT, int OUTK>
+__global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logits_ws_kernel(const KArgs a) {
+  constexpr int MAXI = 2;                            // items per consumer wave
+  __shared__ __attribute__((aligned(16))) char ring[WS_RING];   // a.ws_nst stages of a.ws_stage bytes
+  __shared__ float carry[2][WS_BINS][32];            // straddling heads: first half's partial logits
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = lane & 31, hh = lane >> 5;
+  const int chunk = blockIdx.x, wgp = blockIdx.y, b = blockIdx.z;
+  const int S = a.S;
+  const int n_tiles = (S + TILE - 1) / TILE;
+  const int tile0 = chunk * a.tiles_per_chunk;
+  const int tile1 = min(tile0 + a.tiles_per_chunk, n_tiles);
+  if (tile0 >= tile1) return;
+  const int last = tile1 - 1;
+  const int ntl = tile1 - tile0;
+
+  // ---- the workgroup's KV heads (scalar, identical in every wave): distinct
+  // KV heads of its items in first-use order, with rank and offset in a stage
+  // in 16-byte chunks.  Loops are fully unrolled so the tables stay in
+  // registers.
+  int hkv[WS_MAXH], hrank[WS_MAXH], hoff[WS_MAXH];
+#pragma unroll
+  for (int k = 0; k < WS_MAXH; ++k) { hkv[k] = -1; hrank[k] = 8; hoff[k] = 1 << 30; }
+  int nh = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < WS_BINS; ++w) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t itm = a.items[wgp * WS_BINS + w][i];
+      if (!item_valid(itm) || !item_last(itm)) continue;
+      const int kv = item_kv(itm), r = item_mt(itm) * 32 + item_nv(itm);
+      bool found = false;
+#pragma unroll
+      for (int k = 0; k < WS_MAXH; ++k) found |= hkv[k] == kv;
+      if (found) continue;
+#pragma unroll
+      for (int k = 0; k < WS_MAXH; ++k)
+        if (k == nh) { hkv[k] = kv; hrank[k] = r; hoff[k] = tot; }
+      tot += 4 * r;                         // 16-byte chunks per 32-row tile: 32 * 2r / 16
+      ++nh;
+    }
+  }
+  // stage: latent chunks [0, 64 * nX) then the RoPE operand in the last 8 KB
+  const int nX = (tot + 63) / 64, stage = a.ws_stage, nst = a.ws_nst;
+  if (tot == 0 || nX * 1024 + 8192 > stage || nst < 2 || nst * stage > WS_RING) return;   // uniform
+
+  if (wave >= WS_CONSUMERS) {
+    // ================= producer =================
+    const int pw = wave - WS_CONSUMERS;
+    // DMA instruction m (latent chunks [64m, 64m+64) for m < nX, then the
+    // RoPE operand in 1 KB pieces) belongs to producer m % 4.  Per
+    // instruction k of this wave: the lane's source and stage offset.
+    const int nI = nX + 8, ahead = nst - 1;
+    const char* src[WS_MAXK];
+    int64_t adv[WS_MAXK];   // latent: bytes per position of the head; RoPE: bytes per tile
+    int rowpos[WS_MAXK];    // latent: row within the tile
+    int dst[WS_MAXK];       // wave-uniform stage offset
+    int cnt = 0;
+#pragma unroll
+    for (int k = 0; k < WS_MAXK; ++k) {
+      const int m = pw + WS_PRODUCERS * k;
+      src[k] = (const char*)a.rope; adv[k] = 8192; rowpos[k] = 0; dst[k] = 0;
+      if (m >= nI) continue;
+      ++cnt;
+      if (m >= nX) {
+        const int j = m - nX;
+        src[k] = (const char*)a.rope + (j * 64 + lane) * 16;
+        dst[k] = stage - 8192 + j * 1024;
+        continue;
+      }
+      int q = m * 64 + lane;
+      if (q >= tot) q = tot - 1;            // lanes past the last chunk re-read it into an unused slot
+      int hb = hoff[0], hr = hrank[0], hk = hkv[0];
+#pragma unroll
+      for (int j = 1; j < WS_MAXH; ++j)
+        if (hoff[j] <= q) { hb = hoff[j]; hr = hrank[j]; hk = hkv[j]; }
+      const int n16 = hr / 8, loc = q - hb;
+      const int row = loc / n16, cr = loc % n16;             // stored (rotated) chunk cr of row
+      const int c = (cr - ws_shift(row, n16) % n16 + n16) % n16;   // the row's chunk that lives there
+      src[k] = (const char*)a.x + (b * a.x_sb + a.xoff[hk]) * 2 + (int64_t)c * 16;
+      adv[k] = (int64_t)a.xpitch[hk] * 2;
+      rowpos[k] = row;
+      dst[k] = m * 1024;
+    }
+    auto issue = [&](int i) __attribute__((always_inline)) {
+      const int tl = min(tile0 + i, last);
+      char* st = ring + (i % nst) * stage;
+#pragma unroll
+      for (int k = 0; k < WS_MAXK; ++k) {
+        const int m = pw + WS_PRODUCERS * k;
+        if (m >= nI) break;
+        const int64_t pos = m < nX ? min(tl * TILE + rowpos[k], S - 1) : tl;
+        __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+      }
+    };
+    for (int i = 0; i < ahead; ++i) issue(i);
+    for (int i = 0; i < ntl; ++i) {
+      // this producer's DMA of tile i complete: tiles i+1 .. i+ahead-1 may be in flight
+      wait_vm_n((ahead - 1) * cnt);
+      __builtin_amdgcn_s_barrier();
+      issue(i + ahead);                      // into the stage consumed at tile i-1
+    }
+    __builtin_amdgcn_s_barrier();           // the consumers' extra barrier
+    wait_vm<0>();                            // drain the trailing (clamped) DMA before the wave ends
+    return;
+  }
+
+  // ================= consumer =================
+  const int bin = wave & (WS_BINS - 1), half = wave / WS_BINS;
+  uint32_t it[MAXI];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) it[i] = a.items[wgp * WS_BINS + bin][MAXI * half + i];
+  // the bin's item 1 ends the first half; if it is not its head's last item the head straddles
+  const uint32_t i1 = a.items[wgp * WS_BINS + bin][1];
+  const bool straddle = item_valid(i1) && !item_last(i1);
+  const bool send = straddle && half == 0;   // leaves the partial logits of its last head
+  const bool recv = straddle && half == 1;   // completes its first head one tile later
+
+  const int rho = lane & 31;
+  const int jrow = 16 * ((rho >> 2) & 1) + 4 * (rho >> 3) + (rho & 3);
+  half8 wr[MAXI][8];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    const bool ok = item_valid(it[i]) && jrow < item_nv(it[i]);
+    const int qh = item_qh(it[i]), kv = item_kv(it[i]), mt = item_mt(it[i]);
+    const XT* qrow = (const XT*)a.q + b * a.q_sb + qh * a.q_sh;
+    const XT* brow = (const XT*)a.bk + a.bkoff[kv] + (int64_t)(mt * 32 + jrow) * a.bk_rs;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      half8 w = half8{};
+      if (ok) {
+        const int i0 = 8 * k + 4 * hh;
+        float ql[4], qu[4], bl[4], bu[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ql[e] = to_f32(qrow[i0 + e]); qu[e] = to_f32(qrow[i0 + 64 + e]);
+          bl[e] = to_f32(brow[i0 + e]); bu[e] = to_f32(brow[i0 + 64 + e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          w[2 * e] = (_Float16)(a.wscale * (bl[e] * ql[e] + bu[e] * qu[e]));
+          w[2 * e + 1] = (_Float16)(a.wscale * (bl[e] * qu[e] - bu[e] * ql[e]));
+        }
+      }
+      wr[i][k] = w;
+    }
+  }
+  // LDS byte offsets (within a stage) of this lane's two 16-byte chunks of each item's row t
+  int xo0[MAXI], xo1[MAXI];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    xo0[i] = xo1[i] = 0;
+    if (!item_valid(it[i])) continue;
+    const int kv = item_kv(it[i]), mt = item_mt(it[i]), nvh = item_nv(it[i]) - 16 * hh;
+    int hb = 0, hr = 8;
+#pragma unroll
+    for (int j = 0; j < WS_MAXH; ++j)
+      if (hkv[j] == kv) { hb = hoff[j]; hr = hrank[j]; }
+    const int n16 = hr / 8;
+    const int c0 = nvh > 0 ? mt * 4 + 2 * hh : mt * 4;        // lanes past the valid ranks re-read valid data
+    const int c1 = nvh > 8 ? c0 + 1 : c0;                    // (multiplied by the zero rows of W)
+    const int rowb = (hb + t * n16) * 16;
+    const int sh = ws_shift(t, n16);
+    xo0[i] = rowb + ((c0 + sh) % n16) * 16;
+    xo1[i] = rowb + ((c1 + sh) % n16) * 16;
+  }
+  float mx[MAXI];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) mx[i] = -INFINITY;
+
+  // logit epilogue of one head at position s: mask, store, running maximum
+  auto emit = [&](float v, int qh, int s, float& m) __attribute__((always_inline)) {
+    if (s < S) {
+      if (a.mask != nullptr) v += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
+      const int64_t o = b * a.o_sb + qh * a.o_sh + s;
+      if constexpr (OUTK == 0) ((float*)a.out)[o] = v;
+      else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)v;
+      else ((__bf16*)a.out)[o] = (__bf16)v;
+      m = fmaxf(m, v);
+    }
+  };
+  // the first head of a receiving wave ends at its item j0
+  const int j0 = item_last(it[0]) ? 0 : 1;
+  float pend = 0.f;                          // receiving wave: own partial of the previous tile
+
+  for (int i = 0; i < ntl; ++i) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS reads and writes are done
+    __builtin_amdgcn_s_barrier();
+    if (!item_valid(it[0])) continue;
+    if (recv && i > 0)
+      emit(pend + carry[(i - 1) & 1][bin][t], item_qh(it[j0]), (tile0 + i - 1) * TILE + t, mx[j0]);
+    const char* st = ring + (i % nst) * stage;
+    const int s = (tile0 + i) * TILE + t;
+    half8 T[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) T[k] = *(const half8*)(st + stage - 8192 + (k * 64 + lane) * 16);
+    // both chains every tile (an unused item has zero W rows and reads valid
+    // LDS data), interleaved so the MFMA pipe stays busy
+    uint4 x0[MAXI], x1[MAXI];
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) {
+      x0[j] = *(const uint4*)(st + xo0[j]);
+      x1[j] = *(const uint4*)(st + xo1[j]);
+    }
+    floatx16 acc[MAXI];
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) acc[j] = mfma_f16(wr[j][0], T[0], floatx16{});
+#pragma unroll
+    for (int k = 1; k < 8; ++k)
+#pragma unroll
+      for (int j = 0; j < MAXI; ++j) acc[j] = mfma_f16(wr[j][k], T[k], acc[j]);
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) {
+      if constexpr (__is_same(XT, _Float16)) part += dot16h(x0[j], x1[j], acc[j]);
+      else part += dot16b(x0[j], x1[j], acc[j]);
+      if (item_last(it[j])) {
+        const float v = add_halves(part);
+        part = 0.f;
+        if (recv && j == j0) pend = v;
+        else emit(v, item_qh(it[j]), s, mx[j]);
+      }
+    }
+    if (send) {
+      const float v = add_halves(part);
+      if (hh == 0) carry[i & 1][bin][t] = v;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();              // publishes the last tile's partials
+  if (recv && item_valid(it[0]))
+    emit(pend + carry[(ntl - 1) & 1][bin][t], item_qh(it[j0]), (tile0 + ntl - 1) * TILE + t, mx[j0]);
+  if constexpr (OUTK == 0) {
+    if (a.chunkmax != nullptr) {
+#pragma unroll
+      for (int i = 0; i < MAXI; ++i) {
+        if (!item_valid(it[i]) || !item_last(it[i])) continue;
+        const float m = wave_max32(mx[i]);
+        if (lane == 0) a.chunkmax[((int64_t)b * a.Hq + item_qh(it[i])) * a.n_chunks + chunk] = m;
+      }
+    }
+  }
+}
+
+template <typename XT>
+static int launch_ws_t(const KArgs& a, int outk, int B, hipStream_t st) {
+  dim3 grid(a.n_chunks, a.n_wg, B);
+  if (outk == 0) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 0>), grid, dim3((WS_CONSUMERS + WS_PRODUCERS) * 64), 0, st, a);
+  else if (outk == 1) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 1>), grid, dim3((WS_CONSUMERS + WS_PRODUCERS) * 64), 0, st, a);
+  else hipLaunchKernelGGL((k_logits_ws_kernel<XT, 2>), grid, dim3((WS_CONSUMERS + WS_PRODUCERS) * 64), 0, st, a);
+  return (int)hipGetLastError();
+}
+
+int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st) {
+  const int outk = out_f32 ? 0 : (out_dtype == STARKV_F16 ? 1 : 2);
+  return dtype == STARKV_F16 ? launch_ws_t<_Float16>(a, outk, B, st) : launch_ws_t<__bf16>(a, outk, B, st);
+}
+
+}  // namespace starkv
