@@ -360,26 +360,45 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
 }
 
 // Sum of the chunk partials in fixed chunk order.  Fused: o_lat (fp32, with
-// the denominators L); drop-in: the act-dtype output of bx.
+// the denominators L); drop-in: the act-dtype output of bx.  Each thread sums
+// four columns of a 32x32 output tile; the partial loads are issued eight
+// chunks at a time (32 loads in flight per thread) and added in chunk order.
 template <typename VT, bool FUSED>
 __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
   const int tile = blockIdx.x, b = blockIdx.y;
-  const int Rvp = a.Rvp;
-  const float* pb = a.part + ((int64_t)b * a.n_c2 * 32) * Rvp;
-  for (int e = threadIdx.x; e < 32 * 32; e += 256) {
-    const int q = e >> 5, col = tile * 32 + (e & 31);
-    float s = 0.f;
-    for (int c = 0; c < a.n_c2; ++c) s += pb[((int64_t)c * 32 + q) * Rvp + col];
+  const int Rvp = a.Rvp, n_c2 = a.n_c2;
+  const int q0 = threadIdx.x >> 5, col = tile * 32 + (threadIdx.x & 31);
+  const float* pb = a.part + ((int64_t)b * n_c2 * 32 + q0) * Rvp + col;
+  const int64_t cstride = (int64_t)32 * Rvp, ustride = (int64_t)8 * Rvp;   // next chunk / next row group
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  int c = 0;
+  for (; c + 8 <= n_c2; c += 8) {
+    float v[8][4];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[k][u] = pb[(c + k) * cstride + u * ustride];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s[u] += v[k][u];
+  }
+  for (; c < n_c2; ++c)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s[u] += pb[c * cstride + u * ustride];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int q = q0 + 8 * u;
     if constexpr (FUSED) {
-      a.olat[((int64_t)b * 32 + q) * Rvp + col] = s;
+      a.olat[((int64_t)b * 32 + q) * Rvp + col] = s[u];
     } else {
-      if (q < a.H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + q * a.o_sh + col] = (VT)s;
+      if (q < a.H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + q * a.o_sh + col] = (VT)s[u];
     }
   }
   if constexpr (FUSED) {
     if (tile == 0 && threadIdx.x < 32) {
       float L = 0.f;
-      for (int c = 0; c < a.n_c2; ++c) L += a.psum[((int64_t)b * a.n_c2 + c) * 32 + threadIdx.x];
+      for (int cc = 0; cc < n_c2; ++cc) L += a.psum[((int64_t)b * n_c2 + cc) * 32 + threadIdx.x];
       a.lsum[b * 32 + threadIdx.x] = L;
     }
   }

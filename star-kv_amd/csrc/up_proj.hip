@@ -8,14 +8,17 @@
 // into hi + lo halves of the weight dtype (fp32-accurate), B = U_v rows read
 // straight from the weight layout (the k-contiguous operand needs no
 // transpose).  Workgroup = (32-column block of d, KV head, 32-row M-tile);
-// its 4 waves split the Rv reduction and are summed through LDS.
+// its UP_WAVES waves split the Rv reduction (a handful of K-steps each, so the
+// dependent load chains stay short) and are summed through LDS.
 #include "common.hpp"
 
 namespace starkv {
 
+constexpr int UP_WAVES = 16;
+
 template <typename WT, typename OT, bool FAST>
-__global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
-  __shared__ float red[4][64][17];
+__global__ __launch_bounds__(UP_WAVES * 64) void up_proj_kernel(const UPArgs a) {
+  __shared__ float red[UP_WAVES][64][17];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
@@ -33,7 +36,7 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   const WT* urow = (const WT*)a.uv + (int64_t)(kv * HEAD_DIM + d) * a.uv_rs;
 
   const int nk = a.Rvp / KSTEP;
-  const int per = (nk + 3) / 4;
+  const int per = (nk + UP_WAVES - 1) / UP_WAVES;
   const int k0 = wave * per, k1 = min(nk, k0 + per);
 
   floatx16 acc = floatx16{};
@@ -86,10 +89,12 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
 #pragma unroll
   for (int v = 0; v < 16; ++v) red[wave][lane][v] = acc[v];
   __syncthreads();
-  for (int e = tid; e < 1024; e += 256) {
+  for (int e = tid; e < 1024; e += UP_WAVES * 64) {
     const int row = e >> 5, col = e & 31;          // D[row][col]
     const int ln = col + 32 * ((row >> 2) & 1), v = 4 * (row >> 3) + (row & 3);
-    const float s = red[0][ln][v] + red[1][ln][v] + red[2][ln][v] + red[3][ln][v];
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < UP_WAVES; ++w) s += red[w][ln][v];
     const int rr = mt * 32 + row;
     const int ob = rr / gs, og = rr % gs;
     if (ob < a.B) ((OT*)a.out)[ob * a.o_sb + (kv * gs + og) * a.o_sh + db * 32 + col] = (OT)s;
@@ -104,7 +109,7 @@ static void launch_up_t(const UPArgs& a, bool fast, dim3 grid, dim3 block, hipSt
 
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st) {
   const int n_kv = a.Hq / a.gs;
-  dim3 grid(HEAD_DIM / 32, n_kv, (unsigned)ceil_div((int64_t)a.B * a.gs, 32)), block(256);
+  dim3 grid(HEAD_DIM / 32, n_kv, (unsigned)ceil_div((int64_t)a.B * a.gs, 32)), block(UP_WAVES * 64);
   if (dtype == STARKV_F16) {
     if (a.out_f32) launch_up_t<_Float16, float>(a, fast, grid, block, st);
     else launch_up_t<_Float16, _Float16>(a, fast, grid, block, st);
