@@ -64,6 +64,92 @@ def cpu_baseline(case_cpu_fn, reps):
     return statistics.median(ts), threads, torch.get_num_threads(), len(ts)
 
 
+def build_workload(name, dev):
+    """Seeded synthetic inputs of one workload, resident in HBM; returns the
+    step function and the algorithmic bytes per step."""
+    import torch
+    from _util import cfg2_ranks, cfg4_ranks, make_case
+    from starkv import RopeConfig, VLatentSpec, decode_attention
+    from starkv.cache import LatentCache
+
+    if name == "cfg2":
+        ranks = cfg2_ranks()
+        B, H, S, Rv = 16, 32, 32768, 1640
+        case = make_case(B, H, H, S, ranks, Rv, dtype=torch.float16, device=dev, seed=0)
+        rope = RopeConfig()
+        out = torch.empty(B, H, HEAD_DIM, dtype=torch.float16, device=dev)
+
+        def step(ev=None):
+            decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, out=out, events=ev)
+        cfg = {"workload": "cfg2: Llama-2-7B-shaped decode attention layer, MHA 32x128, fp16, batch 16, "
+                           "context 32768, ragged K ranks (sum 1640), V rank 1640",
+               "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": H}
+        return dict(case=case, bytes=algorithmic_bytes(case), step=step, B=B, S=S, rope=rope, dtype="f16", config=cfg)
+
+    if name in ("cfg3", "cfg3-long"):
+        ranks = cfg2_ranks()
+        B, S = (16, 32768) if name == "cfg3" else (4, 131072)
+        H, Rv, rmax = len(ranks), 1640, max(ranks)
+        g = torch.Generator(device=dev).manual_seed(0)
+        k_new = torch.randn(B, H, S, rmax, generator=g, device=dev, dtype=torch.float16)
+        k_new[..., ::97] *= 10                                   # 1 % outlier channels
+        v_new = torch.randn(B, S, Rv, generator=g, device=dev, dtype=torch.float16)
+        v_new[..., ::97] *= 10
+        bk = (torch.randn(H, rmax, HEAD_DIM, generator=g, device=dev) / math.sqrt(rmax)).half()
+        uv = (torch.randn(H * HEAD_DIM, Rv, generator=g, device=dev) / math.sqrt(Rv)).half()
+        q = torch.randn(B, H, HEAD_DIM, generator=g, device=dev).half()
+        cache = LatentCache(B, ranks, Rv, S, torch.float16, dev, fmt="int8_g64")
+        kspec, vspec, _ = cache.append(k_new, v_new, bk)
+        del k_new, v_new
+        torch.cuda.empty_cache()
+        rope = RopeConfig()
+        out = torch.empty(B, H, HEAD_DIM, dtype=torch.float16, device=dev)
+
+        def step(ev=None):
+            decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=S, out=out, events=ev)
+        G = (Rv + 63) // 64
+        xk = B * S * sum(ranks) + B * H * S * 2                  # int8 + fp16 scale per (b, h, s)
+        xv = B * S * Rv // 2 + B * S * G * 4                     # packed int4 + fp16 scale and zero per group
+        w = sum(ranks) * HEAD_DIM * 2 + H * HEAD_DIM * Rv * 2
+        qo = 2 * B * H * HEAD_DIM * 2
+        nb = {"k_logits": xk + sum(ranks) * HEAD_DIM * 2 + B * H * HEAD_DIM * 2, "pv_latent": xv,
+              "up_proj": H * HEAD_DIM * Rv * 2 + B * H * HEAD_DIM * 2, "total": xk + xv + w + qo}
+        cfg = {"workload": f"{name}: Llama-2-7B-shaped layer, fp16, batch {B}, context {S}, ragged K ranks "
+                           f"(sum 1640) int8 with fp16 scale per (b,h,s), V rank 1640 int4 asymmetric g64 "
+                           f"(fp16 scale+zero), 1 % outlier channels",
+               "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": H}
+        return dict(case=None, bytes=nb, step=step, B=B, S=S, rope=rope, dtype="f16", config=cfg)
+
+    if name.startswith("cfg4-"):
+        S = int(name.split("-", 1)[1])
+        ranks = cfg4_ranks()
+        B, Hq, Hkv, Rv = 1, 32, 8, 512
+        rope = RopeConfig(theta=500000.0, rope_type="llama3", factor=8.0, low_freq_factor=1.0,
+                          high_freq_factor=4.0, original_max_position_embeddings=8192)
+        case = make_case(B, Hq, Hkv, S, ranks, Rv, dtype=torch.bfloat16, device=dev, seed=5)
+        G = (Rv + 63) // 64
+        g = torch.Generator(device=dev).manual_seed(6)
+        vp = torch.randint(0, 256, (B, S, Rv // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        vs = (torch.rand(B, S, G, generator=g, device=dev) * 0.3 + 0.05).half()
+        vz = (-torch.rand(B, S, G, generator=g, device=dev) * 2).half()
+        vspec = VLatentSpec.int4_g64(vp, vs, vz, Rv)
+        out = torch.empty(B, Hq, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+
+        def step(ev=None):
+            decode_attention(case.q, case.kspec, vspec, case.uv, rope=rope, out=out, events=ev)
+        xk = B * S * sum(ranks) * 2
+        xv = B * S * Rv // 2 + B * S * G * 4
+        nb = {"k_logits": xk + sum(ranks) * HEAD_DIM * 2 + B * Hq * HEAD_DIM * 2, "pv_latent": xv,
+              "up_proj": Hkv * HEAD_DIM * Rv * 2 + B * Hq * HEAD_DIM * 2,
+              "total": xk + xv + sum(ranks) * HEAD_DIM * 2 + Hkv * HEAD_DIM * Rv * 2 + 2 * B * Hq * HEAD_DIM * 2}
+        cfg = {"workload": f"{name}: Llama-3.1-8B-shaped GQA layer (32 q / 8 KV heads, llama3 RoPE theta 500000), "
+                           f"bf16, batch 1, context {S}, K ranks per KV head in [32,128] (bf16), V rank 512 int4 "
+                           f"asymmetric g64",
+               "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": Hq, "kv_heads": Hkv}
+        return dict(case=case, bytes=nb, step=step, B=B, S=S, rope=rope, dtype="bf16", config=cfg)
+    raise SystemExit(f"unknown workload {name!r}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -71,6 +157,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=100)
+    ap.add_argument("--workload", default="cfg2",
+                    help="cfg2 (default: the metric's workload), cfg3 (B16 S32768, K int8 + V int4-g64 cache), "
+                         "cfg3-long (B4 S131072, same formats), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S)")
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run three 1 GiB device-to-device copies (the known-size reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE per dispatch) and exit")
@@ -81,9 +170,6 @@ def main():
         sys.exit(2)
 
     import torch
-    from _util import cfg2_ranks, make_case
-    from starkv import RopeConfig, decode_attention
-    from starkv.ops import _workspace  # noqa: F401  (workspace is allocated on first call, outside timing)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -96,15 +182,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration_copy_bytes_read": n, "calibration_copy_bytes_written": n, "copies": 3}))
         return
-    ranks = cfg2_ranks()
-    B, H, S, Rv = 16, 32, 32768, 1640
-    case = make_case(B, H, H, S, ranks, Rv, dtype=torch.float16, device=dev, seed=0)
-    rope = RopeConfig()
-    out = torch.empty(B, H, HEAD_DIM, dtype=torch.float16, device=dev)
-    nbytes = algorithmic_bytes(case)
-
-    def step(ev=None):
-        decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, out=out, events=ev)
+    wl = build_workload(args.workload, dev)
+    case, nbytes, step, B, S = wl["case"], wl["bytes"], wl["step"], wl["B"], wl["S"]
+    rope = wl["rope"]
 
     for _ in range(args.warmup):
         step()
@@ -133,12 +213,12 @@ def main():
     dom_gbs = nbytes[dom] / (dom_ms * 1e-3) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_cfg2.json")
-    if os.path.exists(tpath):
+    if args.workload == "cfg2" and os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get(dom)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload == "cfg2":
         from oracle import starkv_oracle as o
 
         def make_fn():
@@ -174,11 +254,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": wl["dtype"],
         "data": "synthetic",
-        "config": {"workload": "cfg2: Llama-2-7B-shaped decode attention layer, MHA 32x128, fp16, "
-                               "batch 16, context 32768, ragged K ranks (sum 1640), V rank 1640",
-                   "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": H},
+        "config": wl["config"],
         "us_per_layer": round(ms * 1e3, 1),
         "wall_ms_per_step": round(wall_ms, 4),
         "pct_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 1),

@@ -30,20 +30,20 @@ bool al64(int64_t v, int n) { return v % n == 0; }
 
 size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Choose how many position splits give the best whole-GPU fill for
-// `groups` independent (batch, plan) groups; `penalty` prices extra splits.
-int choose_splits(int64_t groups, int slots, int n_units, int max_n, double penalty_per_split) {
+// Choose how many position splits minimise the modelled time of a launch of
+// `groups` independent (batch, plan) groups over `n_units` position units:
+// rounds of `slots` concurrent workgroups, each costing its units plus a fixed
+// `c0` units (setup, pipeline fill), times (1 + frac_per_split * splits) for
+// split partials written and re-read.
+int choose_splits(int64_t groups, int slots, int n_units, int max_n, double c0, double frac_per_split) {
   int best = 1;
-  double best_score = -1.0;
+  double best_t = 1e300;
   for (int n = 1; n <= std::max(1, std::min(max_n, n_units)); ++n) {
     const int len = (int)ceil_div(n_units, n);
     const int ne = (int)ceil_div(n_units, len);
-    const int64_t W = groups * ne;
-    const int64_t rounds = ceil_div(W, slots);
-    const double fill = (double)W / (double)(rounds * slots);
-    const double bal = (double)n_units / (double)((int64_t)ne * len);
-    const double score = fill * bal / (1.0 + penalty_per_split * ne);
-    if (score > best_score * 1.0001) { best_score = score; best = n; }
+    const int64_t rounds = ceil_div(groups * ne, slots);
+    const double t = (double)rounds * (len + c0) * (1.0 + frac_per_split * ne);
+    if (t < best_t * 0.9999) { best_t = t; best = ne; }
   }
   return best;
 }
@@ -146,25 +146,64 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, K
   const bool ws = k_ws(k, dtype);
   const int maxi = ws || max_ni > 2 ? 4 : 2;   // whole heads per (consumer) wave
   const int nw = maxi == 2 ? 8 : 4;
-  std::stable_sort(heads.begin(), heads.end(), [](const QH& x, const QH& y) { return x.ni > y.ni; });
+  // Bins of up to maxi items (whole query heads), first-fit decreasing.  With
+  // GQA the query heads of one KV head are packed together (KV-major), so the
+  // workgroup that stages or streams that head's latent serves all of them.
   std::vector<std::vector<QH>> bins;
   std::vector<int> load;
-  for (const QH& h : heads) {
-    size_t i = 0;
-    for (; i < bins.size(); ++i) if (load[i] + h.ni <= maxi) break;
-    if (i == bins.size()) { bins.emplace_back(); load.push_back(0); }
-    bins[i].push_back(h);
-    load[i] += h.ni;
+  auto pack = [&](const std::vector<QH>& hs) {
+    const size_t first = bins.size();
+    for (const QH& h : hs) {
+      size_t i = first;
+      for (; i < bins.size(); ++i) if (load[i] + h.ni <= maxi) break;
+      if (i == bins.size()) { bins.emplace_back(); load.push_back(0); }
+      bins[i].push_back(h);
+      load[i] += h.ni;
+    }
+  };
+  if (gs == 1) {
+    std::stable_sort(heads.begin(), heads.end(), [](const QH& x, const QH& y) { return x.ni > y.ni; });
+    pack(heads);
+  } else {
+    for (int kv = 0; kv < k.n_kv_heads; ++kv) {
+      std::vector<QH> grp;
+      for (const QH& h : heads) if (h.kv == kv) grp.push_back(h);
+      pack(grp);
+    }
   }
   const int n_waves = (int)bins.size();
   plan.n_wg = (int)ceil_div(n_waves, nw);
   if (plan.n_wg * nw > K_MAX_WAVES) return STARKV_ERR_LIMIT;
+  // bin -> (workgroup, wave).  MHA: the heaviest bins (latent rank sum) first,
+  // each into the least loaded workgroup with a free wave, so workgroups
+  // stream similar byte counts.  GQA: consecutive bins share a workgroup.
+  std::vector<int> wg_of(n_waves), wave_of(n_waves);
+  if (gs == 1) {
+    std::vector<int> order(n_waves), rsum(n_waves, 0);
+    for (int bi = 0; bi < n_waves; ++bi) {
+      order[bi] = bi;
+      for (const QH& h : bins[bi]) rsum[bi] += k.rank[h.kv];
+    }
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return rsum[x] > rsum[y]; });
+    std::vector<int64_t> wload(plan.n_wg, 0);
+    std::vector<int> used(plan.n_wg, 0);
+    for (int bi : order) {
+      int best = -1;
+      for (int g = 0; g < plan.n_wg; ++g)
+        if (used[g] < nw && (best < 0 || wload[g] < wload[best])) best = g;
+      wg_of[bi] = best;
+      wave_of[bi] = used[best]++;
+      wload[best] += rsum[bi];
+    }
+  } else {
+    for (int bi = 0; bi < n_waves; ++bi) { wg_of[bi] = bi / nw; wave_of[bi] = bi % nw; }
+  }
   for (int w = 0; w < K_MAX_WAVES; ++w)
     for (int i = 0; i < K_MAXI; ++i) a.items[w][i] = 0;
   for (int bi = 0; bi < n_waves; ++bi) {
     std::vector<QH> v = bins[bi];
     std::sort(v.begin(), v.end(), [](const QH& x, const QH& y) { return x.qh < y.qh; });
-    const int g = bi % plan.n_wg, w = bi / plan.n_wg;
+    const int g = wg_of[bi], w = wave_of[bi];
     int i = 0;
     for (const QH& h : v) {
       const int r = k.rank[h.kv];
@@ -240,7 +279,7 @@ int check_mask(const void* mask, int mask_dtype) {
 
 // ---- P.V geometry: workgroup = 4 waves x NTW column tiles of one position chunk
 struct PVGeom {
-  int Rvp, n_cb, n_c2, c2_len;
+  int Rvp, n_cb, n_c2, c2_len, n_grp;   // n_grp > 1: two-level split reduction
 };
 
 PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq) {
@@ -250,10 +289,15 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq) {
   g.n_cb = (int)ceil_div(g.Rvp / 32, 4 * ntw);
   const int wg_per_cu = ntw >= 8 ? 1 : 2;    // registers / LDS staging allow one workgroup per CU from NTW 8
   const int n_ks = (int)ceil_div(S, KSTEP);
-  // each extra split writes and re-reads one fp32 partial (~128/S of the X_v stream)
-  int n = choose_splits((int64_t)B * g.n_cb, MI355X_CUS * wg_per_cu, n_ks, 64, 128.0 / std::max(S, 1));
+  // each extra split writes and re-reads one fp32 partial of 32 x Rvp per
+  // column block, against the X_v bytes and logits the split streams
+  const double vbytes = vq == VQ_DENSE ? 2.0 * Rv : Rv / 2.0 + 4.0 * ceil_div(Rv, 64);
+  // (below ~8K positions the launch is latency-bound and partials are cheap)
+  const double frac = 32.0 * g.Rvp * 8.0 / g.n_cb / ((double)std::max(S, 8192) * (vbytes / g.n_cb + 128.0));
+  int n = choose_splits((int64_t)B * g.n_cb, MI355X_CUS * wg_per_cu, n_ks, 512, 4.0, frac);
   g.c2_len = (int)ceil_div(n_ks, n) * KSTEP;
   g.n_c2 = (int)ceil_div(S, g.c2_len);
+  g.n_grp = g.n_c2 > PV_RG ? (int)ceil_div(g.n_c2, PV_RG) : 0;
   return g;
 }
 
@@ -261,14 +305,14 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq) {
 struct DecodeLayout {
   int S_pad, n_c1, tiles_per_chunk;
   PVGeom pv;
-  size_t off_logits, off_cmax, off_part, off_psum, off_olat, off_lsum, total;
+  size_t off_logits, off_cmax, off_part, off_psum, off_part2, off_psum2, off_olat, off_lsum, total;
 };
 
 DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg, int vq) {
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
-  L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
+  L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 256, 3.0, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
   L.pv = pv_geometry(B, S, Rv, true, vq);
@@ -278,6 +322,8 @@ DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg, int vq) {
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
   L.off_part = o; o = a256(o + (size_t)B * n_c2 * 32 * Rvp * 4);
   L.off_psum = o; o = a256(o + (size_t)B * n_c2 * 32 * 4);
+  L.off_part2 = o; o = a256(o + (size_t)B * L.pv.n_grp * 32 * Rvp * 4);
+  L.off_psum2 = o; o = a256(o + (size_t)B * L.pv.n_grp * 32 * 4);
   L.off_olat = o; o = a256(o + (size_t)B * 32 * Rvp * 4);
   L.off_lsum = o; o = a256(o + (size_t)B * 32 * 4);
   L.total = o;
@@ -432,7 +478,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
   const int n_tiles = (int)ceil_div(d->seq_len, TILE);
-  int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 64, 0.0);
+  int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 256, 3.0, 0.0);
   a.tiles_per_chunk = (int)ceil_div(n_tiles, nc);
   a.n_chunks = (int)ceil_div(n_tiles, a.tiles_per_chunk);
   const bool fast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
@@ -445,7 +491,7 @@ size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {
   int vq = 0;
   if (validate_v(d->v, tmp, &vq)) return 0;
   const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq);
-  return a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4);
+  return a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4) + a256((size_t)d->batch * g.n_grp * 32 * g.Rvp * 4);
 }
 
 int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
@@ -461,10 +507,11 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
   if (!workspace || workspace_bytes < need) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq);
-  a.Rv = d->v.rank; a.Rvp = g.Rvp; a.n_cb = g.n_cb; a.n_c2 = g.n_c2; a.c2_len = g.c2_len;
+  a.Rv = d->v.rank; a.Rvp = g.Rvp; a.n_cb = g.n_cb; a.n_c2 = g.n_c2; a.c2_len = g.c2_len; a.n_grp = g.n_grp;
   a.p = d->p; a.p_sb = d->p_stride_b; a.p_sh = d->p_stride_h;
   a.p_vec = al(d->p, 16) && al64(d->p_stride_b * 2, 16) && al64(d->p_stride_h * 2, 16);
   a.part = (float*)workspace;
+  a.part2 = (float*)((char*)workspace + a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4));
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
   a.S = d->seq_len; a.H = d->n_heads;
   return launch_pv(a, d->dtype, vq, false, v_fast(d->v), d->batch, (hipStream_t)stream);
@@ -510,6 +557,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = (int64_t)Hq * L.S_pad; pa.l_sh = L.S_pad;
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
+  pa.part2 = (float*)(ws + L.off_part2); pa.psum2 = (float*)(ws + L.off_psum2); pa.n_grp = L.pv.n_grp;
   pa.olat = (float*)(ws + L.off_olat); pa.lsum = (float*)(ws + L.off_lsum);
   pa.S = d->seq_len; pa.H = Hq; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
   pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;

@@ -18,6 +18,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int HEAD_DIM = 128;
 constexpr int TILE = 32;            // positions per K-logit tile (the MFMA N dimension)
 constexpr int KSTEP = 16;           // positions per P.V MFMA K-step
+constexpr int PV_RG = 16;           // split partials per first-level reduction group
 
 // ---------------------------------------------------------------------------
 // K-logit launch plan (passed by value as a kernel argument, read with
@@ -89,6 +90,7 @@ struct PVArgs {
   int p_vec;                                       // drop-in: P rows allow 16-byte loads
   float* part;                                     // [B][n_c2][32][Rvp] fp32
   float* psum;                                     // [B][n_c2][32]
+  float* part2; float* psum2; int n_grp;           // two-level reduction: [B][n_grp][32][Rvp], [B][n_grp][32]
   float* olat;                                     // [B][32][Rvp] fp32 (fused) ...
   void* out; int64_t o_sb, o_sh;                   // ... or act-dtype [B][H][Rv] (drop-in)
   float* lsum;                                     // [B][32] softmax denominators (fused)

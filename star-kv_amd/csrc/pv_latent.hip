@@ -363,16 +363,24 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
 // the denominators L); drop-in: the act-dtype output of bx.  Each thread sums
 // four columns of a 32x32 output tile; the partial loads are issued eight
 // chunks at a time (32 loads in flight per thread) and added in chunk order.
-template <typename VT, bool FUSED>
+// More than PV_RG chunks are summed in two levels (deterministic, fixed
+// grouping): MODE 1 sums each group of PV_RG chunks into part2 (grid z =
+// group), MODE 2 sums the groups; MODE 0 sums the chunks directly.
+template <typename VT, bool FUSED, int MODE>
 __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
-  const int tile = blockIdx.x, b = blockIdx.y;
-  const int Rvp = a.Rvp, n_c2 = a.n_c2;
+  const int tile = blockIdx.x, b = blockIdx.y, grp = blockIdx.z;
+  const int Rvp = a.Rvp;
   const int q0 = threadIdx.x >> 5, col = tile * 32 + (threadIdx.x & 31);
-  const float* pb = a.part + ((int64_t)b * n_c2 * 32 + q0) * Rvp + col;
+  const int n_src = MODE == 2 ? a.n_grp : a.n_c2;
+  const int c_begin = MODE == 1 ? grp * PV_RG : 0;
+  const int c_end = MODE == 1 ? min(n_src, c_begin + PV_RG) : n_src;
+  const float* part = MODE == 2 ? a.part2 : a.part;
+  const float* psum = MODE == 2 ? a.psum2 : a.psum;
+  const float* pb = part + ((int64_t)b * n_src * 32 + q0) * Rvp + col;
   const int64_t cstride = (int64_t)32 * Rvp, ustride = (int64_t)8 * Rvp;   // next chunk / next row group
   float s[4] = {0.f, 0.f, 0.f, 0.f};
-  int c = 0;
-  for (; c + 8 <= n_c2; c += 8) {
+  int c = c_begin;
+  for (; c + 8 <= c_end; c += 8) {
     float v[8][4];
 #pragma unroll
     for (int k = 0; k < 8; ++k)
@@ -383,13 +391,15 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) s[u] += v[k][u];
   }
-  for (; c < n_c2; ++c)
+  for (; c < c_end; ++c)
 #pragma unroll
     for (int u = 0; u < 4; ++u) s[u] += pb[c * cstride + u * ustride];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int q = q0 + 8 * u;
-    if constexpr (FUSED) {
+    if constexpr (MODE == 1) {
+      a.part2[(((int64_t)b * a.n_grp + grp) * 32 + q) * Rvp + col] = s[u];
+    } else if constexpr (FUSED) {
       a.olat[((int64_t)b * 32 + q) * Rvp + col] = s[u];
     } else {
       if (q < a.H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + q * a.o_sh + col] = (VT)s[u];
@@ -398,8 +408,9 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
   if constexpr (FUSED) {
     if (tile == 0 && threadIdx.x < 32) {
       float L = 0.f;
-      for (int cc = 0; cc < n_c2; ++cc) L += a.psum[((int64_t)b * n_c2 + cc) * 32 + threadIdx.x];
-      a.lsum[b * 32 + threadIdx.x] = L;
+      for (int cc = c_begin; cc < c_end; ++cc) L += psum[((int64_t)b * n_src + cc) * 32 + threadIdx.x];
+      if constexpr (MODE == 1) a.psum2[((int64_t)b * a.n_grp + grp) * 32 + threadIdx.x] = L;
+      else a.lsum[b * 32 + threadIdx.x] = L;
     }
   }
 }
@@ -436,7 +447,12 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
   else if constexpr (FUSED) launch_pv_n13<VT>(a, fast, B, st);
   int e = (int)hipGetLastError();
   if (e) return e;
-  hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
+  if (a.n_grp > 1) {
+    hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED, 1>), dim3(a.Rvp / 32, B, a.n_grp), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED, 2>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED, 0>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
+  }
   return (int)hipGetLastError();
 }
 

@@ -129,3 +129,21 @@ def test_llama3_gqa_bf16_int4_v_sweep(S):
     mx, mr = errors(out, ref)
     _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
     assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
+
+
+@pytest.mark.parametrize("B,S", [(1, 65536), (2, 20000)])
+def test_pv_latent_long_context_split_reduction(B, S):
+    """The drop-in P.V at long context and small batch, where the split-S
+    partials are summed in two levels."""
+    from starkv import pv_latent
+    _flush(f"[pv long] B={B} S={S}")
+    H, Rv = 32, 512
+    g = torch.Generator(device="cuda").manual_seed(7)
+    p = torch.softmax(torch.randn(B, H, S, generator=g, device="cuda") * 4, dim=-1).half()
+    xv = torch.randn(B, S, Rv, generator=g, device="cuda").half()
+    out = pv_latent(p, xv)
+    torch.cuda.synchronize()
+    ref = p.double().cpu() @ xv.double().cpu()
+    mx, mr = errors(out.float(), ref)
+    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
