@@ -417,9 +417,13 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
 
 int pv_tiles_per_wave(int Rvp, bool fused, int vq) {
   const int tiles = Rvp / 32;
-  if (tiles <= 16) return 4;
-  // the drop-in P-input variant and the quantised formats stay at 8 (register budget)
-  if (tiles <= 32 || !fused || vq != VQ_DENSE) return 8;
+  // Quantised formats: 4 tiles per wave, two workgroups per CU.  A quantised
+  // K-step carries a quarter (int4) of the bytes of a dense one, so the wave
+  // count, not the bytes per wave, has to cover the memory latency (measured at
+  // B16 S32768 int4-g64: 8 tiles 446 us, 4 tiles 350 us, 2 tiles 480 us).
+  if (tiles <= 16 || vq != VQ_DENSE) return 4;
+  // the drop-in P-input variant stays at 8 (register budget)
+  if (tiles <= 32 || !fused) return 8;
   return 13;
 }
 
