@@ -150,6 +150,61 @@ def build_workload(name, dev):
     raise SystemExit(f"unknown workload {name!r}")
 
 
+def run_e2e(args):
+    """End-to-end decode: random-init 32-layer
+    Llama-2-7B-shaped model (vocab 32000, MLP 11008, fp16), every attention on
+    the latent cache (cfg3 ranks and formats: K int8, V int4-g64), prefill 8192
+    random tokens at batch 8, then 256 greedy decode steps."""
+    import torch
+    from _util import cfg2_ranks
+    from starkv.e2e import attention_layers, build_model
+    B, P, steps = 8, 8192, args.e2e_steps
+    t0 = time.perf_counter()
+    model = build_model(n_layers=32, hidden=4096, heads=32, kv_heads=32, intermediate=11008, vocab=32000,
+                        ranks=cfg2_ranks(), v_rank=1640, batch=B, capacity=P + steps + 1, fmt="int8_g64", seed=0)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t0
+    g = torch.Generator(device="cuda").manual_seed(0)
+    prompt = torch.randint(0, 32000, (B, P), generator=g, device="cuda")
+    atts = attention_layers(model)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = model(input_ids=prompt, position_ids=torch.arange(P, device="cuda")[None].expand(B, P),
+                    use_cache=False, logits_to_keep=1)
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        for a in atts:
+            a.events = []
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        t0 = time.perf_counter()
+        for t in range(steps):
+            pos = torch.full((B, 1), P + t, device="cuda", dtype=torch.long)
+            out = model(input_ids=tok, position_ids=pos, use_cache=False, logits_to_keep=1)
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) * 1e-3
+    attn_s = sum(x.elapsed_time(y) for a in atts for (x, y) in a.events) * 1e-3
+    rec = {
+        "metric": "e2e decode tok/s", "value": round(B * steps / wall, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": steps, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "e2e: random-init 32-layer Llama-2-7B-shaped model (vocab 32000, MLP 11008, fp16), "
+                               "every attention on a STAR-KV latent cache (ragged K ranks sum 1640 int8, V rank 1640 "
+                               "int4-g64), prefill 8192 random tokens, greedy decode at batch 8",
+                   "batch": B, "prompt": P, "decode_steps": steps},
+        "ms_per_decode_step": round(wall * 1e3 / steps, 3),
+        "gpu_ms_per_decode_step": round(gpu_s * 1e3 / steps, 3),
+        "attention_share": round(attn_s / gpu_s, 4),
+        "attention_ms_per_decode_step": round(attn_s * 1e3 / steps, 3),
+        "prefill_s": round(t_prefill, 3), "build_s": round(t_build, 1),
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,7 +214,9 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=100)
     ap.add_argument("--workload", default="cfg2",
                     help="cfg2 (default: the metric's workload), cfg3 (B16 S32768, K int8 + V int4-g64 cache), "
-                         "cfg3-long (B4 S131072, same formats), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S)")
+                         "cfg3-long (B4 S131072, same formats), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S), "
+                         "e2e (32-layer model, prefill 8192, greedy decode at batch 8; prints e2e decode tok/s)")
+    ap.add_argument("--e2e-steps", type=int, default=256)
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run three 1 GiB device-to-device copies (the known-size reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE per dispatch) and exit")
@@ -173,6 +230,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "e2e":
+        run_e2e(args)
+        return
     if args.pmc_calibrate:
         n = 1 << 30
         src = torch.full((n // 4,), 7, dtype=torch.int32, device=dev)

@@ -116,6 +116,58 @@ class LatentCache:
                            scale2_stride_b=sc2.stride(0) if sc2 is not None else 0,
                            scale2_stride_h=sc2.stride(1) if sc2 is not None else 0)
 
+    # ---- stored values back in the act dtype (torch; prefill and reference paths)
+    def _unpack_nibbles(self, packed: torch.Tensor, r: int) -> torch.Tensor:
+        p = packed.to(torch.int16)
+        n = torch.stack([p & 0xF, (p >> 4) & 0xF], dim=-1).flatten(-2)[..., :r]
+        return n
+
+    def dequant_k(self, length: Optional[int] = None) -> List[torch.Tensor]:
+        """Per KV head the first ``length`` positions [B, S, r_h] in the act
+        dtype, rounded once from the exact products as the kernels do."""
+        S = self.length if length is None else int(length)
+        B, C = self.B, self.cap
+        out = []
+        k = self._k
+        for h, r in enumerate(self.ranks):
+            if self.fmt == "dense":
+                o = k["head_offset"][h]
+                out.append(self.k_data[:, o:o + C * r].view(B, C, r)[:, :S])
+            elif self.fmt == "int8_g64":
+                o = k["head_offset"][h]
+                q = self.k_data[:, o:o + C * r].view(B, C, r)[:, :S].double()
+                out.append((q * self.k_scale[:, h, :S, None].double()).to(self.dtype))
+            else:
+                up = min(r, k["split"])
+                o1, p1 = k["head_offset"][h], k["pos_stride"][h]
+                q = self.k_data[:, o1:o1 + C * p1].view(B, C, p1)[:, :S, :up].double()
+                parts = [q * self.k_scale[:, h, :S, None].double()]
+                if r > up:
+                    o2, p2 = k["head_offset2"][h], k["pos_stride2"][h]
+                    n = self._unpack_nibbles(self.k_data2[:, o2:o2 + C * p2].view(B, C, p2)[:, :S], r - up)
+                    parts.append((n.double() - 8) * self.k_scale2[:, h, :S, None].double())
+                out.append(torch.cat(parts, -1).to(self.dtype))
+        return out
+
+    def dequant_v(self, length: Optional[int] = None) -> torch.Tensor:
+        """The first ``length`` positions of V [B, S, Rv] in the act dtype."""
+        S = self.length if length is None else int(length)
+        if self.fmt == "dense":
+            return self.v_data[:, :S]
+        if self.fmt == "int8_g64":
+            n = self._unpack_nibbles(self.v_data[:, :S], self.Rv).double()
+            G = self.v_scale.shape[-1]
+            s = self.v_scale[:, :S].double().repeat_interleave(64, -1)[..., :self.Rv]
+            z = self.v_zero[:, :S].double().repeat_interleave(64, -1)[..., :self.Rv]
+            assert G * 64 >= self.Rv
+            return (n * s + z).to(self.dtype)
+        up = self.v_data.shape[-1]
+        parts = [self.v_data[:, :S].double() * self.v_scale[:, :S].double()]
+        if self.Rv > up:
+            n = self._unpack_nibbles(self.v_data2[:, :S], self.Rv - up).double()
+            parts.append((n - 8) * self.v_scale2[:, :S].double())
+        return torch.cat(parts, -1).to(self.dtype)
+
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor):
         """Write T new positions (k_new [B, Hkv, T, r_max], v_new [B, T, Rv]) in
         place; returns (K spec, V spec, length) for the attention kernels."""

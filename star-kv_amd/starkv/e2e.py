@@ -1,0 +1,195 @@
+"""End-to-end decode over STAR-KV latent caches (the counterpart of the
+reference's ``latency.py --mode e2e``, latency.py:69-154).
+
+A Llama-shaped ``LlamaForCausalLM`` (transformers) whose every attention is
+``LatentAttention``: latent K and V projections (ragged K ranks per KV head,
+one V latent per layer), a static ``LatentCache`` written in place by the HIP
+cache writer (quantised on the fly), decode on ``starkv_decode_attention``,
+and prefill by causal SDPA over the cache's dequantised latents projected back
+to K and V (the reference materialises K and V the same way, model.py:429-449).
+
+The reference's e2e path replaces the attentions of a trained, exported model
+(model.py:547-585) and grows its caches with ``torch.cat``
+(HF:cache_utils.py:144-145); weights here are random (no checkpoints), and
+HF's own cache is unused (``use_cache=False``): each layer owns its latent
+cache and takes positions from it.
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Sequence
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .cache import LatentCache
+from .ops import decode_attention
+from .rope import RopeConfig
+
+__all__ = ["LatentAttention", "build_model", "generate"]
+
+HEAD_DIM = 128
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class LatentAttention(nn.Module):
+    """One attention layer over a static latent cache.
+
+    Weights: ``q_proj``/``o_proj`` as HF; ``k_vs`` [sum(r), hidden] (the latent K
+    projection, heads back to back), ``bk`` [Hkv, r_max, 128] (B_k = k_u^T, rows
+    past r_h unused), ``v_vs`` [Rv, hidden], ``v_u`` [Hkv*128, Rv] (U_v).
+
+    ``reference = True`` runs decode steps through the torch path (dequantised
+    cache, fp32 SDPA) -- the parity reference of the kernel path; prefill takes
+    the same (fp16 SDPA) path in both modes."""
+
+    def __init__(self, config, layer_idx: int, ranks: Sequence[int], v_rank: int, batch: int, capacity: int,
+                 fmt: str = "int8_g64", device="cuda", dtype=torch.float16):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.n_heads = config.num_attention_heads
+        self.n_kv = config.num_key_value_heads
+        if config.hidden_size // self.n_heads != HEAD_DIM or len(ranks) != self.n_kv:
+            raise ValueError("LatentAttention needs head_dim 128 and one rank per KV head")
+        self.ranks = [int(r) for r in ranks]
+        self.rmax = max(self.ranks)
+        hs = config.hidden_size
+        kw = dict(device=device, dtype=dtype)
+        self.q_proj = nn.Linear(hs, self.n_heads * HEAD_DIM, bias=False, **kw)
+        self.o_proj = nn.Linear(self.n_heads * HEAD_DIM, hs, bias=False, **kw)
+        self.k_vs = nn.Linear(hs, sum(self.ranks), bias=False, **kw)
+        self.v_vs = nn.Linear(hs, v_rank, bias=False, **kw)
+        self.v_u = nn.Linear(v_rank, self.n_kv * HEAD_DIM, bias=False, **kw)
+        self.register_buffer("bk", torch.zeros(self.n_kv, self.rmax, HEAD_DIM, **kw))
+        # scatter map: latent channel j of head h -> column h * r_max + (j - offset_h)
+        idx = []
+        for h, r in enumerate(self.ranks):
+            idx.extend(h * self.rmax + i for i in range(r))
+        self.register_buffer("k_scatter", torch.tensor(idx, device=device, dtype=torch.long), persistent=False)
+        self.cache = LatentCache(batch, self.ranks, v_rank, capacity, dtype, device, fmt=fmt)
+        self.rope = RopeConfig.from_hf_config(config)
+        self.scaling = HEAD_DIM ** -0.5
+        self.reference = False
+        self.events: Optional[list] = None     # (start, end) CUDA events of the decode kernels, when set
+
+    def reset_parameters_(self, gen: Optional[torch.Generator] = None, std: float = 0.02):
+        """Random weights of the scales a trained STAR-KV layer has: N(0, std)
+        projections, B_k rows N(0, 1/r_h), U_v N(0, 1/Rv)."""
+        for lin in (self.q_proj, self.o_proj, self.k_vs, self.v_vs):
+            lin.weight.data.normal_(0.0, std, generator=gen)
+        self.v_u.weight.data.normal_(0.0, 1.0 / math.sqrt(self.v_u.weight.shape[1]), generator=gen)
+        self.bk.zero_()
+        for h, r in enumerate(self.ranks):
+            self.bk[h, :r].normal_(0.0, 1.0 / math.sqrt(r), generator=gen)
+
+    def _attend_torch(self, q: torch.Tensor, S: int, T: int) -> torch.Tensor:
+        """q [B, Hq, T, 128] (rotated) against positions [0, S) of the cache."""
+        B = q.shape[0]
+        gs = self.n_heads // self.n_kv
+        xk = self.cache.dequant_k(S)
+        cos, sin = self.rope.cos_sin(torch.arange(S, device=q.device))
+        ks = []
+        for h in range(self.n_kv):
+            kh = torch.matmul(xk[h], self.bk[h, :self.ranks[h]].contiguous())      # [B, S, 128]
+            ks.append(kh * cos.to(kh.dtype) + _rotate_half(kh) * sin.to(kh.dtype))
+        K = torch.stack(ks, 1)                                                      # [B, Hkv, S, 128]
+        V = F.linear(self.cache.dequant_v(S), self.v_u.weight).view(B, S, self.n_kv, HEAD_DIM).transpose(1, 2)
+        K = K.repeat_interleave(gs, 1)
+        V = V.repeat_interleave(gs, 1)
+        if self.reference and T == 1:
+            qf, Kf, Vf = q.float(), K.float().contiguous(), V.float().contiguous()
+        else:
+            qf, Kf, Vf = q, K.contiguous(), V.contiguous()
+        if T == 1:
+            o = F.scaled_dot_product_attention(qf, Kf, Vf, scale=self.scaling)
+        elif T == S:
+            o = F.scaled_dot_product_attention(qf, Kf, Vf, is_causal=True, scale=self.scaling)
+        else:
+            m = torch.ones(T, S, dtype=torch.bool, device=q.device).tril(S - T)
+            o = F.scaled_dot_product_attention(qf, Kf, Vf, attn_mask=m, scale=self.scaling)
+        return o.to(q.dtype)
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None, past_key_values=None,
+                use_cache=False, position_embeddings=None, **kwargs):
+        B, T, _ = hidden_states.shape
+        q = self.q_proj(hidden_states).view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2)
+        cos, sin = position_embeddings
+        q = q * cos.unsqueeze(1) + _rotate_half(q) * sin.unsqueeze(1)
+        kl = self.k_vs(hidden_states)
+        k_new = torch.zeros(B, T, self.n_kv * self.rmax, dtype=kl.dtype, device=kl.device)
+        k_new.index_copy_(2, self.k_scatter, kl)
+        k_new = k_new.view(B, T, self.n_kv, self.rmax).permute(0, 2, 1, 3)       # [B, Hkv, T, r_max]
+        kspec, vspec, S = self.cache.append(k_new, self.v_vs(hidden_states), self.bk)
+        if T == 1 and not self.reference:
+            if self.events is not None:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope, seq_len=S,
+                                 scale=self.scaling)
+            if self.events is not None:
+                e1.record()
+                self.events.append((e0, e1))
+            o = o.unsqueeze(1)                                                      # [B, 1, Hq, 128]
+        else:
+            o = self._attend_torch(q, S, T).transpose(1, 2)                         # [B, T, Hq, 128]
+        return self.o_proj(o.reshape(B, T, self.n_heads * HEAD_DIM)), None
+
+
+def build_model(n_layers: int, hidden: int, heads: int, kv_heads: int, intermediate: int, vocab: int,
+                ranks: Sequence[int], v_rank: int, batch: int, capacity: int, fmt: str = "int8_g64",
+                seed: int = 0, device="cuda", dtype=torch.float16):
+    """Random-init LlamaForCausalLM with every attention replaced by LatentAttention."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=intermediate,
+                      num_hidden_layers=n_layers, num_attention_heads=heads, num_key_value_heads=kv_heads,
+                      max_position_embeddings=max(4096, capacity), tie_word_embeddings=False)
+    torch.manual_seed(seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        with torch.device(device):
+            model = LlamaForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model.eval()
+    gen = torch.Generator(device=device).manual_seed(seed + 1)
+    for i, layer in enumerate(model.model.layers):
+        att = LatentAttention(cfg, i, ranks, v_rank, batch, capacity, fmt=fmt, device=device, dtype=dtype)
+        att.reset_parameters_(gen)
+        layer.self_attn = att
+    return model
+
+
+def attention_layers(model) -> List[LatentAttention]:
+    return [layer.self_attn for layer in model.model.layers]
+
+
+@torch.no_grad()
+def generate(model, prompt: torch.Tensor, steps: int, reference: bool = False,
+             forced: Optional[torch.Tensor] = None):
+    """Greedy decoding: prefill ``prompt`` [B, P] (one forward), then ``steps``
+    single-token decode forwards.  ``forced`` [B, steps] feeds given tokens
+    instead of the argmax (teacher forcing, for comparing two runs).
+    Returns (tokens [B, steps + 1], logits of the last position per forward)."""
+    for att in attention_layers(model):
+        att.reference = reference
+    B, P = prompt.shape
+    dev = prompt.device
+    out = model(input_ids=prompt, position_ids=torch.arange(P, device=dev)[None].expand(B, P),
+                use_cache=False, logits_to_keep=1)
+    logits = [out.logits[:, -1].float()]
+    tok = logits[-1].argmax(-1, keepdim=True)
+    toks = [tok]
+    for t in range(steps):
+        inp = forced[:, t:t + 1] if forced is not None else tok
+        pos = torch.full((B, 1), P + t, device=dev, dtype=torch.long)
+        out = model(input_ids=inp, position_ids=pos, use_cache=False, logits_to_keep=1)
+        logits.append(out.logits[:, -1].float())
+        tok = logits[-1].argmax(-1, keepdim=True)
+        toks.append(tok)
+    return torch.cat(toks, 1), logits
