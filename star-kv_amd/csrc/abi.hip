@@ -122,15 +122,25 @@ int validate_klayout(const starkv_klatent& k, int dtype) {
 // 4 waves (4-item waves).
 // Warp-specialised K-logit kernel: dense latents with 16-byte aligned rows
 // (ranks a multiple of 8); q and B_k are read element-wise there.
+// Warp-specialised K-logit kernel: dense latents with 16-byte aligned rows
+// (ranks a multiple of 8), or int8 latents with one scale per (b, h, s) whose
+// rows start on 16-byte boundaries (pitch a multiple of 16 bytes, so the 16-byte
+// DMA pieces never straddle rows); q and B_k are read element-wise there.
 bool k_ws(const starkv_klatent& k, int dtype) {
-  if (k.format != STARKV_FMT_DENSE) return false;
-  const int xe = esize(dtype);
+  const bool i8 = k.format == STARKV_FMT_INT8_SYM;
+  if (k.format != STARKV_FMT_DENSE && !i8) return false;
+  const int xe = i8 ? 1 : esize(dtype);
   if (!al(k.data, 16) || !al64(k.stride_b * xe, 16)) return false;
   for (int h = 0; h < k.n_kv_heads; ++h) {
     if (k.rank[h] % 8) return false;
     if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
   }
   return true;
+}
+
+// 16-byte LDS chunks of one 32-position tile row of a head in that kernel
+int ws_row_chunks(const starkv_klatent& k, int h) {
+  return k.format == STARKV_FMT_INT8_SYM ? (int)ceil_div(k.rank[h], 16) : k.rank[h] / 8;
 }
 
 int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, KPlan& plan) {
@@ -229,6 +239,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, K
   a.n_wg = plan.n_wg;
   a.maxi = maxi;
   a.ws = ws;
+  a.ws_i8 = ws && k.format == STARKV_FMT_INT8_SYM;
   a.ws_stage = a.ws_nst = 0;
   if (ws) {
     // stage = the largest workgroup's latent tile (16-byte chunks of its
@@ -243,7 +254,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, K
           const int kv = (it >> 8) & 0xff;
           if (!((it >> 27) & 1) || seen[kv]) continue;
           seen[kv] = true;
-          chunks += 4 * k.rank[kv];
+          chunks += 32 * ws_row_chunks(k, kv);
         }
       max_chunks = std::max(max_chunks, chunks);
     }

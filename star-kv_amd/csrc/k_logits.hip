@@ -86,41 +86,6 @@ struct KBuf {
   uint16_t sq[XFMT == 0 ? 1 : MAXI];  // quantised: fp16 scale bits of the lane's block at that position
 };
 
-typedef _Float16 kh2 __attribute__((ext_vector_type(2)));
-
-// 16 quantised ranks -> 16 fp16 values, bit-exact fp16(n * s): the integer is
-// biased into the fp16 pattern 1024 + n (exact), the bias removed (exact) and
-// one correctly rounded packed-fp16 multiply by the scale.  int8: 16 bytes;
-// int4: 8 bytes (rank 2k in the low nibble of byte k, value nibble - 8).
-__device__ inline void dequant16(uint4 r, bool k8, uint16_t s16, uint4& lo, uint4& hi) {
-  uint32_t pr[8];
-  _Float16 bias;
-  if (k8) {
-    const uint32_t w[4] = {r.x ^ 0x80808080u, r.y ^ 0x80808080u, r.z ^ 0x80808080u, r.w ^ 0x80808080u};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      pr[2 * k] = (w[k] & 0xFFu) | ((w[k] << 8) & 0xFF0000u);
-      pr[2 * k + 1] = ((w[k] >> 16) & 0xFFu) | ((w[k] >> 8) & 0xFF0000u);
-    }
-    bias = (_Float16)-1152.0f;
-  } else {
-    const uint32_t w[2] = {r.x, r.y};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t u = w[k >> 2] >> (8 * (k & 3));
-      pr[k] = (u & 0xFu) | (((u >> 4) & 0xFu) << 16);
-    }
-    bias = (_Float16)-1032.0f;
-  }
-  const kh2 s = __builtin_bit_cast(kh2, (uint32_t)s16 * 0x10001u), b2 = {bias, bias};
-  uint32_t o[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    o[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(kh2, pr[k] | 0x64006400u) + b2) * s);
-  lo = make_uint4(o[0], o[1], o[2], o[3]);
-  hi = make_uint4(o[4], o[5], o[6], o[7]);
-}
-
 // XFMT: 0 = dense act dtype, 1 = quantised blocks (int8 / int4 with per-(b,kv,s)
 //       fp16 scales, dequantised to fp16 before the dot)
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits

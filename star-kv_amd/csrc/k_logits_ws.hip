@@ -58,6 +58,9 @@ __device__ inline int ws_shift(int row, int n16) {
   return row / (8 / g);
 }
 
+// 16-byte chunks of one staged row: fp16/bf16 2r bytes, int8 r bytes rounded up
+template <bool XI8> __device__ inline int ws_n16(int r) { return XI8 ? (r + 15) >> 4 : r >> 3; }
+
 // s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31]
 template <int N> __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
@@ -98,7 +101,9 @@ __device__ inline float dot16b(uint4 u0, uint4 u1, const floatx16& acc) {
 }  // namespace
 
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
-template <typename XT, int OUTK>
+// XI8: int8 latents (rows padded to 16 bytes) with one fp16 scale per (b, h, s),
+//      dequantised bit-exactly to fp16 after the LDS read
+template <typename XT, int OUTK, bool XI8>
 __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logits_ws_kernel(const KArgs a) {
   constexpr int MAXI = 2;                            // items per consumer wave
   __shared__ __attribute__((aligned(16))) char ring[WS_RING];   // a.ws_nst stages of a.ws_stage bytes
@@ -138,7 +143,7 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
 #pragma unroll
       for (int k = 0; k < WS_MAXH; ++k)
         if (k == nh) { hkv[k] = kv; hrank[k] = r; hoff[k] = tot; }
-      tot += 4 * r;                         // 16-byte chunks per 32-row tile: 32 * 2r / 16
+      tot += 32 * ws_n16<XI8>(r);           // 16-byte chunks per 32-row tile
       ++nh;
     }
   }
@@ -176,11 +181,12 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
 #pragma unroll
       for (int j = 1; j < WS_MAXH; ++j)
         if (hoff[j] <= q) { hb = hoff[j]; hr = hrank[j]; hk = hkv[j]; }
-      const int n16 = hr / 8, loc = q - hb;
+      const int n16 = ws_n16<XI8>(hr), loc = q - hb;
       const int row = loc / n16, cr = loc % n16;             // stored (rotated) chunk cr of row
       const int c = (cr - ws_shift(row, n16) % n16 + n16) % n16;   // the row's chunk that lives there
-      src[k] = (const char*)a.x + (b * a.x_sb + a.xoff[hk]) * 2 + (int64_t)c * 16;
-      adv[k] = (int64_t)a.xpitch[hk] * 2;
+      constexpr int XE = XI8 ? 1 : 2;        // quantised offsets are in bytes
+      src[k] = (const char*)a.x + (b * a.x_sb + a.xoff[hk]) * XE + (int64_t)c * 16;
+      adv[k] = (int64_t)a.xpitch[hk] * XE;
       rowpos[k] = row;
       dst[k] = m * 1024;
     }
@@ -247,24 +253,41 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       wr[i][k] = w;
     }
   }
-  // LDS byte offsets (within a stage) of this lane's two 16-byte chunks of each item's row t
+  // LDS byte offsets (within a stage) of this lane's 16 ranks of each item's
+  // row t: two 16-byte chunks (fp16/bf16) or one (int8); lanes past the valid
+  // ranks re-read valid data (multiplied by the zero rows of W)
   int xo0[MAXI], xo1[MAXI];
+  const uint16_t* scb[MAXI];                 // int8: this item's scale row (b, kv)
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     xo0[i] = xo1[i] = 0;
+    scb[i] = (const uint16_t*)a.xscale;
     if (!item_valid(it[i])) continue;
     const int kv = item_kv(it[i]), mt = item_mt(it[i]), nvh = item_nv(it[i]) - 16 * hh;
     int hb = 0, hr = 8;
 #pragma unroll
     for (int j = 0; j < WS_MAXH; ++j)
       if (hkv[j] == kv) { hb = hoff[j]; hr = hrank[j]; }
-    const int n16 = hr / 8;
-    const int c0 = nvh > 0 ? mt * 4 + 2 * hh : mt * 4;        // lanes past the valid ranks re-read valid data
-    const int c1 = nvh > 8 ? c0 + 1 : c0;                    // (multiplied by the zero rows of W)
+    const int n16 = ws_n16<XI8>(hr);
     const int rowb = (hb + t * n16) * 16;
     const int sh = ws_shift(t, n16);
-    xo0[i] = rowb + ((c0 + sh) % n16) * 16;
-    xo1[i] = rowb + ((c1 + sh) % n16) * 16;
+    if constexpr (XI8) {
+      const int c0 = nvh > 0 ? mt * 2 + hh : mt * 2;
+      xo0[i] = xo1[i] = rowb + ((c0 + sh) % n16) * 16;
+      scb[i] = (const uint16_t*)a.xscale + b * a.xs_sb + (int64_t)kv * a.xs_sh;
+    } else {
+      const int c0 = nvh > 0 ? mt * 4 + 2 * hh : mt * 4;
+      const int c1 = nvh > 8 ? c0 + 1 : c0;
+      xo0[i] = rowb + ((c0 + sh) % n16) * 16;
+      xo1[i] = rowb + ((c1 + sh) % n16) * 16;
+    }
+  }
+  // int8: this lane's scales of the current and the next tile (loaded one tile ahead)
+  uint16_t sc_cur[MAXI], sc_nxt[MAXI];
+#pragma unroll
+  for (int j = 0; j < MAXI; ++j) {
+    sc_cur[j] = sc_nxt[j] = 0;
+    if constexpr (XI8) if (item_valid(it[j])) sc_cur[j] = scb[j][min(tile0 * TILE + t, S - 1)];
   }
   float mx[MAXI];
 #pragma unroll
@@ -298,11 +321,16 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
     for (int k = 0; k < 8; ++k) T[k] = *(const half8*)(st + stage - 8192 + (k * 64 + lane) * 16);
     // both chains every tile (an unused item has zero W rows and reads valid
     // LDS data), interleaved so the MFMA pipe stays busy
+    if constexpr (XI8) {
+#pragma unroll
+      for (int j = 0; j < MAXI; ++j)
+        if (item_valid(it[j])) sc_nxt[j] = scb[j][min((tile0 + i + 1) * TILE + t, S - 1)];
+    }
     uint4 x0[MAXI], x1[MAXI];
 #pragma unroll
     for (int j = 0; j < MAXI; ++j) {
       x0[j] = *(const uint4*)(st + xo0[j]);
-      x1[j] = *(const uint4*)(st + xo1[j]);
+      x1[j] = XI8 ? x0[j] : *(const uint4*)(st + xo1[j]);
     }
     floatx16 acc[MAXI];
 #pragma unroll
@@ -314,8 +342,15 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
     float part = 0.f;
 #pragma unroll
     for (int j = 0; j < MAXI; ++j) {
-      if constexpr (__is_same(XT, _Float16)) part += dot16h(x0[j], x1[j], acc[j]);
-      else part += dot16b(x0[j], x1[j], acc[j]);
+      if constexpr (XI8) {
+        uint4 lo, hi;
+        dequant16(x0[j], true, sc_cur[j], lo, hi);
+        part += dot16h(lo, hi, acc[j]);
+      } else if constexpr (__is_same(XT, _Float16)) {
+        part += dot16h(x0[j], x1[j], acc[j]);
+      } else {
+        part += dot16b(x0[j], x1[j], acc[j]);
+      }
       if (item_last(it[j])) {
         const float v = add_halves(part);
         part = 0.f;
@@ -327,6 +362,8 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       const float v = add_halves(part);
       if (hh == 0) carry[i & 1][bin][t] = v;
     }
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) sc_cur[j] = sc_nxt[j];
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();              // publishes the last tile's partials
@@ -344,18 +381,19 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
   }
 }
 
-template <typename XT>
+template <typename XT, bool XI8>
 static int launch_ws_t(const KArgs& a, int outk, int B, hipStream_t st) {
-  dim3 grid(a.n_chunks, a.n_wg, B);
-  if (outk == 0) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 0>), grid, dim3((WS_CONSUMERS + WS_PRODUCERS) * 64), 0, st, a);
-  else if (outk == 1) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 1>), grid, dim3((WS_CONSUMERS + WS_PRODUCERS) * 64), 0, st, a);
-  else hipLaunchKernelGGL((k_logits_ws_kernel<XT, 2>), grid, dim3((WS_CONSUMERS + WS_PRODUCERS) * 64), 0, st, a);
+  dim3 grid(a.n_chunks, a.n_wg, B), block((WS_CONSUMERS + WS_PRODUCERS) * 64);
+  if (outk == 0) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 0, XI8>), grid, block, 0, st, a);
+  else if (outk == 1) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 1, XI8>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((k_logits_ws_kernel<XT, 2, XI8>), grid, block, 0, st, a);
   return (int)hipGetLastError();
 }
 
 int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st) {
   const int outk = out_f32 ? 0 : (out_dtype == STARKV_F16 ? 1 : 2);
-  return dtype == STARKV_F16 ? launch_ws_t<_Float16>(a, outk, B, st) : launch_ws_t<__bf16>(a, outk, B, st);
+  if (a.ws_i8) return dtype == STARKV_F16 ? launch_ws_t<_Float16, true>(a, outk, B, st) : launch_ws_t<__bf16, true>(a, outk, B, st);
+  return dtype == STARKV_F16 ? launch_ws_t<_Float16, false>(a, outk, B, st) : launch_ws_t<__bf16, false>(a, outk, B, st);
 }
 
 }  // namespace starkv

@@ -61,9 +61,11 @@ class LatentCache:
             raise StarKVError("quantised caches need ranks that are multiples of 8")
         self.k_scale = torch.ones(B, Hkv, C, dtype=torch.float16, device=dev)
         if fmt == "int8_g64":
-            offs = [C * sum(self.ranks[:h]) for h in range(Hkv)]
-            self.k_data = torch.zeros(B, C * sum(self.ranks), dtype=torch.int8, device=dev)
-            self._k = dict(data=self.k_data, head_offset=offs, pos_stride=self.ranks, stride_b=self.k_data.stride(0),
+            # rows padded to 16 bytes: the K-logit kernel streams them in 16-byte pieces
+            pitch = [_round(r, 16) for r in self.ranks]
+            offs = [C * sum(pitch[:h]) for h in range(Hkv)]
+            self.k_data = torch.zeros(B, C * sum(pitch), dtype=torch.int8, device=dev)
+            self._k = dict(data=self.k_data, head_offset=offs, pos_stride=pitch, stride_b=self.k_data.stride(0),
                            fmt=FMT_INT8_SYM, scale=self.k_scale)
             G = (self.Rv + 63) // 64
             self.v_data = torch.zeros(B, C, self.Rv // 2, dtype=torch.uint8, device=dev)
@@ -116,6 +118,13 @@ class LatentCache:
                            scale2_stride_b=sc2.stride(0) if sc2 is not None else 0,
                            scale2_stride_h=sc2.stride(1) if sc2 is not None else 0)
 
+    def k_rows(self, h: int) -> torch.Tensor:
+        """Stored K rows of KV head h, [B, capacity, r_h] (the first block of
+        the reference format; the padding of int8 rows excluded)."""
+        k, C, r = self._k, self.cap, self.ranks[h]
+        o, p = k["head_offset"][h], k["pos_stride"][h]
+        return self.k_data[:, o:o + C * p].view(self.B, C, p)[..., :min(r, p)]
+
     # ---- stored values back in the act dtype (torch; prefill and reference paths)
     def _unpack_nibbles(self, packed: torch.Tensor, r: int) -> torch.Tensor:
         p = packed.to(torch.int16)
@@ -134,8 +143,7 @@ class LatentCache:
                 o = k["head_offset"][h]
                 out.append(self.k_data[:, o:o + C * r].view(B, C, r)[:, :S])
             elif self.fmt == "int8_g64":
-                o = k["head_offset"][h]
-                q = self.k_data[:, o:o + C * r].view(B, C, r)[:, :S].double()
+                q = self.k_rows(h)[:, :S].double()
                 out.append((q * self.k_scale[:, h, :S, None].double()).to(self.dtype))
             else:
                 up = min(r, k["split"])

@@ -122,7 +122,7 @@ def test_latent_cache_append_then_decode(fmt):
     if fmt == "int8_g64":
         # stored bytes of head 0 equal the oracle's quantisation of its rows
         q0, s0 = o.quant_int8_sym(np.concatenate(kh, axis=2)[:, 0, :, :ranks[0]])
-        stored = cache.k_data[:, :S * ranks[0]].cpu().numpy().reshape(B, S, ranks[0])
+        stored = cache.k_rows(0)[:, :S].cpu().numpy()
         assert np.array_equal(stored, q0)
         assert np.array_equal(cache.k_scale[:, 0, :S].cpu().numpy().view(np.uint16), s0[..., 0].view(np.uint16))
 
