@@ -183,40 +183,45 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     qg[c] = gcol[c] / 64;
   }
 
+  // Every load of a stage is issued unconditionally from a clamped, in-bounds
+  // address: K-steps past the chunk re-read its last K-step, rows past s_end
+  // its last row and columns past the slab column 0.  Those values reach only
+  // products with P = 0 (positions >= s_end) or discarded output columns, so
+  // nothing is zeroed, and with a fixed number of loads per stage (no branch
+  // in the loop body) the compiler waits for exactly the older stage
+  // (vmcnt(n)) instead of draining every load at the loop head.
   auto load = [&](PVStage<NTW, VQ>& st, int ks) {
-    const int s0 = s_begin + ks * KSTEP;
-    const VT* base = xb + (int64_t)ks * KSTEP * a.x_ss;
-    const bool full = s0 + KSTEP <= s_end;
+    const int kc = min(ks, nks - 1);
+    const int rmax = s_end - 1 - s_begin;                   // last valid row of the chunk
     if constexpr (VQ != VQ_DENSE) {
 #pragma unroll
       for (int c = 0; c < NTW; ++c) {
-        st.q[c] = make_uint2(0, 0);
-        st.s[c] = 0;
-        if constexpr (VQ == VQ_G64) st.z[c] = 0;
-        if (cok[c] && (full || s0 + grow[c] < s_end)) {
-          const int64_t r = (int64_t)ks * KSTEP + grow[c];
-          if constexpr (VQ == VQ_BLOCK) {
-            const uint8_t* p = (qlo[c] ? xq2 + r * a.x2_ss : xq + r * a.x_ss) + qoff[c];
-            if (q8[c]) st.q[c] = *(const uint2*)p;
-            else st.q[c].x = *(const uint32_t*)p;
-            st.s[c] = qlo[c] ? sq2[r * a.xs2_ss] : sq[r * a.xs_ss];
-          } else {
-            st.q[c].x = *(const uint32_t*)(xq + r * a.x_ss + qoff[c]);
-            st.s[c] = sq[r * a.xs_ss + qg[c]];
-            st.z[c] = zq[r * a.xs_ss + qg[c]];
-          }
+        const int64_t r = min(kc * KSTEP + grow[c], rmax);
+        if constexpr (VQ == VQ_BLOCK) {
+          const bool lo = cok[c] && qlo[c];
+          const uint8_t* p = (lo ? xq2 + r * a.x2_ss : xq + r * a.x_ss) + (cok[c] ? qoff[c] : 0);
+          st.q[c].x = *(const uint32_t*)p;
+          st.q[c].y = *(const uint32_t*)(p + (q8[c] ? 4 : 0));
+          st.s[c] = lo ? sq2[r * a.xs2_ss] : sq[r * a.xs_ss];
+        } else {
+          st.q[c].x = *(const uint32_t*)(xq + r * a.x_ss + (cok[c] ? qoff[c] : 0));
+          st.q[c].y = 0;
+          st.s[c] = sq[r * a.xs_ss + (cok[c] ? qg[c] : 0)];
+          st.z[c] = zq[r * a.xs_ss + (cok[c] ? qg[c] : 0)];
         }
       }
     }
 #pragma unroll
     for (int c = 0; c < NTW; ++c) {
       if constexpr (VQ != VQ_DENSE) break;
-      st.r[c] = make_uint4(0, 0, 0, 0);
-      if (cok[c] && (full || s0 + grow[c] < s_end)) {
-        const VT* p = base + goff[c];
-        if (FAST) {
-          st.r[c] = ld_stream16(p);
-        } else {
+      if (FAST) {
+        const int64_t r = min(kc * KSTEP + grow[c], rmax);
+        st.r[c] = ld_stream16(xb + r * a.x_ss + (cok[c] ? gcol[c] : 0));
+      } else {
+        const int s0 = s_begin + ks * KSTEP;
+        st.r[c] = make_uint4(0, 0, 0, 0);
+        if (cok[c] && s0 + grow[c] < s_end) {
+          const VT* p = xb + (int64_t)ks * KSTEP * a.x_ss + goff[c];
           uint16_t tmp[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) tmp[e] = (gcol[c] + e < a.Rv) ? ((const uint16_t*)p)[e] : (uint16_t)0;
@@ -224,21 +229,18 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
         }
       }
     }
-    const int sa = s0 + 8 * hh;
     if constexpr (FUSED) {
-      if (qok) {
-        const float* lp = a.logits + b * a.l_sb + n * a.l_sh + sa;
-        const float4 u = *(const float4*)lp, v = *(const float4*)(lp + 4);
-        st.p[0] = u.x; st.p[1] = u.y; st.p[2] = u.z; st.p[3] = u.w;
-        st.p[4] = v.x; st.p[5] = v.y; st.p[6] = v.z; st.p[7] = v.w;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st.p[e] = 0.f;
-      }
+      // rows past H read row H-1; the logits buffer holds S_pad >= s_end + 8 columns
+      const int sa = s_begin + kc * KSTEP + 8 * hh;
+      const float* lp = a.logits + b * a.l_sb + min(n, H - 1) * a.l_sh + sa;
+      const float4 u = *(const float4*)lp, v = *(const float4*)(lp + 4);
+      st.p[0] = u.x; st.p[1] = u.y; st.p[2] = u.z; st.p[3] = u.w;
+      st.p[4] = v.x; st.p[5] = v.y; st.p[6] = v.z; st.p[7] = v.w;
     } else {
+      const int sa = s_begin + ks * KSTEP + 8 * hh;
       const VT* pp = (const VT*)a.p + b * a.p_sb + n * a.p_sh + sa;
       st.praw = make_uint4(0, 0, 0, 0);
-      if (qok) {
+      if (qok && ks < nks) {
         if (a.p_vec && sa + 8 <= s_end) {
           st.praw = *(const uint4*)pp;
         } else {
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     } else {
       praw = st.praw;
     }
-    if (ks + 2 < nks) load(st, ks + 2);
+    load(st, ks + 2);                       // clamped past the chunk
 
     const int sa = s_begin + ks * KSTEP + 8 * hh;
     float pv[8];
@@ -327,13 +329,14 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     }
   };
 
-  if (nvt > 0) {
+  if (nvt > 0 && nks > 0) {
+    // K-steps in pairs; an odd chunk's last pair computes one K-step past the
+    // chunk with P = 0 (no branch in the loop body)
     PVStage<NTW, VQ> st0, st1;
-    if (nks > 0) load(st0, 0);
-    if (nks > 1) load(st1, 1);
+    load(st0, 0);
+    load(st1, 1);
     for (int ks = 0; ks < nks; ks += 2) {
       compute(st0, ks, 0);
-      if (ks + 1 >= nks) break;
       compute(st1, ks + 1, 1);
     }
   }
