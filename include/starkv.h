@@ -86,7 +86,12 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
  * dequantise-then-multiply path does, LlamaLoRaAttention_headwise_quant.py:
  * 137-144):
  *   INT8_SYM  all ranks int8 in data, x = q * s, fp16 scale per (b,h,s) at
- *             scale + b*scale_stride_b + h*scale_stride_h + s;
+ *             scale + b*scale_stride_b + h*scale_stride_h + s.  Fastest
+ *             layout (LatentCache's): 16-byte aligned data, rows and
+ *             offsets; 16-byte aligned scale, scale strides multiples of 8
+ *             and scale_stride_h >= round_up(seq_len, 8) -- each scale row
+ *             is then read in 8-position pieces through round_up(seq_len, 8)
+ *             (values past seq_len are ignored);
  *   INT4_REF  split == 0: all ranks int4 nibbles in data (rank 2k low nibble
  *             of byte k, x = (nibble - 8) * s), scale as above;
  *             split > 0 (multiple of 16): ranks [0, split) in data (int8 when

@@ -126,11 +126,17 @@ int validate_klayout(const starkv_klatent& k, int dtype) {
 // (ranks a multiple of 8), or int8 latents with one scale per (b, h, s) whose
 // rows start on 16-byte boundaries (pitch a multiple of 16 bytes, so the 16-byte
 // DMA pieces never straddle rows); q and B_k are read element-wise there.
-bool k_ws(const starkv_klatent& k, int dtype) {
+bool k_ws(const starkv_klatent& k, int dtype, int S) {
   const bool i8 = k.format == STARKV_FMT_INT8_SYM;
   if (k.format != STARKV_FMT_DENSE && !i8) return false;
   const int xe = i8 ? 1 : esize(dtype);
   if (!al(k.data, 16) || !al64(k.stride_b * xe, 16)) return false;
+  // int8: the scales of a tile are staged in 16-byte pieces (8 positions), so
+  // each (b, h) scale row is read up to position round_up(S, 8) - 1, inside
+  // its pitch
+  if (i8 && (!al(k.scale, 16) || !al64(k.scale_stride_b * 2, 16) || !al64(k.scale_stride_h * 2, 16) ||
+             k.scale_stride_h < round_up(S, 8)))
+    return false;
   for (int h = 0; h < k.n_kv_heads; ++h) {
     if (k.rank[h] % 8) return false;
     if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
@@ -143,7 +149,7 @@ int ws_row_chunks(const starkv_klatent& k, int h) {
   return k.format == STARKV_FMT_INT8_SYM ? (int)ceil_div(k.rank[h], 16) : k.rank[h] / 8;
 }
 
-int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, KPlan& plan) {
+int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArgs& a, KPlan& plan) {
   struct QH { int qh, kv, ni; };
   std::vector<QH> heads;
   int max_ni = 1;
@@ -153,7 +159,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, K
     max_ni = std::max(max_ni, ni);
     heads.push_back({qh, kv, ni});
   }
-  const bool ws = k_ws(k, dtype);
+  const bool ws = k_ws(k, dtype, S);
   const int maxi = ws || max_ni > 2 ? 4 : 2;   // whole heads per (consumer) wave
   const int nw = maxi == 2 ? 8 : 4;
   // Bins of up to maxi items (whole query heads), first-fit decreasing.  With
@@ -243,7 +249,8 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, K
   a.ws_stage = a.ws_nst = 0;
   if (ws) {
     // stage = the largest workgroup's latent tile (16-byte chunks of its
-    // distinct KV heads, whole 1 KB DMA pieces) + the 8 KB RoPE operand
+    // distinct KV heads, whole 1 KB DMA pieces) [+ 1 KB of int8 scales:
+    // 32 positions of up to 16 heads] + the 8 KB RoPE operand
     int max_chunks = 0;
     for (int g = 0; g < plan.n_wg; ++g) {
       bool seen[K_MAX_KV] = {};
@@ -258,7 +265,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, KArgs& a, K
         }
       max_chunks = std::max(max_chunks, chunks);
     }
-    a.ws_stage = (int)round_up(max_chunks, 64) * 16 + 8192;
+    a.ws_stage = (int)round_up(max_chunks, 64) * 16 + 8192 + (a.ws_i8 ? 1024 : 0);
     a.ws_nst = std::min(4, K1_WS_RING_BYTES / a.ws_stage);
   }
   return STARKV_OK;
@@ -422,7 +429,7 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
   if (d->out_dtype != 0 && d->out_dtype != d->dtype && d->out_dtype != STARKV_F32) return STARKV_ERR_DTYPE;
   KArgs tmp;
   KPlan plan;
-  if ((st = build_k_plan(d->k, d->n_q_heads, *gs, d->dtype, tmp, plan))) return st;
+  if ((st = build_k_plan(d->k, d->n_q_heads, *gs, d->dtype, d->seq_len, tmp, plan))) return st;
   *n_wg = plan.n_wg;
   return STARKV_OK;
 }
@@ -478,7 +485,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   if ((st = check_mask(d->mask, d->mask_dtype))) return st;
   KArgs a;
   KPlan plan;
-  if ((st = build_k_plan(d->k, d->n_q_heads, gs, d->dtype, a, plan))) return st;
+  if ((st = build_k_plan(d->k, d->n_q_heads, gs, d->dtype, d->seq_len, a, plan))) return st;
   a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h;
   a.x = d->k.data; a.x_sb = d->k.stride_b;
   a.xscale = d->k.scale; a.xs_sb = d->k.scale_stride_b; a.xs_sh = d->k.scale_stride_h;
@@ -547,7 +554,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
 
   KArgs ka;
   KPlan plan;
-  if ((st = build_k_plan(d->k, Hq, gs, d->dtype, ka, plan))) return st;
+  if ((st = build_k_plan(d->k, Hq, gs, d->dtype, d->seq_len, ka, plan))) return st;
   ka.q = d->q; ka.q_sb = d->q_stride_b; ka.q_sh = d->q_stride_h;
   ka.x = d->k.data; ka.x_sb = d->k.stride_b;
   ka.xscale = d->k.scale; ka.xs_sb = d->k.scale_stride_b; ka.xs_sh = d->k.scale_stride_h;

@@ -43,7 +43,7 @@ constexpr int WS_PRODUCERS = 4;
 constexpr int WS_CONSUMERS = 8;
 constexpr int WS_BINS = 4;                          // item bins (of up to 4 items) per workgroup
 constexpr int WS_RING = K1_WS_RING_BYTES;           // LDS ring (the straddle carry takes the rest of the 160 KB)
-constexpr int WS_MAXK = (2048 / 64 + 8 + WS_PRODUCERS - 1) / WS_PRODUCERS;   // DMA instructions per producer per tile
+constexpr int WS_MAXK = (2048 / 64 + 9 + WS_PRODUCERS - 1) / WS_PRODUCERS;   // DMA instructions per producer per tile
 constexpr int WS_MAXH = 16;                        // KV heads staged by one workgroup
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -102,7 +102,9 @@ __device__ inline float dot16b(uint4 u0, uint4 u1, const floatx16& acc) {
 
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
 // XI8: int8 latents (rows padded to 16 bytes) with one fp16 scale per (b, h, s),
-//      dequantised bit-exactly to fp16 after the LDS read
+//      dequantised bit-exactly to fp16 after the LDS read; the tile's scales
+//      are staged with its rows (one more DMA instruction), so the consumers
+//      issue no global loads
 template <typename XT, int OUTK, bool XI8>
 __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logits_ws_kernel(const KArgs a) {
   constexpr int MAXI = 2;                            // items per consumer wave
@@ -147,28 +149,49 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       ++nh;
     }
   }
-  // stage: latent chunks [0, 64 * nX) then the RoPE operand in the last 8 KB
+  // stage: latent chunks [0, 64 * nX), int8: the tile's scales in the 1 KB
+  // before the RoPE operand (64 bytes per head slot), the RoPE operand in the
+  // last 8 KB
   const int nX = (tot + 63) / 64, stage = a.ws_stage, nst = a.ws_nst;
-  if (tot == 0 || nX * 1024 + 8192 > stage || nst < 2 || nst * stage > WS_RING) return;   // uniform
+  constexpr int SCB = XI8 ? 1024 : 0;
+  const int sc_off = stage - 8192 - SCB;
+  if (tot == 0 || nX * 1024 + SCB + 8192 > stage || nst < 2 || nst * stage > WS_RING) return;   // uniform
 
   if (wave >= WS_CONSUMERS) {
     // ================= producer =================
     const int pw = wave - WS_CONSUMERS;
     // DMA instruction m (latent chunks [64m, 64m+64) for m < nX, then the
-    // RoPE operand in 1 KB pieces) belongs to producer m % 4.  Per
-    // instruction k of this wave: the lane's source and stage offset.
-    const int nI = nX + 8, ahead = nst - 1;
+    // RoPE operand in 1 KB pieces, then (int8) the scales) belongs to
+    // producer m % 4.  Per instruction k of this wave: the lane's source and
+    // stage offset; it reads position min(tile * tmul + rowpos, pmax).
+    const int nI = nX + 8 + (XI8 ? 1 : 0), ahead = nst - 1;
     const char* src[WS_MAXK];
-    int64_t adv[WS_MAXK];   // latent: bytes per position of the head; RoPE: bytes per tile
-    int rowpos[WS_MAXK];    // latent: row within the tile
+    int64_t adv[WS_MAXK];   // latent / scales: bytes per position; RoPE: bytes per tile
+    int rowpos[WS_MAXK];    // latent: row within the tile; scales: first of the lane's 8 positions
+    int tmul[WS_MAXK];      // positions per tile (RoPE: 1, indexed by tile)
+    int pmax[WS_MAXK];      // last position that may be read
     int dst[WS_MAXK];       // wave-uniform stage offset
     int cnt = 0;
 #pragma unroll
     for (int k = 0; k < WS_MAXK; ++k) {
       const int m = pw + WS_PRODUCERS * k;
-      src[k] = (const char*)a.rope; adv[k] = 8192; rowpos[k] = 0; dst[k] = 0;
+      src[k] = (const char*)a.rope; adv[k] = 8192; rowpos[k] = 0; tmul[k] = 1; pmax[k] = 1 << 30; dst[k] = 0;
       if (m >= nI) continue;
       ++cnt;
+      if (XI8 && m == nX + 8) {
+        // lane = 4 * head slot + piece: 16 bytes = the scales of 8 positions;
+        // pieces past the tile's last position re-read the row's last piece
+        // (the host checked that each row is readable through round_up(S, 8))
+        const int hs = lane >> 2;
+        int hk = hkv[0];
+#pragma unroll
+        for (int j = 1; j < WS_MAXH; ++j)
+          if (j == hs && j < nh) hk = hkv[j];
+        src[k] = (const char*)a.xscale + (b * a.xs_sb + hk * a.xs_sh) * 2;
+        adv[k] = 2; rowpos[k] = 8 * (lane & 3); tmul[k] = TILE; pmax[k] = ((S - 1) >> 3) << 3;
+        dst[k] = sc_off;
+        continue;
+      }
       if (m >= nX) {
         const int j = m - nX;
         src[k] = (const char*)a.rope + (j * 64 + lane) * 16;
@@ -188,6 +211,8 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       src[k] = (const char*)a.x + (b * a.x_sb + a.xoff[hk]) * XE + (int64_t)c * 16;
       adv[k] = (int64_t)a.xpitch[hk] * XE;
       rowpos[k] = row;
+      tmul[k] = TILE;
+      pmax[k] = S - 1;
       dst[k] = m * 1024;
     }
     auto issue = [&](int i) __attribute__((always_inline)) {
@@ -197,7 +222,7 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       for (int k = 0; k < WS_MAXK; ++k) {
         const int m = pw + WS_PRODUCERS * k;
         if (m >= nI) break;
-        const int64_t pos = m < nX ? min(tl * TILE + rowpos[k], S - 1) : tl;
+        const int64_t pos = min(tl * tmul[k] + rowpos[k], pmax[k]);
         __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
       }
     };
@@ -257,37 +282,30 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
   // row t: two 16-byte chunks (fp16/bf16) or one (int8); lanes past the valid
   // ranks re-read valid data (multiplied by the zero rows of W)
   int xo0[MAXI], xo1[MAXI];
-  const uint16_t* scb[MAXI];                 // int8: this item's scale row (b, kv)
+  int sco[MAXI];                             // int8: this lane's scale (position t of the item's head)
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     xo0[i] = xo1[i] = 0;
-    scb[i] = (const uint16_t*)a.xscale;
+    sco[i] = sc_off;
     if (!item_valid(it[i])) continue;
     const int kv = item_kv(it[i]), mt = item_mt(it[i]), nvh = item_nv(it[i]) - 16 * hh;
-    int hb = 0, hr = 8;
+    int hb = 0, hr = 8, hs = 0;
 #pragma unroll
     for (int j = 0; j < WS_MAXH; ++j)
-      if (hkv[j] == kv) { hb = hoff[j]; hr = hrank[j]; }
+      if (hkv[j] == kv) { hb = hoff[j]; hr = hrank[j]; hs = j; }
+    sco[i] = sc_off + hs * 64 + t * 2;
     const int n16 = ws_n16<XI8>(hr);
     const int rowb = (hb + t * n16) * 16;
     const int sh = ws_shift(t, n16);
     if constexpr (XI8) {
       const int c0 = nvh > 0 ? mt * 2 + hh : mt * 2;
       xo0[i] = xo1[i] = rowb + ((c0 + sh) % n16) * 16;
-      scb[i] = (const uint16_t*)a.xscale + b * a.xs_sb + (int64_t)kv * a.xs_sh;
     } else {
       const int c0 = nvh > 0 ? mt * 4 + 2 * hh : mt * 4;
       const int c1 = nvh > 8 ? c0 + 1 : c0;
       xo0[i] = rowb + ((c0 + sh) % n16) * 16;
       xo1[i] = rowb + ((c1 + sh) % n16) * 16;
     }
-  }
-  // int8: this lane's scales of the current and the next tile (loaded one tile ahead)
-  uint16_t sc_cur[MAXI], sc_nxt[MAXI];
-#pragma unroll
-  for (int j = 0; j < MAXI; ++j) {
-    sc_cur[j] = sc_nxt[j] = 0;
-    if constexpr (XI8) if (item_valid(it[j])) sc_cur[j] = scb[j][min(tile0 * TILE + t, S - 1)];
   }
   float mx[MAXI];
 #pragma unroll
@@ -321,16 +339,13 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
     for (int k = 0; k < 8; ++k) T[k] = *(const half8*)(st + stage - 8192 + (k * 64 + lane) * 16);
     // both chains every tile (an unused item has zero W rows and reads valid
     // LDS data), interleaved so the MFMA pipe stays busy
-    if constexpr (XI8) {
-#pragma unroll
-      for (int j = 0; j < MAXI; ++j)
-        if (item_valid(it[j])) sc_nxt[j] = scb[j][min((tile0 + i + 1) * TILE + t, S - 1)];
-    }
     uint4 x0[MAXI], x1[MAXI];
+    uint16_t sc[MAXI];
 #pragma unroll
     for (int j = 0; j < MAXI; ++j) {
       x0[j] = *(const uint4*)(st + xo0[j]);
       x1[j] = XI8 ? x0[j] : *(const uint4*)(st + xo1[j]);
+      sc[j] = XI8 ? *(const uint16_t*)(st + sco[j]) : 0;
     }
     floatx16 acc[MAXI];
 #pragma unroll
@@ -344,7 +359,7 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
     for (int j = 0; j < MAXI; ++j) {
       if constexpr (XI8) {
         uint4 lo, hi;
-        dequant16(x0[j], true, sc_cur[j], lo, hi);
+        dequant16(x0[j], true, sc[j], lo, hi);
         part += dot16h(lo, hi, acc[j]);
       } else if constexpr (__is_same(XT, _Float16)) {
         part += dot16h(x0[j], x1[j], acc[j]);
@@ -362,8 +377,6 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       const float v = add_halves(part);
       if (hh == 0) carry[i & 1][bin][t] = v;
     }
-#pragma unroll
-    for (int j = 0; j < MAXI; ++j) sc_cur[j] = sc_nxt[j];
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();              // publishes the last tile's partials

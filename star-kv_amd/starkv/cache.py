@@ -59,7 +59,8 @@ class LatentCache:
             return
         if any(r % 8 for r in self.ranks) or self.Rv % 8:
             raise StarKVError("quantised caches need ranks that are multiples of 8")
-        self.k_scale = torch.ones(B, Hkv, C, dtype=torch.float16, device=dev)
+        # scale rows padded to 8 positions: the K-logit kernel stages them in 16-byte pieces
+        self.k_scale = torch.ones(B, Hkv, _round(C, 8), dtype=torch.float16, device=dev)
         if fmt == "int8_g64":
             # rows padded to 16 bytes: the K-logit kernel streams them in 16-byte pieces
             pitch = [_round(r, 16) for r in self.ranks]

@@ -87,6 +87,58 @@ def test_k_logits_int8_ragged(dtype):
     assert mr <= 1e-3
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("S,scale_pitch,gqa", [(700, 704, False),   # staged scales, last piece past S
+                                                (700, 700, False),   # pitch < round_up(S, 8): other kernel
+                                                (1000, 1000, False),
+                                                (333, 336, True)])
+def test_k_logits_int8_padded_rows(S, scale_pitch, gqa):
+    """int8 K with rows padded to 16 bytes (the cache's layout): the
+    warp-specialised kernel stages each tile's scales with its rows when the
+    scale rows are readable through round_up(S, 8)."""
+    from oracle import starkv_oracle as o
+    from starkv import KLatentSpec, k_logits
+    from starkv._lib import FMT_INT8_SYM
+    _flush(f"[k int8 padded] S={S} scale_pitch={scale_pitch} gqa={gqa}")
+    B = 3
+    ranks = [32, 48, 16, 64, 32, 56, 16, 96] if gqa else cfg2_ranks()
+    Hkv = len(ranks)
+    Hq = 4 * Hkv if gqa else Hkv
+    pitch = [(r + 15) // 16 * 16 for r in ranks]
+    rng = np.random.default_rng(S)
+    buf = np.zeros((B, S * sum(pitch)), np.int8)
+    scales = np.zeros((B, Hkv, scale_pitch), np.float16)
+    scales[..., S:] = np.float16(np.inf)        # never used: positions past S
+    deq, offs, off = [], [], 0
+    for h, r in enumerate(ranks):
+        x = rng.standard_normal((B, S, r)).astype(np.float32)
+        x[..., ::13] *= 8.0
+        q, s = o.quant_int8_sym(x)
+        rows = np.zeros((B, S, pitch[h]), np.int8)
+        rows[..., :r] = q
+        buf[:, off:off + S * pitch[h]] = rows.reshape(B, -1)
+        scales[:, h, :S] = s[..., 0]
+        deq.append(torch.from_numpy(o.dequant_int8_sym(q, s).astype(np.float64)))
+        offs.append(off)
+        off += S * pitch[h]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn(B, Hq, HEAD, generator=g, device="cuda").half()
+    bko = list(np.cumsum([0] + ranks[:-1]) * HEAD)
+    bk_all = torch.cat([torch.randn(r, HEAD, generator=g, device="cuda") / math.sqrt(r) for r in ranks]).half()
+    sc = _dev(scales)
+    spec = KLatentSpec(_dev(buf), ranks, offs, pitch, buf.shape[1], bk_all, bko, HEAD,
+                       fmt=FMT_INT8_SYM, scale=sc, scale_stride_b=sc.stride(0), scale_stride_h=sc.stride(1))
+    out = k_logits(q, spec, S, scale=0.25)
+    torch.cuda.synchronize()
+    cos, sin = _rope_cs(S)
+    bk_h = [bk_all[bko[h] // HEAD:bko[h] // HEAD + r].cpu() for h, r in enumerate(ranks)]
+    ref = o.k_logits(q.cpu(), bk_h, deq, cos, sin, scale=0.25)
+    mx, mr = errors(out, ref)
+    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert torch.isfinite(out).all()
+    assert mr <= 1e-3
+
+
 def reference_split_k(B, H, S, upper, lower, upper_kind="int8", seed=0):
     """The reference module's split K cache [B, H, S, *] and its dequantised [B, H, S, upper+lower]."""
     from oracle import starkv_oracle as o
