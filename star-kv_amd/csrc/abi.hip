@@ -492,7 +492,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.bk = d->k.bk; a.bk_rs = d->k.bk_row_stride;
   a.rope = (const uint4*)d->rope_table;
   a.mask = d->mask; a.m_sb = d->mask_stride_b; a.m_sh = d->mask_stride_h; a.mask_dtype = d->mask_dtype;
-  a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
+  a.out = d->out; a.o_sb = d->out_stride_b; a.o_st = TILE; a.o_sh = d->out_stride_h;   // rows
   a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
   const int n_tiles = (int)ceil_div(d->seq_len, TILE);
@@ -561,7 +561,9 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   ka.bk = d->k.bk; ka.bk_rs = d->k.bk_row_stride;
   ka.rope = (const uint4*)d->rope_table;
   ka.mask = d->mask; ka.m_sb = d->mask_stride_b; ka.m_sh = d->mask_stride_h; ka.mask_dtype = d->mask_dtype;
-  ka.out = ws + L.off_logits; ka.o_sb = (int64_t)Hq * L.S_pad; ka.o_sh = L.S_pad;
+  // logits in 32-position tiles of all heads: a tile's 4 KB is written together
+  // by the workgroups of one chunk and read contiguously by P.V
+  ka.out = ws + L.off_logits; ka.o_sb = (int64_t)Hq * L.S_pad; ka.o_st = (int64_t)Hq * TILE; ka.o_sh = TILE;
   ka.chunkmax = (float*)(ws + L.off_cmax);
   ka.S = d->seq_len; ka.Hq = Hq; ka.n_chunks = L.n_c1; ka.tiles_per_chunk = L.tiles_per_chunk;
   ka.wscale = d->scale;
@@ -572,7 +574,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
 
   PVArgs pa = {};
   if ((st = validate_v(d->v, pa, &vq))) return st;
-  pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = (int64_t)Hq * L.S_pad; pa.l_sh = L.S_pad;
+  pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = ka.o_sb; pa.l_st = ka.o_st; pa.l_sh = ka.o_sh;
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
   pa.part2 = (float*)(ws + L.off_part2); pa.psum2 = (float*)(ws + L.off_psum2); pa.n_grp = L.pv.n_grp;

@@ -53,7 +53,9 @@ struct KArgs {
   const void* bk; int64_t bk_rs;
   const uint4* rope;                               // RoPE operand table [tile][8][64] x 16 B
   const void* mask; int64_t m_sb, m_sh; int mask_dtype;
-  void* out; int64_t o_sb, o_sh;
+  // logit (b, q, s) at out + b*o_sb + (s / 32)*o_st + q*o_sh + s % 32: rows
+  // (o_st = 32) or 32-position tiles of all heads (o_sh = 32, o_st = Hq*32)
+  void* out; int64_t o_sb, o_st, o_sh;
   float* chunkmax;                                 // [B][Hq][n_chunks] (optional)
   int S, Hq, n_chunks, tiles_per_chunk, n_wg;
   int maxi;                                        // items per wave of the launched variant (2 or 4)
@@ -85,7 +87,7 @@ struct PVArgs {
   const void* xs2; int64_t xs2_sb, xs2_ss;         // fp16 scales of x2
   const void* xz;                                  // VQ_G64 fp16 zero points (strides of xs)
   int split, a_int8;                               // VQ_BLOCK: first rank of x2; x holds int8
-  const float* logits; int64_t l_sb, l_sh;         // fused path: fp32 logits
+  const float* logits; int64_t l_sb, l_st, l_sh;   // fused path: fp32 logits, K1's layout (o_sb, o_st, o_sh)
   const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
   int p_vec;                                       // drop-in: P rows allow 16-byte loads
@@ -190,11 +192,13 @@ __device__ inline void dequant16(uint4 r, bool k8, uint16_t s16, uint4& lo, uint
   uint32_t pr[8];
   _Float16 bias;
   if (k8) {
+    // n + 128 as a byte, placed under the exponent byte 0x64 by one v_perm per
+    // pair (selector 4 picks byte 0 of the 0x64646464 source)
     const uint32_t w[4] = {r.x ^ 0x80808080u, r.y ^ 0x80808080u, r.z ^ 0x80808080u, r.w ^ 0x80808080u};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      pr[2 * k] = (w[k] & 0xFFu) | ((w[k] << 8) & 0xFF0000u);
-      pr[2 * k + 1] = ((w[k] >> 16) & 0xFFu) | ((w[k] >> 8) & 0xFF0000u);
+      pr[2 * k] = __builtin_amdgcn_perm(0x64646464u, w[k], 0x04010400u);
+      pr[2 * k + 1] = __builtin_amdgcn_perm(0x64646464u, w[k], 0x04030402u);
     }
     bias = (_Float16)-1152.0f;
   } else {
@@ -202,7 +206,7 @@ __device__ inline void dequant16(uint4 r, bool k8, uint16_t s16, uint4& lo, uint
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const uint32_t u = w[k >> 2] >> (8 * (k & 3));
-      pr[k] = (u & 0xFu) | (((u >> 4) & 0xFu) << 16);
+      pr[k] = (u & 0xFu) | (((u >> 4) & 0xFu) << 16) | 0x64006400u;
     }
     bias = (_Float16)-1032.0f;
   }
@@ -210,7 +214,7 @@ __device__ inline void dequant16(uint4 r, bool k8, uint16_t s16, uint4& lo, uint
   uint32_t o[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k)
-    o[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(kh2, pr[k] | 0x64006400u) + b2) * s);
+    o[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(kh2, pr[k]) + b2) * s);
   lo = make_uint4(o[0], o[1], o[2], o[3]);
   hi = make_uint4(o[4], o[5], o[6], o[7]);
 }

@@ -291,7 +291,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
         const int qh = item_qh(it[i]);
         if (store) {
           if (a.mask != nullptr) tot += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
-          const int64_t o = b * a.o_sb + qh * a.o_sh + s;
+          const int64_t o = b * a.o_sb + (int64_t)(s >> 5) * a.o_st + qh * a.o_sh + (s & 31);
           if constexpr (OUTK == 0) ((float*)a.out)[o] = tot;
           else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)tot;
           else ((__bf16*)a.out)[o] = (__bf16)tot;

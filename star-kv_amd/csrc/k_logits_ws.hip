@@ -315,10 +315,12 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
   auto emit = [&](float v, int qh, int s, float& m) __attribute__((always_inline)) {
     if (s < S) {
       if (a.mask != nullptr) v += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
-      const int64_t o = b * a.o_sb + qh * a.o_sh + s;
-      if constexpr (OUTK == 0) ((float*)a.out)[o] = v;
-      else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)v;
-      else ((__bf16*)a.out)[o] = (__bf16)v;
+      if (hh == 0) {                         // both halves hold the sum; one stores
+        const int64_t o = b * a.o_sb + (int64_t)(s >> 5) * a.o_st + qh * a.o_sh + (s & 31);
+        if constexpr (OUTK == 0) ((float*)a.out)[o] = v;
+        else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)v;
+        else ((__bf16*)a.out)[o] = (__bf16)v;
+      }
       m = fmaxf(m, v);
     }
   };

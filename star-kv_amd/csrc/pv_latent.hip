@@ -230,9 +230,10 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
       }
     }
     if constexpr (FUSED) {
-      // rows past H read row H-1; the logits buffer holds S_pad >= s_end + 8 columns
+      // rows past H read row H-1; the logits buffer holds S_pad >= s_end + 8
+      // columns; 8 aligned positions never straddle a 32-position tile
       const int sa = s_begin + kc * KSTEP + 8 * hh;
-      const float* lp = a.logits + b * a.l_sb + min(n, H - 1) * a.l_sh + sa;
+      const float* lp = a.logits + b * a.l_sb + (int64_t)(sa >> 5) * a.l_st + min(n, H - 1) * a.l_sh + (sa & 31);
       const float4 u = *(const float4*)lp, v = *(const float4*)(lp + 4);
       st.p[0] = u.x; st.p[1] = u.y; st.p[2] = u.z; st.p[3] = u.w;
       st.p[4] = v.x; st.p[5] = v.y; st.p[6] = v.z; st.p[7] = v.w;
