@@ -15,6 +15,7 @@ constexpr int MI355X_CUS = 256;     // launch geometry is planned for one MI355X
 constexpr int K1_WG_PER_CU = 1;     // k_logits_kernel: one 8-wave (or 4-wave) workgroup per CU
 constexpr int MAX_S = 1 << 24;
 constexpr int MAX_RV = 8192;
+constexpr int64_t V_MAX_PITCH = 1 << 24;   // V row pitch (bytes) of the 24-bit offset multiply in P.V
 constexpr int K2_MAX_H = 32;
 
 int esize(int dt) {
@@ -300,12 +301,14 @@ struct PVGeom {
   int Rvp, n_cb, n_c2, c2_len, n_grp;   // n_grp > 1: two-level split reduction
 };
 
-PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq) {
+// row_bytes: the largest row pitch (bytes) of the V latent's streams; the
+// kernel addresses a chunk with 32-bit offsets, so a chunk stays below 2 GB
+PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) {
   PVGeom g;
   g.Rvp = (int)round_up(Rv, 32);
   const int ntw = pv_tiles_per_wave(g.Rvp, fused, vq);
   g.n_cb = (int)ceil_div(g.Rvp / 32, 4 * ntw);
-  const int wg_per_cu = ntw >= 8 ? 1 : 2;    // registers / LDS staging allow one workgroup per CU from NTW 8
+  const int wg_per_cu = pv_wg_per_cu(ntw, vq);
   const int n_ks = (int)ceil_div(S, KSTEP);
   // each extra split writes and re-reads one fp32 partial of 32 x Rvp per
   // column block, against the X_v bytes and logits the split streams
@@ -313,6 +316,8 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq) {
   // (below ~8K positions the launch is latency-bound and partials are cheap)
   const double frac = 32.0 * g.Rvp * 8.0 / g.n_cb / ((double)std::max(S, 8192) * (vbytes / g.n_cb + 128.0));
   int n = choose_splits((int64_t)B * g.n_cb, MI355X_CUS * wg_per_cu, n_ks, 512, 4.0, frac);
+  const int64_t max_ks = std::max<int64_t>(1, ((int64_t)1 << 31) / std::max<int64_t>(row_bytes, 1) / KSTEP);
+  n = std::max<int64_t>(n, ceil_div(n_ks, max_ks));
   g.c2_len = (int)ceil_div(n_ks, n) * KSTEP;
   g.n_c2 = (int)ceil_div(S, g.c2_len);
   g.n_grp = g.n_c2 > PV_RG ? (int)ceil_div(g.n_c2, PV_RG) : 0;
@@ -326,14 +331,14 @@ struct DecodeLayout {
   size_t off_logits, off_cmax, off_part, off_psum, off_part2, off_psum2, off_olat, off_lsum, total;
 };
 
-DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg, int vq) {
+DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes) {
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
   L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 256, 3.0, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
-  L.pv = pv_geometry(B, S, Rv, true, vq);
+  L.pv = pv_geometry(B, S, Rv, true, vq, v_row_bytes);
   const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
@@ -398,6 +403,7 @@ int validate_v(const starkv_vlatent& v, PVArgs& pa, int* vq) {
         return STARKV_ERR_SHAPE;
       if (!al(v.data, 4) || !al64(v.stride_s, 4) || !al64(v.stride_b, 4) || !al(v.scale, 2) || !al(v.zero, 2))
         return STARKV_ERR_ALIGN;
+      if (v.stride_s >= V_MAX_PITCH || v.scale_stride_s * 2 >= V_MAX_PITCH) return STARKV_ERR_LIMIT;
       pa.xs = v.scale; pa.xs_sb = v.scale_stride_b; pa.xs_ss = v.scale_stride_s;
       pa.xz = v.zero;
       *vq = VQ_G64;
@@ -409,7 +415,14 @@ int validate_v(const starkv_vlatent& v, PVArgs& pa, int* vq) {
 }
 
 bool v_fast(const starkv_vlatent& v) {
-  return al(v.data, 16) && al64(v.stride_s * 2, 16) && al64(v.stride_b * 2, 16) && v.rank % 8 == 0;
+  return al(v.data, 16) && al64(v.stride_s * 2, 16) && al64(v.stride_b * 2, 16) && v.rank % 8 == 0 &&
+         v.stride_s * 2 < V_MAX_PITCH;
+}
+
+// largest row pitch in bytes over the V latent's streams (dense: 16-bit elements)
+int64_t v_row_bytes(const starkv_vlatent& v) {
+  if (v.format == STARKV_FMT_DENSE) return v.stride_s * 2;
+  return std::max({v.stride_s, v.scale_stride_s * 2, v.stride2_s, v.scale2_stride_s * 2});
 }
 
 int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
@@ -508,7 +521,7 @@ size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {
   PVArgs tmp = {};
   int vq = 0;
   if (validate_v(d->v, tmp, &vq)) return 0;
-  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq);
+  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq, v_row_bytes(d->v));
   return a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4) + a256((size_t)d->batch * g.n_grp * 32 * g.Rvp * 4);
 }
 
@@ -524,7 +537,7 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
   const size_t need = starkv_pv_latent_workspace_bytes(d);
   if (!workspace || workspace_bytes < need) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
-  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq);
+  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq, v_row_bytes(d->v));
   a.Rv = d->v.rank; a.Rvp = g.Rvp; a.n_cb = g.n_cb; a.n_c2 = g.n_c2; a.c2_len = g.c2_len; a.n_grp = g.n_grp;
   a.p = d->p; a.p_sb = d->p_stride_b; a.p_sh = d->p_stride_h;
   a.p_vec = al(d->p, 16) && al64(d->p_stride_b * 2, 16) && al64(d->p_stride_h * 2, 16);
@@ -538,14 +551,14 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
   int gs = 0, n_wg = 0, vq = 0;
   if (validate_decode(d, &gs, &n_wg, &vq)) return 0;
-  return decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq).total;
+  return decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v)).total;
 }
 
 static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream,
                        void* const* events) {
   int gs = 0, n_wg = 0, vq = 0, st;
   if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
-  const DecodeLayout L = decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq);
+  const DecodeLayout L = decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v));
   if (!workspace || workspace_bytes < L.total) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   char* ws = (char*)workspace;

@@ -80,9 +80,11 @@ __device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16
     pr[3] = ((y >> 16) & 0xFFu) | ((y >> 8) & 0xFF0000u);
     bias = (_Float16)-1152.0f;                                       // 1024 + 128
   } else {
-    const uint32_t w = q.x;
+    // low nibbles (even ranks) and high nibbles (odd ranks) as bytes; one
+    // v_perm per pair puts byte k of each under a zero byte
+    const uint32_t lo = q.x & 0x0F0F0F0Fu, hi = (q.x >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) pr[k] = ((w >> (8 * k)) & 0xFu) | (((w >> (8 * k + 4)) & 0xFu) << 16);
+    for (int k = 0; k < 4; ++k) pr[k] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u + 0x00010001u * k);
     bias = VQ == VQ_BLOCK ? (_Float16)-1032.0f : (_Float16)-1024.0f;  // nibble - 8 | nibble
   }
   const h2v b2 = {bias, bias};
@@ -113,7 +115,7 @@ __device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
 }
 
 template <typename VT, int NTW, bool FUSED, bool FAST, int VQ>
-__global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
+__global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PVArgs a) {
   constexpr int PITCH = NTW * 32 + 8;            // elements per staged row (16-byte pad)
   constexpr int STAGE = 16 * PITCH;              // elements per staged K-step
   constexpr int CPR = NTW * 4;                   // 16-byte chunks per staged row
@@ -142,6 +144,7 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     __syncthreads();
   }
   const float Mq = FUSED ? Ms[n] : 0.f;
+  const float MqL = -Mq * 1.4426950408889634f;  // exp(l - M) = exp2(l * log2(e) - M * log2(e))
   const bool qok = n < H;
 
   const int s_begin = c2 * a.c2_len;
@@ -174,13 +177,26 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
   const uint8_t* xq2 = (const uint8_t*)a.x2 + b * a.x2_sb + (int64_t)s_begin * a.x2_ss;
   const uint16_t* sq = (const uint16_t*)a.xs + b * a.xs_sb + (int64_t)s_begin * a.xs_ss;
   const uint16_t* sq2 = (const uint16_t*)a.xs2 + b * a.xs2_sb + (int64_t)s_begin * a.xs2_ss;
-  const uint16_t* zq = (const uint16_t*)a.xz + b * a.xs_sb + (int64_t)s_begin * a.xs_ss;
 #pragma unroll
   for (int c = 0; c < NTW; ++c) {
     qlo[c] = VQ == VQ_BLOCK && gcol[c] >= a.split;
     q8[c] = VQ == VQ_BLOCK && !qlo[c] && a.a_int8;
     qoff[c] = qlo[c] ? (gcol[c] - a.split) / 2 : (q8[c] ? gcol[c] : gcol[c] / 2);
     qg[c] = gcol[c] / 64;
+  }
+  // dense (aligned) and group-64 loads: 32-bit byte offsets from the chunk's
+  // first row, row * pitch by a 24-bit multiply (the host keeps row pitches
+  // below 16 MB and a chunk below 2 GB); columns past the slab read column 0
+  const uint32_t xp = (uint32_t)(VQ == VQ_DENSE ? a.x_ss * (int64_t)sizeof(VT) : a.x_ss);
+  const uint32_t sp = (uint32_t)(a.xs_ss * 2);
+  const char* xrow0 = (const char*)a.x + (b * a.x_sb + (int64_t)s_begin * a.x_ss) * (VQ == VQ_DENSE ? (int64_t)sizeof(VT) : 1);
+  const char* srow0 = (const char*)a.xs + (b * a.xs_sb + (int64_t)s_begin * a.xs_ss) * 2;
+  const char* zrow0 = (const char*)a.xz + (b * a.xs_sb + (int64_t)s_begin * a.xs_ss) * 2;
+  uint32_t xco[NTW], sco[NTW];
+#pragma unroll
+  for (int c = 0; c < NTW; ++c) {
+    xco[c] = !cok[c] ? 0u : VQ == VQ_DENSE ? (uint32_t)(gcol[c] * sizeof(VT)) : (uint32_t)qoff[c];
+    sco[c] = cok[c] ? (uint32_t)qg[c] * 2 : 0u;
   }
 
   // Every load of a stage is issued unconditionally from a clamped, in-bounds
@@ -204,10 +220,11 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
           st.q[c].y = *(const uint32_t*)(p + (q8[c] ? 4 : 0));
           st.s[c] = lo ? sq2[r * a.xs2_ss] : sq[r * a.xs_ss];
         } else {
-          st.q[c].x = *(const uint32_t*)(xq + r * a.x_ss + (cok[c] ? qoff[c] : 0));
+          const uint32_t ru = (uint32_t)r, so = __umul24(ru, sp) + sco[c];
+          st.q[c].x = *(const uint32_t*)(xrow0 + (__umul24(ru, xp) + xco[c]));
           st.q[c].y = 0;
-          st.s[c] = sq[r * a.xs_ss + (cok[c] ? qg[c] : 0)];
-          st.z[c] = zq[r * a.xs_ss + (cok[c] ? qg[c] : 0)];
+          st.s[c] = *(const uint16_t*)(srow0 + so);
+          st.z[c] = *(const uint16_t*)(zrow0 + so);
         }
       }
     }
@@ -215,8 +232,8 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     for (int c = 0; c < NTW; ++c) {
       if constexpr (VQ != VQ_DENSE) break;
       if (FAST) {
-        const int64_t r = min(kc * KSTEP + grow[c], rmax);
-        st.r[c] = ld_stream16(xb + r * a.x_ss + (cok[c] ? gcol[c] : 0));
+        const uint32_t ru = (uint32_t)min(kc * KSTEP + grow[c], rmax);
+        st.r[c] = ld_stream16(xrow0 + (__umul24(ru, xp) + xco[c]));
       } else {
         const int s0 = s_begin + ks * KSTEP;
         st.r[c] = make_uint4(0, 0, 0, 0);
@@ -284,7 +301,12 @@ __global__ __launch_bounds__(256, 1) void pv_kernel(const PVArgs a) {
     float pv[8];
     if constexpr (FUSED) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = (qok && sa + e < s_end) ? __builtin_amdgcn_exp2f((pc[e] - Mq) * 1.4426950408889634f) : 0.f;
+      for (int e = 0; e < 8; ++e) {
+        // computed for every lane and selected (the logits past s_end are
+        // unwritten workspace: their exponentials are discarded)
+        const float ex = __builtin_amdgcn_exp2f(fmaf(pc[e], 1.4426950408889634f, MqL));
+        pv[e] = (qok && sa + e < s_end) ? ex : 0.f;
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) psum += pv[e];
     } else {
@@ -421,11 +443,14 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
 
 int pv_tiles_per_wave(int Rvp, bool fused, int vq) {
   const int tiles = Rvp / 32;
-  // Quantised formats: 4 tiles per wave, two workgroups per CU.  A quantised
-  // K-step carries a quarter (int4) of the bytes of a dense one, so the wave
-  // count, not the bytes per wave, has to cover the memory latency (measured at
-  // B16 S32768 int4-g64: 8 tiles 446 us, 4 tiles 350 us, 2 tiles 480 us).
-  if (tiles <= 16 || vq != VQ_DENSE) return 4;
+  // Quantised formats: 8 tiles per wave, two workgroups per CU.  A quantised
+  // K-step carries a quarter (int4) of the bytes of a dense one; its cost is
+  // the VALU work (dequantisation, and the exponentials every wave forms for
+  // its own A operand), so wider waves share it over more columns, while two
+  // workgroups per CU keep 8 waves covering the memory latency (B16 S32768
+  // int4-g64: 4 tiles 285 us, 8 tiles 244 us; 4 tiles x 3 workgroups 325 us).
+  if (tiles <= 16) return 4;
+  if (vq != VQ_DENSE) return 8;
   // the drop-in P-input variant stays at 8 (register budget)
   if (tiles <= 32 || !fused) return 8;
   return 13;
