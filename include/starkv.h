@@ -165,7 +165,8 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
  *   INT8_SYM: all ranks int8 in data, per-token scale.
  *   INT4_G64: nibbles n (rank 2k low nibble of byte k) in data; fp16 scale
  *     and zero of (b, s, group g = rank/64) at scale / zero + b*scale_stride_b
- *     + s*scale_stride_s + g; x = n*s + z.
+ *     + s*scale_stride_s + g; x = n*s + z.  Row pitches (stride_s, and
+ *     scale_stride_s in bytes) below 16 MB, else STARKV_ERR_LIMIT.
  * ------------------------------------------------------------------- */
 typedef struct {
   int rank;

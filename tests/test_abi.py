@@ -204,6 +204,18 @@ def test_rope_build_and_pv_validation():
     assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_LIMIT
     p.n_heads, p.p = 32, None
     assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_NULL
+    # group-64 int4 rows are addressed with a 24-bit row multiply: pitches of
+    # 16 MB or more are refused
+    p.p = FAKE
+    p.v = L.VLatent(rank=256, format=L.FMT_INT4_G64, data=FAKE, stride_b=1 << 30, stride_s=128, scale=FAKE,
+                    scale_stride_b=1 << 20, scale_stride_s=4, zero=FAKE)
+    need = lib.starkv_pv_latent_workspace_bytes(ctypes.byref(p))
+    assert need > 0
+    assert lib.starkv_pv_latent(ctypes.byref(p), None, 0, None) == ERR_WORKSPACE
+    p.v.stride_s = 1 << 24
+    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_LIMIT
+    p.v.stride_s, p.v.scale_stride_s = 128, 1 << 23
+    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_LIMIT
 
 
 def test_k_logits_validation():
