@@ -119,6 +119,12 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   constexpr int PITCH = NTW * 32 + 8;            // elements per staged row (16-byte pad)
   constexpr int STAGE = 16 * PITCH;              // elements per staged K-step
   constexpr int CPR = NTW * 4;                   // 16-byte chunks per staged row
+  // dense aligned rows are fetched cooperatively: the workgroup's 256 lanes
+  // read each K-step's rows as contiguous 16-byte chunks (every 128-byte line
+  // by one instruction) and write them into the owning wave's slab, one
+  // barrier per K-step.  Per-wave column slabs would split lines between waves
+  // and, with non-temporal loads, fetch the split lines twice.
+  constexpr bool COOP = VQ == VQ_DENSE && FAST;
   __shared__ __attribute__((aligned(16))) uint16_t stage[4][2][STAGE];
   __shared__ float Ms[32];
   __shared__ float Ps[4][32];
@@ -156,18 +162,41 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   for (int j = 0; j < NTW; ++j) acc[j] = floatx16{};
   float psum = 0.f;
 
-  // ---- per-lane staging map: chunk c -> (row, 16-byte column chunk) of the 16 x NTW*32 slab
+  // ---- per-lane staging map: chunk c -> (row, 16-byte column chunk) of the
+  // 16 x NTW*32 slab (cooperative: of the workgroup's 16 x 4*NTW*32 block;
+  // soff then counts from stage[0][buf] and includes the owning wave)
   int goff[NTW], soff[NTW], grow[NTW], gcol[NTW];
   bool cok[NTW];
+  const int cb0 = cb * 4 * CPR;                                  // first chunk column of the workgroup
+  const int ncol = max(1, min(4 * CPR, a.Rv / 8 - cb0));         // chunk columns it covers (cooperative)
 #pragma unroll
   for (int c = 0; c < NTW; ++c) {
-    const int f = c * 64 + lane;
-    const int row = f / CPR, c16 = f % CPR;
-    grow[c] = row;
-    gcol[c] = col0 + c16 * 8;
-    goff[c] = row * (int)a.x_ss + gcol[c];
-    soff[c] = row * PITCH + c16 * 8;
-    cok[c] = (c16 / 4 < nvt) && (gcol[c] < a.Rv);
+    if constexpr (COOP) {
+      const int f = min(c * 256 + tid, 16 * ncol - 1);           // lanes past the block repeat its last chunk
+      const int row = f / ncol, cc = f % ncol;
+      grow[c] = row;
+      gcol[c] = (cb0 + cc) * 8;
+      goff[c] = 0;
+      soff[c] = (cc / CPR) * 2 * STAGE + row * PITCH + (cc % CPR) * 8;
+      cok[c] = true;
+    } else {
+      const int f = c * 64 + lane;
+      const int row = f / CPR, c16 = f % CPR;
+      grow[c] = row;
+      gcol[c] = col0 + c16 * 8;
+      goff[c] = row * (int)a.x_ss + gcol[c];
+      soff[c] = row * PITCH + c16 * 8;
+      cok[c] = (c16 / 4 < nvt) && (gcol[c] < a.Rv);
+    }
+  }
+  if constexpr (COOP) {
+    // slab columns past the workgroup's block are never written: zero them
+    // once (both buffers), so the discarded output columns stay finite
+#pragma unroll 1
+    for (int e = lane; e < 2 * 16 * CPR; e += 64) {
+      const int bf = e / (16 * CPR), row = (e / CPR) % 16, c16 = e % CPR;
+      if (wave * CPR + c16 >= ncol) *(uint4*)&stage[wave][bf][row * PITCH + c16 * 8] = make_uint4(0, 0, 0, 0);
+    }
   }
   const VT* xb = (const VT*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
   // quantised: byte offset of the chunk in its row, its block, int8 or int4, its group
@@ -279,7 +308,9 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     uint16_t* sbuf = &stage[wave][buf][0];
 #pragma unroll
     for (int c = 0; c < NTW; ++c) {
-      if constexpr (VQ == VQ_DENSE) {
+      if constexpr (COOP) {
+        *(uint4*)&stage[0][buf][soff[c]] = st.r[c];
+      } else if constexpr (VQ == VQ_DENSE) {
         *(uint4*)&sbuf[soff[c]] = st.r[c];
       } else {
         uint4 h = dequant8<VQ>(st.q[c], q8[c], st.s[c], VQ == VQ_G64 ? st.z[VQ == VQ_G64 ? c : 0] : (uint16_t)0);
@@ -296,6 +327,11 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
       praw = st.praw;
     }
     load(st, ks + 2);                       // clamped past the chunk
+    if constexpr (COOP) {
+      // every wave's chunks of this K-step are in LDS (and every wave has
+      // consumed the buffer's previous K-step, two steps ago)
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
 
     const int sa = s_begin + ks * KSTEP + 8 * hh;
     float pv[8];
@@ -352,7 +388,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     }
   };
 
-  if (nvt > 0 && nks > 0) {
+  if ((COOP || nvt > 0) && nks > 0) {       // cooperative: every wave takes part in the barriers
     // K-steps in pairs; an odd chunk's last pair computes one K-step past the
     // chunk with P = 0 (no branch in the loop body)
     PVStage<NTW, VQ> st0, st1;
