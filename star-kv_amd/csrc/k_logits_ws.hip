@@ -13,19 +13,26 @@
 //   instruction, only as many instructions as the workgroup's chunks need.
 //   Rows are stored with their 16-byte chunks rotated (ws_shift) so the
 //   consumers' row-wise reads are free of LDS bank conflicts.
-// * 8 consumer waves, two per SIMD, so one wave's dot products and stores
-//   overlap the other's MFMA chains.  The plan packs whole heads into bins
-//   of up to 4 items (query head, 32-rank M-tile); consumer wave c runs items
-//   2*(c/4) and 2*(c/4)+1 of bin c%4.  A head whose items straddle the two
-//   halves of a bin is combined through LDS: the first wave leaves its
-//   partial logits for the tile, the second adds them one tile later (after
-//   the next barrier) and stores.
+// * Consumer waves.  The plan packs whole heads into bins of up to 4 items
+//   (query head, 32-rank M-tile), 4 bins per workgroup.
+//   - Dense latents: 4 consumer waves, one per SIMD, wave c runs bin c.  Its
+//     four MFMA chains run one after another and chain j+1's MFMAs carry
+//     chain j's dot products, in an order fixed by scheduling fences, so the
+//     VALU work runs under the MFMA pipe.  One wave per SIMD also halves the
+//     RoPE-operand LDS reads (every consumer wave reads the whole 8 KB tile).
+//   - int8 latents: 8 consumer waves, two per SIMD, wave c runs items
+//     2*(c/4) and 2*(c/4)+1 of bin c%4, so one wave's dequantisation and dot
+//     products overlap the other's MFMA chains.  A head whose items straddle
+//     the two halves of a bin is combined through LDS: the first wave leaves
+//     its partial logits for the tile, the second adds them one tile later
+//     (after the next barrier) and stores.
 //
-// Measured on MI355X (B16, S32768, ragged ranks summing to 1640): the
-// register-streaming kernel of k_logits.hip reaches 3.8 TB/s; this one
-// 4.2 TB/s.  With the consumers idle the producers alone stream 5.6-6.5 TB/s;
-// with them busy the shader clock falls from ~2.3 to ~1.6-2.0 GHz and the
-// per-CU fetch rate with it.
+// Measured on MI355X (B16, S32768, ragged ranks summing to 1640): with the
+// consumers idle the producers alone stream 5.6 TB/s at 2.4 GHz; the full
+// kernel needs only ~5 % more shader cycles than that, but the decode layer
+// runs at the board's 1400 W limit and the shader clock settles near
+// 2.0-2.2 GHz while the consumers run, so the time is set by the energy per
+// tile (MFMA work, LDS traffic, VALU work) as much as by the byte stream.
 //
 // Stage protocol (one s_barrier per tile, no fence): at tile i the producers
 // wait for their own DMA of tile i (vmcnt counts exactly: every lane of an
@@ -40,7 +47,10 @@ namespace starkv {
 namespace {
 
 constexpr int WS_PRODUCERS = 4;
-constexpr int WS_CONSUMERS = 8;
+// consumer waves: dense latents 4 (one per SIMD, a whole bin of up to 4
+// items each); int8 latents 8 (two per SIMD, two items each), whose
+// dequantisation is better hidden by the second wave
+template <bool XI8> constexpr int ws_consumers() { return XI8 ? 8 : 4; }
 constexpr int WS_BINS = 4;                          // item bins (of up to 4 items) per workgroup
 constexpr int WS_RING = K1_WS_RING_BYTES;           // LDS ring (the straddle carry takes the rest of the 160 KB)
 constexpr int WS_MAXK = (2048 / 64 + 9 + WS_PRODUCERS - 1) / WS_PRODUCERS;   // DMA instructions per producer per tile
@@ -98,6 +108,28 @@ __device__ inline float dot16b(uint4 u0, uint4 u1, const floatx16& acc) {
   return (p[0] + p[1]) + (p[2] + p[3]);
 }
 
+// values 2k, 2k+1 of a 16-value dot (word k % 4 of u0 for k < 4, else of
+// u1) into the partial sums p[(2k) & 3], p[(2k+1) & 3]: the order of
+// dot16h / dot16b, split so the pieces can sit between MFMAs
+template <bool BF>
+__device__ inline void dot_piece(const uint4& u0, const uint4& u1, const floatx16& acc, int k, float p[4]) {
+  const uint4& u = k < 4 ? u0 : u1;
+  const uint32_t w = (k & 3) == 0 ? u.x : (k & 3) == 1 ? u.y : (k & 3) == 2 ? u.z : u.w;
+  float a, c;
+  if constexpr (BF) {
+    a = __uint_as_float(w << 16);
+    c = __uint_as_float(w & 0xffff0000u);
+  } else {
+    const kh2 h = __builtin_bit_cast(kh2, w);
+    a = (float)h[0];
+    c = (float)h[1];
+  }
+  p[(2 * k) & 3] = fmaf(a, acc[2 * k], p[(2 * k) & 3]);
+  p[(2 * k + 1) & 3] = fmaf(c, acc[2 * k + 1], p[(2 * k + 1) & 3]);
+}
+
+#define WS_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 }  // namespace
 
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
@@ -106,8 +138,10 @@ __device__ inline float dot16b(uint4 u0, uint4 u1, const floatx16& acc) {
 //      are staged with its rows (one more DMA instruction), so the consumers
 //      issue no global loads
 template <typename XT, int OUTK, bool XI8>
-__global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logits_ws_kernel(const KArgs a) {
-  constexpr int MAXI = 2;                            // items per consumer wave
+__global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void k_logits_ws_kernel(const KArgs a) {
+  constexpr int NCONS = ws_consumers<XI8>();
+  constexpr int MAXI = XI8 ? 2 : 4;                  // items per consumer wave
+  constexpr bool XB = !XI8 && !__is_same(XT, _Float16);   // bf16 latents
   __shared__ __attribute__((aligned(16))) char ring[WS_RING];   // a.ws_nst stages of a.ws_stage bytes
   __shared__ float carry[2][WS_BINS][32];            // straddling heads: first half's partial logits
 
@@ -157,9 +191,9 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
   const int sc_off = stage - 8192 - SCB;
   if (tot == 0 || nX * 1024 + SCB + 8192 > stage || nst < 2 || nst * stage > WS_RING) return;   // uniform
 
-  if (wave >= WS_CONSUMERS) {
+  if (wave >= NCONS) {
     // ================= producer =================
-    const int pw = wave - WS_CONSUMERS;
+    const int pw = wave - NCONS;
     // DMA instruction m (latent chunks [64m, 64m+64) for m < nX, then the
     // RoPE operand in 1 KB pieces, then (int8) the scales) belongs to
     // producer m % 4.  Per instruction k of this wave: the lane's source and
@@ -239,13 +273,16 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
   }
 
   // ================= consumer =================
-  const int bin = wave & (WS_BINS - 1), half = wave / WS_BINS;
+  // int8: consumer wave c runs items 2*(c/4), 2*(c/4)+1 of bin c%4; dense:
+  // wave c runs bin c
+  const int bin = wave & (WS_BINS - 1), half = XI8 ? wave / WS_BINS : 0;
   uint32_t it[MAXI];
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) it[i] = a.items[wgp * WS_BINS + bin][MAXI * half + i];
-  // the bin's item 1 ends the first half; if it is not its head's last item the head straddles
+  // int8: the bin's item 1 ends the first half; if it is not its head's last
+  // item the head straddles the two waves
   const uint32_t i1 = a.items[wgp * WS_BINS + bin][1];
-  const bool straddle = item_valid(i1) && !item_last(i1);
+  const bool straddle = XI8 && item_valid(i1) && !item_last(i1);
   const bool send = straddle && half == 0;   // leaves the partial logits of its last head
   const bool recv = straddle && half == 1;   // completes its first head one tile later
 
@@ -329,6 +366,60 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
   float pend = 0.f;                          // receiving wave: own partial of the previous tile
 
   for (int i = 0; i < ntl; ++i) {
+    if constexpr (!XI8) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS reads are done
+    __builtin_amdgcn_s_barrier();
+    if (!item_valid(it[0])) continue;
+    const char* st = ring + (i % nst) * stage;
+    const int s = (tile0 + i) * TILE + t;
+    uint4 x0[MAXI], x1[MAXI];
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) {
+      x0[j] = *(const uint4*)(st + xo0[j]);
+      x1[j] = *(const uint4*)(st + xo1[j]);
+    }
+    half8 T[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) T[k] = *(const half8*)(st + stage - 8192 + (k * 64 + lane) * 16);
+    // every item's chain (an unused item has zero W rows and reads valid LDS
+    // data); chain j+1's MFMAs carry chain j's dot products, in an order fixed
+    // by scheduling fences (the empty asm keeps each piece where it is), so
+    // the VALU work runs while the MFMA pipe is busy
+    float d[MAXI];
+    floatx16 accp, accc;
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) {
+      float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        accc = mfma_f16(wr[j][k], T[k], k == 0 ? floatx16{} : accc);
+        if (j > 0) {
+          WS_FENCE();
+          dot_piece<XB>(x0[j - 1], x1[j - 1], accp, k, p);
+          asm volatile("" :: "v"(p[(2 * k) & 3]), "v"(p[(2 * k + 1) & 3]));
+          WS_FENCE();
+        }
+      }
+      if (j > 0) d[j - 1] = (p[0] + p[1]) + (p[2] + p[3]);
+      accp = accc;
+    }
+    {
+      float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) dot_piece<XB>(x0[MAXI - 1], x1[MAXI - 1], accp, k, p);
+      d[MAXI - 1] = (p[0] + p[1]) + (p[2] + p[3]);
+    }
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXI; ++j) {
+      part += d[j];
+      if (item_last(it[j])) {
+        const float v = add_halves(part);
+        part = 0.f;
+        emit(v, item_qh(it[j]), s, mx[j]);
+      }
+    }
+    } else {
     __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS reads and writes are done
     __builtin_amdgcn_s_barrier();
     if (!item_valid(it[0])) continue;
@@ -379,6 +470,7 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
       const float v = add_halves(part);
       if (hh == 0) carry[i & 1][bin][t] = v;
     }
+      }
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();              // publishes the last tile's partials
@@ -398,7 +490,7 @@ __global__ __launch_bounds__((WS_CONSUMERS + WS_PRODUCERS) * 64, 1) void k_logit
 
 template <typename XT, bool XI8>
 static int launch_ws_t(const KArgs& a, int outk, int B, hipStream_t st) {
-  dim3 grid(a.n_chunks, a.n_wg, B), block((WS_CONSUMERS + WS_PRODUCERS) * 64);
+  dim3 grid(a.n_chunks, a.n_wg, B), block((ws_consumers<XI8>() + WS_PRODUCERS) * 64);
   if (outk == 0) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 0, XI8>), grid, block, 0, st, a);
   else if (outk == 1) hipLaunchKernelGGL((k_logits_ws_kernel<XT, 1, XI8>), grid, block, 0, st, a);
   else hipLaunchKernelGGL((k_logits_ws_kernel<XT, 2, XI8>), grid, block, 0, st, a);
