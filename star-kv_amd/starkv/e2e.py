@@ -87,6 +87,19 @@ class LatentAttention(nn.Module):
         for h, r in enumerate(self.ranks):
             self.bk[h, :r].normal_(0.0, 1.0 / math.sqrt(r), generator=gen)
 
+    @torch.no_grad()
+    def load_projections(self, p) -> None:
+        """Take the latent K / V projections of an exported layer
+        (`starkv.export.LatentProjections`); the module must have been built
+        with the same ranks and V rank."""
+        if list(p.ranks) != self.ranks or p.v_vs.shape[0] != self.v_vs.weight.shape[0]:
+            raise ValueError("load_projections: ranks differ from the module's")
+        self.k_vs.weight.copy_(p.k_vs)
+        self.bk.zero_()
+        self.bk[:, :p.bk.shape[1]].copy_(p.bk)
+        self.v_vs.weight.copy_(p.v_vs)
+        self.v_u.weight.copy_(p.v_u)
+
     def _attend_torch(self, q: torch.Tensor, S: int, T: int) -> torch.Tensor:
         """q [B, Hq, T, 128] (rotated) against positions [0, S) of the cache."""
         B = q.shape[0]
@@ -142,8 +155,11 @@ class LatentAttention(nn.Module):
 
 def build_model(n_layers: int, hidden: int, heads: int, kv_heads: int, intermediate: int, vocab: int,
                 ranks: Sequence[int], v_rank: int, batch: int, capacity: int, fmt: str = "int8_g64",
-                seed: int = 0, device="cuda", dtype=torch.float16):
-    """Random-init LlamaForCausalLM with every attention replaced by LatentAttention."""
+                seed: int = 0, device="cuda", dtype=torch.float16, projections: Optional[Sequence] = None):
+    """Random-init LlamaForCausalLM with every attention replaced by LatentAttention.
+
+    `projections`: per layer, an exported `LatentProjections` whose ranks and
+    weights replace `ranks`, `v_rank` and the random latent projections."""
     from transformers import LlamaConfig, LlamaForCausalLM
     cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=intermediate,
                       num_hidden_layers=n_layers, num_attention_heads=heads, num_key_value_heads=kv_heads,
@@ -159,8 +175,12 @@ def build_model(n_layers: int, hidden: int, heads: int, kv_heads: int, intermedi
     model.eval()
     gen = torch.Generator(device=device).manual_seed(seed + 1)
     for i, layer in enumerate(model.model.layers):
-        att = LatentAttention(cfg, i, ranks, v_rank, batch, capacity, fmt=fmt, device=device, dtype=dtype)
+        p = projections[i] if projections is not None else None
+        r, rv = (p.ranks, p.v_vs.shape[0]) if p is not None else (ranks, v_rank)
+        att = LatentAttention(cfg, i, r, rv, batch, capacity, fmt=fmt, device=device, dtype=dtype)
         att.reset_parameters_(gen)
+        if p is not None:
+            att.load_projections(p)
         layer.self_attn = att
     return model
 

@@ -41,3 +41,67 @@ def test_e2e_decode_matches_torch_path(kv_heads, ranks, fmt):
         if t == 0:
             assert torch.equal(a, r)               # same prefill path, same caches
         assert mr <= 1e-2, (t, mr)
+
+
+def _random_export(g, hidden, kv_heads, keep, v_keep):
+    """A layer's trained decomposition with orthonormal factors and thresholds
+    that keep `keep[h]` K ranks per head and `v_keep` V ranks, exported with
+    the reference's state-dict keys (model.py:76-205, 286-362)."""
+    from starkv.export import export_state_dict
+    D = 128
+
+    def orth(n, k):
+        q, _ = torch.linalg.qr(torch.randn(n, k, generator=g, dtype=torch.float64))
+        return q[:, :k]
+
+    sd = {}
+    sig = torch.linspace(2.0, 0.02, D)
+    U = torch.zeros(kv_heads * D, kv_heads * D, dtype=torch.float64)
+    V = torch.zeros(kv_heads * D, hidden, dtype=torch.float64)
+    for h in range(kv_heads):
+        U[h * D:(h + 1) * D, h * D:(h + 1) * D] = orth(D, D)
+        V[h * D:(h + 1) * D] = orth(hidden, D).t()
+        sd[f"k_proj.Sigma_blocks.{h}.diag"] = sig
+        sd[f"k_proj.Sigma_blocks.{h}.soft_thres_layer.alpha"] = torch.tensor([float(sig[keep[h]])])
+    sd["k_proj.U.weight"], sd["k_proj.V.weight"] = U.float(), V.float()
+    rv = 512
+    sv = torch.linspace(1.5, 0.01, rv)
+    sd["v_proj.U.weight"] = orth(kv_heads * D, rv).float()
+    sd["v_proj.V.weight"] = orth(hidden, rv).t().float()
+    sd["v_proj.Sigma.diag"] = sv
+    sd["v_proj.Sigma.soft_thres_layer.alpha"] = torch.tensor([float(sv[v_keep])])
+    p = export_state_dict(sd, dtype=torch.float16)
+    for name in ("k_vs", "bk", "v_vs", "v_u"):
+        setattr(p, name, getattr(p, name).cuda())
+    return p
+
+
+@pytest.mark.parametrize("fmt", ["int8_g64", "dense"])
+def test_e2e_decode_over_exported_ragged_projections(fmt):
+    """Layers built from exported trained decompositions (ragged kept ranks,
+    padded to multiples of 8) decode on the HIP kernels as the torch path does."""
+    from starkv.e2e import build_model, generate
+    _flush(f"[e2e export] fmt={fmt}")
+    g = torch.Generator().manual_seed(11)
+    keeps = [[37, 70, 12, 101, 33, 64, 5, 120], [90, 16, 48, 127, 3, 60, 77, 25]]
+    proj = [_random_export(g, 1024, 8, k, 300 + 11 * i) for i, k in enumerate(keeps)]
+    for p in proj:
+        assert all(r % 8 == 0 for r in p.ranks) and p.v_vs.shape[0] % 8 == 0
+    B, P, steps = 2, 40, 4
+    kw = dict(n_layers=2, hidden=1024, heads=8, kv_heads=8, intermediate=2048, vocab=1000, ranks=None,
+              v_rank=None, batch=B, capacity=P + steps + 1, fmt=fmt, seed=3, projections=proj)
+    prompt = torch.randint(0, 1000, (B, P), generator=torch.Generator(device="cuda").manual_seed(5), device="cuda")
+    model = build_model(**kw)
+    toks, logits = generate(model, prompt, steps)
+    torch.cuda.synchronize()
+    ref_model = build_model(**kw)
+    _, ref_logits = generate(ref_model, prompt, steps, reference=True, forced=toks[:, :steps])
+    torch.cuda.synchronize()
+    for t, (a, r) in enumerate(zip(logits, ref_logits)):
+        d = (a.double() - r.double()).abs()
+        mr = float(d.mean() / r.double().abs().mean())
+        _flush(f"   forward {t}: max_abs={float(d.max()):.3e} mean_rel={mr:.3e}")
+        assert torch.isfinite(a).all()
+        if t == 0:
+            assert torch.equal(a, r)
+        assert mr <= 1e-2, (t, mr)
