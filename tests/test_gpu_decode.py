@@ -56,6 +56,9 @@ CASES = [
     ("s33_rv40", 1, 32, 32, 33, [24] * 32, 40, torch.float16, "reference"),
     ("unaligned_r_rv", 2, 32, 32, 129, [20] * 32, 50, torch.float16, "reference"),
     ("mqa_hq8", 2, 8, 1, 300, [128], 128, torch.float16, "ragged"),
+    # V wider than one P.V workgroup's 52 column tiles: several column blocks
+    ("rv2048_two_blocks", 2, 32, 32, 700, [32] * 32, 2048, torch.float16, "ragged"),
+    ("rv8192_max_bf16", 1, 32, 8, 300, [64] * 8, 8192, torch.bfloat16, "ragged"),
 ]
 
 
@@ -106,10 +109,11 @@ def test_k_logits_matches_oracle():
     assert mr <= 1e-3 and mx <= 2e-2 * float(ref.abs().max()), (mx, mr)
 
 
-def test_pv_latent_matches_oracle():
+@pytest.mark.parametrize("Rv", [1640, 3000])
+def test_pv_latent_matches_oracle(Rv):
     from starkv import pv_latent
     g = torch.Generator(device="cuda").manual_seed(6)
-    B, H, S, Rv = 3, 32, 2000, 1640
+    B, H, S = 3, 32, 2000
     p = torch.softmax(torch.randn(B, H, S, device="cuda", generator=g), -1).half()
     xv = torch.randn(B, S, Rv, device="cuda", generator=g).half()
     out = pv_latent(p, xv)
