@@ -126,26 +126,38 @@ def build_workload(name, dev):
         B, Hq, Hkv, Rv = 1, 32, 8, 512
         rope = RopeConfig(theta=500000.0, rope_type="llama3", factor=8.0, low_freq_factor=1.0,
                           high_freq_factor=4.0, original_max_position_embeddings=8192)
-        case = make_case(B, Hq, Hkv, S, ranks, Rv, dtype=torch.bfloat16, device=dev, seed=5)
         G = (Rv + 63) // 64
-        g = torch.Generator(device=dev).manual_seed(6)
-        vp = torch.randint(0, 256, (B, S, Rv // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
-        vs = (torch.rand(B, S, G, generator=g, device=dev) * 0.3 + 0.05).half()
-        vz = (-torch.rand(B, S, G, generator=g, device=dev) * 2).half()
-        vspec = VLatentSpec.int4_g64(vp, vs, vz, Rv)
-        out = torch.empty(B, Hq, HEAD_DIM, dtype=torch.bfloat16, device=dev)
-
-        def step(ev=None):
-            decode_attention(case.q, case.kspec, vspec, case.uv, rope=rope, out=out, events=ev)
         xk = B * S * sum(ranks) * 2
         xv = B * S * Rv // 2 + B * S * G * 4
         nb = {"k_logits": xk + sum(ranks) * HEAD_DIM * 2 + B * Hq * HEAD_DIM * 2, "pv_latent": xv,
               "up_proj": Hkv * HEAD_DIM * Rv * 2 + B * Hq * HEAD_DIM * 2,
               "total": xk + xv + sum(ranks) * HEAD_DIM * 2 + Hkv * HEAD_DIM * Rv * 2 + 2 * B * Hq * HEAD_DIM * 2}
+        # the whole working set of one step is ~0.2 GB at S=131072 and less below,
+        # inside the 256 MB MALL: steps rotate over copies of every input (latents,
+        # scales, weights, q) that together span >= 512 MB, so each step streams
+        # its bytes from HBM
+        n_copies = max(1, min(1024, -(-(512 << 20) // nb["total"])))
+        copies = []
+        g = torch.Generator(device=dev).manual_seed(6)
+        for c in range(n_copies):
+            case = make_case(B, Hq, Hkv, S, ranks, Rv, dtype=torch.bfloat16, device=dev, seed=5 + c)
+            vp = torch.randint(0, 256, (B, S, Rv // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+            vs = (torch.rand(B, S, G, generator=g, device=dev) * 0.3 + 0.05).half()
+            vz = (-torch.rand(B, S, G, generator=g, device=dev) * 2).half()
+            copies.append((case, VLatentSpec.int4_g64(vp, vs, vz, Rv)))
+        case = copies[0][0]
+        out = torch.empty(B, Hq, HEAD_DIM, dtype=torch.bfloat16, device=dev)
+        turn = [0]
+
+        def step(ev=None):
+            c, vspec = copies[turn[0] % n_copies]
+            turn[0] += 1
+            decode_attention(c.q, c.kspec, vspec, c.uv, rope=rope, out=out, events=ev)
         cfg = {"workload": f"{name}: Llama-3.1-8B-shaped GQA layer (32 q / 8 KV heads, llama3 RoPE theta 500000), "
                            f"bf16, batch 1, context {S}, K ranks per KV head in [32,128] (bf16), V rank 512 int4 "
                            f"asymmetric g64",
-               "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": Hq, "kv_heads": Hkv}
+               "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": Hq, "kv_heads": Hkv,
+               "rotated_input_copies": n_copies}
         return dict(case=case, bytes=nb, step=step, B=B, S=S, rope=rope, dtype="bf16", config=cfg)
     raise SystemExit(f"unknown workload {name!r}")
 
