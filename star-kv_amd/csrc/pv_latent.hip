@@ -64,9 +64,10 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 __device__ inline h2v as_h2(uint32_t u) { return __builtin_bit_cast(h2v, u); }
 __device__ inline uint32_t as_u32(h2v h) { return __builtin_bit_cast(uint32_t, h); }
 
-// Eight dequantised fp16 values of one chunk, packed two per dword (even rank
-// in the low half).  kind8: the bytes are int8 (x, y), else eight int4
-// nibbles in x, rank 2k in the low nibble of byte k.
+// Eight dequantised fp16 values of one chunk, packed two per dword.  kind8:
+// the bytes are int8 (x, y), else eight int4 nibbles in x, rank 2k in the low
+// nibble of byte k.  Ranks in order (0..7), except group-64 int4: ranks
+// 0 2 4 6 1 3 5 7 (pv_g64_rank maps an LDS column back to its rank).
 template <int VQ>
 __device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16) {
   const h2v s = as_h2((uint32_t)s16 * 0x10001u);
@@ -79,19 +80,30 @@ __device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16
     pr[2] = (y & 0xFFu) | ((y << 8) & 0xFF0000u);
     pr[3] = ((y >> 16) & 0xFFu) | ((y >> 8) & 0xFF0000u);
     bias = (_Float16)-1152.0f;                                       // 1024 + 128
+  } else if (VQ == VQ_G64) {
+    // even ranks (low nibbles) and odd ranks (high nibbles) as bytes; one
+    // v_perm per pair of same-parity ranks places two of them under the
+    // exponent byte 0x64 (selector 4 picks a byte of the 0x64646464 source)
+    const uint32_t lo = q.x & 0x0F0F0F0Fu, hi = (q.x >> 4) & 0x0F0F0F0Fu;
+    pr[0] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);     // ranks 0, 2
+    pr[1] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);     // ranks 4, 6
+    pr[2] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);     // ranks 1, 3
+    pr[3] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);     // ranks 5, 7
+    bias = (_Float16)-1024.0f;
   } else {
     // low nibbles (even ranks) and high nibbles (odd ranks) as bytes; one
     // v_perm per pair puts byte k of each under a zero byte
     const uint32_t lo = q.x & 0x0F0F0F0Fu, hi = (q.x >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
     for (int k = 0; k < 4; ++k) pr[k] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u + 0x00010001u * k);
-    bias = VQ == VQ_BLOCK ? (_Float16)-1032.0f : (_Float16)-1024.0f;  // nibble - 8 | nibble
+    bias = (_Float16)-1032.0f;                                       // nibble - 8
   }
   const h2v b2 = {bias, bias};
+  const uint32_t ebyte = VQ == VQ_G64 ? 0u : 0x64006400u;            // group-64: already in place
   uint32_t o[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const h2v n = as_h2(pr[k] | 0x64006400u) + b2;                     // exact small integers
+    const h2v n = as_h2(pr[k] | ebyte) + b2;                           // exact small integers
     if constexpr (VQ == VQ_G64) {
       const h2v zz = as_h2((uint32_t)z16 * 0x10001u);
       o[k] = as_u32(__builtin_elementwise_fma(n, s, zz));
@@ -101,6 +113,10 @@ __device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
+
+// group-64 int4 chunks sit in LDS as ranks 0 2 4 6 1 3 5 7: the rank of LDS
+// column n (within a 32-column tile)
+__device__ inline int pv_g64_rank(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
 
 __device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
   const uint32_t w[4] = {h.x, h.y, h.z, h.w};
@@ -409,7 +425,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
-        part[(int64_t)q * Rvp + col0 + 32 * j + n] = acc[j][v];
+        part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = acc[j][v];
       }
     }
   }
