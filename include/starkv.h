@@ -268,6 +268,43 @@ typedef struct {
 int starkv_k_append(const starkv_k_append_desc* d, void* stream);
 int starkv_v_append(const starkv_v_append_desc* d, void* stream);
 
+/* ---------------------------------------------------------------------
+ * starkv_prefill_attention — replaces the reference prefill branch
+ * model.py:429-449 (materialise key_full = RoPE(X_k @ B_k) and
+ * value_full = X_v @ U_v^T, repeat over GQA groups, then SDPA), with the
+ * causal mask the reference leaves to the caller's attention_mask (without
+ * one its SDPA call attends to future tokens):
+ *   out[b, q, t, :] = sum_{s <= pos0 + t} softmax_s(scale * q_rot[b,q,t] . K[b,q//gs,s]) V[b,q//gs,s]
+ *   K[b,h,s] = RoPE_s(X_k[b,h,s] @ B_k[h]),  V[b,h,s] = U_v[h] @ X_v[b,s]
+ * over the pos0 + n_tokens cached positions (the n_tokens new queries sit at
+ * positions pos0 .. pos0 + n_tokens - 1; the latents of every position up to
+ * the last one must already be in the caches, e.g. by starkv_k_append /
+ * starkv_v_append).  q: rotated queries, act dtype, element (b,q,t,d) at
+ * q + b*q_stride_b + q*q_stride_h + t*q_stride_t + d (16-byte aligned, strides
+ * multiples of 8).  out likewise with out_stride_*, act dtype.
+ * K latent: STARKV_FMT_DENSE (ranks, offsets and pitches multiples of 8,
+ * data 16-byte aligned) or STARKV_FMT_INT8_SYM; V latent: STARKV_FMT_DENSE
+ * (rank and strides multiples of 8, data 16-byte aligned) or
+ * STARKV_FMT_INT4_G64; other formats STARKV_ERR_FORMAT.  uv: 16-byte aligned,
+ * row stride a multiple of 8.  Quantised latents are dequantised bit-exactly
+ * as in decode.  The workspace holds the reconstructed K and V
+ * (2 x batch x Hkv x round_up(pos0 + n_tokens, 64) x 128 act-dtype elements).
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int batch, n_q_heads, head_dim, n_tokens, pos0;
+  int dtype;
+  const void* q; int64_t q_stride_b, q_stride_h, q_stride_t;
+  starkv_klatent k;
+  starkv_vlatent v;
+  const void* uv; int64_t uv_row_stride;
+  const void* rope_table; int rope_max_positions;
+  float scale;
+  void* out; int64_t out_stride_b, out_stride_h, out_stride_t;
+} starkv_prefill_desc;
+
+size_t starkv_prefill_workspace_bytes(const starkv_prefill_desc* d);
+int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,6 +19,8 @@ decode path of the reference:
   (model.py:458-470);
 * the "reorder" value path: ``P @ Xv`` then the per-KV-head up-projection
   (model.py:482-487);
+* the prefill branch: K / V materialised from the latents, GQA repeat and
+  SDPA (model.py:429-449), under the causal mask HF passes it;
 * the quantised-cache formats (numpy, integer exact): the reference's int4
   nibble convention (bx_quant.py:75-86) and the build's own int8 / int4-g64
   formats (the reference's ``quant_utils`` is absent, bx_quant.py:18).
@@ -36,6 +38,11 @@ How each function is pinned (tests/test_oracle.py):
 * ``decode_attention``: torch ``scaled_dot_product_attention`` on fully
   materialised K and V (the reorder identity (P Xv) Uv^T == P (Xv Uv^T),
   LlamaLoRaAttention_headwise.py:16, 126-142).
+* ``reconstruct_kv`` / ``prefill_attention``: torch SDPA with
+  ``is_causal=True`` on K / V materialised per query head (pos0 = 0);
+  chunked prefill (pos0 > 0) equals the matching rows of the full prefill;
+  the last query's row equals ``decode_attention``; planted off-by-one mask
+  and transposed V head layout are caught.
 * int4 unpack (reference convention): hand-computed known answers for chosen
   bytes (nibble order, bias 8) and the exhaustive 256-byte table against an
   arithmetic (divmod) decomposition; dequant rounding against torch's own
@@ -168,6 +175,51 @@ def decode_attention(q, bk, xk, xv, uv_weight, cos, sin, mask=None, dtype=torch.
     o_lat = pv_latent(p, xv)
     out = up_proj(o_lat, uv_weight, len(bk))
     return out, p, o_lat
+
+
+# --------------------------------------------------------------------------
+# Prefill path
+# --------------------------------------------------------------------------
+
+def reconstruct_kv(bk: Sequence[torch.Tensor], xk: Sequence[torch.Tensor], xv: torch.Tensor,
+                   uv_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, dtype=torch.float64):
+    """Materialised K and V of the reference's prefill (model.py:431-444):
+    key_full = RoPE_s(X_k[s] @ B_k) per KV head (k_u^T, 431-432) and
+    value_full = (X_v @ U_v^T) viewed [B, S, Hkv, D] -> [B, Hkv, S, D]
+    (438-442).  Returns (K, V), both [B, Hkv, S, D] (before the GQA repeat)."""
+    Hkv = len(bk)
+    B, S, Rv = xv.shape
+    c, s = cos[:S].to(dtype), sin[:S].to(dtype)
+    K = torch.stack([apply_rope(xk[h].to(dtype) @ bk[h].to(dtype), c, s) for h in range(Hkv)], dim=1)
+    V = (xv.to(dtype) @ uv_weight.to(dtype).t()).view(B, S, Hkv, HEAD_DIM).transpose(1, 2)
+    return K, V
+
+
+def prefill_attention(q: torch.Tensor, bk, xk, xv, uv_weight, cos, sin, pos0: int = 0,
+                      scale: Optional[float] = None, dtype=torch.float64) -> torch.Tensor:
+    """Causal prefill over the latent caches: queries q [B, Hq, T, D] (already
+    rotated) at positions pos0 .. pos0+T-1; query t attends to keys
+    s <= pos0 + t of the first pos0 + T cached positions.  This is the
+    reference's prefill (model.py:429-449: materialise, repeat_interleave over
+    the GQA group, SDPA with scale) under HF's causal attention mask.
+    Returns [B, Hq, T, D]."""
+    B, Hq, T, D = q.shape
+    S = pos0 + T
+    K, V = reconstruct_kv(bk, [x[:, :S] for x in xk], xv[:, :S], uv_weight, cos, sin, dtype)
+    gs = Hq // len(bk)
+    K = K.repeat_interleave(gs, dim=1)
+    V = V.repeat_interleave(gs, dim=1)
+    sc = 1.0 / math.sqrt(D) if scale is None else scale
+    logits = (q.to(dtype) @ K.transpose(-1, -2)) * sc                     # [B, Hq, T, S]
+    logits = logits.masked_fill(~causal_visible(T, S, pos0), float("-inf"))
+    return torch.softmax(logits, dim=-1) @ V
+
+
+def causal_visible(T: int, S: int, pos0: int) -> torch.Tensor:
+    """[T, S] bool: query t (position pos0 + t) sees key s iff s <= pos0 + t
+    (HF's causal mask, the mask the reference's SDPA call expects from its
+    caller, model.py:445-449)."""
+    return torch.arange(S)[None, :] <= (pos0 + torch.arange(T))[:, None]
 
 
 def uniform_heads(x: torch.Tensor) -> List[torch.Tensor]:

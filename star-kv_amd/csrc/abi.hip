@@ -447,6 +447,48 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
   return STARKV_OK;
 }
 
+// Prefill: dense (16-byte rows) or int8 K latents, dense (16-byte rows) or
+// group-64 int4 V latents; q, U_v 16-byte aligned.  Positions reconstructed:
+// pos0 + n_tokens, padded to 64 in the workspace.
+int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->batch > 65535 || d->n_tokens < 1 || d->pos0 < 0) return STARKV_ERR_SHAPE;
+  if ((int64_t)d->pos0 + d->n_tokens > MAX_S) return STARKV_ERR_LIMIT;
+  if (d->head_dim != HEAD_DIM) return STARKV_ERR_SHAPE;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  int st = validate_klatent(d->k, d->n_q_heads, d->dtype, gs);
+  if (st) return st;
+  const starkv_klatent& k = d->k;
+  if (k.format != STARKV_FMT_DENSE && k.format != STARKV_FMT_INT8_SYM) return STARKV_ERR_FORMAT;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    if (k.rank[h] % 8) return STARKV_ERR_SHAPE;
+    if (k.format == STARKV_FMT_DENSE && (!al64(k.head_offset[h], 8) || !al64(k.pos_stride[h], 8)))
+      return STARKV_ERR_ALIGN;
+  }
+  if (k.format == STARKV_FMT_DENSE && (!al(k.data, 16) || !al64(k.stride_b, 8))) return STARKV_ERR_ALIGN;
+  PVArgs vtmp = {};
+  int vq = 0;
+  if ((st = validate_v(d->v, vtmp, &vq))) return st;
+  if (vq != VQ_DENSE && vq != VQ_G64) return STARKV_ERR_FORMAT;
+  if (d->v.rank % 8) return STARKV_ERR_SHAPE;
+  if (vq == VQ_DENSE && (!al(d->v.data, 16) || !al64(d->v.stride_s, 8) || !al64(d->v.stride_b, 8)))
+    return STARKV_ERR_ALIGN;
+  if (!d->q || !d->uv || !d->out || !d->rope_table) return STARKV_ERR_NULL;
+  if ((int64_t)d->pos0 + d->n_tokens > d->rope_max_positions) return STARKV_ERR_SHAPE;
+  if (d->uv_row_stride < d->v.rank) return STARKV_ERR_SHAPE;
+  if (!al(d->uv, 16) || !al64(d->uv_row_stride, 8)) return STARKV_ERR_ALIGN;
+  if (d->q_stride_b < 0 || d->q_stride_h < 0 || d->q_stride_t < 0) return STARKV_ERR_SHAPE;
+  if (!al(d->q, 16) || !al64(d->q_stride_b, 8) || !al64(d->q_stride_h, 8) || !al64(d->q_stride_t, 8))
+    return STARKV_ERR_ALIGN;
+  if (d->out_stride_b < 0 || d->out_stride_h < 0 || d->out_stride_t < 0) return STARKV_ERR_SHAPE;
+  *S_pad = round_up((int64_t)d->pos0 + d->n_tokens, 64);
+  return STARKV_OK;
+}
+
+size_t prefill_kv_bytes(const starkv_prefill_desc* d, int64_t S_pad) {
+  return a256((size_t)d->batch * d->k.n_kv_heads * S_pad * HEAD_DIM * 2);
+}
+
 }  // namespace
 
 extern "C" {
@@ -669,6 +711,49 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   a.data2 = (void*)pa.x2; a.stride2_b = pa.x2_sb; a.stride2_s = pa.x2_ss;
   a.scale2 = (void*)pa.xs2; a.sc2_sb = pa.xs2_sb; a.sc2_ss = pa.xs2_ss;
   return launch_v_append(a, d->dtype, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+size_t starkv_prefill_workspace_bytes(const starkv_prefill_desc* d) {
+  int gs = 0;
+  int64_t S_pad = 0;
+  if (validate_prefill(d, &gs, &S_pad)) return 0;
+  return 2 * prefill_kv_bytes(d, S_pad);
+}
+
+int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  int gs = 0, st;
+  int64_t S_pad = 0;
+  if ((st = validate_prefill(d, &gs, &S_pad))) return st;
+  const size_t kvb = prefill_kv_bytes(d, S_pad);
+  if (!workspace || workspace_bytes < 2 * kvb) return STARKV_ERR_WORKSPACE;
+  if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
+  const starkv_klatent& k = d->k;
+  PFArgs a = {};
+  a.S = d->pos0 + d->n_tokens; a.S_pad = (int)S_pad;
+  a.Hkv = k.n_kv_heads; a.Hq = d->n_q_heads; a.gs = gs; a.T = d->n_tokens; a.pos0 = d->pos0;
+  a.kx = k.data; a.kx_sb = k.stride_b; a.k_i8 = k.format == STARKV_FMT_INT8_SYM;
+  a.kscale = k.scale; a.ks_sb = k.scale_stride_b; a.ks_sh = k.scale_stride_h;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    a.krank[h] = k.rank[h];
+    a.kxoff[h] = k.head_offset[h]; a.kxpitch[h] = k.pos_stride[h];
+    a.bkoff[h] = k.bk_head_offset[h];
+  }
+  a.bk = k.bk; a.bk_rs = k.bk_row_stride;
+  const starkv_vlatent& v = d->v;
+  a.vx = v.data; a.vx_sb = v.stride_b; a.vx_ss = v.stride_s;
+  a.v_g64 = v.format == STARKV_FMT_INT4_G64; a.Rv = v.rank;
+  a.vscale = v.scale; a.vzero = v.zero; a.vs_sb = v.scale_stride_b; a.vs_ss = v.scale_stride_s;
+  a.uv = d->uv; a.uv_rs = d->uv_row_stride;
+  a.rope = d->rope_table;
+  a.kbuf = workspace; a.vbuf = (char*)workspace + kvb;
+  a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h; a.q_st = d->q_stride_t;
+  a.scale_log2 = d->scale * 1.4426950408889634f;
+  a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h; a.o_st = d->out_stride_t;
+  return launch_prefill(a, d->dtype, d->batch, (hipStream_t)stream);
 }
 
 }  // extern "C"

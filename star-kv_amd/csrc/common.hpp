@@ -141,6 +141,30 @@ struct UPArgs {
 };
 
 // ---------------------------------------------------------------------------
+// Prefill arguments (prefill.hip).
+// ---------------------------------------------------------------------------
+struct PFArgs {
+  int S, S_pad, Hkv, Hq, gs, T, pos0;              // S = pos0 + T positions reconstructed, S_pad = round_up(S, 64)
+  // K latent: dense act dtype (offsets / pitches in elements) or int8 (bytes) with fp16 scales (b, h, s)
+  const void* kx; int64_t kx_sb; int k_i8;
+  const void* kscale; int64_t ks_sb, ks_sh;
+  int krank[K_MAX_KV];
+  int64_t kxoff[K_MAX_KV];
+  int64_t kxpitch[K_MAX_KV];
+  const void* bk; int64_t bk_rs;
+  int64_t bkoff[K_MAX_KV];
+  // V latent: dense act dtype (elements) or group-64 int4 (bytes) with fp16 scale / zero (b, s, g)
+  const void* vx; int64_t vx_sb, vx_ss; int v_g64, Rv;
+  const void* vscale; const void* vzero; int64_t vs_sb, vs_ss;
+  const void* uv; int64_t uv_rs;                   // [Hkv*128][Rv]
+  const void* rope;                                // RoPE table (rope.hip layout)
+  void* kbuf; void* vbuf;                          // [B][Hkv][S_pad][128] act dtype
+  const void* q; int64_t q_sb, q_sh, q_st;         // rotated queries (b, qh, t)
+  float scale_log2;                                // softmax scale * log2(e)
+  void* out; int64_t o_sb, o_sh, o_st;             // (b, qh, t), act dtype
+};
+
+// ---------------------------------------------------------------------------
 // small helpers
 // ---------------------------------------------------------------------------
 template <typename T> struct ElemTraits;
@@ -236,5 +260,6 @@ int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);
+int launch_prefill(const PFArgs& a, int dtype, int B, hipStream_t st);
 
 }  // namespace starkv

@@ -119,6 +119,22 @@ class VAppendDesc(ctypes.Structure):
     ]
 
 
+class PrefillDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int), ("n_q_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("n_tokens", ctypes.c_int),
+        ("pos0", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("q", ctypes.c_void_p), ("q_stride_b", ctypes.c_int64), ("q_stride_h", ctypes.c_int64),
+        ("q_stride_t", ctypes.c_int64),
+        ("k", KLatent),
+        ("v", VLatent),
+        ("uv", ctypes.c_void_p), ("uv_row_stride", ctypes.c_int64),
+        ("rope_table", ctypes.c_void_p), ("rope_max_positions", ctypes.c_int),
+        ("scale", ctypes.c_float),
+        ("out", ctypes.c_void_p), ("out_stride_b", ctypes.c_int64), ("out_stride_h", ctypes.c_int64),
+        ("out_stride_t", ctypes.c_int64),
+    ]
+
+
 EXPORTS = (
     "starkv_abi_version", "starkv_status_string",
     "starkv_rope_table_bytes", "starkv_rope_build",
@@ -126,6 +142,7 @@ EXPORTS = (
     "starkv_pv_latent_workspace_bytes", "starkv_pv_latent",
     "starkv_decode_workspace_bytes", "starkv_decode_attention", "starkv_decode_attention_timed",
     "starkv_k_append", "starkv_v_append",
+    "starkv_prefill_workspace_bytes", "starkv_prefill_attention",
 )
 
 _lib = None
@@ -148,11 +165,12 @@ def lib() -> ctypes.CDLL:
     L.starkv_rope_build.restype = ctypes.c_int
     L.starkv_rope_build.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_float, ctypes.c_int,
                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-    for name, desc in (("k_logits", KLogitsDesc), ("pv_latent", PVDesc), ("decode", DecodeDesc)):
+    for name, desc in (("k_logits", KLogitsDesc), ("pv_latent", PVDesc), ("decode", DecodeDesc), ("prefill", PrefillDesc)):
         wsf = getattr(L, f"starkv_{name}_workspace_bytes")
         wsf.restype = ctypes.c_size_t
         wsf.argtypes = [ctypes.POINTER(desc)]
-    for name, desc in (("k_logits", KLogitsDesc), ("pv_latent", PVDesc), ("decode_attention", DecodeDesc)):
+    for name, desc in (("k_logits", KLogitsDesc), ("pv_latent", PVDesc), ("decode_attention", DecodeDesc),
+                       ("prefill_attention", PrefillDesc)):
         f = getattr(L, f"starkv_{name}")
         f.restype = ctypes.c_int
         f.argtypes = [ctypes.POINTER(desc), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]

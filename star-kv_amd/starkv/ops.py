@@ -14,6 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KAppendDesc,
+                   PrefillDesc,
                    KLatent, KLogitsDesc, PVDesc, StarKVError, VAppendDesc, VLatent, check, i64_array, int_array)
 from .rope import RopeConfig, rope_table
 
@@ -226,7 +227,7 @@ def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = R
     d.q, d.q_stride_b, d.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
     d.k = k.c_struct(keep)
     d.rope_table, d.rope_max_positions = table.data_ptr(), cap
-    d.scale = float(scale) * rope.attention_scaling
+    d.scale = float(scale)
     d.mask = m.data_ptr() if m is not None else None
     d.mask_dtype, d.mask_stride_b, d.mask_stride_h = mdt, msb, msh
     d.out, d.out_dtype, d.out_stride_b, d.out_stride_h = out.data_ptr(), _dt(out), out.stride(0), out.stride(1)
@@ -378,7 +379,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     d.v = v.c_struct()
     d.uv, d.uv_row_stride = uv_weight.data_ptr(), uv_weight.stride(0)
     d.rope_table, d.rope_max_positions = table.data_ptr(), cap
-    d.scale = float(scale if scale is not None else 1.0 / math.sqrt(HEAD_DIM)) * rope.attention_scaling
+    d.scale = float(scale if scale is not None else 1.0 / math.sqrt(HEAD_DIM))
     d.mask = m.data_ptr() if m is not None else None
     d.mask_dtype, d.mask_stride_b, d.mask_stride_h = mdt, msb, msh
     d.out, d.out_stride_b, d.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
@@ -399,6 +400,50 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
         handles = (ctypes.c_void_p * 4)(*[e.cuda_event for e in events])
         check(L.starkv_decode_attention_timed(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                               _stream(q.device), handles), "starkv_decode_attention_timed")
+    return out
+
+
+def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tensor,
+                      rope: RopeConfig = RopeConfig(), pos0: int = 0, scale: Optional[float] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal prefill attention over the latent caches (the reference's prefill
+    branch, model.py:429-449, with the causal mask applied): [B, Hq, T, 128]
+    in q's dtype.
+
+    q: rotated queries [B, Hq, T, 128] (last dim contiguous) at positions
+    pos0 .. pos0 + T - 1; k / xv: the K and V latent caches holding at least
+    pos0 + T positions (K dense or int8, V dense [B, S, Rv] or a group-64 int4
+    VLatentSpec); uv_weight: v_proj.U.weight [Hkv*128, Rv]."""
+    if q.dim() != 4 or q.shape[-1] != HEAD_DIM or q.stride(-1) != 1:
+        raise StarKVError("q must be [B, Hq, T, 128] with a contiguous last dim")
+    v = _vspec(xv)
+    _require_cuda(q, uv_weight, *k.tensors, *v.tensors)
+    B, Hq, T, _ = q.shape
+    if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape != (k.n_kv_heads * HEAD_DIM, v.rank):
+        raise StarKVError("uv_weight must be [Hkv*128, Rv] with a contiguous last dim")
+    if out is None:
+        out = torch.empty(B, Hq, T, HEAD_DIM, dtype=q.dtype, device=q.device)
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise StarKVError("out must be [B, Hq, T, 128] of q's dtype with a contiguous last dim")
+    table, cap = rope_table(rope, int(pos0) + T, q.device)
+    keep: list = []
+    d = PrefillDesc()
+    d.batch, d.n_q_heads, d.head_dim, d.n_tokens, d.pos0 = B, Hq, HEAD_DIM, T, int(pos0)
+    d.dtype = _dt(q)
+    d.q, d.q_stride_b, d.q_stride_h, d.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1), q.stride(2)
+    d.k = k.c_struct(keep)
+    d.v = v.c_struct()
+    d.uv, d.uv_row_stride = uv_weight.data_ptr(), uv_weight.stride(0)
+    d.rope_table, d.rope_max_positions = table.data_ptr(), cap
+    d.scale = float(scale if scale is not None else 1.0 / math.sqrt(HEAD_DIM))
+    d.out, d.out_stride_b, d.out_stride_h, d.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
+    L = _lib.lib()
+    nb = L.starkv_prefill_workspace_bytes(ctypes.byref(d))
+    if nb == 0:
+        check(L.starkv_prefill_attention(ctypes.byref(d), None, 0, _stream(q.device)), "starkv_prefill_attention")
+    ws = _workspace(q.device, nb)
+    check(L.starkv_prefill_attention(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q.device)),
+          "starkv_prefill_attention")
     return out
 
 

@@ -63,12 +63,17 @@ int main(void) {
   S(starkv_decode_desc) F(starkv_decode_desc, k) F(starkv_decode_desc, v) F(starkv_decode_desc, uv)
   F(starkv_decode_desc, rope_table) F(starkv_decode_desc, scale) F(starkv_decode_desc, mask) F(starkv_decode_desc, out_dtype)
   F(starkv_decode_desc, out_stride_h)
+  S(starkv_prefill_desc) F(starkv_prefill_desc, pos0) F(starkv_prefill_desc, dtype) F(starkv_prefill_desc, q)
+  F(starkv_prefill_desc, q_stride_t) F(starkv_prefill_desc, k) F(starkv_prefill_desc, v) F(starkv_prefill_desc, uv)
+  F(starkv_prefill_desc, rope_table) F(starkv_prefill_desc, scale) F(starkv_prefill_desc, out)
+  F(starkv_prefill_desc, out_stride_t)
   return 0;
 }
 """
 
 _PY = {"starkv_klatent": L.KLatent, "starkv_klogits_desc": L.KLogitsDesc, "starkv_vlatent": L.VLatent,
-       "starkv_pv_desc": L.PVDesc, "starkv_decode_desc": L.DecodeDesc}
+       "starkv_pv_desc": L.PVDesc, "starkv_decode_desc": L.DecodeDesc,
+       "starkv_prefill_desc": L.PrefillDesc}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
@@ -278,3 +283,70 @@ def test_cache_writer_validation():
     v.v.stride_s, v.v.data = 32, FAKE + 2
     assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_ALIGN
     assert lib.starkv_v_append(None, None) == ERR_NULL
+
+
+# ---------------------------------------------------------------- prefill validation
+
+def _prefill_desc(keep, B=2, Hq=8, Hkv=4, T=100, pos0=20, Rv=64, ranks=None):
+    ranks = ranks or [32] * Hkv
+    d = L.PrefillDesc()
+    d.batch, d.n_q_heads, d.head_dim, d.n_tokens, d.pos0, d.dtype = B, Hq, 128, T, pos0, L.F16
+    d.q, d.q_stride_b, d.q_stride_h, d.q_stride_t = FAKE, Hq * T * 128, T * 128, 128
+    d.k = _klatent(ranks, keep)
+    S = pos0 + T
+    d.v = L.VLatent(rank=Rv, format=L.FMT_DENSE, data=FAKE, stride_b=S * Rv, stride_s=Rv)
+    d.uv, d.uv_row_stride = FAKE, Rv
+    d.rope_table, d.rope_max_positions = FAKE, 4096
+    d.scale = 128 ** -0.5
+    d.out, d.out_stride_b, d.out_stride_h, d.out_stride_t = FAKE, Hq * T * 128, T * 128, 128
+    return d
+
+
+def test_prefill_workspace_holds_the_reconstructed_k_and_v():
+    keep = []
+    d = _prefill_desc(keep)
+    need = L.lib().starkv_prefill_workspace_bytes(ctypes.byref(d))
+    assert need == 2 * 2 * 4 * 128 * 128 * 2          # B * Hkv * round_up(120, 64) * 128 fp16, twice
+    call = lambda ws, n: L.lib().starkv_prefill_attention(ctypes.byref(d), ws, n, None)
+    assert call(None, 0) == ERR_WORKSPACE
+    assert call(FAKE, need - 1) == ERR_WORKSPACE
+    assert call(FAKE + 16, need) == ERR_ALIGN
+
+
+@pytest.mark.parametrize("what,code", [
+    ("n_tokens0", ERR_SHAPE), ("pos0_neg", ERR_SHAPE), ("rope_short", ERR_SHAPE), ("head_dim", ERR_SHAPE),
+    ("k_int4", ERR_FORMAT), ("v_int8", ERR_FORMAT), ("k_rank_odd", ERR_SHAPE), ("v_rank_odd", ERR_SHAPE),
+    ("q_stride", ERR_ALIGN), ("q_null", ERR_NULL), ("uv_stride", ERR_ALIGN), ("gqa", ERR_SHAPE),
+    ("dtype", ERR_DTYPE),
+])
+def test_prefill_rejects(what, code):
+    keep = []
+    d = _prefill_desc(keep)
+    if what == "n_tokens0":
+        d.n_tokens = 0
+    elif what == "pos0_neg":
+        d.pos0 = -1
+    elif what == "rope_short":
+        d.rope_max_positions = 119
+    elif what == "head_dim":
+        d.head_dim = 64
+    elif what == "k_int4":
+        d.k.format, d.k.scale = L.FMT_INT4_REF, FAKE
+    elif what == "v_int8":
+        d.v.format, d.v.scale = L.FMT_INT8_SYM, FAKE
+    elif what == "k_rank_odd":
+        d.k.rank[2] = 20
+    elif what == "v_rank_odd":
+        d.v.rank, d.uv_row_stride = 60, 60
+    elif what == "q_stride":
+        d.q_stride_t = 132
+    elif what == "q_null":
+        d.q = None
+    elif what == "uv_stride":
+        d.uv_row_stride = 68
+    elif what == "gqa":
+        d.n_q_heads = 6
+    elif what == "dtype":
+        d.dtype = L.F32
+    assert L.lib().starkv_prefill_attention(ctypes.byref(d), FAKE, 1 << 30, None) == code
+    assert L.lib().starkv_prefill_workspace_bytes(ctypes.byref(d)) == 0

@@ -1,0 +1,150 @@
+"""GPU parity of the causal prefill over the latent caches
+(starkv_prefill_attention; the reference's prefill branch model.py:429-449
+under a causal mask) against the CPU oracle's prefill_attention.
+
+Inputs are rounded to the act dtype first and the oracle runs in float64 on
+those values (quantised latents: on the oracle-dequantised fp16 values,
+rounded to bf16 for bf16 cases, as the kernel dequantises).  Tolerances:
+fp16 max-abs 2e-2 and mean-rel 1e-3; bf16 (K, V and the output each stored in
+bf16, unit roundoff 2^-9) max-abs 4e-2 and mean-rel 6e-3.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from _util import errors
+
+HEAD = 128
+TOL = {torch.float16: (2e-2, 1e-3), torch.bfloat16: (4e-2, 6e-3)}
+
+
+def _flush(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _dense_k(B, S, ranks, dtype, g):
+    """Ragged dense K latent: one buffer [B, S*sum(r)], head h at S*cumsum(r)[h]."""
+    from starkv import KLatentSpec
+    per_b = S * sum(ranks)
+    buf = torch.randn(B, per_b, generator=g, device="cuda").to(dtype)
+    offs = list(np.cumsum([0] + ranks[:-1]) * S)
+    heads = [buf[:, o:o + S * r].view(B, S, r) for o, r in zip(offs, ranks)]
+    return buf, offs, heads
+
+
+def _bk(ranks, dtype, g):
+    bk_all = torch.empty(sum(ranks), HEAD, device="cuda")
+    bko, heads, row = [], [], 0
+    for r in ranks:
+        bk_all[row:row + r] = torch.randn(r, HEAD, generator=g, device="cuda") / math.sqrt(r)
+        bko.append(row * HEAD)
+        row += r
+    bk_all = bk_all.to(dtype)
+    row = 0
+    for r in ranks:
+        heads.append(bk_all[row:row + r])
+        row += r
+    return bk_all, bko, heads
+
+
+def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0):
+    from oracle import starkv_oracle as o
+    from starkv import KLatentSpec, RopeConfig, prefill_attention
+    from starkv._lib import FMT_INT8_SYM
+    _flush(f"[prefill] B={B} Hq={Hq} Hkv={len(ranks)} T={T} pos0={pos0} Rv={Rv} {dtype} K={kfmt} V={vfmt}")
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Hkv = len(ranks)
+    S = pos0 + T
+    bk_all, bko, bk_heads = _bk(ranks, dtype, g)
+    if kfmt == "dense":
+        buf, offs, xk_dev = _dense_k(B, S, ranks, dtype, g)
+        kspec = KLatentSpec(buf, ranks, offs, ranks, buf.stride(0), bk_all, bko, HEAD)
+        xk = [x.double().cpu() for x in xk_dev]
+    else:
+        from test_gpu_quant_k import ragged_int8_k
+        kb, scales, offs, deq = ragged_int8_k(B, S, ranks, seed=seed + 1)
+        sc = torch.from_numpy(scales).cuda()
+        kspec = KLatentSpec(torch.from_numpy(kb).cuda(), ranks, offs, ranks, kb.shape[1], bk_all, bko, HEAD,
+                            fmt=FMT_INT8_SYM, scale=sc, scale_stride_b=sc.stride(0), scale_stride_h=sc.stride(1))
+        xk = [d.to(dtype).double() for d in deq]
+    if vfmt == "dense":
+        xv_dev = torch.randn(B, S, Rv, generator=g, device="cuda").to(dtype)
+        v = xv_dev
+        xv = xv_dev.double().cpu()
+    else:
+        from test_gpu_quant import make_quant_v
+        v, dq, _ = make_quant_v("g64", B, S, Rv, seed=seed + 2)
+        xv = torch.from_numpy(dq.astype(np.float64)).to(dtype).double()
+    uv = (torch.randn(Hkv * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).to(dtype)
+    q = torch.randn(B, Hq, T, HEAD, generator=g, device="cuda").to(dtype)
+    rope = RopeConfig()
+    out = prefill_attention(q, kspec, v, uv, rope=rope, pos0=pos0)
+    torch.cuda.synchronize()
+    cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), rope.attention_scaling)
+    ref = o.prefill_attention(q.double().cpu(), [b.double().cpu() for b in bk_heads], xk, xv, uv.double().cpu(),
+                              cos.double(), sin.double(), pos0=pos0)
+    assert torch.isfinite(out).all()
+    mx, mr = errors(out, ref)
+    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    tmx, tmr = TOL[dtype]
+    assert mx <= tmx and mr <= tmr, (mx, mr)
+    return out
+
+
+CASES = [
+    # name, B, Hq, ranks, Rv, T, pos0, dtype, K format, V format
+    ("mha_ragged_f16", 2, 4, [8, 24, 64, 128], 96, 200, 0, torch.float16, "dense", "dense"),
+    ("gqa4_bf16", 2, 8, [32, 80], 160, 300, 0, torch.bfloat16, "dense", "dense"),
+    ("chunk_pos0", 1, 8, [16, 40], 64, 77, 150, torch.float16, "dense", "dense"),
+    ("one_token", 2, 4, [24, 8, 128, 56], 40, 1, 500, torch.float16, "dense", "dense"),
+    ("t1024_f16", 1, 2, [48, 128], 256, 1024, 0, torch.float16, "dense", "dense"),
+    ("int8k_g64v_f16", 2, 4, [64, 32, 96, 128], 200, 129, 0, torch.float16, "int8", "g64"),
+    ("int8k_g64v_bf16_chunk", 1, 8, [32, 128], 1640, 96, 64, torch.bfloat16, "int8", "g64"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_prefill_matches_oracle(case):
+    _run(*case[1:])
+
+
+@pytest.mark.gpu
+def test_prefill_last_row_matches_decode():
+    """The last prefill query is the decode step over the same caches."""
+    from starkv import KLatentSpec, RopeConfig, decode_attention, prefill_attention
+    _flush("[prefill] last row vs decode")
+    g = torch.Generator(device="cuda").manual_seed(7)
+    B, Hq, ranks, Rv, T = 2, 8, [40, 104], 120, 333
+    bk_all, bko, _ = _bk(ranks, torch.float16, g)
+    buf, offs, _ = _dense_k(B, T, ranks, torch.float16, g)
+    kspec = KLatentSpec(buf, ranks, offs, ranks, buf.stride(0), bk_all, bko, HEAD)
+    xv = torch.randn(B, T, Rv, generator=g, device="cuda").half()
+    uv = (torch.randn(len(ranks) * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).half()
+    q = torch.randn(B, Hq, T, HEAD, generator=g, device="cuda").half()
+    pre = prefill_attention(q, kspec, xv, uv, rope=RopeConfig())
+    dec = decode_attention(q[:, :, -1].contiguous(), kspec, xv, uv, rope=RopeConfig(), out_dtype=torch.float32)
+    mx, mr = errors(pre[:, :, -1], dec)
+    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mx <= 2e-2 and mr <= 2e-3, (mx, mr)
+
+
+@pytest.mark.gpu
+def test_prefill_rejects_unsupported_formats():
+    from starkv import KLatentSpec, StarKVError, VLatentSpec, prefill_attention
+    from starkv._lib import FMT_INT4_REF
+    g = torch.Generator(device="cuda").manual_seed(3)
+    bk_all, bko, _ = _bk([16], torch.float16, g)
+    kb = torch.zeros(1, 64 * 8, dtype=torch.uint8, device="cuda")
+    sc = torch.ones(1, 1, 64, dtype=torch.float16, device="cuda")
+    kspec = KLatentSpec(kb, [16], [0], [8], kb.stride(0), bk_all, bko, HEAD, fmt=FMT_INT4_REF, scale=sc,
+                        scale_stride_b=64, scale_stride_h=64)
+    xv = torch.zeros(1, 64, 16, dtype=torch.float16, device="cuda")
+    uv = torch.zeros(HEAD, 16, dtype=torch.float16, device="cuda")
+    q = torch.zeros(1, 1, 64, HEAD, dtype=torch.float16, device="cuda")
+    with pytest.raises(StarKVError, match="format"):
+        prefill_attention(q, kspec, xv, uv)

@@ -181,8 +181,68 @@ def test_decode_attention_matches_sdpa(with_mask):
 
 
 # --------------------------------------------------------------------------
+# prefill (model.py:429-449 under a causal mask)
+# --------------------------------------------------------------------------
+
+def _prefill_case(seed, B=2, Hkv=2, gs=2, S=29, Rv=24, ranks=(8, 16)):
+    g = torch.Generator().manual_seed(seed)
+    bk = [torch.randn(r, D, generator=g, dtype=torch.float64) / math.sqrt(r) for r in ranks]
+    xk = [torch.randn(B, S, r, generator=g, dtype=torch.float64) for r in ranks]
+    xv = torch.randn(B, S, Rv, generator=g, dtype=torch.float64)
+    uv = torch.randn(Hkv * D, Rv, generator=g, dtype=torch.float64) / math.sqrt(Rv)
+    q = torch.randn(B, Hkv * gs, S, D, generator=g, dtype=torch.float64)
+    cos, sin = [t.double() for t in o.rope_cos_sin(o.rope_inv_freq(), torch.arange(S))]
+    return q, bk, xk, xv, uv, cos, sin
+
+
+def test_prefill_matches_causal_sdpa():
+    """pos0 = 0: torch SDPA with is_causal=True on K / V materialised per
+    query head by the decode pin's own route."""
+    q, bk, xk, xv, uv, cos, sin = _prefill_case(11)
+    B, Hq, S, _ = q.shape
+    gs = Hq // len(bk)
+    U = uv.view(len(bk), D, -1)
+    ref = torch.stack([torch.nn.functional.scaled_dot_product_attention(
+        q[:, qh], o.apply_rope(xk[qh // gs] @ bk[qh // gs], cos, sin), xv @ U[qh // gs].t(), is_causal=True)
+        for qh in range(Hq)], dim=1)
+    out = o.prefill_attention(q, bk, xk, xv, uv, cos, sin)
+    torch.testing.assert_close(out, ref, atol=1e-10, rtol=1e-10)
+
+
+def test_prefill_chunk_and_last_query_agree_with_full_and_decode():
+    """Queries at positions pos0.. see what they see in a full prefill
+    (chunked prefill), and the last query's row is the decode step."""
+    q, bk, xk, xv, uv, cos, sin = _prefill_case(12)
+    S = q.shape[2]
+    full = o.prefill_attention(q, bk, xk, xv, uv, cos, sin)
+    for pos0 in (1, 13, S - 1):
+        part = o.prefill_attention(q[:, :, pos0:], bk, xk, xv, uv, cos, sin, pos0=pos0)
+        torch.testing.assert_close(part, full[:, :, pos0:], atol=1e-12, rtol=1e-12)
+    dec, _, _ = o.decode_attention(q[:, :, -1], bk, xk, xv, uv, cos, sin)
+    torch.testing.assert_close(full[:, :, -1], dec, atol=1e-12, rtol=1e-12)
+
+
+# --------------------------------------------------------------------------
 # planted mistakes: each pin above must catch a plausible oracle bug
 # --------------------------------------------------------------------------
+
+def test_planted_causal_off_by_one_is_caught(monkeypatch):
+    monkeypatch.setattr(o, "causal_visible",
+                        lambda T, S, pos0: torch.arange(S)[None, :] < (pos0 + torch.arange(T))[:, None])
+    with pytest.raises(AssertionError):
+        test_prefill_matches_causal_sdpa()
+
+
+def test_planted_value_head_layout_is_caught(monkeypatch):
+    real = o.reconstruct_kv
+
+    def wrong(bk, xk, xv, uv, cos, sin, dtype=torch.float64):
+        K, V = real(bk, xk, xv, uv, cos, sin, dtype)
+        B, H, S, _ = V.shape
+        return K, V.transpose(1, 2).reshape(B, H, S, D)      # (S, H) order read as (H, S)
+    monkeypatch.setattr(o, "reconstruct_kv", wrong)
+    with pytest.raises(AssertionError):
+        test_prefill_matches_causal_sdpa()
 
 def test_planted_rotate_half_sign_is_caught(monkeypatch):
     monkeypatch.setattr(o, "rotate_half", lambda x: torch.cat((x[..., 64:], -x[..., :64]), dim=-1))
