@@ -217,6 +217,154 @@ def run_e2e(args):
     print(json.dumps(rec), flush=True)
 
 
+MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 / bf16 MFMA
+
+
+def prefill_flops(B, Hq, Hkv, T, pos0, ranks, Rv):
+    """Algorithmic FLOPs of one causal prefill layer: K reconstruction
+    2*B*S*sum(r)*128, V reconstruction 2*B*S*Rv*Hkv*128 (S = pos0 + T), and
+    the attention 4*128 per visible (query, key) pair per query head (q.K and
+    P.V), sum over t of pos0 + t + 1 visible keys."""
+    S = pos0 + T
+    recon_k = 2 * B * S * sum(ranks) * HEAD_DIM
+    recon_v = 2 * B * S * Rv * Hkv * HEAD_DIM
+    pairs = T * pos0 + T * (T + 1) // 2
+    attn = 4 * HEAD_DIM * B * Hq * pairs
+    return {"recon": recon_k + recon_v, "attention": attn, "total": recon_k + recon_v + attn}
+
+
+def run_prefill(args):
+    """Prefill of one attention layer: the 8192-token prompt at batch 8 of the
+    e2e workload (Llama-2-7B-shaped MHA 32 x 128, fp16, ragged K ranks sum 1640
+    as int8, V rank 1640 as int4-g64).  A step is starkv_prefill_attention:
+    K / V reconstruction from the latents + causal flash attention."""
+    import torch
+    from _util import cfg2_ranks
+    from starkv import RopeConfig, prefill_attention
+    from starkv.cache import LatentCache
+    B, T, Hq, Rv = 8, 8192, 32, 1640
+    ranks = cfg2_ranks()
+    Hkv = len(ranks)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    rmax = max(ranks)
+    bk = torch.zeros(Hkv, rmax, HEAD_DIM, device=dev)
+    k_new = torch.zeros(B, Hkv, T, rmax, device=dev, dtype=torch.float16)
+    for h, r in enumerate(ranks):
+        bk[h, :r] = torch.randn(r, HEAD_DIM, generator=g, device=dev) / math.sqrt(r)
+        k_new[:, h, :, :r] = torch.randn(B, T, r, generator=g, device=dev).half()
+    bk = bk.half()
+    v_new = torch.randn(B, T, Rv, generator=g, device=dev).half()
+    cache = LatentCache(B, ranks, Rv, T, torch.float16, dev, fmt="int8_g64")
+    kspec, vspec, S = cache.append(k_new, v_new, bk)
+    del k_new, v_new
+    uv = (torch.randn(Hkv * HEAD_DIM, Rv, generator=g, device=dev) / math.sqrt(Rv)).half()
+    q = torch.randn(B, Hq, T, HEAD_DIM, generator=g, device=dev).half()
+    out = torch.empty_like(q)
+    rope = RopeConfig()
+    fl = prefill_flops(B, Hq, Hkv, T, 0, ranks, Rv)
+
+    def step(ev=None):
+        prefill_attention(q, kspec, vspec, uv, rope=rope, out=out, events=ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for e3 in evs:
+        for e in e3:
+            e.record()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    rec_ms = statistics.mean([e[0].elapsed_time(e[1]) for e in evs])
+    fa_ms = statistics.mean([e[1].elapsed_time(e[2]) for e in evs])
+    ms = statistics.mean([e[0].elapsed_time(e[2]) for e in evs])
+    tflops = fl["total"] / (ms * 1e-3) / 1e12
+    fa_tflops = fl["attention"] / (fa_ms * 1e-3) / 1e12
+
+    # the reference's own prefill route on this GPU (model.py:429-449: K / V
+    # materialised by torch matmuls from the dequantised latents, RoPE, GQA
+    # repeat, SDPA with the causal mask), timed for comparison
+    torch_ms = None
+    try:
+        xk = cache.dequant_k(S)
+        xv = cache.dequant_v(S)
+        cos, sin = rope.cos_sin(torch.arange(S, device=dev))
+        cos, sin = cos.half(), sin.half()
+
+        def torch_step():
+            ks = []
+            for h in range(Hkv):
+                kh = torch.matmul(xk[h], bk[h, :ranks[h]])
+                ks.append(kh * cos + torch.cat((-kh[..., 64:], kh[..., :64]), -1) * sin)
+            K = torch.stack(ks, 1)
+            V = torch.nn.functional.linear(xv, uv).view(B, S, Hkv, HEAD_DIM).transpose(1, 2)
+            return torch.nn.functional.scaled_dot_product_attention(q, K, V.contiguous(), is_causal=True)
+
+        for _ in range(2):
+            torch_step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        n_t = max(1, min(5, args.steps))
+        for _ in range(n_t):
+            torch_step()
+        torch.cuda.synchronize()
+        torch_ms = (time.perf_counter() - t1) * 1e3 / n_t
+        del xk, xv
+    except torch.cuda.OutOfMemoryError:
+        torch_ms = None
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import starkv_oracle as o
+        Ts = 4096
+
+        def make_fn():
+            xk1 = [cache.dequant_k(Ts)[0][:1].float().cpu()]
+            xv1 = cache.dequant_v(Ts)[:1].float().cpu()
+            c = dict(q=q[:1, :1, :Ts].float().cpu(), bk=[bk[0, :ranks[0]].float().cpu()], xk=xk1, xv=xv1,
+                     uv=uv[:HEAD_DIM].float().cpu())
+            cs, sn = o.rope_cos_sin(rope.inv_freq(), torch.arange(Ts), 1.0)
+
+            def fn():
+                with torch.no_grad():
+                    o.prefill_attention(c["q"], c["bk"], c["xk"], c["xv"], c["uv"], cs, sn, dtype=torch.float32)
+            return fn
+
+        med, cores, nthreads, n = cpu_baseline(make_fn, args.cpu_reps)
+        sfl = prefill_flops(1, 1, 1, Ts, 0, ranks[:1], Rv)["total"]
+        cpu = {"value": round(sfl / med / 1e12, 5), "unit": "TFLOP/s", "cores": nthreads, "kind": "port",
+               "host_cpus": cores, "ms_per_sample": round(med * 1e3, 1),
+               "sample": f"batch 1, query head 0 (KV head 0, rank {ranks[0]}), {Ts} tokens, fp32 torch eager "
+                         f"restatement of the reference prefill (oracle.starkv_oracle.prefill_attention, causal), "
+                         f"median of {n} reps; FLOPs counted as for the GPU line"}
+
+    rec = {
+        "metric": "prefill attention TFLOP/s per layer (MFMA roofline)",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "prefill: one Llama-2-7B-shaped layer (MHA 32 x 128, fp16), batch 8, 8192-token "
+                               "causal prompt over a latent cache (ragged K ranks sum 1640 int8, V rank 1640 "
+                               "int4-g64) -- the e2e workload's prefill",
+                   "batch": B, "tokens": T, "k_ranks_sum": sum(ranks), "v_rank": Rv},
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "prefill_tokens_per_s": round(B * T / (ms * 1e-3), 1),
+        "kernels_ms": {"kv_recon": round(rec_ms, 4), "fa_causal": round(fa_ms, 4)},
+        "algorithmic_flops": fl,
+        "torch_reference_gpu_ms": round(torch_ms, 3) if torch_ms else None,
+        "roofline": {"bound": "mfma", "kernel": "fa_causal", "achieved": round(fa_tflops, 1),
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(fa_tflops / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -227,7 +375,9 @@ def main():
     ap.add_argument("--workload", default="cfg2",
                     help="cfg2 (default: the metric's workload), cfg3 (B16 S32768, K int8 + V int4-g64 cache), "
                          "cfg3-long (B4 S131072, same formats), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S), "
-                         "e2e (32-layer model, prefill 8192, greedy decode at batch 8; prints e2e decode tok/s)")
+                         "e2e (32-layer model, prefill 8192, greedy decode at batch 8; prints e2e decode tok/s), "
+                         "prefill (one layer's 8192-token causal prefill at batch 8 over the int8 / int4-g64 "
+                         "latent cache; prints TFLOP/s against the MFMA roofline)")
     ap.add_argument("--e2e-steps", type=int, default=256)
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run three 1 GiB device-to-device copies (the known-size reference for rocprofv3 "
@@ -244,6 +394,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "e2e":
         run_e2e(args)
+        return
+    if args.workload == "prefill":
+        run_prefill(args)
         return
     if args.pmc_calibrate:
         n = 1 << 30

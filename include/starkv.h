@@ -1,6 +1,6 @@
 /*
- * starkv.h — C ABI of the MI355X (gfx950) STAR-KV decode-attention library
- * (libstarkv.so, built from star-kv_amd/csrc/).
+ * starkv.h — C ABI of the MI355X (gfx950) STAR-KV decode- and
+ * prefill-attention library (libstarkv.so, built from star-kv_amd/csrc/).
  *
  * Every entry point takes plain pointers and sizes, returns an int status
  * (0 = OK, negative = argument validation error, positive = HIP error code)
@@ -304,6 +304,12 @@ typedef struct {
 
 size_t starkv_prefill_workspace_bytes(const starkv_prefill_desc* d);
 int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Same as starkv_prefill_attention, and records events[0..2] (hipEvent_t) on
+ * the stream before the K / V reconstruction, after it and after the
+ * attention kernel (per-kernel timing, as starkv_decode_attention_timed). */
+int starkv_prefill_attention_timed(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes,
+                                   void* stream, void* const* events);
 
 #ifdef __cplusplus
 }

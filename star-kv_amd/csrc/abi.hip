@@ -724,7 +724,8 @@ size_t starkv_prefill_workspace_bytes(const starkv_prefill_desc* d) {
   return 2 * prefill_kv_bytes(d, S_pad);
 }
 
-int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+static int prefill_impl(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream,
+                        void* const* events) {
   int gs = 0, st;
   int64_t S_pad = 0;
   if ((st = validate_prefill(d, &gs, &S_pad))) return st;
@@ -753,7 +754,21 @@ int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size
   a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h; a.q_st = d->q_stride_t;
   a.scale_log2 = d->scale * 1.4426950408889634f;
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h; a.o_st = d->out_stride_t;
-  return launch_prefill(a, d->dtype, d->batch, (hipStream_t)stream);
+  hipStream_t s = (hipStream_t)stream;
+  if (events && (st = (int)hipEventRecord((hipEvent_t)events[0], s))) return st;
+  if ((st = launch_prefill(a, d->dtype, d->batch, s, events ? (hipEvent_t)events[1] : nullptr))) return st;
+  if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
+  return STARKV_OK;
+}
+
+int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
+  return prefill_impl(d, workspace, workspace_bytes, stream, nullptr);
+}
+
+int starkv_prefill_attention_timed(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes,
+                                   void* stream, void* const* events) {
+  if (!events || !events[0] || !events[1] || !events[2]) return STARKV_ERR_NULL;
+  return prefill_impl(d, workspace, workspace_bytes, stream, events);
 }
 
 }  // extern "C"

@@ -62,7 +62,7 @@ struct KArgs {
   int ws;                                          // warp-specialised kernel (dense, 16-byte aligned latents)
   int ws_stage, ws_nst;                            // its LDS stage bytes and stage count
   int ws_i8;                                       // ... over int8 latents (per-(b,h,s) fp16 scales)
-  float wscale;                                    // softmax scale * rope attention scaling
+  float wscale;                                    // softmax scale (the RoPE table carries the attention scaling)
   int64_t xoff[K_MAX_KV];                          // per KV head: elements (dense) or bytes (quantised)
   int xpitch[K_MAX_KV];
   int64_t xoff2[K_MAX_KV];                         // lower block (bytes)
@@ -145,6 +145,8 @@ struct UPArgs {
 // ---------------------------------------------------------------------------
 struct PFArgs {
   int S, S_pad, Hkv, Hq, gs, T, pos0;              // S = pos0 + T positions reconstructed, S_pad = round_up(S, 64)
+  int rc_nb, rc_blocks;                            // reconstruction: position blocks per batch, times B
+  int fa_nqb, fa_nkvi;                             // attention: query blocks per head, B * Hkv
   // K latent: dense act dtype (offsets / pitches in elements) or int8 (bytes) with fp16 scales (b, h, s)
   const void* kx; int64_t kx_sb; int k_i8;
   const void* kscale; int64_t ks_sb, ks_sh;
@@ -260,6 +262,6 @@ int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);
-int launch_prefill(const PFArgs& a, int dtype, int B, hipStream_t st);
+int launch_prefill(const PFArgs& a, int dtype, int B, hipStream_t st, hipEvent_t mid);   // mid: after K/V
 
 }  // namespace starkv

@@ -3,7 +3,7 @@
 // from the latents and runs SDPA -- without a causal mask (the defect the
 // build fixes: query t sees keys <= pos0 + t).
 //
-// 1. kv_recon_kernel: per (b, KV head, 64 positions) one MFMA GEMM tile,
+// 1. recon_kernel: per (KV head, 512 positions, b) one MFMA GEMM tile,
 //    K = RoPE(X_k[s] . B_k) (RoPE applied in the epilogue from the decode's
 //    RoPE table) and V = X_v[s] . U_v[h]^T, into [B][Hkv][S_pad][128] act-dtype
 //    buffers.  Quantised latents are dequantised on the way in, bit-exactly
@@ -88,105 +88,324 @@ __device__ inline uint4 pf_dq_g64(uint32_t w, uint16_t s16, uint16_t z16) {
 
 }  // namespace
 
-// KIND 0: K (dense or int8 latents), 1: V (dense or group-64 int4 latents)
-template <typename XT, int KIND>
-__global__ __launch_bounds__(256) void kv_recon_kernel(const PFArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t wT[KIND == 0 ? 128 * WT_PITCH : 8];   // K: B_k^T [d][j]
+// ---------------------------------------------------------------------------
+// K / V reconstruction: per (KV head h, b, 512 positions) one workgroup of 4
+// waves; wave w computes C^T[d][p] for all 128 dims d and its 128 positions
+// p as 4 x 4 MFMA tiles (A = the projection, dims as rows; B = latent rows,
+// positions as columns, loaded from global straight into registers one
+// K-step ahead).  A K-step is 64 ranks; within it lane half hh takes ranks
+// [32 hh, 32 hh + 32) (MFMA K-chunk kk: ranks 32 hh + 8 kk .. + 7) in both
+// operands, so each lane reads one contiguous 32-rank run of a latent row.
+// K: A = B_k[h] (staged whole in LDS as [j][d], read with the transposed LDS
+// load), K-depth r_h; RoPE pairs (d, d + 64) sit in M-tiles mt and mt + 2 of
+// the same lane.  V: A = U_v rows h*128 + d ([d][j] 64-rank stages,
+// double-buffered in LDS), K-depth Rv.  The epilogue stages each wave's
+// 128 x 128 tile in LDS and writes whole 256-byte rows.
+// ---------------------------------------------------------------------------
+constexpr int RC_WAVE_POS = 128;                 // positions per wave
+constexpr int RC_POS = 4 * RC_WAVE_POS;          // positions per workgroup
+constexpr int RC_KS = 64;                        // ranks per K-step
+constexpr int UV_PITCH = 72;                     // halves per staged U_v row (64 ranks + 8)
+constexpr int UV_BUF = HEAD_DIM * UV_PITCH;      // halves per U_v stage
+constexpr int BK_PITCH = 136;                    // halves per staged B_k row (128 dims + 8)
+constexpr int C_PITCH = 136;                     // halves per epilogue row
+constexpr int RC_LDS = 4 * RC_WAVE_POS * C_PITCH;
+
+// raw latent data of one K-step for this lane: [N-tile][K-chunk]
+template <int KIND, bool Q> struct RcRaw { uint4 d[4][4]; };             // dense: 8 ranks per chunk
+template <> struct RcRaw<0, true> { uint2 d[4][4]; };                    // int8
+template <> struct RcRaw<1, true> { uint4 d[4]; uint32_t sz[4]; };       // group-64 int4 (word kk) + scale | zero << 16
+
+// Q: quantised latents (K int8, V group-64 int4)
+template <typename XT, int KIND, bool Q>
+__global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
-  const int p0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+  // XCD-aware order: workgroup L runs on XCD L % 8, and the Hkv heads of one
+  // (batch, 512-position block) all land on one XCD, sharing its L2 for the
+  // latent rows
+  const int L = blockIdx.x, t8 = L >> 3;
+  const int h = t8 % a.Hkv, blk = (t8 / a.Hkv) * 8 + (L & 7);
+  if (blk >= a.rc_blocks) return;
+  const int b = blk / a.rc_nb;
+  const int pw = (blk - b * a.rc_nb) * RC_POS + wave * RC_WAVE_POS;
   const int S = a.S;
-  const int R = KIND == 0 ? a.krank[h] : a.Rv;            // multiple of 8 (host-checked)
-  const int Rp = (R + 15) & ~15;
+  const int R = KIND == 0 ? a.krank[h] : a.Rv;     // multiple of 8 (host-checked)
+  const int nks = (R + RC_KS - 1) / RC_KS;
+
+  // per N-tile latent row (clamped position) and K's int8 scales
+  const uint8_t* xrow[4];
+  uint16_t ksc[4] = {0, 0, 0, 0};
+  int64_t vso[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int pc = min(pw + nt * 32 + n, S - 1);
+    constexpr int64_t es = Q ? 1 : 2;                // latent offsets: bytes (quantised) or elements
+    if constexpr (KIND == 0) {
+      xrow[nt] = (const uint8_t*)a.kx + (b * a.kx_sb + a.kxoff[h] + (int64_t)pc * a.kxpitch[h]) * es;
+      if constexpr (Q) ksc[nt] = ((const uint16_t*)a.kscale)[b * a.ks_sb + h * a.ks_sh + pc];
+      vso[nt] = 0;
+    } else {
+      xrow[nt] = (const uint8_t*)a.vx + (b * a.vx_sb + (int64_t)pc * a.vx_ss) * es;
+      vso[nt] = b * a.vs_sb + (int64_t)pc * a.vs_ss;
+    }
+  }
+
+  auto load = [&](int ks, RcRaw<KIND, Q>& r) {
+    const int j0 = ks * RC_KS + 32 * hh;             // this lane's first rank of the step
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      if constexpr (KIND == 1 && Q) {
+        const uint8_t* src = xrow[nt] + j0 / 2;
+        if (j0 + 32 <= R) {
+          r.d[nt] = *(const uint4*)src;
+        } else {
+          uint32_t w[4];
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) w[kk] = j0 + 8 * kk < R ? *(const uint32_t*)(src + 4 * kk) : 0u;
+          r.d[nt] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        const int g = min(ks * RC_KS, R - 1) >> 6;
+        r.sz[nt] = (uint32_t)((const uint16_t*)a.vscale)[vso[nt] + g] |
+                   ((uint32_t)((const uint16_t*)a.vzero)[vso[nt] + g] << 16);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int j = j0 + 8 * kk;
+          const bool ok = j < R;
+          if constexpr (!Q) r.d[nt][kk] = ok ? *(const uint4*)(xrow[nt] + 2 * j) : make_uint4(0, 0, 0, 0);
+          else r.d[nt][kk] = ok ? *(const uint2*)(xrow[nt] + j) : make_uint2(0, 0);
+        }
+      }
+    }
+  };
+  // raw -> B fragment (act dtype).  Ranks past R read as zero bytes (int4:
+  // the zero point); the A rows of those ranks are zero, so they add nothing.
+  auto frag = [&](const RcRaw<KIND, Q>& r, int nt, int kk) -> uint4 {
+    if constexpr (!Q) {
+      return r.d[nt][kk];
+    } else {
+      uint4 f;
+      if constexpr (KIND == 0) {
+        f = pf_dq_int8(r.d[nt][kk], ksc[nt]);
+      } else {
+        const uint32_t w = kk == 0 ? r.d[nt].x : kk == 1 ? r.d[nt].y : kk == 2 ? r.d[nt].z : r.d[nt].w;
+        f = pf_dq_g64(w, (uint16_t)(r.sz[nt] & 0xffff), (uint16_t)(r.sz[nt] >> 16));
+      }
+      if constexpr (!__is_same(XT, _Float16)) f = pf_f16_to_bf16(f);
+      return f;
+    }
+  };
+
+  // A operand staging
+  const int g4 = lane >> 4, rho = lane & 15;
+  const int tr_off = (32 * hh + (rho >> 2)) * BK_PITCH + 16 * (g4 & 1) + 4 * (rho & 3);
+  const XT* uvh = (const XT*)a.uv + (int64_t)h * HEAD_DIM * a.uv_rs;
+  const int ur = tid >> 1, uc = (tid & 1) * 32;       // V: this thread's U_v row and 32-rank half
+  auto uv_load = [&](int ks, uint4* u) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int j = ks * RC_KS + uc + 8 * c;
+      u[c] = j < R ? *(const uint4*)(uvh + (int64_t)ur * a.uv_rs + j) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto uv_store = [&](int buf, const uint4* u) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *(uint4*)&lds[buf * UV_BUF + ur * UV_PITCH + uc + 8 * c] = u[c];
+  };
+  uint4 un[4];
   if constexpr (KIND == 0) {
     const XT* bk = (const XT*)a.bk + a.bkoff[h];
-    for (int e = tid; e < Rp * 128; e += 256) {
-      const int j = e >> 7, d = e & 127;
-      wT[d * WT_PITCH + j] = j < R ? __builtin_bit_cast(uint16_t, bk[(int64_t)j * a.bk_rs + d]) : (uint16_t)0;
-    }
-    __syncthreads();
-  }
-  const int pr = min(p0 + 32 * (wave & 1) + n, S - 1);      // A-operand row (position), clamped
-  const int dc0 = 32 * (wave >> 1), dc1 = dc0 + 64;          // output dims dc + n (RoPE pairs in one lane)
-  floatx16 acc0 = floatx16{}, acc1 = floatx16{};
-  for (int j0 = 0; j0 < Rp; j0 += 16) {
-    const int jj = j0 + 8 * hh;                               // this lane's 8 K indices
-    const bool jok = jj < R;
-    uint4 A = make_uint4(0, 0, 0, 0), B0 = A, B1 = A;
-    if constexpr (KIND == 0) {
-      if (a.k_i8) {
-        const uint8_t* x = (const uint8_t*)a.kx + b * a.kx_sb + a.kxoff[h] + (int64_t)pr * a.kxpitch[h];
-        const uint16_t s = ((const uint16_t*)a.kscale)[b * a.ks_sb + h * a.ks_sh + pr];
-        if (jok) {
-          A = pf_dq_int8(*(const uint2*)(x + jj), s);
-          if constexpr (!__is_same(XT, _Float16)) A = pf_f16_to_bf16(A);
-        }
-      } else {
-        const XT* x = (const XT*)a.kx + b * a.kx_sb + a.kxoff[h] + (int64_t)pr * a.kxpitch[h];
-        if (jok) A = *(const uint4*)(x + jj);
-      }
-      B0 = *(const uint4*)&wT[(dc0 + n) * WT_PITCH + jj];
-      B1 = *(const uint4*)&wT[(dc1 + n) * WT_PITCH + jj];
-    } else {
-      if (a.v_g64) {
-        const uint8_t* x = (const uint8_t*)a.vx + b * a.vx_sb + (int64_t)pr * a.vx_ss;
-        const int64_t so = b * a.vs_sb + (int64_t)pr * a.vs_ss + (jok ? jj / 64 : 0);
-        if (jok) {
-          A = pf_dq_g64(*(const uint32_t*)(x + jj / 2), ((const uint16_t*)a.vscale)[so], ((const uint16_t*)a.vzero)[so]);
-          if constexpr (!__is_same(XT, _Float16)) A = pf_f16_to_bf16(A);
-        }
-      } else {
-        const XT* x = (const XT*)a.vx + b * a.vx_sb + (int64_t)pr * a.vx_ss;
-        if (jok) A = *(const uint4*)(x + jj);
-      }
-      const XT* u = (const XT*)a.uv + (int64_t)h * HEAD_DIM * a.uv_rs;
-      if (jok) {
-        B0 = *(const uint4*)(u + (int64_t)(dc0 + n) * a.uv_rs + jj);
-        B1 = *(const uint4*)(u + (int64_t)(dc1 + n) * a.uv_rs + jj);
-      }
-    }
-    acc0 = pf_mfma<XT>(A, B0, acc0);
-    acc1 = pf_mfma<XT>(A, B1, acc1);
-  }
-  // epilogue: lane holds rows (positions) 8(v/4) + 4hh + v%4 of dims dc0 + n and dc1 + n
-  XT* dst = (XT*)(KIND == 0 ? a.kbuf : a.vbuf) + (((int64_t)b * a.Hkv + h) * a.S_pad) * HEAD_DIM;
-  const int i = dc0 + n;                                      // RoPE frequency of this lane (< 64)
+    const int Rp = nks * RC_KS;
+    for (int e = tid; e < Rp * 16; e += 256) {        // 16-byte pieces of rows [0, Rp)
+      const int j = e >> 4, d8 = (e & 15) * 8;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (j < R) {
+        const XT* src = bk + (int64_t)j * a.bk_rs + d8;
+        half8 t;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int p = p0 + 32 * (wave & 1) + 8 * (v >> 2) + 4 * hh + (v & 3);
-    float y0 = acc0[v], y1 = acc1[v];
-    if (p >= S) {
-      y0 = y1 = 0.f;
-    } else if constexpr (KIND == 0) {
-      // RoPE table: (cos, sin) of position p and frequency i, times the attention scaling
-      const int64_t te = ((int64_t)((p >> 5) * 8 + (i >> 3)) * 64 + ((i & 7) >> 2) * 32 + (p & 31)) * 8 + 2 * (i & 3);
-      const uint32_t cs = ((const uint32_t*)a.rope)[te >> 1];
-      const kh2 c2 = __builtin_bit_cast(kh2, cs);
-      const float c = (float)c2[0], s = (float)c2[1];
-      const float k0 = y0, k1 = y1;
-      y0 = k0 * c - k1 * s;
-      y1 = k1 * c + k0 * s;
+        for (int i = 0; i < 8; ++i) t[i] = __builtin_bit_cast(_Float16, __builtin_bit_cast(uint16_t, src[i]));
+        v = __builtin_bit_cast(uint4, t);
+      }
+      *(uint4*)&lds[j * BK_PITCH + d8] = v;
     }
-    if (p < a.S_pad) {
-      dst[(int64_t)p * HEAD_DIM + dc0 + n] = (XT)y0;
-      dst[(int64_t)p * HEAD_DIM + dc1 + n] = (XT)y1;
+  } else {
+    uv_load(0, un);
+    uv_store(0, un);
+  }
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = floatx16{};
+
+  // one K-step over latent data `cur` (the next U_v stage is fetched meanwhile)
+  auto step = [&](int ks, const RcRaw<KIND, Q>& cur) {
+    const bool more = ks + 1 < nks;
+    if constexpr (KIND == 1) {
+      if (more) uv_load(ks + 1, un);
     }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4 bf[4];
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) bf[nt] = frag(cur, nt, kk);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        uint4 af;
+        if constexpr (KIND == 0) {
+          const uint16_t* sb = lds + (ks * RC_KS + 8 * kk) * BK_PITCH + tr_off + 32 * mt;
+          const uint2 lo = pf_read_tr16(sb), hi = pf_read_tr16(sb + 4 * BK_PITCH);
+          af = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+          af = *(const uint4*)&lds[(ks & 1) * UV_BUF + (mt * 32 + n) * UV_PITCH + 32 * hh + 8 * kk];
+        }
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = pf_mfma<XT>(af, bf[nt], acc[mt][nt]);
+      }
+    }
+    if constexpr (KIND == 1) {
+      if (more) uv_store((ks + 1) & 1, un);
+      __syncthreads();
+    }
+  };
+
+  if constexpr (KIND == 1 && Q) {
+    // packed latents are small: keep two K-steps in flight (three raw sets)
+    RcRaw<KIND, Q> r0, r1, r2;
+    load(0, r0);
+    if (nks > 1) load(1, r1);
+    __syncthreads();
+    // at the top of each round r0 / r1 hold (or are loading) K-steps ks / ks + 1
+    int ks = 0;
+    for (; ks + 3 <= nks; ks += 3) {
+      load(ks + 2, r2);
+      step(ks, r0);
+      if (ks + 3 < nks) load(ks + 3, r0);
+      step(ks + 1, r1);
+      if (ks + 4 < nks) load(ks + 4, r1);
+      step(ks + 2, r2);
+    }
+    if (ks < nks) step(ks, r0);
+    if (ks + 1 < nks) step(ks + 1, r1);
+  } else {
+    RcRaw<KIND, Q> cur, nxt;
+    load(0, cur);
+    __syncthreads();
+    for (int ks = 0; ks < nks; ++ks) {
+      const bool more = ks + 1 < nks;
+      if (more) load(ks + 1, nxt);
+      step(ks, cur);
+      if (more) cur = nxt;
+    }
+  }
+  if constexpr (KIND == 0) __syncthreads();          // B_k reads done before the epilogue reuses LDS
+
+  // epilogue: lane holds positions pw + 32 nt + n, dims 32 mt + 8 q + 4 hh + c in acc[mt][nt][4q + c]
+  uint16_t* cw = lds + wave * RC_WAVE_POS * C_PITCH;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int p = pw + nt * 32 + n;
+    const bool live = p < S;
+    uint16_t* crow = cw + (nt * 32 + n) * C_PITCH + 4 * hh;
+    if constexpr (KIND == 0) {
+      const uint4* rt = (const uint4*)a.rope + ((int64_t)(min(p, S - 1) >> 5) * 8) * 64 + hh * 32 + (p & 31);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint4 cs4 = rt[(mt * 4 + q) * 64];       // (cos, sin) of frequencies 32 mt + 8 q + 4 hh + 0..3
+          const uint32_t cw4[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+          uint32_t y0w[2], y1w[2];
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            float y0[2], y1[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int c = 2 * c2 + e;
+              const kh2 t = __builtin_bit_cast(kh2, cw4[c]);
+              const float co = (float)t[0], si = (float)t[1];
+              const float k0 = acc[mt][nt][4 * q + c], k1 = acc[mt + 2][nt][4 * q + c];
+              y0[e] = live ? k0 * co - k1 * si : 0.f;
+              y1[e] = live ? k1 * co + k0 * si : 0.f;
+            }
+            y0w[c2] = (uint32_t)pf_bits<XT>(y0[0]) | ((uint32_t)pf_bits<XT>(y0[1]) << 16);
+            y1w[c2] = (uint32_t)pf_bits<XT>(y1[0]) | ((uint32_t)pf_bits<XT>(y1[1]) << 16);
+          }
+          *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(y0w[0], y0w[1]);
+          *(uint2*)(crow + (mt + 2) * 32 + 8 * q) = make_uint2(y1w[0], y1w[1]);
+        }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t w[2];
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            const float v0 = live ? acc[mt][nt][4 * q + 2 * c2] : 0.f;
+            const float v1 = live ? acc[mt][nt][4 * q + 2 * c2 + 1] : 0.f;
+            w[c2] = (uint32_t)pf_bits<XT>(v0) | ((uint32_t)pf_bits<XT>(v1) << 16);
+          }
+          *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(w[0], w[1]);
+        }
+    }
+  }
+  __syncthreads();
+  XT* dst = (XT*)(KIND == 0 ? a.kbuf : a.vbuf) + (((int64_t)b * a.Hkv + h) * a.S_pad) * HEAD_DIM;
+#pragma unroll 4
+  for (int it = 0; it < RC_WAVE_POS * 16 / 64; ++it) {
+    const int idx = it * 64 + lane, row = idx >> 4, ch = idx & 15;
+    const int p = pw + row;
+    if (p < a.S_pad) *(uint4*)(dst + (int64_t)p * HEAD_DIM + ch * 8) = *(const uint4*)&cw[row * C_PITCH + ch * 8];
   }
 }
 
+// ---------------------------------------------------------------------------
+// Causal flash attention over the reconstructed K / V.  Workgroup: 8 waves x
+// 32 queries of one (b, query head); key blocks of 64 staged in LDS, the next
+// block loaded into registers while the current one is computed.  Per block
+// and wave: S^T = K . Q^T as two 32-key MFMA tiles, the online softmax (the
+// causal mask only on blocks that reach past the wave's first query; blocks
+// wholly in the wave's future skipped), then O^T += V^T . P^T.  The running
+// maximum moves only when a block's maximum exceeds it by more than
+// 2^FA_RESCALE_LOG2 in exp2 units, so the O rescale is rare and every
+// probability stays <= 2^FA_RESCALE_LOG2 (exact in the final O / l).
+// ---------------------------------------------------------------------------
+constexpr int FA_KB = 64;                        // keys per block
+constexpr int FA_WAVES = 8;                      // waves per workgroup, 32 queries each
+constexpr int FA_QB = 32 * FA_WAVES;             // queries per workgroup
+constexpr float FA_RESCALE_LOG2 = 8.0f;
+
 template <typename XT>
-__global__ __launch_bounds__(256) void fa_causal_kernel(const PFArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[32 * WT_PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[32 * WT_PITCH];
+__global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][FA_KB * WT_PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][FA_KB * WT_PITCH];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
-  const int qb = blockIdx.x, qh = blockIdx.y, b = blockIdx.z;
-  const int kv = qh / a.gs, T = a.T, pos0 = a.pos0;
-  const int t = qb * 128 + 32 * wave + n;                     // this lane's query
+  // XCD-aware order: workgroup L runs on XCD L % 8; every query block of
+  // every query head of one (b, KV head) runs on one XCD, consecutively, so
+  // that XCD's L2 serves their shared K / V.  Within it the latest (longest)
+  // query blocks start first.
+  const int L = blockIdx.x, t8 = L >> 3;
+  const int per_kv = a.gs * a.fa_nqb;
+  const int kvi = (t8 / per_kv) * 8 + (L & 7);      // b * Hkv + kv
+  if (kvi >= a.fa_nkvi) return;
+  const int rem = t8 % per_kv;
+  const int qb = a.fa_nqb - 1 - rem % a.fa_nqb;
+  const int b = kvi / a.Hkv, kv = kvi - b * a.Hkv;
+  const int qh = kv * a.gs + rem / a.fa_nqb;
+  const int T = a.T, pos0 = a.pos0;
+  const int t = qb * FA_QB + 32 * wave + n;         // this lane's query
   const int tc = min(t, T - 1);
-  const int P = pos0 + tc;                                    // its position: sees keys <= P
+  const int P = pos0 + tc;                          // its position: sees keys <= P
+  const int w_first = pos0 + min(qb * FA_QB + 32 * wave, T - 1);
+  const int w_last = pos0 + min(qb * FA_QB + 32 * wave + 31, T - 1);
+  const int last_t = min(T, qb * FA_QB + FA_QB) - 1;
+  const int nkb = (pos0 + last_t) / FA_KB + 1;      // key blocks the workgroup needs
   const XT* qrow = (const XT*)a.q + b * a.q_sb + qh * a.q_sh + (int64_t)tc * a.q_st;
   uint4 Qb[8];
 #pragma unroll
@@ -194,91 +413,124 @@ __global__ __launch_bounds__(256) void fa_causal_kernel(const PFArgs a) {
   floatx16 o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) o[j] = floatx16{};
+  const float c = a.scale_log2;
+  const float thr = FA_RESCALE_LOG2 / c;            // in raw logit units
   float m = -INFINITY, l = 0.f;
-  const int last_t = min(T, qb * 128 + 128) - 1;
-  const int nkb = (pos0 + last_t) / 32 + 1;                   // 32-key blocks the workgroup needs
   const size_t hbase = (((size_t)b * a.Hkv + kv) * a.S_pad) * HEAD_DIM;
   const XT* kg = (const XT*)a.kbuf + hbase;
   const XT* vg = (const XT*)a.vbuf + hbase;
-  // S^T A operand: MFMA row r = n takes key pi(r) (see the file comment)
+  // S^T A operand: MFMA row r = n takes key pi(r) of the 32-key tile
   const int ra = n >> 3, rh = (n >> 2) & 1, rc = n & 3;
   const int key_r = 16 * (ra >> 1) + 8 * rh + 4 * (ra & 1) + rc;
   // V^T A operand: transposed reads (lane group g = lane/16, rho = lane%16)
   const int g = lane >> 4, rho = lane & 15;
   const int tr_off = (8 * hh + (rho >> 2)) * WT_PITCH + 16 * (g & 1) + 4 * (rho & 3);
+  // staging: thread piece i (of 2) covers key 32 i + tid / 16, dims (tid % 16) * 8 .. + 7
+  static_assert(FA_KB * 16 == 2 * FA_WAVES * 64, "two 16-byte pieces per thread and tensor");
+  const int skey = tid >> 4, sd8 = (tid & 15) * 8;
+  const size_t so0 = (size_t)skey * HEAD_DIM + sd8, so1 = so0 + (size_t)32 * HEAD_DIM;
+  const int lo0 = skey * WT_PITCH + sd8, lo1 = lo0 + 32 * WT_PITCH;
+  // K / V pieces in flight (plain variables: they stay in registers)
+  uint4 k0 = *(const uint4*)(kg + so0), k1 = *(const uint4*)(kg + so1);
+  uint4 v0 = *(const uint4*)(vg + so0), v1 = *(const uint4*)(vg + so1);
+  *(uint4*)&Ks[0][lo0] = k0; *(uint4*)&Ks[0][lo1] = k1;
+  *(uint4*)&Vs[0][lo0] = v0; *(uint4*)&Vs[0][lo1] = v1;
+  __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
-    // stage the block's 32 keys of K and V (rows < S_pad: nkb * 32 <= S_pad)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int e = c * 256 + tid, key = e >> 4, d8 = (e & 15) * 8;
-      const size_t go = (size_t)(kb * 32 + key) * HEAD_DIM + d8;
-      *(uint4*)&Ks[key * WT_PITCH + d8] = *(const uint4*)(kg + go);
-      *(uint4*)&Vs[key * WT_PITCH + d8] = *(const uint4*)(vg + go);
+    const int buf = kb & 1;
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      const size_t go = (size_t)(kb + 1) * FA_KB * HEAD_DIM;
+      k0 = *(const uint4*)(kg + go + so0); k1 = *(const uint4*)(kg + go + so1);
+      v0 = *(const uint4*)(vg + go + so0); v1 = *(const uint4*)(vg + go + so1);
     }
-    __syncthreads();
-    floatx16 s = floatx16{};
+    if (kb * FA_KB <= w_last) {                     // wave-uniform: the block has keys this wave sees
+      floatx16 s[2];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-      s = pf_mfma<XT>(*(const uint4*)&Ks[key_r * WT_PITCH + 16 * k + 8 * hh], Qb[k], s);
-    // lane: keys kb*32 + 16(v/8) + 8hh + v%8 of query t
-    float x[16];
-    float mb = -INFINITY;
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = floatx16{};
+        const uint16_t* kbase = &Ks[buf][(kt * 32 + key_r) * WT_PITCH + 8 * hh];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = kb * 32 + 16 * (v >> 3) + 8 * hh + (v & 7);
-      x[v] = key <= P ? s[v] * a.scale_log2 : -INFINITY;
-      mb = fmaxf(mb, x[v]);
-    }
-    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-    const float mn = fmaxf(m, mb);                            // finite: key 0 <= P in block 0
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);
-    float ps = 0.f;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      x[v] = __builtin_amdgcn_exp2f(x[v] - mn);
-      ps += x[v];
-    }
-    ps += __shfl_xor(ps, 32, 64);
-    l = l * alpha + ps;
-    m = mn;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[j][v] *= alpha;
-    // O^T += V^T . P^T over the block's two 16-key halves
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const uint16_t* sb = Vs + 16 * kk * WT_PITCH + tr_off;
-      if constexpr (__is_same(XT, _Float16)) {
-        half8 ph;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ph[e] = (_Float16)x[8 * kk + e];
-        const uint4 pb = __builtin_bit_cast(uint4, ph);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 4 * WT_PITCH);
-          o[j] = pf_mfma<XT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[j]);
-        }
-      } else {
-        bf16x8 ph, pl;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const __bf16 hv = (__bf16)x[8 * kk + e];
-          ph[e] = hv;
-          pl[e] = (__bf16)(x[8 * kk + e] - (float)hv);
-        }
-        const uint4 pbh = __builtin_bit_cast(uint4, ph), pbl = __builtin_bit_cast(uint4, pl);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 4 * WT_PITCH);
-          const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          o[j] = pf_mfma<XT>(va, pbh, o[j]);
-          o[j] = pf_mfma<XT>(va, pbl, o[j]);
-        }
+        for (int k = 0; k < 8; ++k) s[kt] = pf_mfma<XT>(*(const uint4*)(kbase + 16 * k), Qb[k], s[kt]);
       }
+      // lane: keys kb*64 + 32 kt + 16 (v/8) + 8 hh + v%8 of query t
+      if (kb * FA_KB + FA_KB - 1 > w_first) {         // the block reaches past some query of the wave
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = kb * FA_KB + 32 * kt + 16 * (v >> 3) + 8 * hh + (v & 7);
+            if (key > P) s[kt][v] = -INFINITY;
+          }
+      }
+      float mb = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mb = fmaxf(mb, s[kt][v]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+      if (__ballot(mb > m + thr)) {                  // some query of the wave moves its maximum
+        const float mn = fmaxf(m, mb);                // finite: key 0 <= P in block 0
+        const float alpha = __builtin_amdgcn_exp2f((m - mn) * c);
+        l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[j][v] *= alpha;
+        m = mn;
+      }
+      const float mc = m * c;
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          s[kt][v] = __builtin_amdgcn_exp2f(fmaf(s[kt][v], c, -mc));
+          ps += s[kt][v];
+        }
+      l += ps;                                        // this half's keys; halves joined at the end
+      // O^T += V^T . P^T over the block's four 16-key chunks
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const uint16_t* sb = &Vs[buf][(32 * kt + 16 * kk) * WT_PITCH + tr_off];
+          if constexpr (__is_same(XT, _Float16)) {
+            half8 ph;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ph[e] = (_Float16)s[kt][8 * kk + e];
+            const uint4 pb = __builtin_bit_cast(uint4, ph);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 4 * WT_PITCH);
+              o[j] = pf_mfma<XT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[j]);
+            }
+          } else {
+            bf16x8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const __bf16 hv = (__bf16)s[kt][8 * kk + e];
+              ph[e] = hv;
+              pl[e] = (__bf16)(s[kt][8 * kk + e] - (float)hv);
+            }
+            const uint4 pbh = __builtin_bit_cast(uint4, ph), pbl = __builtin_bit_cast(uint4, pl);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 4 * WT_PITCH);
+              const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
+              o[j] = pf_mfma<XT>(va, pbh, o[j]);
+              o[j] = pf_mfma<XT>(va, pbl, o[j]);
+            }
+          }
+        }
     }
-    __syncthreads();                                          // before the next block overwrites Ks / Vs
+    if (more) {
+      *(uint4*)&Ks[buf ^ 1][lo0] = k0; *(uint4*)&Ks[buf ^ 1][lo1] = k1;
+      *(uint4*)&Vs[buf ^ 1][lo0] = v0; *(uint4*)&Vs[buf ^ 1][lo1] = v1;
+    }
+    __syncthreads();                                // next block staged; this one free to overwrite
   }
+  l += __shfl_xor(l, 32, 64);
   if (t < T) {
     const float inv = 1.0f / l;
     XT* orow = (XT*)a.out + b * a.o_sb + qh * a.o_sh + (int64_t)t * a.o_st;
@@ -290,16 +542,27 @@ __global__ __launch_bounds__(256) void fa_causal_kernel(const PFArgs a) {
 }
 
 template <typename XT>
-static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st) {
-  const dim3 rg((unsigned)ceil_div(a.S, 64), a.Hkv, B);
-  hipLaunchKernelGGL((kv_recon_kernel<XT, 0>), rg, dim3(256), 0, st, a);
-  hipLaunchKernelGGL((kv_recon_kernel<XT, 1>), rg, dim3(256), 0, st, a);
-  hipLaunchKernelGGL((fa_causal_kernel<XT>), dim3((unsigned)ceil_div(a.T, 128), a.Hq, B), dim3(256), 0, st, a);
+static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t mid) {
+  PFArgs r = a;
+  r.rc_nb = (int)ceil_div(a.S, RC_POS);
+  r.rc_blocks = r.rc_nb * B;
+  const dim3 rg((unsigned)(ceil_div(r.rc_blocks, 8) * 8 * a.Hkv));
+  if (a.k_i8) hipLaunchKernelGGL((recon_kernel<XT, 0, true>), rg, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL((recon_kernel<XT, 0, false>), rg, dim3(256), 0, st, r);
+  if (a.v_g64) hipLaunchKernelGGL((recon_kernel<XT, 1, true>), rg, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL((recon_kernel<XT, 1, false>), rg, dim3(256), 0, st, r);
+  int e = (int)hipGetLastError();
+  if (e) return e;
+  if (mid && (e = (int)hipEventRecord(mid, st))) return e;
+  r.fa_nqb = (int)ceil_div(a.T, FA_QB);
+  r.fa_nkvi = B * a.Hkv;
+  const dim3 fg((unsigned)(ceil_div(r.fa_nkvi, 8) * 8 * a.gs * r.fa_nqb));
+  hipLaunchKernelGGL((fa_causal_kernel<XT>), fg, dim3(FA_WAVES * 64), 0, st, r);
   return (int)hipGetLastError();
 }
 
-int launch_prefill(const PFArgs& a, int dtype, int B, hipStream_t st) {
-  return dtype == STARKV_F16 ? launch_prefill_t<_Float16>(a, B, st) : launch_prefill_t<__bf16>(a, B, st);
+int launch_prefill(const PFArgs& a, int dtype, int B, hipStream_t st, hipEvent_t mid) {
+  return dtype == STARKV_F16 ? launch_prefill_t<_Float16>(a, B, st, mid) : launch_prefill_t<__bf16>(a, B, st, mid);
 }
 
 }  // namespace starkv

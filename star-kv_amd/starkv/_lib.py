@@ -142,7 +142,7 @@ EXPORTS = (
     "starkv_pv_latent_workspace_bytes", "starkv_pv_latent",
     "starkv_decode_workspace_bytes", "starkv_decode_attention", "starkv_decode_attention_timed",
     "starkv_k_append", "starkv_v_append",
-    "starkv_prefill_workspace_bytes", "starkv_prefill_attention",
+    "starkv_prefill_workspace_bytes", "starkv_prefill_attention", "starkv_prefill_attention_timed",
 )
 
 _lib = None
@@ -165,7 +165,8 @@ def lib() -> ctypes.CDLL:
     L.starkv_rope_build.restype = ctypes.c_int
     L.starkv_rope_build.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_float, ctypes.c_int,
                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-    for name, desc in (("k_logits", KLogitsDesc), ("pv_latent", PVDesc), ("decode", DecodeDesc), ("prefill", PrefillDesc)):
+    for name, desc in (("k_logits", KLogitsDesc), ("pv_latent", PVDesc), ("decode", DecodeDesc),
+                       ("prefill", PrefillDesc)):
         wsf = getattr(L, f"starkv_{name}_workspace_bytes")
         wsf.restype = ctypes.c_size_t
         wsf.argtypes = [ctypes.POINTER(desc)]
@@ -177,6 +178,9 @@ def lib() -> ctypes.CDLL:
     L.starkv_decode_attention_timed.restype = ctypes.c_int
     L.starkv_decode_attention_timed.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.c_void_p, ctypes.c_size_t,
                                                 ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    L.starkv_prefill_attention_timed.restype = ctypes.c_int
+    L.starkv_prefill_attention_timed.argtypes = [ctypes.POINTER(PrefillDesc), ctypes.c_void_p, ctypes.c_size_t,
+                                                 ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
     L.starkv_k_append.restype = ctypes.c_int
     L.starkv_k_append.argtypes = [ctypes.POINTER(KAppendDesc), ctypes.c_void_p]
     L.starkv_v_append.restype = ctypes.c_int

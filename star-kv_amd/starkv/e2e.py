@@ -4,9 +4,10 @@ reference's ``latency.py --mode e2e``, latency.py:69-154).
 A Llama-shaped ``LlamaForCausalLM`` (transformers) whose every attention is
 ``LatentAttention``: latent K and V projections (ragged K ranks per KV head,
 one V latent per layer), a static ``LatentCache`` written in place by the HIP
-cache writer (quantised on the fly), decode on ``starkv_decode_attention``,
-and prefill by causal SDPA over the cache's dequantised latents projected back
-to K and V (the reference materialises K and V the same way, model.py:429-449).
+cache writer (quantised on the fly), decode on ``starkv_decode_attention`` and
+prefill on ``starkv_prefill_attention`` (K and V reconstructed from the cache's
+latents by MFMA, then causal flash attention -- the reference materialises K
+and V from the latents and calls SDPA, model.py:429-449).
 
 The reference's e2e path replaces the attentions of a trained, exported model
 (model.py:547-585) and grows its caches with ``torch.cat``
@@ -24,7 +25,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .cache import LatentCache
-from .ops import decode_attention
+from .ops import decode_attention, prefill_attention
 from .rope import RopeConfig
 
 __all__ = ["LatentAttention", "build_model", "generate"]
@@ -44,9 +45,10 @@ class LatentAttention(nn.Module):
     projection, heads back to back), ``bk`` [Hkv, r_max, 128] (B_k = k_u^T, rows
     past r_h unused), ``v_vs`` [Rv, hidden], ``v_u`` [Hkv*128, Rv] (U_v).
 
-    ``reference = True`` runs decode steps through the torch path (dequantised
-    cache, fp32 SDPA) -- the parity reference of the kernel path; prefill takes
-    the same (fp16 SDPA) path in both modes."""
+    ``reference = True`` runs every forward through the torch path (dequantised
+    cache, K / V materialised as the reference does; SDPA in fp32 for decode
+    steps, in the act dtype for prefill) -- the parity reference of the kernel
+    path."""
 
     def __init__(self, config, layer_idx: int, ranks: Sequence[int], v_rank: int, batch: int, capacity: int,
                  fmt: str = "int8_g64", device="cuda", dtype=torch.float16):
@@ -138,7 +140,10 @@ class LatentAttention(nn.Module):
         k_new.index_copy_(2, self.k_scatter, kl)
         k_new = k_new.view(B, T, self.n_kv, self.rmax).permute(0, 2, 1, 3)       # [B, Hkv, T, r_max]
         kspec, vspec, S = self.cache.append(k_new, self.v_vs(hidden_states), self.bk)
-        if T == 1 and not self.reference:
+        if T > 1 and not self.reference:
+            o = prefill_attention(q, kspec, vspec, self.v_u.weight, rope=self.rope, pos0=S - T,
+                                  scale=self.scaling).transpose(1, 2)               # [B, T, Hq, 128]
+        elif T == 1 and not self.reference:
             if self.events is not None:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()

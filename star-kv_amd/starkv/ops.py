@@ -405,7 +405,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
 
 def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tensor,
                       rope: RopeConfig = RopeConfig(), pos0: int = 0, scale: Optional[float] = None,
-                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      out: Optional[torch.Tensor] = None, events: Optional[Sequence] = None) -> torch.Tensor:
     """Causal prefill attention over the latent caches (the reference's prefill
     branch, model.py:429-449, with the causal mask applied): [B, Hq, T, 128]
     in q's dtype.
@@ -413,7 +413,9 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
     q: rotated queries [B, Hq, T, 128] (last dim contiguous) at positions
     pos0 .. pos0 + T - 1; k / xv: the K and V latent caches holding at least
     pos0 + T positions (K dense or int8, V dense [B, S, Rv] or a group-64 int4
-    VLatentSpec); uv_weight: v_proj.U.weight [Hkv*128, Rv]."""
+    VLatentSpec); uv_weight: v_proj.U.weight [Hkv*128, Rv].  ``events``:
+    three torch.cuda.Event recorded before the K / V reconstruction, after it
+    and after the attention kernel (timing)."""
     if q.dim() != 4 or q.shape[-1] != HEAD_DIM or q.stride(-1) != 1:
         raise StarKVError("q must be [B, Hq, T, 128] with a contiguous last dim")
     v = _vspec(xv)
@@ -442,8 +444,16 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
     if nb == 0:
         check(L.starkv_prefill_attention(ctypes.byref(d), None, 0, _stream(q.device)), "starkv_prefill_attention")
     ws = _workspace(q.device, nb)
-    check(L.starkv_prefill_attention(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q.device)),
-          "starkv_prefill_attention")
+    if events is None:
+        check(L.starkv_prefill_attention(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                         _stream(q.device)), "starkv_prefill_attention")
+    else:
+        for e in events:
+            if e.cuda_event == 0:
+                e.record()   # creates the underlying hipEvent
+        handles = (ctypes.c_void_p * 3)(*[e.cuda_event for e in events])
+        check(L.starkv_prefill_attention_timed(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                               _stream(q.device), handles), "starkv_prefill_attention_timed")
     return out
 
 

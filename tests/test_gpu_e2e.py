@@ -1,8 +1,8 @@
 """GPU test of the end-to-end decode harness (starkv.e2e): a small random-init
-Llama-shaped model whose attentions decode on the HIP kernels over
-quantised latent caches, against the same model decoding every step through
-the torch path (dequantised caches, fp32 SDPA), fed the same tokens.  Both
-runs prefill the same way, so their caches start identical."""
+Llama-shaped model whose attentions prefill and decode on the HIP kernels over
+quantised latent caches, against the same model running every forward through
+the torch path (dequantised caches, K / V materialised, SDPA), fed the same
+tokens."""
 import sys
 
 import pytest
@@ -38,8 +38,6 @@ def test_e2e_decode_matches_torch_path(kv_heads, ranks, fmt):
         mr = float(d.mean() / r.double().abs().mean())
         _flush(f"   forward {t}: max_abs={float(d.max()):.3e} mean_rel={mr:.3e}")
         assert torch.isfinite(a).all()
-        if t == 0:
-            assert torch.equal(a, r)               # same prefill path, same caches
         assert mr <= 1e-2, (t, mr)
 
 
@@ -102,6 +100,4 @@ def test_e2e_decode_over_exported_ragged_projections(fmt):
         mr = float(d.mean() / r.double().abs().mean())
         _flush(f"   forward {t}: max_abs={float(d.max()):.3e} mean_rel={mr:.3e}")
         assert torch.isfinite(a).all()
-        if t == 0:
-            assert torch.equal(a, r)
         assert mr <= 1e-2, (t, mr)
