@@ -11,12 +11,12 @@
 //    rounded once more to bf16 for bf16 activations.  Rows in [S, S_pad) are
 //    written as zeros.
 // 2. fa_causal_kernel: flash attention over those buffers, one workgroup per
-//    (b, query head, 128 queries), 4 waves of 32 queries.  Per 32-key block
-//    it forms S^T = K . Q^T (so each lane holds 16 keys of one query and the
-//    online softmax needs one cross-half exchange), with the K rows taken in
-//    the order that makes the lane's probabilities the B operand of
-//    O^T += V^T . P^T directly; V^T is read from LDS with the transpose load.
-//    bf16 splits P into hi + lo so P.V keeps fp32-class accuracy.
+//    (b, query head, 256 queries), 8 waves of 32 queries.  Per 64-key block
+//    it forms S^T = K . Q^T (so each lane holds 32 keys of one query and the
+//    online softmax needs one cross-half exchange); the lane's probabilities
+//    are the B operand of O^T += V^T . P^T as they stand, V^T read from LDS
+//    with the transpose load in the matching key order.  bf16 splits P into
+//    hi + lo so P.V keeps fp32-class accuracy.
 #include "common.hpp"
 
 namespace starkv {
@@ -153,18 +153,21 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
     }
   }
 
+  // Ranks past R (the last step only) read a valid chunk instead (address
+  // clamped to rank R - 8): the A rows of those ranks are zero, so any finite
+  // value adds nothing, and no load is conditional (a conditional load would
+  // zero its register first and wait for the previous load into it).
   auto load = [&](int ks, RcRaw<KIND, Q>& r) {
     const int j0 = ks * RC_KS + 32 * hh;             // this lane's first rank of the step
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       if constexpr (KIND == 1 && Q) {
-        const uint8_t* src = xrow[nt] + j0 / 2;
-        if (j0 + 32 <= R) {
-          r.d[nt] = *(const uint4*)src;
+        if (ks * RC_KS + RC_KS <= R) {               // whole step in range (uniform)
+          r.d[nt] = *(const uint4*)(xrow[nt] + j0 / 2);
         } else {
           uint32_t w[4];
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) w[kk] = j0 + 8 * kk < R ? *(const uint32_t*)(src + 4 * kk) : 0u;
+          for (int kk = 0; kk < 4; ++kk) w[kk] = *(const uint32_t*)(xrow[nt] + min(j0 + 8 * kk, R - 8) / 2);
           r.d[nt] = make_uint4(w[0], w[1], w[2], w[3]);
         }
         const int g = min(ks * RC_KS, R - 1) >> 6;
@@ -173,16 +176,14 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
       } else {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const int j = j0 + 8 * kk;
-          const bool ok = j < R;
-          if constexpr (!Q) r.d[nt][kk] = ok ? *(const uint4*)(xrow[nt] + 2 * j) : make_uint4(0, 0, 0, 0);
-          else r.d[nt][kk] = ok ? *(const uint2*)(xrow[nt] + j) : make_uint2(0, 0);
+          const int j = min(j0 + 8 * kk, R - 8);
+          if constexpr (!Q) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * j);
+          else r.d[nt][kk] = *(const uint2*)(xrow[nt] + j);
         }
       }
     }
   };
-  // raw -> B fragment (act dtype).  Ranks past R read as zero bytes (int4:
-  // the zero point); the A rows of those ranks are zero, so they add nothing.
+  // raw -> B fragment (act dtype)
   auto frag = [&](const RcRaw<KIND, Q>& r, int nt, int kk) -> uint4 {
     if constexpr (!Q) {
       return r.d[nt][kk];
@@ -204,16 +205,16 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   const int tr_off = (32 * hh + (rho >> 2)) * BK_PITCH + 16 * (g4 & 1) + 4 * (rho & 3);
   const XT* uvh = (const XT*)a.uv + (int64_t)h * HEAD_DIM * a.uv_rs;
   const int ur = tid >> 1, uc = (tid & 1) * 32;       // V: this thread's U_v row and 32-rank half
-  auto uv_load = [&](int ks, uint4* u) {
+  auto uv_load = [&](int ks, uint4* u) {              // clamped like the latent loads
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j = ks * RC_KS + uc + 8 * c;
-      u[c] = j < R ? *(const uint4*)(uvh + (int64_t)ur * a.uv_rs + j) : make_uint4(0, 0, 0, 0);
-    }
+    for (int c = 0; c < 4; ++c)
+      u[c] = *(const uint4*)(uvh + (int64_t)ur * a.uv_rs + min(ks * RC_KS + uc + 8 * c, R - 8));
   };
-  auto uv_store = [&](int buf, const uint4* u) {
+  auto uv_store = [&](int buf, int ks, const uint4* u) {   // ranks past R stored as zero rows of A
 #pragma unroll
-    for (int c = 0; c < 4; ++c) *(uint4*)&lds[buf * UV_BUF + ur * UV_PITCH + uc + 8 * c] = u[c];
+    for (int c = 0; c < 4; ++c)
+      *(uint4*)&lds[buf * UV_BUF + ur * UV_PITCH + uc + 8 * c] =
+          ks * RC_KS + uc + 8 * c < R ? u[c] : make_uint4(0, 0, 0, 0);
   };
   uint4 un[4];
   if constexpr (KIND == 0) {
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
     }
   } else {
     uv_load(0, un);
-    uv_store(0, un);
+    uv_store(0, 0, un);
   }
   floatx16 acc[4][4];
 #pragma unroll
@@ -241,12 +242,10 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = floatx16{};
 
-  // one K-step over latent data `cur` (the next U_v stage is fetched meanwhile)
+  // one K-step over latent data `cur`; the next U_v stage (already requested
+  // into `un`) is stored to LDS after it
   auto step = [&](int ks, const RcRaw<KIND, Q>& cur) {
     const bool more = ks + 1 < nks;
-    if constexpr (KIND == 1) {
-      if (more) uv_load(ks + 1, un);
-    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       uint4 bf[4];
@@ -267,7 +266,7 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
       }
     }
     if constexpr (KIND == 1) {
-      if (more) uv_store((ks + 1) & 1, un);
+      if (more) uv_store((ks + 1) & 1, ks + 1, un);
       __syncthreads();
     }
   };
@@ -279,23 +278,37 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
     if (nks > 1) load(1, r1);
     __syncthreads();
     // at the top of each round r0 / r1 hold (or are loading) K-steps ks / ks + 1
+    // (the U_v stage is requested before the latent loads: loads complete in
+    // order, so storing it waits only for itself)
     int ks = 0;
     for (; ks + 3 <= nks; ks += 3) {
+      uv_load(ks + 1, un);
       load(ks + 2, r2);
       step(ks, r0);
+      if (ks + 2 < nks) uv_load(ks + 2, un);
       if (ks + 3 < nks) load(ks + 3, r0);
       step(ks + 1, r1);
+      if (ks + 3 < nks) uv_load(ks + 3, un);
       if (ks + 4 < nks) load(ks + 4, r1);
       step(ks + 2, r2);
     }
-    if (ks < nks) step(ks, r0);
-    if (ks + 1 < nks) step(ks + 1, r1);
+    if (ks < nks) {
+      if (ks + 1 < nks) uv_load(ks + 1, un);
+      step(ks, r0);
+    }
+    if (ks + 1 < nks) {
+      if (ks + 2 < nks) uv_load(ks + 2, un);
+      step(ks + 1, r1);
+    }
   } else {
     RcRaw<KIND, Q> cur, nxt;
     load(0, cur);
     __syncthreads();
     for (int ks = 0; ks < nks; ++ks) {
       const bool more = ks + 1 < nks;
+      if constexpr (KIND == 1) {
+        if (more) uv_load(ks + 1, un);
+      }
       if (more) load(ks + 1, nxt);
       step(ks, cur);
       if (more) cur = nxt;
@@ -364,6 +377,231 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// V reconstruction, two KV heads per workgroup of 8 waves: 256 positions x
+// 256 dims, wave w computing head 2 hp + (w & 1) for positions
+// 64 (w >> 1) .. + 63 as 4 x 2 MFMA tiles (128 accumulators, so two waves fit
+// a SIMD and hide each other's latencies; the two heads' waves read the same
+// latent rows, the second from L1).  Per 64-rank step the U_v rows of both
+// heads are staged in LDS; group-64 scale and zero of the workgroup's
+// positions are staged 16 groups at a time.  Same lane / K-chunk layout and
+// epilogue as recon_kernel.
+// ---------------------------------------------------------------------------
+constexpr int RV_POS = 256;                          // positions per workgroup
+constexpr int RV_WAVE_POS = 64;                      // positions per wave (2 N-tiles)
+constexpr int RV_UVBUF = 2 * HEAD_DIM * UV_PITCH;    // halves per U_v stage (two heads)
+constexpr int RV_SZG = 16;                           // scale / zero groups per LDS chunk
+constexpr int RV_SZ_OFF = 2 * RV_UVBUF;              // halves: chunk [position][RV_SZG] x (scale | zero << 16)
+static_assert(RV_SZ_OFF + RV_POS * RV_SZG * 2 <= RC_LDS, "V reconstruction LDS");
+static_assert(8 * RV_WAVE_POS * C_PITCH <= RC_LDS, "V reconstruction epilogue LDS");
+
+template <bool Q> struct RvRaw { uint4 d[2][4]; };                       // dense: [N-tile][K-chunk]
+template <> struct RvRaw<true> { uint4 d[2]; };                          // group-64 int4: word kk = chunk kk
+
+template <typename XT, bool Q>
+__global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hh = lane >> 5;
+  // XCD-aware order as in recon_kernel: the head pairs of one (b, 256
+  // positions) share an XCD
+  const int L = blockIdx.x, t8 = L >> 3;
+  const int nhp = (a.Hkv + 1) >> 1;
+  const int hp = t8 % nhp, blk = (t8 / nhp) * 8 + (L & 7);
+  if (blk >= a.rv_blocks) return;
+  const int b = blk / a.rv_nb;
+  const int p0 = (blk - b * a.rv_nb) * RV_POS;
+  const int hw = 2 * hp + (wave & 1);
+  const bool hlive = hw < a.Hkv;                     // an odd Hkv leaves the last pair's second head empty
+  const int pl0 = RV_WAVE_POS * (wave >> 1);         // first local position of this wave
+  const int pw = p0 + pl0;
+  const int S = a.S, R = a.Rv;
+  const int nks = (R + RC_KS - 1) / RC_KS;
+
+  const uint8_t* xrow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int pc = min(pw + nt * 32 + n, S - 1);
+    constexpr int64_t es = Q ? 1 : 2;
+    xrow[nt] = (const uint8_t*)a.vx + (b * a.vx_sb + (int64_t)pc * a.vx_ss) * es;
+  }
+  uint32_t* szl = (uint32_t*)(lds + RV_SZ_OFF);
+  auto sz_stage = [&](int ks) {                      // groups ks .. ks + RV_SZG - 1 of every position
+    const int pl = tid >> 1, gh = (tid & 1) * (RV_SZG / 2);
+    const int pc = min(p0 + pl, S - 1);
+    const int64_t o = b * a.vs_sb + (int64_t)pc * a.vs_ss;
+    const int G = (R + 63) >> 6;
+#pragma unroll
+    for (int i = 0; i < RV_SZG / 2; ++i) {
+      const int g = min(ks + gh + i, G - 1);
+      szl[pl * RV_SZG + gh + i] = (uint32_t)((const uint16_t*)a.vscale)[o + g] |
+                                  ((uint32_t)((const uint16_t*)a.vzero)[o + g] << 16);
+    }
+  };
+
+  // latent loads: as in recon_kernel, clamped to rank R - 8 past the end
+  typedef RvRaw<Q> Raw;
+  auto load = [&](int ks, Raw& r) {
+    const int j0 = ks * RC_KS + 32 * hh;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      if constexpr (Q) {
+        if (ks * RC_KS + RC_KS <= R) {
+          r.d[nt] = *(const uint4*)(xrow[nt] + j0 / 2);
+        } else {
+          uint32_t w[4];
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) w[kk] = *(const uint32_t*)(xrow[nt] + min(j0 + 8 * kk, R - 8) / 2);
+          r.d[nt] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * min(j0 + 8 * kk, R - 8));
+      }
+    }
+  };
+
+  // U_v stage: thread row tid / 2 (head 2 hp + row / 128, dim row % 128), ranks 32 (tid % 2) .. + 31
+  const int ur = tid >> 1, uc = (tid & 1) * 32;
+  const int uh = min(2 * hp + (ur >> 7), a.Hkv - 1);
+  const XT* urow = (const XT*)a.uv + ((int64_t)uh * HEAD_DIM + (ur & 127)) * a.uv_rs;
+  uint4 un[4];
+  auto uv_load = [&](int ks) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) un[c] = *(const uint4*)(urow + min(ks * RC_KS + uc + 8 * c, R - 8));
+  };
+  auto uv_store = [&](int buf, int ks) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *(uint4*)&lds[buf * RV_UVBUF + ur * UV_PITCH + uc + 8 * c] =
+          ks * RC_KS + uc + 8 * c < R ? un[c] : make_uint4(0, 0, 0, 0);
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = floatx16{};
+  const int abase = (wave & 1) * HEAD_DIM * UV_PITCH;  // this wave's head within a U_v stage
+
+  auto step = [&](int ks, const Raw& cur) {
+    const bool more = ks + 1 < nks;
+    uint32_t sz[2] = {0, 0};
+    if constexpr (Q) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) sz[nt] = szl[(pl0 + nt * 32 + n) * RV_SZG + ks % RV_SZG];
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4 bf[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        if constexpr (Q) {
+          const uint32_t w = kk == 0 ? cur.d[nt].x : kk == 1 ? cur.d[nt].y : kk == 2 ? cur.d[nt].z : cur.d[nt].w;
+          bf[nt] = pf_dq_g64(w, (uint16_t)(sz[nt] & 0xffff), (uint16_t)(sz[nt] >> 16));
+          if constexpr (!__is_same(XT, _Float16)) bf[nt] = pf_f16_to_bf16(bf[nt]);
+        } else {
+          bf[nt] = cur.d[nt][kk];
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const uint4 af = *(const uint4*)&lds[(ks & 1) * RV_UVBUF + abase + (mt * 32 + n) * UV_PITCH + 32 * hh + 8 * kk];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = pf_mfma<XT>(af, bf[nt], acc[mt][nt]);
+      }
+    }
+    if (more) uv_store((ks + 1) & 1, ks + 1);
+    if constexpr (Q) {
+      if (more && (ks + 1) % RV_SZG == 0) {
+        __syncthreads();                             // everyone done with the old chunk
+        sz_stage(ks + 1);
+      }
+    }
+    __syncthreads();
+  };
+
+  uv_load(0);
+  uv_store(0, 0);
+  if constexpr (Q) sz_stage(0);
+  if constexpr (!Q) {
+    // dense latents: one step ahead (a step's fragments take 32 registers)
+    Raw cur, nxt;
+    load(0, cur);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int ks = 0; ks < nks; ++ks) {
+      const bool more = ks + 1 < nks;
+      if (more) {
+        uv_load(ks + 1);
+        load(ks + 1, nxt);
+      }
+      step(ks, cur);
+      if (more) cur = nxt;
+    }
+  } else {
+    // packed latents two steps ahead, the U_v stage one step ahead (requested
+    // first: loads complete in order, so storing it waits only for itself)
+    Raw r0, r1, r2;
+    load(0, r0);
+    if (nks > 1) load(1, r1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int ks = 0;
+    for (; ks + 3 <= nks; ks += 3) {
+      uv_load(ks + 1);
+      load(ks + 2, r2);
+      step(ks, r0);
+      if (ks + 2 < nks) uv_load(ks + 2);
+      if (ks + 3 < nks) load(ks + 3, r0);
+      step(ks + 1, r1);
+      if (ks + 3 < nks) uv_load(ks + 3);
+      if (ks + 4 < nks) load(ks + 4, r1);
+      step(ks + 2, r2);
+    }
+    if (ks < nks) {
+      if (ks + 1 < nks) uv_load(ks + 1);
+      step(ks, r0);
+    }
+    if (ks + 1 < nks) {
+      if (ks + 2 < nks) uv_load(ks + 2);
+      step(ks + 1, r1);
+    }
+  }
+
+  // epilogue (the last step ended with a barrier): stage 64 x 128 per wave, write whole rows
+  uint16_t* cw = lds + wave * RV_WAVE_POS * C_PITCH;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const bool live = pw + nt * 32 + n < S;
+    uint16_t* crow = cw + (nt * 32 + n) * C_PITCH + 4 * hh;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t w[2];
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const float v0 = live ? acc[mt][nt][4 * q + 2 * c2] : 0.f;
+          const float v1 = live ? acc[mt][nt][4 * q + 2 * c2 + 1] : 0.f;
+          w[c2] = (uint32_t)pf_bits<XT>(v0) | ((uint32_t)pf_bits<XT>(v1) << 16);
+        }
+        *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(w[0], w[1]);
+      }
+  }
+  __syncthreads();
+  if (hlive) {
+    XT* dst = (XT*)a.vbuf + (((int64_t)b * a.Hkv + hw) * a.S_pad) * HEAD_DIM;
+#pragma unroll 4
+    for (int it = 0; it < RV_WAVE_POS * 16 / 64; ++it) {
+      const int idx = it * 64 + lane, row = idx >> 4, ch = idx & 15;
+      const int p = pw + row;
+      if (p < a.S_pad) *(uint4*)(dst + (int64_t)p * HEAD_DIM + ch * 8) = *(const uint4*)&cw[row * C_PITCH + ch * 8];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Causal flash attention over the reconstructed K / V.  Workgroup: 8 waves x
 // 32 queries of one (b, query head); key blocks of 64 staged in LDS, the next
 // block loaded into registers while the current one is computed.  Per block
@@ -375,6 +613,8 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 // probability stays <= 2^FA_RESCALE_LOG2 (exact in the final O / l).
 // ---------------------------------------------------------------------------
 constexpr int FA_KB = 64;                        // keys per block
+constexpr int FA_VPITCH = 144;                   // halves per staged V row: rows 8 banks apart for the
+                                                 // transposed reads (K keeps WT_PITCH for 16-byte reads)
 constexpr int FA_WAVES = 8;                      // waves per workgroup, 32 queries each
 constexpr int FA_QB = 32 * FA_WAVES;             // queries per workgroup
 constexpr float FA_RESCALE_LOG2 = 8.0f;
@@ -382,7 +622,7 @@ constexpr float FA_RESCALE_LOG2 = 8.0f;
 template <typename XT>
 __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][FA_KB * WT_PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][FA_KB * WT_PITCH];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][FA_KB * FA_VPITCH];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
@@ -419,22 +659,27 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
   const size_t hbase = (((size_t)b * a.Hkv + kv) * a.S_pad) * HEAD_DIM;
   const XT* kg = (const XT*)a.kbuf + hbase;
   const XT* vg = (const XT*)a.vbuf + hbase;
-  // S^T A operand: MFMA row r = n takes key pi(r) of the 32-key tile
-  const int ra = n >> 3, rh = (n >> 2) & 1, rc = n & 3;
-  const int key_r = 16 * (ra >> 1) + 8 * rh + 4 * (ra & 1) + rc;
-  // V^T A operand: transposed reads (lane group g = lane/16, rho = lane%16)
+  // S^T = K . Q^T puts key 8 (v/4) + 4 hh + v%4 of its 32-key tile in
+  // element v of lane (n, hh).  The P.V MFMA takes its 16-key chunk kk in that
+  // order: lane half hh holds keys 16 kk + 4 hh + 0..3 and 16 kk + 8 + 4 hh +
+  // 0..3 of both P^T (elements 8 kk .. 8 kk + 7) and V^T (transposed reads of
+  // rows 4 hh + 0..3 and 8 + 4 hh + 0..3; lane group g = lane/16, rho = lane%16).
   const int g = lane >> 4, rho = lane & 15;
-  const int tr_off = (8 * hh + (rho >> 2)) * WT_PITCH + 16 * (g & 1) + 4 * (rho & 3);
+  const int tr_off = (4 * hh + (rho >> 2)) * FA_VPITCH + 16 * (g & 1) + 4 * (rho & 3);
   // staging: thread piece i (of 2) covers key 32 i + tid / 16, dims (tid % 16) * 8 .. + 7
   static_assert(FA_KB * 16 == 2 * FA_WAVES * 64, "two 16-byte pieces per thread and tensor");
   const int skey = tid >> 4, sd8 = (tid & 15) * 8;
   const size_t so0 = (size_t)skey * HEAD_DIM + sd8, so1 = so0 + (size_t)32 * HEAD_DIM;
   const int lo0 = skey * WT_PITCH + sd8, lo1 = lo0 + 32 * WT_PITCH;
+  const int vo0 = skey * FA_VPITCH + sd8, vo1 = vo0 + 32 * FA_VPITCH;
   // K / V pieces in flight (plain variables: they stay in registers)
   uint4 k0 = *(const uint4*)(kg + so0), k1 = *(const uint4*)(kg + so1);
   uint4 v0 = *(const uint4*)(vg + so0), v1 = *(const uint4*)(vg + so1);
   *(uint4*)&Ks[0][lo0] = k0; *(uint4*)&Ks[0][lo1] = k1;
-  *(uint4*)&Vs[0][lo0] = v0; *(uint4*)&Vs[0][lo1] = v1;
+  *(uint4*)&Vs[0][vo0] = v0; *(uint4*)&Vs[0][vo1] = v1;
+  // every load so far (Q included) complete: the loop's MFMAs then wait only
+  // on LDS, never on the next block's loads in flight
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
@@ -445,21 +690,25 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
       v0 = *(const uint4*)(vg + go + so0); v1 = *(const uint4*)(vg + go + so1);
     }
     if (kb * FA_KB <= w_last) {                     // wave-uniform: the block has keys this wave sees
-      floatx16 s[2];
+      // the two key tiles' MFMA chains interleaved, all 16 K fragments read up front
+      floatx16 s[2] = {floatx16{}, floatx16{}};
+      const uint16_t* kbase = &Ks[buf][n * WT_PITCH + 8 * hh];
+      uint4 kf[2][8];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = floatx16{};
-        const uint16_t* kbase = &Ks[buf][(kt * 32 + key_r) * WT_PITCH + 8 * hh];
+      for (int k = 0; k < 8; ++k)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) s[kt] = pf_mfma<XT>(*(const uint4*)(kbase + 16 * k), Qb[k], s[kt]);
-      }
-      // lane: keys kb*64 + 32 kt + 16 (v/8) + 8 hh + v%8 of query t
+        for (int kt = 0; kt < 2; ++kt) kf[kt][k] = *(const uint4*)(kbase + kt * 32 * WT_PITCH + 16 * k);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[kt] = pf_mfma<XT>(kf[kt][k], Qb[k], s[kt]);
+      // lane: keys kb*64 + 32 kt + 8 (v/4) + 4 hh + v%4 of query t
       if (kb * FA_KB + FA_KB - 1 > w_first) {         // the block reaches past some query of the wave
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int key = kb * FA_KB + 32 * kt + 16 * (v >> 3) + 8 * hh + (v & 7);
+            const int key = kb * FA_KB + 32 * kt + 8 * (v >> 2) + 4 * hh + (v & 3);
             if (key > P) s[kt][v] = -INFINITY;
           }
       }
@@ -494,7 +743,7 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const uint16_t* sb = &Vs[buf][(32 * kt + 16 * kk) * WT_PITCH + tr_off];
+          const uint16_t* sb = &Vs[buf][(32 * kt + 16 * kk) * FA_VPITCH + tr_off];
           if constexpr (__is_same(XT, _Float16)) {
             half8 ph;
 #pragma unroll
@@ -502,7 +751,7 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
             const uint4 pb = __builtin_bit_cast(uint4, ph);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 4 * WT_PITCH);
+              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 8 * FA_VPITCH);
               o[j] = pf_mfma<XT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[j]);
             }
           } else {
@@ -516,7 +765,7 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
             const uint4 pbh = __builtin_bit_cast(uint4, ph), pbl = __builtin_bit_cast(uint4, pl);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 4 * WT_PITCH);
+              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 8 * FA_VPITCH);
               const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
               o[j] = pf_mfma<XT>(va, pbh, o[j]);
               o[j] = pf_mfma<XT>(va, pbl, o[j]);
@@ -526,7 +775,7 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
     }
     if (more) {
       *(uint4*)&Ks[buf ^ 1][lo0] = k0; *(uint4*)&Ks[buf ^ 1][lo1] = k1;
-      *(uint4*)&Vs[buf ^ 1][lo0] = v0; *(uint4*)&Vs[buf ^ 1][lo1] = v1;
+      *(uint4*)&Vs[buf ^ 1][vo0] = v0; *(uint4*)&Vs[buf ^ 1][vo1] = v1;
     }
     __syncthreads();                                // next block staged; this one free to overwrite
   }
@@ -549,8 +798,11 @@ static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t m
   const dim3 rg((unsigned)(ceil_div(r.rc_blocks, 8) * 8 * a.Hkv));
   if (a.k_i8) hipLaunchKernelGGL((recon_kernel<XT, 0, true>), rg, dim3(256), 0, st, r);
   else hipLaunchKernelGGL((recon_kernel<XT, 0, false>), rg, dim3(256), 0, st, r);
-  if (a.v_g64) hipLaunchKernelGGL((recon_kernel<XT, 1, true>), rg, dim3(256), 0, st, r);
-  else hipLaunchKernelGGL((recon_kernel<XT, 1, false>), rg, dim3(256), 0, st, r);
+  r.rv_nb = (int)ceil_div(a.S, RV_POS);
+  r.rv_blocks = r.rv_nb * B;
+  const dim3 vg((unsigned)(ceil_div(r.rv_blocks, 8) * 8 * ((a.Hkv + 1) / 2)));
+  if (a.v_g64) hipLaunchKernelGGL((recon_v_kernel<XT, true>), vg, dim3(512), 0, st, r);
+  else hipLaunchKernelGGL((recon_v_kernel<XT, false>), vg, dim3(512), 0, st, r);
   int e = (int)hipGetLastError();
   if (e) return e;
   if (mid && (e = (int)hipEventRecord(mid, st))) return e;
