@@ -81,6 +81,19 @@ def test_decode_llama3_rope_gqa_bf16():
     _check(case, ref, rope=rope)
 
 
+def test_decode_attention_scaling_applied_once():
+    """A RoPE attention scaling a != 1 multiplies cos and sin (HF
+    LlamaRotaryEmbedding); the rotated query already carries one factor, the
+    keys get theirs from the table, and the softmax scale is not multiplied
+    again."""
+    from starkv import RopeConfig
+    rope = RopeConfig(attention_scaling=1.25)
+    case = make_case(2, 32, 8, 700, cfg4_ranks(), 256, seed=5)
+    _flush("[decode] attention_scaling 1.25")
+    ref, _, _ = oracle_decode(case, rope=rope)
+    _check(case, ref, rope=rope)
+
+
 def test_decode_with_mask():
     case = make_case(2, 32, 32, 500, [32] * 32, 256, seed=3, layout="reference")
     mask = torch.zeros(2, 1, 1, 500, device="cuda", dtype=torch.float16)

@@ -51,7 +51,7 @@ def _bk(ranks, dtype, g):
     return bk_all, bko, heads
 
 
-def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0):
+def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0, rope=None):
     from oracle import starkv_oracle as o
     from starkv import KLatentSpec, RopeConfig, prefill_attention
     from starkv._lib import FMT_INT8_SYM
@@ -81,7 +81,7 @@ def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0):
         xv = torch.from_numpy(dq.astype(np.float64)).to(dtype).double()
     uv = (torch.randn(Hkv * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).to(dtype)
     q = torch.randn(B, Hq, T, HEAD, generator=g, device="cuda").to(dtype)
-    rope = RopeConfig()
+    rope = rope or RopeConfig()
     out = prefill_attention(q, kspec, v, uv, rope=rope, pos0=pos0)
     torch.cuda.synchronize()
     cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), rope.attention_scaling)
@@ -111,6 +111,16 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_prefill_matches_oracle(case):
     _run(*case[1:])
+
+
+@pytest.mark.gpu
+def test_prefill_llama3_rope_attention_scaling():
+    """llama3 inverse frequencies and an attention scaling != 1 (applied once,
+    through the keys' RoPE table), chunked, GQA."""
+    from starkv import RopeConfig
+    rope = RopeConfig(theta=500000.0, rope_type="llama3", factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                      original_max_position_embeddings=8192, attention_scaling=1.25)
+    _run(1, 8, [32, 128], 96, 150, 260, torch.float16, rope=rope)
 
 
 @pytest.mark.gpu
