@@ -256,6 +256,10 @@ typedef struct {
   int dtype;
   const void* src; int64_t src_stride_b, src_stride_h, src_stride_t;
   starkv_klatent k;
+  const int* pos0_device;   /* optional (NULL: use pos0): device int read by the kernel at
+                               run time, for calls captured once in a HIP graph and replayed
+                               at advancing positions; rows landing at or past capacity are
+                               then skipped by the kernel instead of rejected by the host */
 } starkv_k_append_desc;
 
 typedef struct {
@@ -263,6 +267,7 @@ typedef struct {
   int dtype;
   const void* src; int64_t src_stride_b, src_stride_t;
   starkv_vlatent v;
+  const int* pos0_device;   /* as in starkv_k_append_desc */
 } starkv_v_append_desc;
 
 int starkv_k_append(const starkv_k_append_desc* d, void* stream);

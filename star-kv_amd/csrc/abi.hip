@@ -664,7 +664,7 @@ int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, 
 int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;
-  if ((int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
+  if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
   if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
   const starkv_klatent& k = d->k;
   int st = validate_klayout(k, d->dtype);
@@ -673,7 +673,8 @@ int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
   if (d->src_stride_b < 0 || d->src_stride_h < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
   KAppendArgs a = {};
   a.src = d->src; a.src_sb = d->src_stride_b; a.src_sh = d->src_stride_h; a.src_st = d->src_stride_t;
-  a.B = d->batch; a.H = k.n_kv_heads; a.T = d->n_tokens; a.pos0 = d->pos0;
+  a.B = d->batch; a.H = k.n_kv_heads; a.T = d->n_tokens; a.pos0 = d->pos0; a.cap = d->capacity;
+  a.pos0_dev = d->pos0_device;
   a.fmt = k.format;
   a.data = (void*)k.data; a.stride_b = k.stride_b;
   a.scale = (void*)k.scale; a.sc_sb = k.scale_stride_b; a.sc_sh = k.scale_stride_h;
@@ -694,7 +695,7 @@ int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
 int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;
-  if ((int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
+  if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
   if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
   PVArgs pa = {};
   int vq = 0, st;
@@ -703,7 +704,8 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   if (d->src_stride_b < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
   VAppendArgs a = {};
   a.src = d->src; a.src_sb = d->src_stride_b; a.src_st = d->src_stride_t;
-  a.B = d->batch; a.T = d->n_tokens; a.pos0 = d->pos0; a.R = d->v.rank; a.vq = vq;
+  a.B = d->batch; a.T = d->n_tokens; a.pos0 = d->pos0; a.cap = d->capacity; a.R = d->v.rank; a.vq = vq;
+  a.pos0_dev = d->pos0_device;
   a.data = (void*)pa.x; a.stride_b = pa.x_sb; a.stride_s = pa.x_ss;
   a.scale = (void*)pa.xs; a.sc_sb = pa.xs_sb; a.sc_ss = pa.xs_ss;
   a.zero = (void*)pa.xz;

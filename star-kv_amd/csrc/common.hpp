@@ -105,7 +105,8 @@ struct PVArgs {
 // ---------------------------------------------------------------------------
 struct KAppendArgs {
   const void* src; int64_t src_sb, src_sh, src_st;   // new rows (b, h, t), act dtype, elements
-  int B, H, T, pos0;
+  int B, H, T, pos0, cap;
+  const int* pos0_dev;                              // optional: position read at run time
   int fmt;                                          // STARKV_FMT_DENSE or a quantised format
   void* data; int64_t stride_b;                     // dense: elements; quantised: bytes
   void* scale; int64_t sc_sb, sc_sh;
@@ -119,7 +120,9 @@ struct KAppendArgs {
 
 struct VAppendArgs {
   const void* src; int64_t src_sb, src_st;          // new rows (b, t), act dtype, elements
-  int B, T, pos0, R, vq;
+  int B, T, pos0, cap, R, vq;
+  int gw;                                           // waves per row (group-64: one per group)
+  const int* pos0_dev;                              // optional: position read at run time
   void* data; int64_t stride_b, stride_s;
   void* scale; int64_t sc_sb, sc_ss;
   void* zero;                                       // VQ_G64 (strides of scale)

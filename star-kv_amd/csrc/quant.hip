@@ -64,9 +64,10 @@ __device__ void quant_block(const T* x, int j0, int j1, bool int8, uint8_t* q, u
 }
 
 // Group-64 asymmetric int4 of the row: nibbles into q, scale / zero of group g at sp[g] / zp[g].
+// one group of 64 ranks (ranks g0 .. g0 + 63 of the row)
 template <typename T>
-__device__ void quant_g64(const T* x, int R, uint8_t* q, uint16_t* sp, uint16_t* zp, int lane) {
-  for (int g0 = 0; g0 < R; g0 += 64) {
+__device__ void quant_g64(const T* x, int R, int g0, uint8_t* q, uint16_t* sp, uint16_t* zp, int lane) {
+  {
     const int j = g0 + lane;
     const bool ok = j < R;
     const float v = ok ? ldx(x, j) : 0.f;
@@ -93,7 +94,8 @@ __global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= (int64_t)a.B * a.H * a.T) return;
   const int t = (int)(row % a.T), h = (int)((row / a.T) % a.H), b = (int)(row / ((int64_t)a.T * a.H));
-  const int s = a.pos0 + t, r = a.rank[h];
+  const int s = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t, r = a.rank[h];
+  if (s < 0 || s >= a.cap) return;                  // only a run-time position can land here
   const T* x = (const T*)a.src + b * a.src_sb + h * a.src_sh + (int64_t)t * a.src_st;
   if (a.fmt == STARKV_FMT_DENSE) {
     T* d = (T*)a.data + b * a.stride_b + a.off[h] + (int64_t)s * a.pitch[h];
@@ -111,13 +113,17 @@ __global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
   }
 }
 
+// one row per wave; group-64 int4: one (row, group) per wave
 template <typename T>
 __global__ __launch_bounds__(256) void v_append_kernel(const VAppendArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = wid / a.gw;
+  const int grp = (int)(wid - row * a.gw);
   if (row >= (int64_t)a.B * a.T) return;
   const int t = (int)(row % a.T), b = (int)(row / a.T);
-  const int s = a.pos0 + t, R = a.R;
+  const int s = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t, R = a.R;
+  if (s < 0 || s >= a.cap) return;                  // only a run-time position can land here
   const T* x = (const T*)a.src + b * a.src_sb + (int64_t)t * a.src_st;
   if (a.vq == VQ_DENSE) {
     T* d = (T*)a.data + b * a.stride_b + (int64_t)s * a.stride_s;
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(256) void v_append_kernel(const VAppendArgs a) {
   uint8_t* q = (uint8_t*)a.data + b * a.stride_b + (int64_t)s * a.stride_s;
   uint16_t* sp = (uint16_t*)a.scale + b * a.sc_sb + (int64_t)s * a.sc_ss;
   if (a.vq == VQ_G64) {
-    quant_g64(x, R, q, sp, (uint16_t*)a.zero + b * a.sc_sb + (int64_t)s * a.sc_ss, lane);
+    quant_g64(x, R, 64 * grp, q, sp, (uint16_t*)a.zero + b * a.sc_sb + (int64_t)s * a.sc_ss, lane);
     return;
   }
   quant_block(x, 0, min(R, a.split), a.a_int8, q, sp, lane);
@@ -150,9 +156,11 @@ int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st) {
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st) {
   const int64_t rows = (int64_t)a.B * a.T;
   if (rows == 0) return 0;
-  const dim3 grid((unsigned)ceil_div(rows, 4));
-  if (dtype == STARKV_F16) hipLaunchKernelGGL(v_append_kernel<_Float16>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(v_append_kernel<__bf16>, grid, dim3(256), 0, st, a);
+  VAppendArgs r = a;
+  r.gw = a.vq == VQ_G64 ? (int)ceil_div(a.R, 64) : 1;
+  const dim3 grid((unsigned)ceil_div(rows * r.gw, 4));
+  if (dtype == STARKV_F16) hipLaunchKernelGGL(v_append_kernel<_Float16>, grid, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL(v_append_kernel<__bf16>, grid, dim3(256), 0, st, r);
   return (int)hipGetLastError();
 }
 

@@ -107,6 +107,7 @@ class KAppendDesc(ctypes.Structure):
         ("src", ctypes.c_void_p), ("src_stride_b", ctypes.c_int64), ("src_stride_h", ctypes.c_int64),
         ("src_stride_t", ctypes.c_int64),
         ("k", KLatent),
+        ("pos0_device", ctypes.c_void_p),
     ]
 
 
@@ -116,6 +117,7 @@ class VAppendDesc(ctypes.Structure):
         ("dtype", ctypes.c_int),
         ("src", ctypes.c_void_p), ("src_stride_b", ctypes.c_int64), ("src_stride_t", ctypes.c_int64),
         ("v", VLatent),
+        ("pos0_device", ctypes.c_void_p),
     ]
 
 

@@ -177,6 +177,18 @@ class LatentCache:
             parts.append((n - 8) * self.v_scale2[:, :S].double())
         return torch.cat(parts, -1).to(self.dtype)
 
+    def append_at(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor, pos: torch.Tensor):
+        """Write k_new / v_new at the position held by the int32 device tensor
+        ``pos`` (read when the writer kernels run, so the call can be captured in
+        a CUDA/HIP graph and replayed at advancing positions); the host-side
+        ``length`` is left to the caller.  Returns the (K spec, V spec)."""
+        if v_new.shape[1] != k_new.shape[2]:
+            raise StarKVError("k_new and v_new must hold the same number of positions")
+        ks = self.k_spec(bk)
+        k_append(k_new.contiguous() if k_new.stride(3) != 1 else k_new, ks, 0, self.cap, pos0_device=pos)
+        v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, 0, self.cap, pos0_device=pos)
+        return ks, self.v_spec
+
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor):
         """Write T new positions (k_new [B, Hkv, T, r_max], v_new [B, T, Rv]) in
         place; returns (K spec, V spec, length) for the attention kernels."""

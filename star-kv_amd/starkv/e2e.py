@@ -28,7 +28,7 @@ from .cache import LatentCache
 from .ops import decode_attention, prefill_attention
 from .rope import RopeConfig
 
-__all__ = ["LatentAttention", "build_model", "generate"]
+__all__ = ["LatentAttention", "DecodeGraphState", "build_model", "generate", "generate_graphed", "decode_graphed"]
 
 HEAD_DIM = 128
 
@@ -36,6 +36,26 @@ HEAD_DIM = 128
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class DecodeGraphState:
+    """Device-side decode position and mask shared by every layer of a decode
+    step captured once in a CUDA/HIP graph.  Each replay writes the new latents
+    at ``pos`` and attends over the whole cache capacity, the positions not
+    yet written masked off by an additive -1e30; ``open_position`` and
+    ``advance`` run inside the graph."""
+
+    def __init__(self, batch: int, capacity: int, length: int, device):
+        self.capacity = int(capacity)
+        self.pos = torch.tensor([length], dtype=torch.int32, device=device)
+        self.mask = torch.full((batch, 1, self.capacity), -1e30, dtype=torch.float32, device=device)
+        self.mask[:, :, :length] = 0.0
+
+    def open_position(self):
+        self.mask.index_fill_(2, self.pos.long(), 0.0)
+
+    def advance(self):
+        self.pos.add_(1)
 
 
 class LatentAttention(nn.Module):
@@ -78,6 +98,7 @@ class LatentAttention(nn.Module):
         self.scaling = HEAD_DIM ** -0.5
         self.reference = False
         self.events: Optional[list] = None     # (start, end) CUDA events of the decode kernels, when set
+        self.graph: Optional[DecodeGraphState] = None   # set: single-token forwards in graph-replay form
 
     def reset_parameters_(self, gen: Optional[torch.Generator] = None, std: float = 0.02):
         """Random weights of the scales a trained STAR-KV layer has: N(0, std)
@@ -139,6 +160,11 @@ class LatentAttention(nn.Module):
         k_new = torch.zeros(B, T, self.n_kv * self.rmax, dtype=kl.dtype, device=kl.device)
         k_new.index_copy_(2, self.k_scatter, kl)
         k_new = k_new.view(B, T, self.n_kv, self.rmax).permute(0, 2, 1, 3)       # [B, Hkv, T, r_max]
+        if self.graph is not None and T == 1 and not self.reference:
+            kspec, vspec = self.cache.append_at(k_new, self.v_vs(hidden_states), self.bk, self.graph.pos)
+            o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope,
+                                 seq_len=self.graph.capacity, scale=self.scaling, mask=self.graph.mask)
+            return self.o_proj(o.unsqueeze(1).reshape(B, T, self.n_heads * HEAD_DIM)), None
         kspec, vspec, S = self.cache.append(k_new, self.v_vs(hidden_states), self.bk)
         if T > 1 and not self.reference:
             o = prefill_attention(q, kspec, vspec, self.v_u.weight, rope=self.rope, pos0=S - T,
@@ -217,4 +243,82 @@ def generate(model, prompt: torch.Tensor, steps: int, reference: bool = False,
         logits.append(out.logits[:, -1].float())
         tok = logits[-1].argmax(-1, keepdim=True)
         toks.append(tok)
+    return torch.cat(toks, 1), logits
+
+
+@torch.no_grad()
+def generate_graphed(model, prompt: torch.Tensor, steps: int, keep_logits: bool = True):
+    """``generate`` with the decode steps replayed from one captured graph
+    (``decode_graphed``).  Returns (tokens [B, steps + 1], logits of the last
+    position per forward, or [] when ``keep_logits`` is False)."""
+    for att in attention_layers(model):
+        att.reference = False
+    B, P = prompt.shape
+    dev = prompt.device
+    out = model(input_ids=prompt, position_ids=torch.arange(P, device=dev)[None].expand(B, P),
+                use_cache=False, logits_to_keep=1)
+    logits = [out.logits[:, -1].float()] if keep_logits else []
+    tok = out.logits[:, -1].argmax(-1, keepdim=True)
+    if steps == 0:
+        return tok, logits
+    toks, more = decode_graphed(model, tok, steps, keep_logits)
+    return torch.cat([tok, toks], 1), logits + more
+
+
+@torch.no_grad()
+def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = True):
+    """``steps`` greedy decode steps from token ``tok`` [B, 1] at the caches'
+    current length: the first step runs eagerly in graph form (which also
+    warms up every table and workspace), one step is captured, and the rest
+    replay it, each step's argmax feeding the next inside the graph.  Returns
+    (tokens [B, steps], logits per step or [])."""
+    atts = attention_layers(model)
+    B = tok.shape[0]
+    dev = tok.device
+    P = atts[0].cache.length
+    cap = atts[0].cache.cap
+    if any(a.cache.cap != cap or a.cache.length != P for a in atts) or P + steps > cap:
+        raise ValueError("decode_graphed: every layer's cache must hold the decode steps")
+    state = DecodeGraphState(B, cap, P, dev)
+    for att in atts:
+        att.reference = False
+        att.graph = state
+    tok_buf = tok.clone()
+    pos_buf = torch.full((B, 1), P, device=dev, dtype=torch.long)
+    logit_buf = None
+    toks, logits = [], []
+
+    def step():
+        nonlocal logit_buf
+        state.open_position()
+        o = model(input_ids=tok_buf, position_ids=pos_buf, use_cache=False, logits_to_keep=1)
+        if logit_buf is None:
+            logit_buf = torch.empty(B, o.logits.shape[-1], device=dev, dtype=torch.float32)
+        logit_buf.copy_(o.logits[:, -1])
+        tok_buf.copy_(logit_buf.argmax(-1, keepdim=True))
+        state.advance()
+        pos_buf.add_(1)
+
+    try:
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            step()                                    # first decode step, eager, graph form
+        torch.cuda.current_stream(dev).wait_stream(side)
+        if keep_logits:
+            logits.append(logit_buf.clone())
+        toks.append(tok_buf.clone())
+        if steps > 1:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            for _ in range(steps - 1):
+                graph.replay()
+                if keep_logits:
+                    logits.append(logit_buf.clone())
+                toks.append(tok_buf.clone())
+    finally:
+        for att in atts:
+            att.graph = None
+            att.cache.length = P + steps
     return torch.cat(toks, 1), logits

@@ -457,10 +457,13 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
     return out
 
 
-def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int) -> None:
+def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
+             pos0_device: Optional[torch.Tensor] = None) -> None:
     """Write the new K latent rows src [B, Hkv, T, >= r_h] (act dtype, last dim
     contiguous) into the cache described by ``k`` at positions
-    [pos0, pos0 + T), quantising to its format (starkv_k_append)."""
+    [pos0, pos0 + T), quantising to its format (starkv_k_append).
+    ``pos0_device``: an int32 device tensor holding the position, read when
+    the kernel runs (graph capture / replay)."""
     if src.dim() != 4 or src.stride(3) != 1:
         raise StarKVError("src must be [B, Hkv, T, r] with a contiguous last dim")
     _require_cuda(src, *[t for t in (k.data, k.scale, k.data2, k.scale2) if t is not None])
@@ -469,10 +472,20 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int) -> Non
     d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[2], int(pos0), int(capacity), _dt(src)
     d.src, d.src_stride_b, d.src_stride_h, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1), src.stride(2)
     d.k = k.c_struct(keep)
+    d.pos0_device = _pos_ptr(pos0_device)
     check(_lib.lib().starkv_k_append(ctypes.byref(d), _stream(src.device)), "starkv_k_append")
 
 
-def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int) -> None:
+def _pos_ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or not t.is_cuda:
+        raise StarKVError("pos0_device must be an int32 device tensor")
+    return t.data_ptr()
+
+
+def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int,
+             pos0_device: Optional[torch.Tensor] = None) -> None:
     """Write the new V latent rows src [B, T, Rv] (act dtype, last dim
     contiguous) into the cache described by ``v`` at positions
     [pos0, pos0 + T), quantising to its format (starkv_v_append)."""
@@ -483,4 +496,5 @@ def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int) -> Non
     d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[1], int(pos0), int(capacity), _dt(src)
     d.src, d.src_stride_b, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1)
     d.v = v.c_struct()
+    d.pos0_device = _pos_ptr(pos0_device)
     check(_lib.lib().starkv_v_append(ctypes.byref(d), _stream(src.device)), "starkv_v_append")
