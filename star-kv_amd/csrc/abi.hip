@@ -3,6 +3,7 @@
 // Nothing here allocates device memory or synchronises; validation runs
 // before any HIP call so that every argument error is reported without a GPU.
 #include <algorithm>
+#include <climits>
 #include <vector>
 
 #include "common.hpp"
@@ -481,7 +482,13 @@ int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
   if (!al(d->q, 16) || !al64(d->q_stride_b, 8) || !al64(d->q_stride_h, 8) || !al64(d->q_stride_t, 8))
     return STARKV_ERR_ALIGN;
   if (d->out_stride_b < 0 || d->out_stride_h < 0 || d->out_stride_t < 0) return STARKV_ERR_SHAPE;
-  *S_pad = round_up((int64_t)d->pos0 + d->n_tokens, 64);
+  // one-dimensional grids of the three launches (workgroup counts, ints in the kernels)
+  const int64_t S = (int64_t)d->pos0 + d->n_tokens, Hkv = d->k.n_kv_heads;
+  const int64_t g_k = round_up((int64_t)d->batch * ceil_div(S, PF_K_POS), 8) * Hkv;
+  const int64_t g_v = round_up((int64_t)d->batch * ceil_div(S, PF_V_POS), 8) * ((Hkv + 1) / 2);
+  const int64_t g_a = round_up((int64_t)d->batch * Hkv, 8) * *gs * ceil_div(d->n_tokens, PF_Q_POS);
+  if (std::max({g_k, g_v, g_a}) > INT32_MAX) return STARKV_ERR_LIMIT;
+  *S_pad = round_up(S, 64);
   return STARKV_OK;
 }
 

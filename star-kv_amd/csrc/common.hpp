@@ -146,6 +146,9 @@ struct UPArgs {
 // ---------------------------------------------------------------------------
 // Prefill arguments (prefill.hip).
 // ---------------------------------------------------------------------------
+constexpr int PF_K_POS = 512;    // positions per K-reconstruction workgroup
+constexpr int PF_V_POS = 256;    // positions per V-reconstruction workgroup (two KV heads)
+constexpr int PF_Q_POS = 256;    // queries per attention workgroup
 struct PFArgs {
   int S, S_pad, Hkv, Hq, gs, T, pos0;              // S = pos0 + T positions reconstructed, S_pad = round_up(S, 64)
   int rc_nb, rc_blocks;                            // K reconstruction: position blocks per batch, times B

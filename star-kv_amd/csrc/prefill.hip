@@ -104,6 +104,7 @@ __device__ inline uint4 pf_dq_g64(uint32_t w, uint16_t s16, uint16_t z16) {
 // ---------------------------------------------------------------------------
 constexpr int RC_WAVE_POS = 128;                 // positions per wave
 constexpr int RC_POS = 4 * RC_WAVE_POS;          // positions per workgroup
+static_assert(RC_POS == PF_K_POS, "host grid sizing");
 constexpr int RC_KS = 64;                        // ranks per K-step
 constexpr int UV_PITCH = 72;                     // halves per staged U_v row (64 ranks + 8)
 constexpr int UV_BUF = HEAD_DIM * UV_PITCH;      // halves per U_v stage
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 // positions are staged 16 groups at a time.  Same lane / K-chunk layout and
 // epilogue as recon_kernel.
 // ---------------------------------------------------------------------------
-constexpr int RV_POS = 256;                          // positions per workgroup
+constexpr int RV_POS = PF_V_POS;                     // positions per workgroup
 constexpr int RV_WAVE_POS = 64;                      // positions per wave (2 N-tiles)
 constexpr int RV_UVBUF = 2 * HEAD_DIM * UV_PITCH;    // halves per U_v stage (two heads)
 constexpr int RV_SZG = 16;                           // scale / zero groups per LDS chunk
@@ -617,6 +618,7 @@ constexpr int FA_VPITCH = 144;                   // halves per staged V row: row
                                                  // transposed reads (K keeps WT_PITCH for 16-byte reads)
 constexpr int FA_WAVES = 8;                      // waves per workgroup, 32 queries each
 constexpr int FA_QB = 32 * FA_WAVES;             // queries per workgroup
+static_assert(FA_QB == PF_Q_POS, "host grid sizing");
 constexpr float FA_RESCALE_LOG2 = 8.0f;
 
 template <typename XT>
