@@ -387,6 +387,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch-reference", action="store_true",
+                    help="skip timing the reference's eager torch decode route on the GPU (cfg2)")
     ap.add_argument("--cpu-reps", type=int, default=100)
     ap.add_argument("--workload", default="cfg2",
                     help="cfg2 (default: the metric's workload), cfg3 (B16 S32768, K int8 + V int4-g64 cache), "
@@ -458,6 +460,41 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get(dom)
 
+    # the reference's eager torch decode route on this GPU (model.py:450-487 with
+    # torch_abx's per-head reconstruction, abx_rope_batched.py:189-202), timed
+    # for comparison: K materialised per KV head, RoPE, q.K, softmax in fp32,
+    # P @ X_v, per-head up-projection
+    torch_ref_us = None
+    if args.workload == "cfg2" and not args.no_torch_reference:
+        try:
+            cos, sin = rope.cos_sin(torch.arange(S, device=dev))
+            cos, sin = cos.half(), sin.half()
+            gs = case.Hq // case.Hkv
+            U = case.uv.view(case.Hkv, HEAD_DIM, case.Rv)
+
+            def torch_step():
+                logits = torch.empty(B, case.Hq, S, dtype=torch.float16, device=dev)
+                for h in range(case.Hkv):
+                    K = torch.matmul(case.xk_heads[h], case.bk_heads[h])
+                    K = K * cos + torch.cat((-K[..., 64:], K[..., :64]), -1) * sin
+                    qh = case.q[:, h * gs:(h + 1) * gs].contiguous()
+                    logits[:, h * gs:(h + 1) * gs] = torch.matmul(qh, K.transpose(1, 2).contiguous())
+                p = torch.softmax(logits.float() / math.sqrt(HEAD_DIM), dim=-1).half()
+                o_lat = torch.matmul(p, case.xv)                                   # [B, Hq, Rv]
+                Uq = U.repeat_interleave(gs, 0)                                    # [Hq, 128, Rv]
+                return torch.matmul(o_lat.transpose(0, 1), Uq.transpose(1, 2).contiguous()).transpose(0, 1)
+
+            for _ in range(2):
+                torch_step()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(5):
+                torch_step()
+            torch.cuda.synchronize()
+            torch_ref_us = (time.perf_counter() - t1) * 1e6 / 5
+        except torch.cuda.OutOfMemoryError:
+            torch_ref_us = None
+
     cpu = None
     if not args.no_cpu_baseline and args.workload == "cfg2":
         from oracle import starkv_oracle as o
@@ -506,6 +543,7 @@ def main():
         "algorithmic_bytes": nbytes,
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "torch_reference_gpu_us": round(torch_ref_us, 1) if torch_ref_us else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
