@@ -118,12 +118,6 @@ int validate_klayout(const starkv_klatent& k, int dtype) {
   return STARKV_OK;
 }
 
-// Pack (query head, 32-rank M-tile) items into waves of up to 2 or 4 items
-// (first fit decreasing, whole heads per wave; 4 once any head has rank > 64)
-// and deal the waves round-robin over workgroups of 8 waves (2-item waves) or
-// 4 waves (4-item waves).
-// Warp-specialised K-logit kernel: dense latents with 16-byte aligned rows
-// (ranks a multiple of 8); q and B_k are read element-wise there.
 // Warp-specialised K-logit kernel: dense latents with 16-byte aligned rows
 // (ranks a multiple of 8), or int8 latents with one scale per (b, h, s) whose
 // rows start on 16-byte boundaries (pitch a multiple of 16 bytes, so the 16-byte
@@ -151,6 +145,10 @@ int ws_row_chunks(const starkv_klatent& k, int h) {
   return k.format == STARKV_FMT_INT8_SYM ? (int)ceil_div(k.rank[h], 16) : k.rank[h] / 8;
 }
 
+// Pack (query head, 32-rank M-tile) items into waves of up to 2 or 4 items
+// (first fit decreasing, whole heads per wave; 4 once any head has rank > 64)
+// and deal the waves round-robin over workgroups of 8 waves (2-item waves) or
+// 4 waves (4-item waves).
 int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArgs& a, KPlan& plan) {
   struct QH { int qh, kv, ni; };
   std::vector<QH> heads;
