@@ -307,6 +307,8 @@ def run_prefill(args):
     # repeat, SDPA with the causal mask), timed for comparison
     torch_ms = None
     try:
+        if args.no_torch_reference:
+            raise torch.cuda.OutOfMemoryError("skipped")
         xk = cache.dequant_k(S)
         xv = cache.dequant_v(S)
         cos, sin = rope.cos_sin(torch.arange(S, device=dev))
@@ -359,6 +361,11 @@ def run_prefill(args):
                          f"restatement of the reference prefill (oracle.starkv_oracle.prefill_attention, causal), "
                          f"median of {n} reps; FLOPs counted as for the GPU line"}
 
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_prefill.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("fa_causal")
     rec = {
         "metric": "prefill attention TFLOP/s per layer (MFMA roofline)",
         "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -375,7 +382,7 @@ def run_prefill(args):
         "torch_reference_gpu_ms": round(torch_ms, 3) if torch_ms else None,
         "roofline": {"bound": "mfma", "kernel": "fa_causal", "achieved": round(fa_tflops, 1),
                      "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(fa_tflops / MFMA_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": traffic},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
