@@ -3,13 +3,14 @@
 // from the latents and runs SDPA -- without a causal mask (the defect the
 // build fixes: query t sees keys <= pos0 + t).
 //
-// 1. recon_kernel: per (KV head, 512 positions, b) one MFMA GEMM tile,
+// 1. recon_kernel / recon_v_kernel: MFMA GEMM tiles computing
 //    K = RoPE(X_k[s] . B_k) (RoPE applied in the epilogue from the decode's
-//    RoPE table) and V = X_v[s] . U_v[h]^T, into [B][Hkv][S_pad][128] act-dtype
-//    buffers.  Quantised latents are dequantised on the way in, bit-exactly
-//    as everywhere else (int8: fp16(q s); group-64 int4: fp16(n s + z)), then
-//    rounded once more to bf16 for bf16 activations.  Rows in [S, S_pad) are
-//    written as zeros.
+//    RoPE table; per (KV head, b, 512 positions)) and V = X_v[s] . U_v[h]^T
+//    (per (KV-head pair, b, 256 positions)), into [B][Hkv][S_pad][128]
+//    act-dtype buffers.  Quantised latents are dequantised on the way in,
+//    bit-exactly as everywhere else (int8: fp16(q s); group-64 int4:
+//    fp16(n s + z)), then rounded once more to bf16 for bf16 activations.
+//    Rows in [S, S_pad) are written as zeros.
 // 2. fa_causal_kernel: flash attention over those buffers, one workgroup per
 //    (b, query head, 256 queries), 8 waves of 32 queries.  Per 64-key block
 //    it forms S^T = K . Q^T (so each lane holds 32 keys of one query and the
@@ -89,136 +90,89 @@ __device__ inline uint4 pf_dq_g64(uint32_t w, uint16_t s16, uint16_t z16) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// K / V reconstruction: per (KV head h, b, 512 positions) one workgroup of 4
+// K reconstruction: per (KV head h, b, 512 positions) one workgroup of 4
 // waves; wave w computes C^T[d][p] for all 128 dims d and its 128 positions
-// p as 4 x 4 MFMA tiles (A = the projection, dims as rows; B = latent rows,
-// positions as columns, loaded from global straight into registers one
-// K-step ahead).  A K-step is 64 ranks; within it lane half hh takes ranks
-// [32 hh, 32 hh + 32) (MFMA K-chunk kk: ranks 32 hh + 8 kk .. + 7) in both
-// operands, so each lane reads one contiguous 32-rank run of a latent row.
-// K: A = B_k[h] (staged whole in LDS as [j][d], read with the transposed LDS
-// load), K-depth r_h; RoPE pairs (d, d + 64) sit in M-tiles mt and mt + 2 of
-// the same lane.  V: A = U_v rows h*128 + d ([d][j] 64-rank stages,
-// double-buffered in LDS), K-depth Rv.  The epilogue stages each wave's
-// 128 x 128 tile in LDS and writes whole 256-byte rows.
+// p as 4 x 4 MFMA tiles (A = B_k[h], dims as rows, staged whole in LDS as
+// [j][d] and read with the transposed LDS load; B = latent rows, positions as
+// columns, loaded from global straight into registers one K-step ahead).  A
+// K-step is 64 ranks; within it lane half hh takes ranks [32 hh, 32 hh + 32)
+// (MFMA K-chunk kk: ranks 32 hh + 8 kk .. + 7) in both operands, so each lane
+// reads one contiguous 32-rank run of a latent row.  RoPE pairs (d, d + 64)
+// sit in M-tiles mt and mt + 2 of the same lane.  The epilogue stages each
+// wave's 128 x 128 tile in LDS and writes whole 256-byte rows.
 // ---------------------------------------------------------------------------
 constexpr int RC_WAVE_POS = 128;                 // positions per wave
 constexpr int RC_POS = 4 * RC_WAVE_POS;          // positions per workgroup
 static_assert(RC_POS == PF_K_POS, "host grid sizing");
 constexpr int RC_KS = 64;                        // ranks per K-step
-constexpr int UV_PITCH = 72;                     // halves per staged U_v row (64 ranks + 8)
-constexpr int UV_BUF = HEAD_DIM * UV_PITCH;      // halves per U_v stage
+constexpr int UV_PITCH = 72;                     // halves per staged U_v row (64 ranks + 8), V kernel
 constexpr int BK_PITCH = 136;                    // halves per staged B_k row (128 dims + 8)
 constexpr int C_PITCH = 136;                     // halves per epilogue row
 constexpr int RC_LDS = 4 * RC_WAVE_POS * C_PITCH;
 
-// raw latent data of one K-step for this lane: [N-tile][K-chunk]
-template <int KIND, bool Q> struct RcRaw { uint4 d[4][4]; };             // dense: 8 ranks per chunk
-template <> struct RcRaw<0, true> { uint2 d[4][4]; };                    // int8
-template <> struct RcRaw<1, true> { uint4 d[4]; uint32_t sz[4]; };       // group-64 int4 (word kk) + scale | zero << 16
+// raw K latent data of one K-step for this lane: [N-tile][K-chunk]
+template <bool Q> struct RkRaw { uint4 d[4][4]; };                        // dense: 8 ranks per chunk
+template <> struct RkRaw<true> { uint2 d[4][4]; };                        // int8
 
-// Q: quantised latents (K int8, V group-64 int4)
-template <typename XT, int KIND, bool Q>
+// Q: int8 latents (else dense act dtype)
+template <typename XT, bool Q>
 __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
   // XCD-aware order: workgroup L runs on XCD L % 8, and the Hkv heads of one
-  // (batch, 512-position block) all land on one XCD, sharing its L2 for the
-  // latent rows
+  // (batch, 512-position block) all land on one XCD
   const int L = blockIdx.x, t8 = L >> 3;
   const int h = t8 % a.Hkv, blk = (t8 / a.Hkv) * 8 + (L & 7);
   if (blk >= a.rc_blocks) return;
   const int b = blk / a.rc_nb;
   const int pw = (blk - b * a.rc_nb) * RC_POS + wave * RC_WAVE_POS;
   const int S = a.S;
-  const int R = KIND == 0 ? a.krank[h] : a.Rv;     // multiple of 8 (host-checked)
+  const int R = a.krank[h];                         // multiple of 8 (host-checked)
   const int nks = (R + RC_KS - 1) / RC_KS;
 
-  // per N-tile latent row (clamped position) and K's int8 scales
+  // per N-tile latent row (clamped position) and int8 scales
   const uint8_t* xrow[4];
   uint16_t ksc[4] = {0, 0, 0, 0};
-  int64_t vso[4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int pc = min(pw + nt * 32 + n, S - 1);
-    constexpr int64_t es = Q ? 1 : 2;                // latent offsets: bytes (quantised) or elements
-    if constexpr (KIND == 0) {
-      xrow[nt] = (const uint8_t*)a.kx + (b * a.kx_sb + a.kxoff[h] + (int64_t)pc * a.kxpitch[h]) * es;
-      if constexpr (Q) ksc[nt] = ((const uint16_t*)a.kscale)[b * a.ks_sb + h * a.ks_sh + pc];
-      vso[nt] = 0;
-    } else {
-      xrow[nt] = (const uint8_t*)a.vx + (b * a.vx_sb + (int64_t)pc * a.vx_ss) * es;
-      vso[nt] = b * a.vs_sb + (int64_t)pc * a.vs_ss;
-    }
+    constexpr int64_t es = Q ? 1 : 2;                // latent offsets: bytes (int8) or elements
+    xrow[nt] = (const uint8_t*)a.kx + (b * a.kx_sb + a.kxoff[h] + (int64_t)pc * a.kxpitch[h]) * es;
+    if constexpr (Q) ksc[nt] = ((const uint16_t*)a.kscale)[b * a.ks_sb + h * a.ks_sh + pc];
   }
 
   // Ranks past R (the last step only) read a valid chunk instead (address
   // clamped to rank R - 8): the A rows of those ranks are zero, so any finite
   // value adds nothing, and no load is conditional (a conditional load would
   // zero its register first and wait for the previous load into it).
-  auto load = [&](int ks, RcRaw<KIND, Q>& r) {
+  auto load = [&](int ks, RkRaw<Q>& r) {
     const int j0 = ks * RC_KS + 32 * hh;             // this lane's first rank of the step
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      if constexpr (KIND == 1 && Q) {
-        if (ks * RC_KS + RC_KS <= R) {               // whole step in range (uniform)
-          r.d[nt] = *(const uint4*)(xrow[nt] + j0 / 2);
-        } else {
-          uint32_t w[4];
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) w[kk] = *(const uint32_t*)(xrow[nt] + min(j0 + 8 * kk, R - 8) / 2);
-          r.d[nt] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-        const int g = min(ks * RC_KS, R - 1) >> 6;
-        r.sz[nt] = (uint32_t)((const uint16_t*)a.vscale)[vso[nt] + g] |
-                   ((uint32_t)((const uint16_t*)a.vzero)[vso[nt] + g] << 16);
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const int j = min(j0 + 8 * kk, R - 8);
-          if constexpr (!Q) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * j);
-          else r.d[nt][kk] = *(const uint2*)(xrow[nt] + j);
-        }
+      for (int kk = 0; kk < 4; ++kk) {
+        const int j = min(j0 + 8 * kk, R - 8);
+        if constexpr (!Q) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * j);
+        else r.d[nt][kk] = *(const uint2*)(xrow[nt] + j);
       }
-    }
   };
   // raw -> B fragment (act dtype)
-  auto frag = [&](const RcRaw<KIND, Q>& r, int nt, int kk) -> uint4 {
+  auto frag = [&](const RkRaw<Q>& r, int nt, int kk) -> uint4 {
     if constexpr (!Q) {
       return r.d[nt][kk];
     } else {
-      uint4 f;
-      if constexpr (KIND == 0) {
-        f = pf_dq_int8(r.d[nt][kk], ksc[nt]);
-      } else {
-        const uint32_t w = kk == 0 ? r.d[nt].x : kk == 1 ? r.d[nt].y : kk == 2 ? r.d[nt].z : r.d[nt].w;
-        f = pf_dq_g64(w, (uint16_t)(r.sz[nt] & 0xffff), (uint16_t)(r.sz[nt] >> 16));
-      }
+      uint4 f = pf_dq_int8(r.d[nt][kk], ksc[nt]);
       if constexpr (!__is_same(XT, _Float16)) f = pf_f16_to_bf16(f);
       return f;
     }
   };
 
-  // A operand staging
+  // B_k[h] rows [0, nks * 64) in LDS as [j][d] (rows past R zero)
   const int g4 = lane >> 4, rho = lane & 15;
   const int tr_off = (32 * hh + (rho >> 2)) * BK_PITCH + 16 * (g4 & 1) + 4 * (rho & 3);
-  const XT* uvh = (const XT*)a.uv + (int64_t)h * HEAD_DIM * a.uv_rs;
-  const int ur = tid >> 1, uc = (tid & 1) * 32;       // V: this thread's U_v row and 32-rank half
-  auto uv_load = [&](int ks, uint4* u) {              // clamped like the latent loads
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      u[c] = *(const uint4*)(uvh + (int64_t)ur * a.uv_rs + min(ks * RC_KS + uc + 8 * c, R - 8));
-  };
-  auto uv_store = [&](int buf, int ks, const uint4* u) {   // ranks past R stored as zero rows of A
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *(uint4*)&lds[buf * UV_BUF + ur * UV_PITCH + uc + 8 * c] =
-          ks * RC_KS + uc + 8 * c < R ? u[c] : make_uint4(0, 0, 0, 0);
-  };
-  uint4 un[4];
-  if constexpr (KIND == 0) {
+  {
     const XT* bk = (const XT*)a.bk + a.bkoff[h];
     const int Rp = nks * RC_KS;
     for (int e = tid; e < Rp * 16; e += 256) {        // 16-byte pieces of rows [0, Rp)
@@ -233,9 +187,6 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
       }
       *(uint4*)&lds[j * BK_PITCH + d8] = v;
     }
-  } else {
-    uv_load(0, un);
-    uv_store(0, 0, un);
   }
   floatx16 acc[4][4];
 #pragma unroll
@@ -243,10 +194,12 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = floatx16{};
 
-  // one K-step over latent data `cur`; the next U_v stage (already requested
-  // into `un`) is stored to LDS after it
-  auto step = [&](int ks, const RcRaw<KIND, Q>& cur) {
+  RkRaw<Q> cur, nxt;
+  load(0, cur);
+  __syncthreads();
+  for (int ks = 0; ks < nks; ++ks) {
     const bool more = ks + 1 < nks;
+    if (more) load(ks + 1, nxt);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       uint4 bf[4];
@@ -254,68 +207,16 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
       for (int nt = 0; nt < 4; ++nt) bf[nt] = frag(cur, nt, kk);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        uint4 af;
-        if constexpr (KIND == 0) {
-          const uint16_t* sb = lds + (ks * RC_KS + 8 * kk) * BK_PITCH + tr_off + 32 * mt;
-          const uint2 lo = pf_read_tr16(sb), hi = pf_read_tr16(sb + 4 * BK_PITCH);
-          af = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        } else {
-          af = *(const uint4*)&lds[(ks & 1) * UV_BUF + (mt * 32 + n) * UV_PITCH + 32 * hh + 8 * kk];
-        }
+        const uint16_t* sb = lds + (ks * RC_KS + 8 * kk) * BK_PITCH + tr_off + 32 * mt;
+        const uint2 lo = pf_read_tr16(sb), hi = pf_read_tr16(sb + 4 * BK_PITCH);
+        const uint4 af = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = pf_mfma<XT>(af, bf[nt], acc[mt][nt]);
       }
     }
-    if constexpr (KIND == 1) {
-      if (more) uv_store((ks + 1) & 1, ks + 1, un);
-      __syncthreads();
-    }
-  };
-
-  if constexpr (KIND == 1 && Q) {
-    // packed latents are small: keep two K-steps in flight (three raw sets)
-    RcRaw<KIND, Q> r0, r1, r2;
-    load(0, r0);
-    if (nks > 1) load(1, r1);
-    __syncthreads();
-    // at the top of each round r0 / r1 hold (or are loading) K-steps ks / ks + 1
-    // (the U_v stage is requested before the latent loads: loads complete in
-    // order, so storing it waits only for itself)
-    int ks = 0;
-    for (; ks + 3 <= nks; ks += 3) {
-      uv_load(ks + 1, un);
-      load(ks + 2, r2);
-      step(ks, r0);
-      if (ks + 2 < nks) uv_load(ks + 2, un);
-      if (ks + 3 < nks) load(ks + 3, r0);
-      step(ks + 1, r1);
-      if (ks + 3 < nks) uv_load(ks + 3, un);
-      if (ks + 4 < nks) load(ks + 4, r1);
-      step(ks + 2, r2);
-    }
-    if (ks < nks) {
-      if (ks + 1 < nks) uv_load(ks + 1, un);
-      step(ks, r0);
-    }
-    if (ks + 1 < nks) {
-      if (ks + 2 < nks) uv_load(ks + 2, un);
-      step(ks + 1, r1);
-    }
-  } else {
-    RcRaw<KIND, Q> cur, nxt;
-    load(0, cur);
-    __syncthreads();
-    for (int ks = 0; ks < nks; ++ks) {
-      const bool more = ks + 1 < nks;
-      if constexpr (KIND == 1) {
-        if (more) uv_load(ks + 1, un);
-      }
-      if (more) load(ks + 1, nxt);
-      step(ks, cur);
-      if (more) cur = nxt;
-    }
+    if (more) cur = nxt;
   }
-  if constexpr (KIND == 0) __syncthreads();          // B_k reads done before the epilogue reuses LDS
+  __syncthreads();                                   // B_k reads done before the epilogue reuses LDS
 
   // epilogue: lane holds positions pw + 32 nt + n, dims 32 mt + 8 q + 4 hh + c in acc[mt][nt][4q + c]
   uint16_t* cw = lds + wave * RC_WAVE_POS * C_PITCH;
@@ -324,51 +225,35 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
     const int p = pw + nt * 32 + n;
     const bool live = p < S;
     uint16_t* crow = cw + (nt * 32 + n) * C_PITCH + 4 * hh;
-    if constexpr (KIND == 0) {
-      const uint4* rt = (const uint4*)a.rope + ((int64_t)(min(p, S - 1) >> 5) * 8) * 64 + hh * 32 + (p & 31);
+    const uint4* rt = (const uint4*)a.rope + ((int64_t)(min(p, S - 1) >> 5) * 8) * 64 + hh * 32 + (p & 31);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint4 cs4 = rt[(mt * 4 + q) * 64];       // (cos, sin) of frequencies 32 mt + 8 q + 4 hh + 0..3
-          const uint32_t cw4[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
-          uint32_t y0w[2], y1w[2];
+      for (int q = 0; q < 4; ++q) {
+        const uint4 cs4 = rt[(mt * 4 + q) * 64];       // (cos, sin) of frequencies 32 mt + 8 q + 4 hh + 0..3
+        const uint32_t cw4[4] = {cs4.x, cs4.y, cs4.z, cs4.w};
+        uint32_t y0w[2], y1w[2];
 #pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            float y0[2], y1[2];
+        for (int c2 = 0; c2 < 2; ++c2) {
+          float y0[2], y1[2];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const int c = 2 * c2 + e;
-              const kh2 t = __builtin_bit_cast(kh2, cw4[c]);
-              const float co = (float)t[0], si = (float)t[1];
-              const float k0 = acc[mt][nt][4 * q + c], k1 = acc[mt + 2][nt][4 * q + c];
-              y0[e] = live ? k0 * co - k1 * si : 0.f;
-              y1[e] = live ? k1 * co + k0 * si : 0.f;
-            }
-            y0w[c2] = (uint32_t)pf_bits<XT>(y0[0]) | ((uint32_t)pf_bits<XT>(y0[1]) << 16);
-            y1w[c2] = (uint32_t)pf_bits<XT>(y1[0]) | ((uint32_t)pf_bits<XT>(y1[1]) << 16);
+          for (int e = 0; e < 2; ++e) {
+            const int c = 2 * c2 + e;
+            const kh2 t = __builtin_bit_cast(kh2, cw4[c]);
+            const float co = (float)t[0], si = (float)t[1];
+            const float k0 = acc[mt][nt][4 * q + c], k1 = acc[mt + 2][nt][4 * q + c];
+            y0[e] = live ? k0 * co - k1 * si : 0.f;
+            y1[e] = live ? k1 * co + k0 * si : 0.f;
           }
-          *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(y0w[0], y0w[1]);
-          *(uint2*)(crow + (mt + 2) * 32 + 8 * q) = make_uint2(y1w[0], y1w[1]);
+          y0w[c2] = (uint32_t)pf_bits<XT>(y0[0]) | ((uint32_t)pf_bits<XT>(y0[1]) << 16);
+          y1w[c2] = (uint32_t)pf_bits<XT>(y1[0]) | ((uint32_t)pf_bits<XT>(y1[1]) << 16);
         }
-    } else {
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint32_t w[2];
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            const float v0 = live ? acc[mt][nt][4 * q + 2 * c2] : 0.f;
-            const float v1 = live ? acc[mt][nt][4 * q + 2 * c2 + 1] : 0.f;
-            w[c2] = (uint32_t)pf_bits<XT>(v0) | ((uint32_t)pf_bits<XT>(v1) << 16);
-          }
-          *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(w[0], w[1]);
-        }
-    }
+        *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(y0w[0], y0w[1]);
+        *(uint2*)(crow + (mt + 2) * 32 + 8 * q) = make_uint2(y1w[0], y1w[1]);
+      }
   }
   __syncthreads();
-  XT* dst = (XT*)(KIND == 0 ? a.kbuf : a.vbuf) + (((int64_t)b * a.Hkv + h) * a.S_pad) * HEAD_DIM;
+  XT* dst = (XT*)a.kbuf + (((int64_t)b * a.Hkv + h) * a.S_pad) * HEAD_DIM;
 #pragma unroll 4
   for (int it = 0; it < RC_WAVE_POS * 16 / 64; ++it) {
     const int idx = it * 64 + lane, row = idx >> 4, ch = idx & 15;
@@ -798,8 +683,8 @@ static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t m
   r.rc_nb = (int)ceil_div(a.S, RC_POS);
   r.rc_blocks = r.rc_nb * B;
   const dim3 rg((unsigned)(ceil_div(r.rc_blocks, 8) * 8 * a.Hkv));
-  if (a.k_i8) hipLaunchKernelGGL((recon_kernel<XT, 0, true>), rg, dim3(256), 0, st, r);
-  else hipLaunchKernelGGL((recon_kernel<XT, 0, false>), rg, dim3(256), 0, st, r);
+  if (a.k_i8) hipLaunchKernelGGL((recon_kernel<XT, true>), rg, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL((recon_kernel<XT, false>), rg, dim3(256), 0, st, r);
   r.rv_nb = (int)ceil_div(a.S, RV_POS);
   r.rv_blocks = r.rv_nb * B;
   const dim3 vg((unsigned)(ceil_div(r.rv_blocks, 8) * 8 * ((a.Hkv + 1) / 2)));
