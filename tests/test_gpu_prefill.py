@@ -104,6 +104,9 @@ CASES = [
     ("t1024_f16", 1, 2, [48, 128], 256, 1024, 0, torch.float16, "dense", "dense"),
     ("int8k_g64v_f16", 2, 4, [64, 32, 96, 128], 200, 129, 0, torch.float16, "int8", "g64"),
     ("int8k_g64v_bf16_chunk", 1, 8, [32, 128], 1640, 96, 64, torch.bfloat16, "int8", "g64"),
+    # an odd KV-head count leaves the last V head pair half empty; MQA has one KV head
+    ("odd_hkv3_gqa2", 2, 6, [24, 64, 40], 72, 130, 5, torch.float16, "dense", "dense"),
+    ("mqa_int8_g64", 1, 8, [96], 136, 300, 0, torch.float16, "int8", "g64"),
 ]
 
 
