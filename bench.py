@@ -1,6 +1,6 @@
 """Benchmark of the STAR-KV fused decode-attention path on one MI355X.
 
-Workload ("cfg2"): Llama-2-7B-shaped layer, MHA
+Workload (the metric's configuration, "cfg2"): Llama-2-7B-shaped layer, MHA
 32 heads x 128, fp16, batch 16, context 32768, head-wise K ranks from
 {16..96} (sum 1640, committed fixture), V rank 1640, one decode query token.
 Synthetic seeded data, inputs resident in HBM before timing.
@@ -163,7 +163,7 @@ def build_workload(name, dev):
 
 
 def run_e2e(args):
-    """End-to-end decode: random-init 32-layer
+    """End-to-end decode (the e2e configuration): random-init 32-layer
     Llama-2-7B-shaped model (vocab 32000, MLP 11008, fp16), every attention on
     the latent cache (cfg3 ranks and formats: K int8, V int4-g64), prefill 8192
     random tokens at batch 8 (starkv_prefill_attention), then greedy decode

@@ -1,7 +1,7 @@
 """GPU parity of the fused decode path and the K-logit / P.V entry points
 against the CPU oracle (oracle/starkv_oracle.py), same seeded inputs.
 
-Gates (BASELINE north star): attention outputs within max-abs 2e-2 and
+Gates: attention outputs within max-abs 2e-2 and
 mean-rel 1e-3 of the fp32/fp64 eager oracle."""
 import math
 
