@@ -73,6 +73,27 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
                       void* table, size_t table_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
+ * starkv_rope_apply — replaces the query rotation of the reference attention
+ * forward, _rope(query_states, cos, sin) (model.py:423, HF apply_rotary_pos_emb,
+ * HF:models/llama/modeling_llama.py:130-153): in place, for i < 64,
+ *   x[i]      <- x[i] c - x[i + 64] s,   x[i + 64] <- x[i + 64] c + x[i] s
+ * with (c, s) the table's (attention-scaled) cos / sin of frequency i at
+ * position pos0 + t.  x: act dtype [B, H, T, 128], element (b,h,t,d) at
+ * x + b*stride_b + h*stride_h + t*stride_t + d.  pos0_device (optional): a
+ * device int read at run time instead of pos0 (graph replay).  Computed in
+ * fp32 and rounded once (the reference rounds each of its three operations).
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int batch, n_heads, n_tokens, dtype;
+  void* x; int64_t stride_b, stride_h, stride_t;
+  const void* rope_table; int rope_max_positions;
+  int pos0;
+  const int* pos0_device;
+} starkv_rope_apply_desc;
+
+int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream);
+
+/* ---------------------------------------------------------------------
  * K-latent description shared by the K-logit and decode entry points.
  * KV head h has rank r_h = rank[h] (1..128); element (b, h, s, j) of the
  * latent lives at  base + b*stride_b + head_offset[h] + s*pos_stride[h] + j.

@@ -666,6 +666,21 @@ int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, 
   return decode_impl(d, workspace, workspace_bytes, stream, events);
 }
 
+int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->batch < 1 || d->n_heads < 1 || d->n_tokens < 0 || d->pos0 < 0) return STARKV_ERR_SHAPE;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  if (!d->x || !d->rope_table) return STARKV_ERR_NULL;
+  if (d->stride_b < 0 || d->stride_h < 0 || d->stride_t < 0) return STARKV_ERR_SHAPE;
+  if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->rope_max_positions) return STARKV_ERR_SHAPE;
+  if ((int64_t)d->batch * d->n_heads * d->n_tokens * 64 > ((int64_t)1 << 40)) return STARKV_ERR_LIMIT;
+  RopeApplyArgs a;
+  a.x = d->x; a.sb = d->stride_b; a.sh = d->stride_h; a.st = d->stride_t;
+  a.B = d->batch; a.H = d->n_heads; a.T = d->n_tokens; a.pos0 = d->pos0; a.max_pos = d->rope_max_positions;
+  a.pos0_dev = d->pos0_device; a.table = d->rope_table;
+  return launch_rope_apply(a, d->dtype, (hipStream_t)stream);
+}
+
 int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;

@@ -144,6 +144,16 @@ struct UPArgs {
 };
 
 // ---------------------------------------------------------------------------
+// In-place RoPE of query rows (rope.hip).
+// ---------------------------------------------------------------------------
+struct RopeApplyArgs {
+  void* x; int64_t sb, sh, st;                     // [B][H][T][128], act dtype, elements
+  int B, H, T, pos0, max_pos;
+  const int* pos0_dev;                             // optional: position read at run time
+  const void* table;
+};
+
+// ---------------------------------------------------------------------------
 // Prefill arguments (prefill.hip).
 // ---------------------------------------------------------------------------
 constexpr int PF_K_POS = 512;    // positions per K-reconstruction workgroup
@@ -258,6 +268,7 @@ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 // launchers (return hipError_t as int; 0 on success)
 int rope_table_tiles(int max_positions);
 int launch_rope_table(const float* inv_freq_host, int max_positions, float scaling, void* table, hipStream_t st);
+int launch_rope_apply(const RopeApplyArgs& a, int dtype, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
 int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
 int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st);

@@ -4,9 +4,9 @@ The compute lives in libstarkv.so (HIP kernels behind the C ABI of
 include/starkv.h); this package binds it to torch tensors.
 """
 from ._lib import StarKVError, lib
-from .ops import KLatentSpec, VLatentSpec, decode_attention, k_logits, prefill_attention, pv_latent
+from .ops import KLatentSpec, VLatentSpec, decode_attention, k_logits, prefill_attention, pv_latent, rope_apply
 from .rope import RopeConfig, rope_table
 
 __all__ = ["StarKVError", "lib", "KLatentSpec", "VLatentSpec", "decode_attention", "k_logits", "prefill_attention",
-           "pv_latent",
+           "pv_latent", "rope_apply",
            "RopeConfig", "rope_table"]

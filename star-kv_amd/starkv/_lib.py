@@ -137,9 +137,20 @@ class PrefillDesc(ctypes.Structure):
     ]
 
 
+class RopeApplyDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int), ("n_heads", ctypes.c_int), ("n_tokens", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("x", ctypes.c_void_p), ("stride_b", ctypes.c_int64), ("stride_h", ctypes.c_int64),
+        ("stride_t", ctypes.c_int64),
+        ("rope_table", ctypes.c_void_p), ("rope_max_positions", ctypes.c_int),
+        ("pos0", ctypes.c_int),
+        ("pos0_device", ctypes.c_void_p),
+    ]
+
+
 EXPORTS = (
     "starkv_abi_version", "starkv_status_string",
-    "starkv_rope_table_bytes", "starkv_rope_build",
+    "starkv_rope_table_bytes", "starkv_rope_build", "starkv_rope_apply",
     "starkv_k_logits_workspace_bytes", "starkv_k_logits",
     "starkv_pv_latent_workspace_bytes", "starkv_pv_latent",
     "starkv_decode_workspace_bytes", "starkv_decode_attention", "starkv_decode_attention_timed",
@@ -183,6 +194,8 @@ def lib() -> ctypes.CDLL:
     L.starkv_prefill_attention_timed.restype = ctypes.c_int
     L.starkv_prefill_attention_timed.argtypes = [ctypes.POINTER(PrefillDesc), ctypes.c_void_p, ctypes.c_size_t,
                                                  ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    L.starkv_rope_apply.restype = ctypes.c_int
+    L.starkv_rope_apply.argtypes = [ctypes.POINTER(RopeApplyDesc), ctypes.c_void_p]
     L.starkv_k_append.restype = ctypes.c_int
     L.starkv_k_append.argtypes = [ctypes.POINTER(KAppendDesc), ctypes.c_void_p]
     L.starkv_v_append.restype = ctypes.c_int

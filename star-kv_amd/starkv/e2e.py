@@ -25,7 +25,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .cache import LatentCache
-from .ops import decode_attention, prefill_attention
+from .ops import decode_attention, prefill_attention, rope_apply
 from .rope import RopeConfig
 
 __all__ = ["LatentAttention", "DecodeGraphState", "build_model", "generate", "generate_graphed", "decode_graphed"]
@@ -154,8 +154,13 @@ class LatentAttention(nn.Module):
                 use_cache=False, position_embeddings=None, **kwargs):
         B, T, _ = hidden_states.shape
         q = self.q_proj(hidden_states).view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2)
-        cos, sin = position_embeddings
-        q = q * cos.unsqueeze(1) + _rotate_half(q) * sin.unsqueeze(1)
+        if self.reference:
+            cos, sin = position_embeddings
+            q = q * cos.unsqueeze(1) + _rotate_half(q) * sin.unsqueeze(1)
+        elif self.graph is not None and T == 1:
+            rope_apply(q, self.rope, pos0_device=self.graph.pos, max_positions=self.graph.capacity)
+        else:
+            rope_apply(q, self.rope, pos0=self.cache.length)     # positions continue the cache
         kl = self.k_vs(hidden_states)
         k_new = torch.zeros(B, T, self.n_kv * self.rmax, dtype=kl.dtype, device=kl.device)
         k_new.index_copy_(2, self.k_scatter, kl)

@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KAppendDesc,
-                   PrefillDesc,
+                   PrefillDesc, RopeApplyDesc,
                    KLatent, KLogitsDesc, PVDesc, StarKVError, VAppendDesc, VLatent, check, i64_array, int_array)
 from .rope import RopeConfig, rope_table
 
@@ -455,6 +455,28 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
         check(L.starkv_prefill_attention_timed(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                                _stream(q.device), handles), "starkv_prefill_attention_timed")
     return out
+
+
+def rope_apply(x: torch.Tensor, rope: RopeConfig = RopeConfig(), pos0: int = 0,
+               pos0_device: Optional[torch.Tensor] = None, max_positions: Optional[int] = None) -> torch.Tensor:
+    """Rotate query rows x [B, H, T, 128] (act dtype, last dim contiguous) in
+    place by the RoPE of positions pos0 + t (the query half of HF's
+    apply_rotary_pos_emb, model.py:423); ``pos0_device``: an int32 device
+    tensor read when the kernel runs (graph capture / replay), with
+    ``max_positions`` bounding the positions it may hold.  Returns x."""
+    if x.dim() != 4 or x.shape[-1] != HEAD_DIM or x.stride(-1) != 1:
+        raise StarKVError("x must be [B, H, T, 128] with a contiguous last dim")
+    _require_cuda(x)
+    B, H, T, _ = x.shape
+    table, cap = rope_table(rope, max(int(pos0) + T, int(max_positions or 0)), x.device)
+    d = RopeApplyDesc()
+    d.batch, d.n_heads, d.n_tokens, d.dtype = B, H, T, _dt(x)
+    d.x, d.stride_b, d.stride_h, d.stride_t = x.data_ptr(), x.stride(0), x.stride(1), x.stride(2)
+    d.rope_table, d.rope_max_positions = table.data_ptr(), cap
+    d.pos0 = int(pos0)
+    d.pos0_device = _pos_ptr(pos0_device)
+    check(_lib.lib().starkv_rope_apply(ctypes.byref(d), _stream(x.device)), "starkv_rope_apply")
+    return x
 
 
 def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,

@@ -353,3 +353,16 @@ def test_prefill_rejects(what, code):
         d.dtype = L.F32
     assert L.lib().starkv_prefill_attention(ctypes.byref(d), FAKE, 1 << 30, None) == code
     assert L.lib().starkv_prefill_workspace_bytes(ctypes.byref(d)) == 0
+
+
+def test_rope_apply_validation():
+    lib = L.lib()
+    d = L.RopeApplyDesc(batch=1, n_heads=2, n_tokens=10, dtype=L.F16, x=FAKE, stride_b=2560, stride_h=1280,
+                        stride_t=128, rope_table=FAKE, rope_max_positions=64, pos0=60)
+    assert lib.starkv_rope_apply(ctypes.byref(d), None) == ERR_SHAPE        # positions 60..69 past the table
+    d.pos0 = 0
+    d.x = None
+    assert lib.starkv_rope_apply(ctypes.byref(d), None) == ERR_NULL
+    d.x, d.dtype = FAKE, L.F32
+    assert lib.starkv_rope_apply(ctypes.byref(d), None) == ERR_DTYPE
+

@@ -147,3 +147,27 @@ def test_decode_cfg2_full_shape(batch_sel):
     mx, mr = errors(out[batch_sel], ref)
     _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
     assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
+
+
+@pytest.mark.parametrize("dtype,device_pos", [(torch.float16, False), (torch.bfloat16, True)])
+def test_rope_apply_matches_oracle(dtype, device_pos):
+    """The fused query rotation (model.py:423) against the oracle's apply_rope
+    at positions pos0 + t, in place on a strided [B, H, T, 128] view; the
+    position from the host or from a device int.  One rounding of the fp32
+    result: within one unit in the last place of the act dtype."""
+    from oracle import starkv_oracle as o
+    from starkv import RopeConfig, rope_apply
+    rope = RopeConfig(theta=500000.0, rope_type="llama3", factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                      original_max_position_embeddings=8192, attention_scaling=1.25)
+    B, H, T, pos0 = 3, 8, 37, 1000
+    g = torch.Generator(device="cuda").manual_seed(9)
+    base = torch.randn(B, T, H, 128, generator=g, device="cuda").to(dtype)
+    x = base.clone().transpose(1, 2)                                      # [B, H, T, 128], strided
+    pos = torch.tensor([pos0], dtype=torch.int32, device="cuda") if device_pos else None
+    rope_apply(x, rope, pos0=0 if device_pos else pos0, pos0_device=pos, max_positions=pos0 + T)
+    torch.cuda.synchronize()
+    cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(pos0, pos0 + T), rope.attention_scaling)
+    ref = o.apply_rope(base.transpose(1, 2).double().cpu(), cos.double(), sin.double())
+    err = (x.double().cpu() - ref).abs()
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    assert float((err / ref.abs().clamp_min(1e-3)).max()) <= ulp or float(err.max()) <= ulp * 4, float(err.max())
