@@ -80,7 +80,8 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
  * with (c, s) the table's (attention-scaled) cos / sin of frequency i at
  * position pos0 + t.  x: act dtype [B, H, T, 128], element (b,h,t,d) at
  * x + b*stride_b + h*stride_h + t*stride_t + d.  pos0_device (optional): a
- * device int read at run time instead of pos0 (graph replay).  Computed in
+ * device int read at run time instead of pos0 (graph replay); rows whose
+ * position then falls past rope_max_positions are left unrotated.  Computed in
  * fp32 and rounded once (the reference rounds each of its three operations).
  * ------------------------------------------------------------------- */
 typedef struct {
