@@ -278,6 +278,9 @@ typedef struct {
   int dtype;
   const void* src; int64_t src_stride_b, src_stride_h, src_stride_t;
   starkv_klatent k;
+  const int64_t* src_head_offset;   /* optional host [Hkv] (NULL: h*src_stride_h): element offset
+                                       of head h's row, for sources with the heads back to back
+                                       ([B, T, sum of ranks], as the latent projection writes them) */
   const int* pos0_device;   /* optional (NULL: use pos0): device int read by the kernel at
                                run time, for calls captured once in a HIP graph and replayed
                                at advancing positions; rows landing at or past capacity are

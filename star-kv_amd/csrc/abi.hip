@@ -708,6 +708,8 @@ int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
     a.off[h] = k.head_offset[h]; a.pitch[h] = k.pos_stride[h];
     const bool lo = two && k.rank[h] > k.split;
     a.off2[h] = lo ? k.head_offset2[h] : 0; a.pitch2[h] = lo ? k.pos_stride2[h] : 0;
+    a.src_off[h] = d->src_head_offset ? d->src_head_offset[h] : h * d->src_stride_h;
+    if (a.src_off[h] < 0) return STARKV_ERR_SHAPE;
   }
   return launch_k_append(a, d->dtype, (hipStream_t)stream);
 }

@@ -116,6 +116,7 @@ struct KAppendArgs {
   int rank[K_MAX_KV];
   int64_t off[K_MAX_KV], pitch[K_MAX_KV];
   int64_t off2[K_MAX_KV], pitch2[K_MAX_KV];
+  int64_t src_off[K_MAX_KV];                        // source row offset of head h (elements)
 };
 
 struct VAppendArgs {

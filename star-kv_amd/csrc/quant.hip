@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
   const int t = (int)(row % a.T), h = (int)((row / a.T) % a.H), b = (int)(row / ((int64_t)a.T * a.H));
   const int s = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t, r = a.rank[h];
   if (s < 0 || s >= a.cap) return;                  // only a run-time position can land here
-  const T* x = (const T*)a.src + b * a.src_sb + h * a.src_sh + (int64_t)t * a.src_st;
+  const T* x = (const T*)a.src + b * a.src_sb + a.src_off[h] + (int64_t)t * a.src_st;
   if (a.fmt == STARKV_FMT_DENSE) {
     T* d = (T*)a.data + b * a.stride_b + a.off[h] + (int64_t)s * a.pitch[h];
     for (int j = lane; j < r; j += 64) d[j] = x[j];

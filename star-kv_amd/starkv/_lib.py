@@ -107,6 +107,7 @@ class KAppendDesc(ctypes.Structure):
         ("src", ctypes.c_void_p), ("src_stride_b", ctypes.c_int64), ("src_stride_h", ctypes.c_int64),
         ("src_stride_t", ctypes.c_int64),
         ("k", KLatent),
+        ("src_head_offset", ctypes.POINTER(ctypes.c_int64)),
         ("pos0_device", ctypes.c_void_p),
     ]
 

@@ -177,28 +177,38 @@ class LatentCache:
             parts.append((n - 8) * self.v_scale2[:, :S].double())
         return torch.cat(parts, -1).to(self.dtype)
 
+    @staticmethod
+    def _k_src(k_new: torch.Tensor):
+        """(source for the writer, its position count): k_new is [B, Hkv, T, r_max]
+        or [B, T, sum(ranks)] with the heads back to back."""
+        if k_new.dim() == 3:
+            return (k_new if k_new.stride(2) == 1 else k_new.contiguous()), k_new.shape[1]
+        return (k_new if k_new.stride(3) == 1 else k_new.contiguous()), k_new.shape[2]
+
     def append_at(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor, pos: torch.Tensor):
         """Write k_new / v_new at the position held by the int32 device tensor
         ``pos`` (read when the writer kernels run, so the call can be captured in
         a CUDA/HIP graph and replayed at advancing positions); the host-side
         ``length`` is left to the caller.  Returns the (K spec, V spec)."""
-        if v_new.shape[1] != k_new.shape[2]:
+        src, T = self._k_src(k_new)
+        if v_new.shape[1] != T:
             raise StarKVError("k_new and v_new must hold the same number of positions")
         ks = self.k_spec(bk)
-        k_append(k_new.contiguous() if k_new.stride(3) != 1 else k_new, ks, 0, self.cap, pos0_device=pos)
+        k_append(src, ks, 0, self.cap, pos0_device=pos)
         v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, 0, self.cap, pos0_device=pos)
         return ks, self.v_spec
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor):
-        """Write T new positions (k_new [B, Hkv, T, r_max], v_new [B, T, Rv]) in
-        place; returns (K spec, V spec, length) for the attention kernels."""
-        T = k_new.shape[2]
+        """Write T new positions (k_new [B, Hkv, T, r_max] or [B, T, sum(ranks)],
+        v_new [B, T, Rv]) in place; returns (K spec, V spec, length) for the
+        attention kernels."""
+        src, T = self._k_src(k_new)
         if v_new.shape[1] != T:
             raise StarKVError("k_new and v_new must hold the same number of positions")
         if self.length + T > self.cap:
             raise StarKVError(f"cache full: {self.length} + {T} > capacity {self.cap}")
         ks = self.k_spec(bk)
-        k_append(k_new.contiguous() if k_new.stride(3) != 1 else k_new, ks, self.length, self.cap)
+        k_append(src, ks, self.length, self.cap)
         v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, self.length, self.cap)
         self.length += T
         return ks, self.v_spec, self.length

@@ -88,11 +88,6 @@ class LatentAttention(nn.Module):
         self.v_vs = nn.Linear(hs, v_rank, bias=False, **kw)
         self.v_u = nn.Linear(v_rank, self.n_kv * HEAD_DIM, bias=False, **kw)
         self.register_buffer("bk", torch.zeros(self.n_kv, self.rmax, HEAD_DIM, **kw))
-        # scatter map: latent channel j of head h -> column h * r_max + (j - offset_h)
-        idx = []
-        for h, r in enumerate(self.ranks):
-            idx.extend(h * self.rmax + i for i in range(r))
-        self.register_buffer("k_scatter", torch.tensor(idx, device=device, dtype=torch.long), persistent=False)
         self.cache = LatentCache(batch, self.ranks, v_rank, capacity, dtype, device, fmt=fmt)
         self.rope = RopeConfig.from_hf_config(config)
         self.scaling = HEAD_DIM ** -0.5
@@ -161,10 +156,7 @@ class LatentAttention(nn.Module):
             rope_apply(q, self.rope, pos0_device=self.graph.pos, max_positions=self.graph.capacity)
         else:
             rope_apply(q, self.rope, pos0=self.cache.length)     # positions continue the cache
-        kl = self.k_vs(hidden_states)
-        k_new = torch.zeros(B, T, self.n_kv * self.rmax, dtype=kl.dtype, device=kl.device)
-        k_new.index_copy_(2, self.k_scatter, kl)
-        k_new = k_new.view(B, T, self.n_kv, self.rmax).permute(0, 2, 1, 3)       # [B, Hkv, T, r_max]
+        k_new = self.k_vs(hidden_states)                    # [B, T, sum(r)]: the writer takes the heads packed
         if self.graph is not None and T == 1 and not self.reference:
             kspec, vspec = self.cache.append_at(k_new, self.v_vs(hidden_states), self.bk, self.graph.pos)
             o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope,

@@ -481,12 +481,18 @@ def rope_apply(x: torch.Tensor, rope: RopeConfig = RopeConfig(), pos0: int = 0,
 
 def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
              pos0_device: Optional[torch.Tensor] = None) -> None:
-    """Write the new K latent rows src [B, Hkv, T, >= r_h] (act dtype, last dim
-    contiguous) into the cache described by ``k`` at positions
-    [pos0, pos0 + T), quantising to its format (starkv_k_append).
+    """Write the new K latent rows into the cache described by ``k`` at
+    positions [pos0, pos0 + T), quantising to its format (starkv_k_append).
+    src: [B, Hkv, T, >= r_h], or [B, T, sum(r_h)] with the heads back to back
+    (the latent projection's own output); act dtype, last dim contiguous.
     ``pos0_device``: an int32 device tensor holding the position, read when
     the kernel runs (graph capture / replay)."""
-    if src.dim() != 4 or src.stride(3) != 1:
+    packed = src.dim() == 3
+    if packed:
+        if src.stride(2) != 1 or src.shape[2] < sum(k.ranks):
+            raise StarKVError("packed src must be [B, T, sum(ranks)] with a contiguous last dim")
+        src = src.unsqueeze(1)                       # [B, 1, T, sum(r)]: head h at a column offset
+    elif src.dim() != 4 or src.stride(3) != 1:
         raise StarKVError("src must be [B, Hkv, T, r] with a contiguous last dim")
     _require_cuda(src, *[t for t in (k.data, k.scale, k.data2, k.scale2) if t is not None])
     keep: list = []
@@ -494,6 +500,10 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
     d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[2], int(pos0), int(capacity), _dt(src)
     d.src, d.src_stride_b, d.src_stride_h, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1), src.stride(2)
     d.k = k.c_struct(keep)
+    if packed:
+        offs = i64_array([sum(k.ranks[:h]) for h in range(k.n_kv_heads)])
+        keep.append(offs)
+        d.src_head_offset = offs
     d.pos0_device = _pos_ptr(pos0_device)
     check(_lib.lib().starkv_k_append(ctypes.byref(d), _stream(src.device)), "starkv_k_append")
 

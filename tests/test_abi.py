@@ -63,7 +63,8 @@ int main(void) {
   S(starkv_decode_desc) F(starkv_decode_desc, k) F(starkv_decode_desc, v) F(starkv_decode_desc, uv)
   F(starkv_decode_desc, rope_table) F(starkv_decode_desc, scale) F(starkv_decode_desc, mask) F(starkv_decode_desc, out_dtype)
   F(starkv_decode_desc, out_stride_h)
-  S(starkv_k_append_desc) F(starkv_k_append_desc, k) F(starkv_k_append_desc, pos0_device)
+  S(starkv_k_append_desc) F(starkv_k_append_desc, k) F(starkv_k_append_desc, src_head_offset)
+  F(starkv_k_append_desc, pos0_device)
   S(starkv_v_append_desc) F(starkv_v_append_desc, v) F(starkv_v_append_desc, pos0_device)
   S(starkv_prefill_desc) F(starkv_prefill_desc, pos0) F(starkv_prefill_desc, dtype) F(starkv_prefill_desc, q)
   F(starkv_prefill_desc, q_stride_t) F(starkv_prefill_desc, k) F(starkv_prefill_desc, v) F(starkv_prefill_desc, uv)

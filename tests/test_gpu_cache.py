@@ -190,3 +190,33 @@ def test_quant_module_decode_matches_dequantised_history():
             mx, mr = errors(out.float(), ref)
             _flush(f"   decode t={t} S={S} max_abs={mx:.3e} mean_rel={mr:.3e}")
             assert mr <= 1e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["dense", "int8_g64"])
+def test_k_append_packed_heads_equals_padded_layout(fmt):
+    """The K writer fed the latent projection's packed rows [B, T, sum(r)]
+    (per-head source offsets) stores exactly what it stores from the padded
+    [B, Hkv, T, r_max] layout."""
+    from starkv.cache import LatentCache
+    print(f"[cache] packed K source fmt={fmt}", flush=True)
+    ranks, Rv, B, T = [24, 8, 40, 16], 64, 2, 19
+    g = torch.Generator(device="cuda").manual_seed(12)
+    packed = torch.randn(B, T, sum(ranks), generator=g, device="cuda").half()
+    padded = torch.zeros(B, len(ranks), T, max(ranks), device="cuda", dtype=torch.float16)
+    off = 0
+    for h, r in enumerate(ranks):
+        padded[:, h, :, :r] = packed[:, :, off:off + r]
+        off += r
+    v_new = torch.randn(B, T, Rv, generator=g, device="cuda").half()
+    bk = torch.zeros(len(ranks), max(ranks), 128, device="cuda", dtype=torch.float16)
+    caches = []
+    for src in (padded, packed):
+        c = LatentCache(B, ranks, Rv, T + 5, torch.float16, "cuda", fmt=fmt)
+        c.append(src[:, :, :7] if src.dim() == 4 else src[:, :7], v_new[:, :7], bk)
+        c.append(src[:, :, 7:] if src.dim() == 4 else src[:, 7:], v_new[:, 7:], bk)
+        caches.append(c)
+    torch.cuda.synchronize()
+    assert torch.equal(caches[0].k_data, caches[1].k_data)
+    if fmt != "dense":
+        assert torch.equal(caches[0].k_scale, caches[1].k_scale)
