@@ -22,7 +22,9 @@
 extern "C" {
 #endif
 
-#define STARKV_ABI_VERSION 1
+/* Bumped on every change of a struct layout or of an entry point's meaning;
+ * the Python binding refuses a library of another version. */
+#define STARKV_ABI_VERSION 2
 
 /* element types */
 enum {
@@ -81,8 +83,12 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
  * position pos0 + t.  x: act dtype [B, H, T, 128], element (b,h,t,d) at
  * x + b*stride_b + h*stride_h + t*stride_t + d.  pos0_device (optional): a
  * device int read at run time instead of pos0 (graph replay); rows whose
- * position then falls past rope_max_positions are left unrotated.  Computed in
- * fp32 and rounded once (the reference rounds each of its three operations).
+ * position then falls outside [0, rope_max_positions) are left unrotated and,
+ * when error_flag (optional device int) is given, the kernel stores 1 there
+ * (the library never clears it; the caller zeroes it and checks it after
+ * synchronising).  Computed in fp32 and rounded once (the reference rounds
+ * each of its three operations).  batch * n_heads * n_tokens * 64 must stay
+ * below 2^32 - 256 (STARKV_ERR_LIMIT).
  * ------------------------------------------------------------------- */
 typedef struct {
   int batch, n_heads, n_tokens, dtype;
@@ -90,6 +96,7 @@ typedef struct {
   const void* rope_table; int rope_max_positions;
   int pos0;
   const int* pos0_device;
+  int* error_flag;
 } starkv_rope_apply_desc;
 
 int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream);
@@ -283,8 +290,10 @@ typedef struct {
                                        ([B, T, sum of ranks], as the latent projection writes them) */
   const int* pos0_device;   /* optional (NULL: use pos0): device int read by the kernel at
                                run time, for calls captured once in a HIP graph and replayed
-                               at advancing positions; rows landing at or past capacity are
+                               at advancing positions; rows landing outside [0, capacity) are
                                then skipped by the kernel instead of rejected by the host */
+  int* error_flag;          /* optional device int: the kernel stores 1 there when it skips a
+                               row (never cleared by the library) */
 } starkv_k_append_desc;
 
 typedef struct {
@@ -293,6 +302,7 @@ typedef struct {
   const void* src; int64_t src_stride_b, src_stride_t;
   starkv_vlatent v;
   const int* pos0_device;   /* as in starkv_k_append_desc */
+  int* error_flag;          /* as in starkv_k_append_desc */
 } starkv_v_append_desc;
 
 int starkv_k_append(const starkv_k_append_desc* d, void* stream);
@@ -318,7 +328,9 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream);
  * STARKV_FMT_INT4_G64; other formats STARKV_ERR_FORMAT.  uv: 16-byte aligned,
  * row stride a multiple of 8.  Quantised latents are dequantised bit-exactly
  * as in decode.  The workspace holds the reconstructed K and V
- * (2 x batch x Hkv x round_up(pos0 + n_tokens, 64) x 128 act-dtype elements).
+ * (2 x batch x Hkv x round_up(pos0 + n_tokens, 64) x 128 fp16 elements, for
+ * either act dtype: bf16 activations attend in fp16, exact for |values| up to
+ * 65504, with 8x finer rounding of K and V than bf16 storage).
  * ------------------------------------------------------------------- */
 typedef struct {
   int batch, n_q_heads, head_dim, n_tokens, pos0;

@@ -196,16 +196,22 @@ def reconstruct_kv(bk: Sequence[torch.Tensor], xk: Sequence[torch.Tensor], xv: t
 
 
 def prefill_attention(q: torch.Tensor, bk, xk, xv, uv_weight, cos, sin, pos0: int = 0,
-                      scale: Optional[float] = None, dtype=torch.float64) -> torch.Tensor:
+                      scale: Optional[float] = None, dtype=torch.float64,
+                      kv_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """Causal prefill over the latent caches: queries q [B, Hq, T, D] (already
     rotated) at positions pos0 .. pos0+T-1; query t attends to keys
     s <= pos0 + t of the first pos0 + T cached positions.  This is the
     reference's prefill (model.py:429-449: materialise, repeat_interleave over
     the GQA group, SDPA with scale) under HF's causal attention mask.
+    ``kv_dtype``: round the materialised K (after RoPE) and V once to this
+    dtype before the attention, as the reference materialises key_full and
+    value_full in the activation dtype (model.py:431-442).
     Returns [B, Hq, T, D]."""
     B, Hq, T, D = q.shape
     S = pos0 + T
     K, V = reconstruct_kv(bk, [x[:, :S] for x in xk], xv[:, :S], uv_weight, cos, sin, dtype)
+    if kv_dtype is not None:
+        K, V = K.to(kv_dtype).to(dtype), V.to(kv_dtype).to(dtype)
     gs = Hq // len(bk)
     K = K.repeat_interleave(gs, dim=1)
     V = V.repeat_interleave(gs, dim=1)

@@ -17,7 +17,8 @@ constexpr int K1_WG_PER_CU = 1;     // k_logits_kernel: one 8-wave (or 4-wave) w
 constexpr int MAX_S = 1 << 24;
 constexpr int MAX_RV = 8192;
 constexpr int64_t V_MAX_PITCH = 1 << 24;   // V row pitch (bytes) of the 24-bit offset multiply in P.V
-constexpr int K2_MAX_H = 32;
+constexpr int K2_MAX_H = 64;       // P.V: up to two 32-head groups
+constexpr int64_t MAX_THREADS_1D = ((int64_t)1 << 32) - 256;   // one-dimensional grids: grid x block < 2^32
 
 int esize(int dt) {
   switch (dt) {
@@ -324,30 +325,33 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
 }
 
 // ---- decode workspace layout (shared by the size query and the call)
+int head_groups(int H) { return (int)ceil_div(H, 32); }   // P.V passes of 32 heads
+
 struct DecodeLayout {
-  int S_pad, n_c1, tiles_per_chunk;
+  int S_pad, n_c1, tiles_per_chunk, n_hg, n_sl;
   PVGeom pv;
-  size_t off_logits, off_cmax, off_part, off_psum, off_part2, off_psum2, off_olat, off_lsum, total;
+  size_t off_logits, off_cmax, off_part, off_psum, off_ctr, off_ypart, total;
 };
 
-DecodeLayout decode_layout(int B, int Hq, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes) {
+DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes) {
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
   L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 256, 3.0, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
-  L.pv = pv_geometry(B, S, Rv, true, vq, v_row_bytes);
+  L.n_hg = head_groups(Hq);
+  L.pv = pv_geometry(B * L.n_hg, S, Rv, true, vq, v_row_bytes);
+  L.n_sl = (int)ceil_div(Rv, UP_SW);
   const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
+  const size_t BQ = (size_t)B * L.n_hg;
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
-  L.off_part = o; o = a256(o + (size_t)B * n_c2 * 32 * Rvp * 4);
-  L.off_psum = o; o = a256(o + (size_t)B * n_c2 * 32 * 4);
-  L.off_part2 = o; o = a256(o + (size_t)B * L.pv.n_grp * 32 * Rvp * 4);
-  L.off_psum2 = o; o = a256(o + (size_t)B * L.pv.n_grp * 32 * 4);
-  L.off_olat = o; o = a256(o + (size_t)B * 32 * Rvp * 4);
-  L.off_lsum = o; o = a256(o + (size_t)B * 32 * 4);
+  L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * 4);
+  L.off_psum = o; o = a256(o + BQ * n_c2 * 32 * 4);
+  L.off_ctr = o; o = a256(o + (size_t)Hkv * 4);
+  L.off_ypart = o; o = a256(o + (size_t)Hkv * L.n_sl * ((size_t)B * (Hq / Hkv)) * HEAD_DIM * 4);
   L.total = o;
   return L;
 }
@@ -568,8 +572,9 @@ size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {
   PVArgs tmp = {};
   int vq = 0;
   if (validate_v(d->v, tmp, &vq)) return 0;
-  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq, v_row_bytes(d->v));
-  return a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4) + a256((size_t)d->batch * g.n_grp * 32 * g.Rvp * 4);
+  const int BQ = d->batch * head_groups(d->n_heads);
+  const PVGeom g = pv_geometry(BQ, d->seq_len, d->v.rank, false, vq, v_row_bytes(d->v));
+  return a256((size_t)BQ * g.n_c2 * 32 * g.Rvp * 4) + a256((size_t)BQ * g.n_grp * 32 * g.Rvp * 4);
 }
 
 int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
@@ -584,12 +589,14 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
   const size_t need = starkv_pv_latent_workspace_bytes(d);
   if (!workspace || workspace_bytes < need) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
-  const PVGeom g = pv_geometry(d->batch, d->seq_len, d->v.rank, false, vq, v_row_bytes(d->v));
+  const int n_hg = head_groups(d->n_heads), BQ = d->batch * n_hg;
+  const PVGeom g = pv_geometry(BQ, d->seq_len, d->v.rank, false, vq, v_row_bytes(d->v));
+  a.n_hg = n_hg;
   a.Rv = d->v.rank; a.Rvp = g.Rvp; a.n_cb = g.n_cb; a.n_c2 = g.n_c2; a.c2_len = g.c2_len; a.n_grp = g.n_grp;
   a.p = d->p; a.p_sb = d->p_stride_b; a.p_sh = d->p_stride_h;
   a.p_vec = al(d->p, 16) && al64(d->p_stride_b * 2, 16) && al64(d->p_stride_h * 2, 16);
   a.part = (float*)workspace;
-  a.part2 = (float*)((char*)workspace + a256((size_t)d->batch * g.n_c2 * 32 * g.Rvp * 4));
+  a.part2 = (float*)((char*)workspace + a256((size_t)BQ * g.n_c2 * 32 * g.Rvp * 4));
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
   a.S = d->seq_len; a.H = d->n_heads;
   return launch_pv(a, d->dtype, vq, false, v_fast(d->v), d->batch, (hipStream_t)stream);
@@ -598,14 +605,15 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
   int gs = 0, n_wg = 0, vq = 0;
   if (validate_decode(d, &gs, &n_wg, &vq)) return 0;
-  return decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v)).total;
+  return decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v)).total;
 }
 
 static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream,
                        void* const* events) {
   int gs = 0, n_wg = 0, vq = 0, st;
   if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
-  const DecodeLayout L = decode_layout(d->batch, d->n_q_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v));
+  const DecodeLayout L =
+      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v));
   if (!workspace || workspace_bytes < L.total) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   char* ws = (char*)workspace;
@@ -637,18 +645,18 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = ka.o_sb; pa.l_st = ka.o_st; pa.l_sh = ka.o_sh;
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
-  pa.part2 = (float*)(ws + L.off_part2); pa.psum2 = (float*)(ws + L.off_psum2); pa.n_grp = L.pv.n_grp;
-  pa.olat = (float*)(ws + L.off_olat); pa.lsum = (float*)(ws + L.off_lsum);
-  pa.S = d->seq_len; pa.H = Hq; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
+  pa.ctr = (int*)(ws + L.off_ctr); pa.n_ctr = d->k.n_kv_heads;
+  pa.S = d->seq_len; pa.H = Hq; pa.n_hg = L.n_hg; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
   pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;
   if ((st = launch_pv(pa, d->dtype, vq, true, v_fast(d->v), B, s))) return st;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
 
   UPArgs ua;
-  ua.olat = pa.olat; ua.Rvp = L.pv.Rvp; ua.lsum = pa.lsum;
+  ua.part = pa.part; ua.psum = pa.psum; ua.n_c2 = L.pv.n_c2; ua.Rvp = L.pv.Rvp; ua.n_hg = L.n_hg;
   ua.uv = d->uv; ua.uv_rs = d->uv_row_stride;
   ua.out = d->out; ua.o_sb = d->out_stride_b; ua.o_sh = d->out_stride_h;
   ua.B = B; ua.Hq = Hq; ua.gs = gs; ua.Rv = d->v.rank;
+  ua.n_sl = L.n_sl; ua.ypart = (float*)(ws + L.off_ypart); ua.ctr = pa.ctr;
   ua.out_f32 = d->out_dtype == STARKV_F32;
   const bool ufast = al(d->uv, 16) && al64(d->uv_row_stride * 2, 16);
   if ((st = launch_up_proj(ua, d->dtype, ufast, s))) return st;
@@ -673,11 +681,12 @@ int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
   if (!d->x || !d->rope_table) return STARKV_ERR_NULL;
   if (d->stride_b < 0 || d->stride_h < 0 || d->stride_t < 0) return STARKV_ERR_SHAPE;
   if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->rope_max_positions) return STARKV_ERR_SHAPE;
-  if ((int64_t)d->batch * d->n_heads * d->n_tokens * 64 > ((int64_t)1 << 40)) return STARKV_ERR_LIMIT;
+  // one thread per (row, frequency); HIP keeps grid x block below 2^32
+  if ((int64_t)d->batch * d->n_heads * d->n_tokens * 64 > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
   RopeApplyArgs a;
   a.x = d->x; a.sb = d->stride_b; a.sh = d->stride_h; a.st = d->stride_t;
   a.B = d->batch; a.H = d->n_heads; a.T = d->n_tokens; a.pos0 = d->pos0; a.max_pos = d->rope_max_positions;
-  a.pos0_dev = d->pos0_device; a.table = d->rope_table;
+  a.pos0_dev = d->pos0_device; a.err = d->error_flag; a.table = d->rope_table;
   return launch_rope_apply(a, d->dtype, (hipStream_t)stream);
 }
 
@@ -691,10 +700,12 @@ int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
   if (st) return st;
   if (!d->src) return STARKV_ERR_NULL;
   if (d->src_stride_b < 0 || d->src_stride_h < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
+  // one wave (64 threads) per row
+  if ((int64_t)d->batch * k.n_kv_heads * d->n_tokens * 64 > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
   KAppendArgs a = {};
   a.src = d->src; a.src_sb = d->src_stride_b; a.src_sh = d->src_stride_h; a.src_st = d->src_stride_t;
   a.B = d->batch; a.H = k.n_kv_heads; a.T = d->n_tokens; a.pos0 = d->pos0; a.cap = d->capacity;
-  a.pos0_dev = d->pos0_device;
+  a.pos0_dev = d->pos0_device; a.err = d->error_flag;
   a.fmt = k.format;
   a.data = (void*)k.data; a.stride_b = k.stride_b;
   a.scale = (void*)k.scale; a.sc_sb = k.scale_stride_b; a.sc_sh = k.scale_stride_h;
@@ -724,10 +735,13 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   if ((st = validate_v(d->v, pa, &vq))) return st;
   if (!d->src) return STARKV_ERR_NULL;
   if (d->src_stride_b < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
+  // one wave per row (group-64: per row and group of 64 ranks)
+  const int64_t waves_per_row = vq == VQ_G64 ? ceil_div(d->v.rank, 64) : 1;
+  if ((int64_t)d->batch * d->n_tokens * waves_per_row * 64 > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
   VAppendArgs a = {};
   a.src = d->src; a.src_sb = d->src_stride_b; a.src_st = d->src_stride_t;
   a.B = d->batch; a.T = d->n_tokens; a.pos0 = d->pos0; a.cap = d->capacity; a.R = d->v.rank; a.vq = vq;
-  a.pos0_dev = d->pos0_device;
+  a.pos0_dev = d->pos0_device; a.err = d->error_flag;
   a.data = (void*)pa.x; a.stride_b = pa.x_sb; a.stride_s = pa.x_ss;
   a.scale = (void*)pa.xs; a.sc_sb = pa.xs_sb; a.sc_ss = pa.xs_ss;
   a.zero = (void*)pa.xz;

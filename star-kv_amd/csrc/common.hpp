@@ -91,13 +91,13 @@ struct PVArgs {
   const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
   int p_vec;                                       // drop-in: P rows allow 16-byte loads
-  float* part;                                     // [B][n_c2][32][Rvp] fp32
-  float* psum;                                     // [B][n_c2][32]
-  float* part2; float* psum2; int n_grp;           // two-level reduction: [B][n_grp][32][Rvp], [B][n_grp][32]
-  float* olat;                                     // [B][32][Rvp] fp32 (fused) ...
-  void* out; int64_t o_sb, o_sh;                   // ... or act-dtype [B][H][Rv] (drop-in)
-  float* lsum;                                     // [B][32] softmax denominators (fused)
-  int S, H, Rv, Rvp, n_cb, n_c2, c2_len;
+  // bq = b * n_hg + head group (32 heads each) indexes the partials
+  float* part;                                     // [B*n_hg][n_c2][32][Rvp] fp32
+  float* psum;                                     // fused: [B*n_hg][n_c2][32] softmax partial sums
+  float* part2; int n_grp;                         // drop-in two-level reduction: [B*n_hg][n_grp][32][Rvp]
+  void* out; int64_t o_sb, o_sh;                   // drop-in: act-dtype [B][H][Rv]
+  int* ctr; int n_ctr;                             // fused: the up-projection's arrival counters, zeroed here
+  int S, H, n_hg, Rv, Rvp, n_cb, n_c2, c2_len;
 };
 
 // ---------------------------------------------------------------------------
@@ -107,6 +107,7 @@ struct KAppendArgs {
   const void* src; int64_t src_sb, src_sh, src_st;   // new rows (b, h, t), act dtype, elements
   int B, H, T, pos0, cap;
   const int* pos0_dev;                              // optional: position read at run time
+  int* err;                                         // optional: set to 1 when a row is skipped
   int fmt;                                          // STARKV_FMT_DENSE or a quantised format
   void* data; int64_t stride_b;                     // dense: elements; quantised: bytes
   void* scale; int64_t sc_sb, sc_sh;
@@ -124,6 +125,7 @@ struct VAppendArgs {
   int B, T, pos0, cap, R, vq;
   int gw;                                           // waves per row (group-64: one per group)
   const int* pos0_dev;                              // optional: position read at run time
+  int* err;                                         // optional: set to 1 when a row is skipped
   void* data; int64_t stride_b, stride_s;
   void* scale; int64_t sc_sb, sc_ss;
   void* zero;                                       // VQ_G64 (strides of scale)
@@ -136,13 +138,17 @@ struct VAppendArgs {
 // Up-projection arguments.
 // ---------------------------------------------------------------------------
 struct UPArgs {
-  const float* olat; int Rvp;                      // [B][32][Rvp]
-  const float* lsum;                               // [B][32]
+  const float* part; const float* psum;            // P.V split partials and softmax sums (PVArgs layout)
+  int n_c2, Rvp, n_hg;
   const void* uv; int64_t uv_rs;                   // [Hkv*128][Rv]
   void* out; int64_t o_sb, o_sh;                   // [B][Hq][128]
   int B, Hq, gs, Rv;
+  int n_sl;                                        // column slices of the V rank (UP_SW columns each)
+  float* ypart;                                    // [Hkv][n_sl][B*gs][128] partial up-projections
+  int* ctr;                                        // [Hkv] arrival counters, zero on entry
   int out_f32;                                     // 1: fp32 output, 0: weight dtype
 };
+constexpr int UP_SW = 64;                          // V-rank columns per up-projection workgroup
 
 // ---------------------------------------------------------------------------
 // In-place RoPE of query rows (rope.hip).
@@ -151,6 +157,7 @@ struct RopeApplyArgs {
   void* x; int64_t sb, sh, st;                     // [B][H][T][128], act dtype, elements
   int B, H, T, pos0, max_pos;
   const int* pos0_dev;                             // optional: position read at run time
+  int* err;                                        // optional: set to 1 when a row is skipped
   const void* table;
 };
 

@@ -7,17 +7,19 @@
 //    K = RoPE(X_k[s] . B_k) (RoPE applied in the epilogue from the decode's
 //    RoPE table; per (KV head, b, 512 positions)) and V = X_v[s] . U_v[h]^T
 //    (per (KV-head pair, b, 256 positions)), into [B][Hkv][S_pad][128]
-//    act-dtype buffers.  Quantised latents are dequantised on the way in,
-//    bit-exactly as everywhere else (int8: fp16(q s); group-64 int4:
-//    fp16(n s + z)), then rounded once more to bf16 for bf16 activations.
-//    Rows in [S, S_pad) are written as zeros.
+//    fp16 buffers (for either activation dtype: the reference materialises
+//    K and V in the activation dtype, model.py:431-442; fp16 holds bf16
+//    models' K and V with 2^-12 instead of 2^-9 unit roundoff).  Quantised
+//    latents are dequantised on the way in, bit-exactly as everywhere else
+//    (int8: fp16(q s); group-64 int4: fp16(n s + z)), then rounded once more
+//    to bf16 for bf16 activations.  Rows in [S, S_pad) are written as zeros.
 // 2. fa_causal_kernel: flash attention over those buffers, one workgroup per
-//    (b, query head, 256 queries), 8 waves of 32 queries.  Per 64-key block
-//    it forms S^T = K . Q^T (so each lane holds 32 keys of one query and the
-//    online softmax needs one cross-half exchange); the lane's probabilities
-//    are the B operand of O^T += V^T . P^T as they stand, V^T read from LDS
-//    with the transpose load in the matching key order.  bf16 splits P into
-//    hi + lo so P.V keeps fp32-class accuracy.
+//    (b, query head, 256 queries), 8 waves of 32 queries, fp16 MFMAs (bf16
+//    queries converted to fp16 on load).  Per 64-key block it forms
+//    S^T = K . Q^T (so each lane holds 32 keys of one query and the online
+//    softmax needs one cross-half exchange); the lane's probabilities are the
+//    B operand of O^T += V^T . P^T as they stand, V^T read from LDS with the
+//    transpose load in the matching key order.
 #include "common.hpp"
 
 namespace starkv {
@@ -41,6 +43,24 @@ template <typename XT> __device__ inline floatx16 pf_mfma(uint4 a, uint4 b, floa
 
 template <typename XT> __device__ inline uint16_t pf_bits(float x) {
   return __builtin_bit_cast(uint16_t, (XT)x);
+}
+
+// The reconstructed K and V are held in fp16 for both activation dtypes: for
+// bf16 activations fp16 keeps 3 more significand bits (unit roundoff 2^-12
+// instead of 2^-9), so the attention over them stays within the decode path's
+// accuracy.  Values beyond +-65504 are not representable (far outside what
+// attention keys and values reach).
+typedef _Float16 KVT;
+
+// bf16 pairs -> fp16 pairs (exact for values inside fp16's normal range)
+__device__ inline uint4 pf_bf16_to_f16(uint4 h) {
+  const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    o[k] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(w[k] << 16)) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(w[k] & 0xffff0000u)) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // fp16 pairs -> bf16 pairs (one rounding), for bf16 activations over
@@ -245,15 +265,15 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
             y0[e] = live ? k0 * co - k1 * si : 0.f;
             y1[e] = live ? k1 * co + k0 * si : 0.f;
           }
-          y0w[c2] = (uint32_t)pf_bits<XT>(y0[0]) | ((uint32_t)pf_bits<XT>(y0[1]) << 16);
-          y1w[c2] = (uint32_t)pf_bits<XT>(y1[0]) | ((uint32_t)pf_bits<XT>(y1[1]) << 16);
+          y0w[c2] = (uint32_t)pf_bits<KVT>(y0[0]) | ((uint32_t)pf_bits<KVT>(y0[1]) << 16);
+          y1w[c2] = (uint32_t)pf_bits<KVT>(y1[0]) | ((uint32_t)pf_bits<KVT>(y1[1]) << 16);
         }
         *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(y0w[0], y0w[1]);
         *(uint2*)(crow + (mt + 2) * 32 + 8 * q) = make_uint2(y1w[0], y1w[1]);
       }
   }
   __syncthreads();
-  XT* dst = (XT*)a.kbuf + (((int64_t)b * a.Hkv + h) * a.S_pad) * HEAD_DIM;
+  KVT* dst = (KVT*)a.kbuf + (((int64_t)b * a.Hkv + h) * a.S_pad) * HEAD_DIM;
 #pragma unroll 4
   for (int it = 0; it < RC_WAVE_POS * 16 / 64; ++it) {
     const int idx = it * 64 + lane, row = idx >> 4, ch = idx & 15;
@@ -470,14 +490,14 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
         for (int c2 = 0; c2 < 2; ++c2) {
           const float v0 = live ? acc[mt][nt][4 * q + 2 * c2] : 0.f;
           const float v1 = live ? acc[mt][nt][4 * q + 2 * c2 + 1] : 0.f;
-          w[c2] = (uint32_t)pf_bits<XT>(v0) | ((uint32_t)pf_bits<XT>(v1) << 16);
+          w[c2] = (uint32_t)pf_bits<KVT>(v0) | ((uint32_t)pf_bits<KVT>(v1) << 16);
         }
         *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(w[0], w[1]);
       }
   }
   __syncthreads();
   if (hlive) {
-    XT* dst = (XT*)a.vbuf + (((int64_t)b * a.Hkv + hw) * a.S_pad) * HEAD_DIM;
+    KVT* dst = (KVT*)a.vbuf + (((int64_t)b * a.Hkv + hw) * a.S_pad) * HEAD_DIM;
 #pragma unroll 4
     for (int it = 0; it < RV_WAVE_POS * 16 / 64; ++it) {
       const int idx = it * 64 + lane, row = idx >> 4, ch = idx & 15;
@@ -536,7 +556,10 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
   const XT* qrow = (const XT*)a.q + b * a.q_sb + qh * a.q_sh + (int64_t)tc * a.q_st;
   uint4 Qb[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) Qb[k] = *(const uint4*)(qrow + 16 * k + 8 * hh);
+  for (int k = 0; k < 8; ++k) {
+    Qb[k] = *(const uint4*)(qrow + 16 * k + 8 * hh);
+    if constexpr (!__is_same(XT, _Float16)) Qb[k] = pf_bf16_to_f16(Qb[k]);   // exact in fp16's range
+  }
   floatx16 o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) o[j] = floatx16{};
@@ -544,8 +567,8 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
   const float thr = FA_RESCALE_LOG2 / c;            // in raw logit units
   float m = -INFINITY, l = 0.f;
   const size_t hbase = (((size_t)b * a.Hkv + kv) * a.S_pad) * HEAD_DIM;
-  const XT* kg = (const XT*)a.kbuf + hbase;
-  const XT* vg = (const XT*)a.vbuf + hbase;
+  const KVT* kg = (const KVT*)a.kbuf + hbase;
+  const KVT* vg = (const KVT*)a.vbuf + hbase;
   // S^T = K . Q^T puts key 8 (v/4) + 4 hh + v%4 of its 32-key tile in
   // element v of lane (n, hh).  The P.V MFMA takes its 16-key chunk kk in that
   // order: lane half hh holds keys 16 kk + 4 hh + 0..3 and 16 kk + 8 + 4 hh +
@@ -588,7 +611,7 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
 #pragma unroll
       for (int k = 0; k < 8; ++k)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) s[kt] = pf_mfma<XT>(kf[kt][k], Qb[k], s[kt]);
+        for (int kt = 0; kt < 2; ++kt) s[kt] = pf_mfma<KVT>(kf[kt][k], Qb[k], s[kt]);
       // lane: keys kb*64 + 32 kt + 8 (v/4) + 4 hh + v%4 of query t
       if (kb * FA_KB + FA_KB - 1 > w_first) {         // the block reaches past some query of the wave
 #pragma unroll
@@ -631,32 +654,14 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const uint16_t* sb = &Vs[buf][(32 * kt + 16 * kk) * FA_VPITCH + tr_off];
-          if constexpr (__is_same(XT, _Float16)) {
-            half8 ph;
+          half8 ph;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ph[e] = (_Float16)s[kt][8 * kk + e];
-            const uint4 pb = __builtin_bit_cast(uint4, ph);
+          for (int e = 0; e < 8; ++e) ph[e] = (_Float16)s[kt][8 * kk + e];
+          const uint4 pb = __builtin_bit_cast(uint4, ph);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 8 * FA_VPITCH);
-              o[j] = pf_mfma<XT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[j]);
-            }
-          } else {
-            bf16x8 ph, pl;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const __bf16 hv = (__bf16)s[kt][8 * kk + e];
-              ph[e] = hv;
-              pl[e] = (__bf16)(s[kt][8 * kk + e] - (float)hv);
-            }
-            const uint4 pbh = __builtin_bit_cast(uint4, ph), pbl = __builtin_bit_cast(uint4, pl);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 8 * FA_VPITCH);
-              const uint4 va = make_uint4(lo.x, lo.y, hi.x, hi.y);
-              o[j] = pf_mfma<XT>(va, pbh, o[j]);
-              o[j] = pf_mfma<XT>(va, pbl, o[j]);
-            }
+          for (int j = 0; j < 4; ++j) {
+            const uint2 lo = pf_read_tr16(sb + 32 * j), hi = pf_read_tr16(sb + 32 * j + 8 * FA_VPITCH);
+            o[j] = pf_mfma<KVT>(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[j]);
           }
         }
     }

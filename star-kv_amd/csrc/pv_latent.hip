@@ -27,12 +27,14 @@
 // Fused mode: P = exp(logit - M) is formed in registers from the fp32 logits
 // of K1 with M the global row max (from K1's chunk maxima); the softmax
 // denominators are summed on the side and normalisation happens in K3.
+// More than 32 heads take one more pass per group of 32 (blockIdx.y counts
+// (batch, head group)).
 // Drop-in mode (bx): P is read as given.
 //
-// Split-S: each workgroup writes its chunk's partial sums; pv_reduce_kernel
-// adds the chunk partials in fixed chunk order (deterministic; no float
-// atomics, unlike the fp16 atomics into an uninitialised tensor of
-// bx_quant.py:113-114, 147).
+// Split-S: each workgroup writes its chunk's partial sums; they are added in
+// fixed chunk order (deterministic; no float atomics, unlike the fp16 atomics
+// into an uninitialised tensor of bx_quant.py:113-114, 147) by
+// pv_reduce_kernel (drop-in) or by the up-projection kernel (fused decode).
 #include "common.hpp"
 
 namespace starkv {
@@ -148,7 +150,10 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
-  const int cb = blockIdx.x % a.n_cb, c2 = blockIdx.x / a.n_cb, b = blockIdx.y;
+  // blockIdx.y = (batch, group of 32 heads): the MFMA M dimension holds 32
+  // heads, so more than 32 heads take one more pass over the latent
+  const int cb = blockIdx.x % a.n_cb, c2 = blockIdx.x / a.n_cb, bq = blockIdx.y;
+  const int b = bq / a.n_hg, h0 = (bq - b * a.n_hg) * 32;     // batch, first head of the group
   const int tile0 = (cb * 4 + wave) * NTW;                    // first 32-column tile of this wave
   const int nvt = max(0, min(NTW, a.Rvp / 32 - tile0));       // valid tiles (wave-uniform)
   const int col0 = tile0 * 32;
@@ -158,16 +163,18 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     const int q = tid >> 3, j = tid & 7;
     float m = -INFINITY;
     if (q < H)
-      for (int c = j; c < a.n_chunk1; c += 8) m = fmaxf(m, a.chunkmax[((int64_t)b * H + q) * a.n_chunk1 + c]);
+      for (int c = j; c < a.n_chunk1; c += 8) m = fmaxf(m, a.chunkmax[((int64_t)b * H + h0 + q) * a.n_chunk1 + c]);
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
-    if (j == 0) Ms[q] = q < H ? m : 0.f;
+    if (j == 0) Ms[q] = h0 + q < H ? m : 0.f;
+    // the up-projection's arrival counters start at zero (it runs after this kernel)
+    if (a.ctr != nullptr && blockIdx.x == 0 && bq == 0 && tid < a.n_ctr) a.ctr[tid] = 0;
     __syncthreads();
   }
   const float Mq = FUSED ? Ms[n] : 0.f;
   const float MqL = -Mq * 1.4426950408889634f;  // exp(l - M) = exp2(l * log2(e) - M * log2(e))
-  const bool qok = n < H;
+  const bool qok = h0 + n < H;
 
   const int s_begin = c2 * a.c2_len;
   const int s_end = min(a.S, s_begin + a.c2_len);
@@ -295,13 +302,13 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
       // rows past H read row H-1; the logits buffer holds S_pad >= s_end + 8
       // columns; 8 aligned positions never straddle a 32-position tile
       const int sa = s_begin + kc * KSTEP + 8 * hh;
-      const float* lp = a.logits + b * a.l_sb + (int64_t)(sa >> 5) * a.l_st + min(n, H - 1) * a.l_sh + (sa & 31);
+      const float* lp = a.logits + b * a.l_sb + (int64_t)(sa >> 5) * a.l_st + min(h0 + n, H - 1) * a.l_sh + (sa & 31);
       const float4 u = *(const float4*)lp, v = *(const float4*)(lp + 4);
       st.p[0] = u.x; st.p[1] = u.y; st.p[2] = u.z; st.p[3] = u.w;
       st.p[4] = v.x; st.p[5] = v.y; st.p[6] = v.z; st.p[7] = v.w;
     } else {
       const int sa = s_begin + ks * KSTEP + 8 * hh;
-      const VT* pp = (const VT*)a.p + b * a.p_sb + n * a.p_sh + sa;
+      const VT* pp = (const VT*)a.p + b * a.p_sb + min(h0 + n, H - 1) * a.p_sh + sa;
       st.praw = make_uint4(0, 0, 0, 0);
       if (qok && ks < nks) {
         if (a.p_vec && sa + 8 <= s_end) {
@@ -418,7 +425,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
 
   // ---- this chunk's partial sums: D[row q][col] -> part[b][c2][q][col]
   const int Rvp = a.Rvp;
-  float* part = a.part + (((int64_t)b * a.n_c2 + c2) * 32) * Rvp;
+  float* part = a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
     if (j < nvt) {
@@ -433,28 +440,29 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     const float ps = add_halves(psum);
     if (hh == 0) Ps[wave][n] = ps;
     __syncthreads();
-    if (cb == 0 && tid < 32) a.psum[((int64_t)b * a.n_c2 + c2) * 32 + tid] = Ps[0][tid];
+    if (cb == 0 && tid < 32) a.psum[((int64_t)bq * a.n_c2 + c2) * 32 + tid] = Ps[0][tid];
   }
 }
 
-// Sum of the chunk partials in fixed chunk order.  Fused: o_lat (fp32, with
-// the denominators L); drop-in: the act-dtype output of bx.  Each thread sums
-// four columns of a 32x32 output tile; the partial loads are issued eight
-// chunks at a time (32 loads in flight per thread) and added in chunk order.
-// More than PV_RG chunks are summed in two levels (deterministic, fixed
-// grouping): MODE 1 sums each group of PV_RG chunks into part2 (grid z =
-// group), MODE 2 sums the groups; MODE 0 sums the chunks directly.
-template <typename VT, bool FUSED, int MODE>
+// Drop-in path (bx): sum of the chunk partials in fixed chunk order into the
+// act-dtype output.  Each thread sums four columns of a 32x32 output tile;
+// the partial loads are issued eight chunks at a time (32 loads in flight per
+// thread) and added in chunk order.  More than PV_RG chunks are summed in two
+// levels (deterministic, fixed grouping): MODE 1 sums each group of PV_RG
+// chunks into part2 (grid z = group), MODE 2 sums the groups; MODE 0 sums the
+// chunks directly.  blockIdx.y = (batch, group of 32 heads), as in pv_kernel.
+// (The fused decode path reduces inside its up-projection, up_proj.hip.)
+template <typename VT, int MODE>
 __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
-  const int tile = blockIdx.x, b = blockIdx.y, grp = blockIdx.z;
+  const int tile = blockIdx.x, bq = blockIdx.y, grp = blockIdx.z;
+  const int b = bq / a.n_hg, h0 = (bq - b * a.n_hg) * 32;
   const int Rvp = a.Rvp;
   const int q0 = threadIdx.x >> 5, col = tile * 32 + (threadIdx.x & 31);
   const int n_src = MODE == 2 ? a.n_grp : a.n_c2;
   const int c_begin = MODE == 1 ? grp * PV_RG : 0;
   const int c_end = MODE == 1 ? min(n_src, c_begin + PV_RG) : n_src;
   const float* part = MODE == 2 ? a.part2 : a.part;
-  const float* psum = MODE == 2 ? a.psum2 : a.psum;
-  const float* pb = part + ((int64_t)b * n_src * 32 + q0) * Rvp + col;
+  const float* pb = part + ((int64_t)bq * n_src * 32 + q0) * Rvp + col;
   const int64_t cstride = (int64_t)32 * Rvp, ustride = (int64_t)8 * Rvp;   // next chunk / next row group
   float s[4] = {0.f, 0.f, 0.f, 0.f};
   int c = c_begin;
@@ -476,19 +484,9 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
   for (int u = 0; u < 4; ++u) {
     const int q = q0 + 8 * u;
     if constexpr (MODE == 1) {
-      a.part2[(((int64_t)b * a.n_grp + grp) * 32 + q) * Rvp + col] = s[u];
-    } else if constexpr (FUSED) {
-      a.olat[((int64_t)b * 32 + q) * Rvp + col] = s[u];
+      a.part2[(((int64_t)bq * a.n_grp + grp) * 32 + q) * Rvp + col] = s[u];
     } else {
-      if (q < a.H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + q * a.o_sh + col] = (VT)s[u];
-    }
-  }
-  if constexpr (FUSED) {
-    if (tile == 0 && threadIdx.x < 32) {
-      float L = 0.f;
-      for (int cc = c_begin; cc < c_end; ++cc) L += psum[((int64_t)b * n_src + cc) * 32 + threadIdx.x];
-      if constexpr (MODE == 1) a.psum2[((int64_t)b * a.n_grp + grp) * 32 + threadIdx.x] = L;
-      else a.lsum[b * 32 + threadIdx.x] = L;
+      if (h0 + q < a.H && col < a.Rv) ((VT*)a.out)[b * a.o_sb + (h0 + q) * a.o_sh + col] = (VT)s[u];
     }
   }
 }
@@ -527,22 +525,24 @@ static void launch_pv_n13(const PVArgs& a, bool fast, int B, hipStream_t st) {
 template <typename VT, bool FUSED>
 static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st) {
   const int ntw = pv_tiles_per_wave(a.Rvp, FUSED, vq);
-  if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, vq, fast, B, st);
-  else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, vq, fast, B, st);
-  else if constexpr (FUSED) launch_pv_n13<VT>(a, fast, B, st);
+  const int BQ = B * a.n_hg;
+  if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, vq, fast, BQ, st);
+  else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, vq, fast, BQ, st);
+  else if constexpr (FUSED) launch_pv_n13<VT>(a, fast, BQ, st);
   int e = (int)hipGetLastError();
-  if (e) return e;
+  if (e || FUSED) return e;
   if (a.n_grp > 1) {
-    hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED, 1>), dim3(a.Rvp / 32, B, a.n_grp), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED, 2>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pv_reduce_kernel<VT, 1>), dim3(a.Rvp / 32, BQ, a.n_grp), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pv_reduce_kernel<VT, 2>), dim3(a.Rvp / 32, BQ), dim3(256), 0, st, a);
   } else {
-    hipLaunchKernelGGL((pv_reduce_kernel<VT, FUSED, 0>), dim3(a.Rvp / 32, B), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pv_reduce_kernel<VT, 0>), dim3(a.Rvp / 32, BQ), dim3(256), 0, st, a);
   }
   return (int)hipGetLastError();
 }
 
 // Quantised formats always take the vector-load variant (the C ABI checks the
-// alignment they need).
+// alignment they need).  Fused: the P.V kernel alone (its partials are reduced
+// by the up-projection kernel); drop-in: P.V and the partial reduction.
 int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st) {
   if (dtype == STARKV_F16)
     return fused ? launch_pv_t<_Float16, true>(a, vq, fast, B, st) : launch_pv_t<_Float16, false>(a, vq, fast, B, st);

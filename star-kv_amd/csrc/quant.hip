@@ -95,7 +95,10 @@ __global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
   if (row >= (int64_t)a.B * a.H * a.T) return;
   const int t = (int)(row % a.T), h = (int)((row / a.T) % a.H), b = (int)(row / ((int64_t)a.T * a.H));
   const int s = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t, r = a.rank[h];
-  if (s < 0 || s >= a.cap) return;                  // only a run-time position can land here
+  if (s < 0 || s >= a.cap) {                        // only a run-time position can land here
+    if (a.err != nullptr && lane == 0) *a.err = 1;
+    return;
+  }
   const T* x = (const T*)a.src + b * a.src_sb + a.src_off[h] + (int64_t)t * a.src_st;
   if (a.fmt == STARKV_FMT_DENSE) {
     T* d = (T*)a.data + b * a.stride_b + a.off[h] + (int64_t)s * a.pitch[h];
@@ -123,7 +126,10 @@ __global__ __launch_bounds__(256) void v_append_kernel(const VAppendArgs a) {
   if (row >= (int64_t)a.B * a.T) return;
   const int t = (int)(row % a.T), b = (int)(row / a.T);
   const int s = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t, R = a.R;
-  if (s < 0 || s >= a.cap) return;                  // only a run-time position can land here
+  if (s < 0 || s >= a.cap) {                        // only a run-time position can land here
+    if (a.err != nullptr && lane == 0) *a.err = 1;
+    return;
+  }
   const T* x = (const T*)a.src + b * a.src_sb + (int64_t)t * a.src_st;
   if (a.vq == VQ_DENSE) {
     T* d = (T*)a.data + b * a.stride_b + (int64_t)s * a.stride_s;

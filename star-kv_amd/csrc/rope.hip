@@ -53,7 +53,10 @@ __global__ void rope_apply_kernel(RopeApplyArgs a) {
   const int h = (int)((row / a.T) % a.H);
   const int b = (int)(row / ((int64_t)a.T * a.H));
   const int p = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t;
-  if (p < 0 || p >= a.max_pos) return;            // only a run-time position can land here
+  if (p < 0 || p >= a.max_pos) {                 // only a run-time position can land here
+    if (a.err != nullptr) *a.err = 1;
+    return;
+  }
   T* x = (T*)a.x + b * a.sb + h * a.sh + (int64_t)t * a.st;
   const int64_t te = ((int64_t)((p >> 5) * 8 + (i >> 3)) * 64 + ((i & 7) >> 2) * 32 + (p & 31)) * 8 + 2 * (i & 3);
   const uint32_t cs = ((const uint32_t*)a.table)[te >> 1];

@@ -1,121 +1,152 @@
-// K3: softmax normalisation + per-head up-projection on gfx950.
+// K3: split-S reduction, softmax normalisation and per-head up-projection on
+// gfx950, in one launch.
 //
 // Replaces model.py:485-487 (v_u.weight viewed [Hkv, 128, Rv], repeated per
-// query-head group, out = prob_v @ U^T):
-//     out[b, q, d] = (1 / L[b,q]) * sum_j U_v[kv*128 + d][j] * o_lat[b, q, j]
-// For KV head kv the rows (b, q in group(kv)) form one M x Rv matrix, so the
-// product is a small GEMM per KV head on MFMA 32x32x16: A = o_lat rows split
-// into hi + lo halves of the weight dtype (fp32-accurate), B = U_v rows read
-// straight from the weight layout (the k-contiguous operand needs no
-// transpose).  Workgroup = (32-column block of d, KV head, 32-row M-tile);
-// its UP_WAVES waves split the Rv reduction (a handful of K-steps each, so the
-// dependent load chains stay short) and are summed through LDS.
+// query-head group, out = prob_v @ U^T) together with the sum over the P.V
+// kernel's position chunks:
+//     out[b, q, d] = (1 / L[b,q]) * sum_j U_v[kv*128 + d][j] * sum_c part_c[b, q, j]
+//     L[b, q] = sum_c psum_c[b, q]
+// Workgroup = (slice of UP_SW V-rank columns, KV head kv).  Its rows are the
+// M = B * gs (batch, query head of kv's group) pairs.  It sums the chunk
+// partials of its columns in fixed chunk order into LDS, multiplies them by
+// its U_v columns (fp32, the weights converted exactly) and writes the
+// [M][128] partial up-projection of its slice.  The workgroup that completes
+// a KV head last (an arrival counter per KV head, zeroed by the P.V kernel
+// that runs before) adds the slices in slice order and divides by L, so the
+// result does not depend on which workgroup arrives last: the output is
+// deterministic, with no float atomics and no second launch.  Nothing waits
+// on another workgroup.
 #include "common.hpp"
 
 namespace starkv {
 
-constexpr int UP_WAVES = 16;
+constexpr int UP_MB = 64;          // rows per LDS block
 
 template <typename WT, typename OT, bool FAST>
-__global__ __launch_bounds__(UP_WAVES * 64) void up_proj_kernel(const UPArgs a) {
-  __shared__ float red[UP_WAVES][64][17];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 31, hh = lane >> 5;
-  const int db = blockIdx.x, kv = blockIdx.y, mt = blockIdx.z;
-  const int gs = a.gs;
+__global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
+  __shared__ float os[UP_MB][UP_SW + 4];
+  __shared__ float Ls[UP_MB];
+  __shared__ int is_last;
+  const int tid = threadIdx.x;
+  const int sl = blockIdx.x, kv = blockIdx.y;
+  const int gs = a.gs, M = a.B * gs;
+  const int j0 = sl * UP_SW, nj = min(UP_SW, a.Rv - j0);   // valid columns of the slice
+  const int64_t cstr = (int64_t)32 * a.Rvp;               // next chunk's partials
 
-  // A row (lane n): M-row rho -> (b, g)
-  const int rho = mt * 32 + n;
-  const int rb = rho / gs, rg = rho % gs;
-  const bool rok = rb < a.B;
-  const int q = kv * gs + rg;
-  const float invL = rok ? 1.0f / a.lsum[rb * 32 + q] : 0.f;
-  const float* orow = a.olat + ((int64_t)(rok ? rb : 0) * 32 + q) * a.Rvp;
-  const int d = db * 32 + n;
-  const WT* urow = (const WT*)a.uv + (int64_t)(kv * HEAD_DIM + d) * a.uv_rs;
-
-  const int nk = a.Rvp / KSTEP;
-  const int per = (nk + UP_WAVES - 1) / UP_WAVES;
-  const int k0 = wave * per, k1 = min(nk, k0 + per);
-
-  floatx16 acc = floatx16{};
-  for (int kk = k0; kk < k1; ++kk) {
-    const int r0 = kk * KSTEP + 8 * hh;
-    float o[8];
-    if (rok) {
-      const float4 u = *(const float4*)(orow + r0), v = *(const float4*)(orow + r0 + 4);
-      o[0] = u.x; o[1] = u.y; o[2] = u.z; o[3] = u.w; o[4] = v.x; o[5] = v.y; o[6] = v.z; o[7] = v.w;
-    } else {
+  // this thread's U_v row (d) over the slice, in fp32
+  const int d = tid & (HEAD_DIM - 1), mh = tid >> 7;
+  float u[UP_SW];
+  const WT* urow = (const WT*)a.uv + (int64_t)(kv * HEAD_DIM + d) * a.uv_rs + j0;
+  if (FAST && nj == UP_SW) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = 0.f;
-    }
-    uint4 bu = make_uint4(0, 0, 0, 0);
-    if (FAST && r0 + 8 <= a.Rv) {
-      bu = *(const uint4*)(urow + r0);
-    } else {
-      uint16_t tmp[8];
+    for (int k = 0; k < UP_SW / 8; ++k) {
+      const uint4 w = *(const uint4*)(urow + 8 * k);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tmp[e] = (r0 + e < a.Rv) ? ((const uint16_t*)urow)[r0 + e] : (uint16_t)0;
-      bu = make_uint4(tmp[0] | (tmp[1] << 16), tmp[2] | (tmp[3] << 16), tmp[4] | (tmp[5] << 16), tmp[6] | (tmp[7] << 16));
-    }
-    if constexpr (__is_same(WT, _Float16)) {
-      half8 ah, al;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = o[e] * invL;
-        const _Float16 h = (_Float16)x;
-        ah[e] = h;
-        al[e] = (_Float16)(x - (float)h);
+      for (int e = 0; e < 4; ++e) {
+        u[8 * k + 2 * e] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] & 0xffffu)));
+        u[8 * k + 2 * e + 1] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] >> 16)));
       }
-      const half8 bv = __builtin_bit_cast(half8, bu);
-      acc = mfma_f16(ah, bv, acc);
-      acc = mfma_f16(al, bv, acc);
-    } else {
-      bf16x8 ah, al;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = o[e] * invL;
-        const __bf16 h = (__bf16)x;
-        ah[e] = h;
-        al[e] = (__bf16)(x - (float)h);
-      }
-      const bf16x8 bv = __builtin_bit_cast(bf16x8, bu);
-      acc = mfma_bf16(ah, bv, acc);
-      acc = mfma_bf16(al, bv, acc);
     }
+  } else {
+#pragma unroll
+    for (int j = 0; j < UP_SW; ++j) u[j] = j < nj ? to_f32(urow[j]) : 0.f;
   }
 
+  float* yp = a.ypart + ((int64_t)kv * a.n_sl + sl) * M * HEAD_DIM;
+  for (int m0 = 0; m0 < M; m0 += UP_MB) {
+    const int mb = min(UP_MB, M - m0);
+    // chunk sums of rows m0 .. m0+mb over the slice's columns
+    for (int e = tid; e < mb * UP_SW; e += 256) {
+      const int mm = e / UP_SW, jj = e % UP_SW;
+      const int m = m0 + mm, q = kv * gs + m % gs;
+      const int bq = (m / gs) * a.n_hg + (q >> 5);
+      float s = 0.f;
+      if (jj < nj) {
+        const float* p = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + j0 + jj;
+        int c = 0;
+        for (; c + 8 <= a.n_c2; c += 8) {
+          float v[8];
 #pragma unroll
-  for (int v = 0; v < 16; ++v) red[wave][lane][v] = acc[v];
+          for (int k = 0; k < 8; ++k) v[k] = p[(c + k) * cstr];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) s += v[k];
+        }
+        for (; c < a.n_c2; ++c) s += p[c * cstr];
+      }
+      os[mm][jj] = s;
+    }
+    __syncthreads();
+    // partial up-projection of the slice: two rows per pass (one per half block)
+    for (int mm = mh; mm < mb; mm += 2) {
+      float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < UP_SW; j += 4) {
+        const float4 o4 = *(const float4*)&os[mm][j];
+        y[0] = fmaf(u[j], o4.x, y[0]);
+        y[1] = fmaf(u[j + 1], o4.y, y[1]);
+        y[2] = fmaf(u[j + 2], o4.z, y[2]);
+        y[3] = fmaf(u[j + 3], o4.w, y[3]);
+      }
+      yp[(int64_t)(m0 + mm) * HEAD_DIM + d] = (y[0] + y[1]) + (y[2] + y[3]);
+    }
+    __syncthreads();
+  }
+
+  // arrival: the last slice of this KV head finishes the head
+  __threadfence();
   __syncthreads();
-  for (int e = tid; e < 1024; e += UP_WAVES * 64) {
-    const int row = e >> 5, col = e & 31;          // D[row][col]
-    const int ln = col + 32 * ((row >> 2) & 1), v = 4 * (row >> 3) + (row & 3);
-    float s = 0.f;
+  if (tid == 0) is_last = atomicAdd(&a.ctr[kv], 1) == a.n_sl - 1;
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  const float* y0 = a.ypart + (int64_t)kv * a.n_sl * M * HEAD_DIM;
+  const int64_t sstr = (int64_t)M * HEAD_DIM;             // next slice
+  for (int m0 = 0; m0 < M; m0 += UP_MB) {
+    const int mb = min(UP_MB, M - m0);
+    if (tid < mb) {
+      const int m = m0 + tid, q = kv * gs + m % gs;
+      const int bq = (m / gs) * a.n_hg + (q >> 5);
+      const float* ps = a.psum + (int64_t)bq * a.n_c2 * 32 + (q & 31);
+      float L = 0.f;
+      for (int c = 0; c < a.n_c2; ++c) L += ps[c * 32];
+      Ls[tid] = 1.0f / L;
+    }
+    __syncthreads();
+    for (int mm = mh; mm < mb; mm += 2) {
+      const float* yr = y0 + (int64_t)(m0 + mm) * HEAD_DIM + d;
+      float s = 0.f;
+      int k = 0;
+      for (; k + 8 <= a.n_sl; k += 8) {
+        float v[8];
 #pragma unroll
-    for (int w = 0; w < UP_WAVES; ++w) s += red[w][ln][v];
-    const int rr = mt * 32 + row;
-    const int ob = rr / gs, og = rr % gs;
-    if (ob < a.B) ((OT*)a.out)[ob * a.o_sb + (kv * gs + og) * a.o_sh + db * 32 + col] = (OT)s;
+        for (int e = 0; e < 8; ++e) v[e] = yr[(k + e) * sstr];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+      }
+      for (; k < a.n_sl; ++k) s += yr[k * sstr];
+      const int m = m0 + mm, b = m / gs, q = kv * gs + m % gs;
+      ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s * Ls[mm]);
+    }
+    __syncthreads();
   }
+  if (tid == 0) a.ctr[kv] = 0;
 }
 
 template <typename WT, typename OT>
-static void launch_up_t(const UPArgs& a, bool fast, dim3 grid, dim3 block, hipStream_t st) {
-  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, OT, true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((up_proj_kernel<WT, OT, false>), grid, block, 0, st, a);
+static void launch_up_t(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
+  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, OT, true>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((up_proj_kernel<WT, OT, false>), grid, dim3(256), 0, st, a);
 }
 
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st) {
-  const int n_kv = a.Hq / a.gs;
-  dim3 grid(HEAD_DIM / 32, n_kv, (unsigned)ceil_div((int64_t)a.B * a.gs, 32)), block(UP_WAVES * 64);
+  const dim3 grid(a.n_sl, a.Hq / a.gs);
   if (dtype == STARKV_F16) {
-    if (a.out_f32) launch_up_t<_Float16, float>(a, fast, grid, block, st);
-    else launch_up_t<_Float16, _Float16>(a, fast, grid, block, st);
+    if (a.out_f32) launch_up_t<_Float16, float>(a, fast, grid, st);
+    else launch_up_t<_Float16, _Float16>(a, fast, grid, st);
   } else {
-    if (a.out_f32) launch_up_t<__bf16, float>(a, fast, grid, block, st);
-    else launch_up_t<__bf16, __bf16>(a, fast, grid, block, st);
+    if (a.out_f32) launch_up_t<__bf16, float>(a, fast, grid, st);
+    else launch_up_t<__bf16, __bf16>(a, fast, grid, st);
   }
   return (int)hipGetLastError();
 }

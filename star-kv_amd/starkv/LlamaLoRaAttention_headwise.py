@@ -15,9 +15,13 @@ the reference installs on it (model.py:387-491):
 Decode (one query position) runs the fused kernel chain of
 ``starkv_decode_attention`` (K logits with per-position RoPE, softmax, P.Xv,
 per-KV-head up-projection) on the latent caches as ``past_key_values.update``
-returns them: keys [B, Hkv, S, r], values [B, S, Rv].  Prefill materialises K
-and V and runs torch SDPA, as the reference does (model.py:429-449), but
-causally when no mask is given (the reference omits ``is_causal``).
+returns them: keys [B, Hkv, S, r], values [B, S, Rv].  Prefill without a mask
+(HF passes none when there is no padding) runs causally on
+``starkv_prefill_attention`` (K and V reconstructed from the latent caches by
+MFMA, flash attention) when the caches meet its layout (ranks and strides
+multiples of 8); with a mask, or another layout, it materialises K and V and
+runs torch SDPA, as the reference does (model.py:429-449), causally when no
+mask is given (the reference omits ``is_causal``).
 
 Differences kept on purpose: keys are rotated by their own positions (the
 reference's torch branch uses the last position for all keys,
@@ -33,7 +37,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ._lib import StarKVError
-from .ops import KLatentSpec, decode_attention
+from .ops import KLatentSpec, decode_attention, prefill_attention
 from .rope import RopeConfig
 
 # the reference module's switches (LlamaLoRaAttention_headwise.py:16-19);
@@ -45,6 +49,19 @@ triton_kernel = True
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def _prefill_layout_ok(k: torch.Tensor, v: torch.Tensor, uv: torch.Tensor) -> bool:
+    """Whether the caches meet starkv_prefill_attention's layout (dense latents:
+    ranks, strides and offsets multiples of 8 elements, 16-byte aligned data).
+    Other layouts keep the reference's torch route."""
+    def a16(t):
+        return t.data_ptr() % 16 == 0
+    return (k.dim() == 4 and v.dim() == 3 and k.dtype == v.dtype == uv.dtype and k.dtype in (torch.float16, torch.bfloat16)
+            and k.stride(3) == 1 and v.stride(2) == 1 and uv.stride(1) == 1 and k.shape[3] % 8 == 0
+            and v.shape[2] % 8 == 0 and all(s % 8 == 0 for s in (k.stride(0), k.stride(1), k.stride(2), v.stride(0),
+                                                                   v.stride(1), uv.stride(0)))
+            and a16(k) and a16(v) and a16(uv))
 
 
 def _additive(mask: Optional[torch.Tensor], dtype: torch.dtype) -> Optional[torch.Tensor]:
@@ -111,7 +128,13 @@ class LlamaCustomAttention(nn.Module):
         S = key_states.shape[-2]
         mask = _additive(attention_mask, q.dtype)
 
-        if query_len > 1:
+        if query_len > 1 and mask is None and _prefill_layout_ok(key_states, value_states, v_u.weight):
+            # causal prefill on the HIP kernels: K / V reconstructed from the
+            # latent caches by MFMA, then flash attention
+            spec = KLatentSpec.from_reference(key_states, self._k_basis(k_u))
+            out = prefill_attention(q, spec, value_states, v_u.weight, rope=self.rope, pos0=S - query_len,
+                                    scale=self.scaling)
+        elif query_len > 1:
             pos = torch.arange(S, device=q.device)
             kc, ks = self.rope.cos_sin(pos)
             K = torch.matmul(key_states, k_u.transpose(-2, -1).to(key_states.dtype))

@@ -109,6 +109,7 @@ class KAppendDesc(ctypes.Structure):
         ("k", KLatent),
         ("src_head_offset", ctypes.POINTER(ctypes.c_int64)),
         ("pos0_device", ctypes.c_void_p),
+        ("error_flag", ctypes.c_void_p),
     ]
 
 
@@ -119,6 +120,7 @@ class VAppendDesc(ctypes.Structure):
         ("src", ctypes.c_void_p), ("src_stride_b", ctypes.c_int64), ("src_stride_t", ctypes.c_int64),
         ("v", VLatent),
         ("pos0_device", ctypes.c_void_p),
+        ("error_flag", ctypes.c_void_p),
     ]
 
 
@@ -146,6 +148,7 @@ class RopeApplyDesc(ctypes.Structure):
         ("rope_table", ctypes.c_void_p), ("rope_max_positions", ctypes.c_int),
         ("pos0", ctypes.c_int),
         ("pos0_device", ctypes.c_void_p),
+        ("error_flag", ctypes.c_void_p),
     ]
 
 
@@ -158,6 +161,8 @@ EXPORTS = (
     "starkv_k_append", "starkv_v_append",
     "starkv_prefill_workspace_bytes", "starkv_prefill_attention", "starkv_prefill_attention_timed",
 )
+
+ABI_VERSION = 2          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
 
 _lib = None
 
@@ -201,8 +206,9 @@ def lib() -> ctypes.CDLL:
     L.starkv_k_append.argtypes = [ctypes.POINTER(KAppendDesc), ctypes.c_void_p]
     L.starkv_v_append.restype = ctypes.c_int
     L.starkv_v_append.argtypes = [ctypes.POINTER(VAppendDesc), ctypes.c_void_p]
-    if L.starkv_abi_version() != 1:
-        raise StarKVError("libstarkv ABI version mismatch")
+    if L.starkv_abi_version() != ABI_VERSION:
+        raise StarKVError(f"{LIB_PATH} has ABI version {L.starkv_abi_version()}, this binding needs "
+                          f"{ABI_VERSION}: rebuild it with `make -C star-kv_amd`")
     _lib = L
     return L
 

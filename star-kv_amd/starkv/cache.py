@@ -185,17 +185,21 @@ class LatentCache:
             return (k_new if k_new.stride(2) == 1 else k_new.contiguous()), k_new.shape[1]
         return (k_new if k_new.stride(3) == 1 else k_new.contiguous()), k_new.shape[2]
 
-    def append_at(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor, pos: torch.Tensor):
+    def append_at(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor, pos: torch.Tensor,
+                  error_flag: Optional[torch.Tensor] = None):
         """Write k_new / v_new at the position held by the int32 device tensor
         ``pos`` (read when the writer kernels run, so the call can be captured in
         a CUDA/HIP graph and replayed at advancing positions); the host-side
-        ``length`` is left to the caller.  Returns the (K spec, V spec)."""
+        ``length`` is left to the caller.  Rows that would land past the
+        capacity are skipped and set ``error_flag`` (int32 device tensor) to 1.
+        Returns the (K spec, V spec)."""
         src, T = self._k_src(k_new)
         if v_new.shape[1] != T:
             raise StarKVError("k_new and v_new must hold the same number of positions")
         ks = self.k_spec(bk)
-        k_append(src, ks, 0, self.cap, pos0_device=pos)
-        v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, 0, self.cap, pos0_device=pos)
+        k_append(src, ks, 0, self.cap, pos0_device=pos, error_flag=error_flag)
+        v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, 0, self.cap, pos0_device=pos,
+                 error_flag=error_flag)
         return ks, self.v_spec
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor):

@@ -50,6 +50,15 @@ class DecodeGraphState:
         self.pos = torch.tensor([length], dtype=torch.int32, device=device)
         self.mask = torch.full((batch, 1, self.capacity), -1e30, dtype=torch.float32, device=device)
         self.mask[:, :, :length] = 0.0
+        # set by the RoPE and cache-writer kernels when a replay's position
+        # falls outside the capacity (they skip those rows)
+        self.error = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def check(self):
+        """Raise if any replay ran past the capacity (synchronises)."""
+        if int(self.error.item()) != 0:
+            from ._lib import StarKVError
+            raise StarKVError("a graph-replayed decode step ran past the latent cache's capacity")
 
     def open_position(self):
         self.mask.index_fill_(2, self.pos.long(), 0.0)
@@ -66,9 +75,8 @@ class LatentAttention(nn.Module):
     past r_h unused), ``v_vs`` [Rv, hidden], ``v_u`` [Hkv*128, Rv] (U_v).
 
     ``reference = True`` runs every forward through the torch path (dequantised
-    cache, K / V materialised as the reference does; SDPA in fp32 for decode
-    steps, in the act dtype for prefill) -- the parity reference of the kernel
-    path."""
+    cache, K / V materialised in the act dtype as the reference does, then SDPA
+    in fp32) -- the whole-model consistency reference of the kernel path."""
 
     def __init__(self, config, layer_idx: int, ranks: Sequence[int], v_rank: int, batch: int, capacity: int,
                  fmt: str = "int8_g64", device="cuda", dtype=torch.float16):
@@ -132,7 +140,7 @@ class LatentAttention(nn.Module):
         V = F.linear(self.cache.dequant_v(S), self.v_u.weight).view(B, S, self.n_kv, HEAD_DIM).transpose(1, 2)
         K = K.repeat_interleave(gs, 1)
         V = V.repeat_interleave(gs, 1)
-        if self.reference and T == 1:
+        if self.reference:
             qf, Kf, Vf = q.float(), K.float().contiguous(), V.float().contiguous()
         else:
             qf, Kf, Vf = q, K.contiguous(), V.contiguous()
@@ -153,12 +161,14 @@ class LatentAttention(nn.Module):
             cos, sin = position_embeddings
             q = q * cos.unsqueeze(1) + _rotate_half(q) * sin.unsqueeze(1)
         elif self.graph is not None and T == 1:
-            rope_apply(q, self.rope, pos0_device=self.graph.pos, max_positions=self.graph.capacity)
+            rope_apply(q, self.rope, pos0_device=self.graph.pos, max_positions=self.graph.capacity,
+                       error_flag=self.graph.error)
         else:
             rope_apply(q, self.rope, pos0=self.cache.length)     # positions continue the cache
         k_new = self.k_vs(hidden_states)                    # [B, T, sum(r)]: the writer takes the heads packed
         if self.graph is not None and T == 1 and not self.reference:
-            kspec, vspec = self.cache.append_at(k_new, self.v_vs(hidden_states), self.bk, self.graph.pos)
+            kspec, vspec = self.cache.append_at(k_new, self.v_vs(hidden_states), self.bk, self.graph.pos,
+                                                error_flag=self.graph.error)
             o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope,
                                  seq_len=self.graph.capacity, scale=self.scaling, mask=self.graph.mask)
             return self.o_proj(o.unsqueeze(1).reshape(B, T, self.n_heads * HEAD_DIM)), None
@@ -318,4 +328,5 @@ def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = Tru
         for att in atts:
             att.graph = None
             att.cache.length = P + steps
+    state.check()
     return torch.cat(toks, 1), logits

@@ -46,14 +46,26 @@ def _require_cuda(*ts):
 
 
 _WS: dict = {}
+_WS_RETIRED: list = []
 
 
 def _workspace(device, nbytes: int) -> torch.Tensor:
-    """Per-device scratch reused across calls (ordered on one stream)."""
+    """Per-device scratch reused across calls (ordered on one stream).
+
+    A captured CUDA/HIP graph keeps the address of the workspace it was
+    captured with, so a buffer that is outgrown is retired, never freed: the
+    replays of an earlier graph keep writing memory that nothing else owns.
+    Growing during a capture is refused (run the call once eagerly first)."""
     key = torch.device(device)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        if key.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            raise StarKVError("the libstarkv workspace would grow inside a graph capture: run the same call "
+                              "once before capturing it")
+        if ws is not None:
+            _WS_RETIRED.append(ws)
+        ws = torch.empty(max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20), dtype=torch.uint8,
+                         device=device)
         _WS[key] = ws
     return ws
 
@@ -190,7 +202,7 @@ def _q3(q: torch.Tensor) -> torch.Tensor:
     return q
 
 
-def _mask_args(mask: Optional[torch.Tensor], B: int, S: int):
+def _mask_args(mask: Optional[torch.Tensor], B: int, S: int, Hq: int):
     """Accept an additive mask broadcastable to [B, Hq, S] (HF's [B, 1, 1, S>=S] included)."""
     if mask is None:
         return None, 0, 0, 0
@@ -203,6 +215,8 @@ def _mask_args(mask: Optional[torch.Tensor], B: int, S: int):
         m = m[:, None, :]
     if m.shape[-1] < S or m.stride(-1) != 1:
         raise StarKVError("mask must cover S positions with a contiguous last dim")
+    if m.shape[0] not in (1, B) or m.shape[1] not in (1, Hq):
+        raise StarKVError(f"mask of shape {tuple(mask.shape)} does not broadcast to [B={B}, Hq={Hq}, S]")
     sb = m.stride(0) if m.shape[0] == B else 0
     sh = m.stride(1) if m.shape[1] != 1 else 0
     return m, _dt(m), sb, sh
@@ -219,7 +233,7 @@ def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = R
     out_dtype = out_dtype or torch.float32
     out = torch.empty(B, Hq, S, dtype=out_dtype, device=q.device)
     table, cap = rope_table(rope, S, q.device)
-    m, mdt, msb, msh = _mask_args(mask, B, S)
+    m, mdt, msb, msh = _mask_args(mask, B, S, Hq)
     keep: list = []
     d = KLogitsDesc()
     d.batch, d.n_q_heads, d.head_dim, d.seq_len = B, Hq, HEAD_DIM, S
@@ -369,7 +383,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     if out.dtype not in (q.dtype, torch.float32) or out.stride(-1) != 1:
         raise StarKVError("out must be [B, Hq, 128] of q's dtype or float32")
     table, cap = rope_table(rope, S, q.device)
-    m, mdt, msb, msh = _mask_args(mask, B, S)
+    m, mdt, msb, msh = _mask_args(mask, B, S, Hq)
     keep: list = []
     d = DecodeDesc()
     d.batch, d.n_q_heads, d.head_dim, d.seq_len = B, Hq, HEAD_DIM, S
@@ -458,12 +472,15 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
 
 
 def rope_apply(x: torch.Tensor, rope: RopeConfig = RopeConfig(), pos0: int = 0,
-               pos0_device: Optional[torch.Tensor] = None, max_positions: Optional[int] = None) -> torch.Tensor:
+               pos0_device: Optional[torch.Tensor] = None, max_positions: Optional[int] = None,
+               error_flag: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Rotate query rows x [B, H, T, 128] (act dtype, last dim contiguous) in
     place by the RoPE of positions pos0 + t (the query half of HF's
     apply_rotary_pos_emb, model.py:423); ``pos0_device``: an int32 device
     tensor read when the kernel runs (graph capture / replay), with
-    ``max_positions`` bounding the positions it may hold.  Returns x."""
+    ``max_positions`` bounding the positions it may hold; a row whose run-time
+    position falls outside them is left as it is and sets ``error_flag`` (an
+    int32 device tensor the caller zeroes and checks) to 1.  Returns x."""
     if x.dim() != 4 or x.shape[-1] != HEAD_DIM or x.stride(-1) != 1:
         raise StarKVError("x must be [B, H, T, 128] with a contiguous last dim")
     _require_cuda(x)
@@ -475,18 +492,33 @@ def rope_apply(x: torch.Tensor, rope: RopeConfig = RopeConfig(), pos0: int = 0,
     d.rope_table, d.rope_max_positions = table.data_ptr(), cap
     d.pos0 = int(pos0)
     d.pos0_device = _pos_ptr(pos0_device)
+    d.error_flag = _flag_ptr(error_flag)
     check(_lib.lib().starkv_rope_apply(ctypes.byref(d), _stream(x.device)), "starkv_rope_apply")
     return x
 
 
+def _flag_ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or not t.is_cuda or t.numel() < 1:
+        raise StarKVError("error_flag must be an int32 device tensor")
+    return t.data_ptr()
+
+
+def _cache_batch(t: torch.Tensor) -> int:
+    """Batch size of a cache buffer (its leading dimension)."""
+    return t.shape[0]
+
+
 def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
-             pos0_device: Optional[torch.Tensor] = None) -> None:
+             pos0_device: Optional[torch.Tensor] = None, error_flag: Optional[torch.Tensor] = None) -> None:
     """Write the new K latent rows into the cache described by ``k`` at
     positions [pos0, pos0 + T), quantising to its format (starkv_k_append).
     src: [B, Hkv, T, >= r_h], or [B, T, sum(r_h)] with the heads back to back
     (the latent projection's own output); act dtype, last dim contiguous.
     ``pos0_device``: an int32 device tensor holding the position, read when
-    the kernel runs (graph capture / replay)."""
+    the kernel runs (graph capture / replay); rows it would place outside the
+    capacity are skipped and set ``error_flag`` (int32 device tensor) to 1."""
     packed = src.dim() == 3
     if packed:
         if src.stride(2) != 1 or src.shape[2] < sum(k.ranks):
@@ -494,6 +526,11 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
         src = src.unsqueeze(1)                       # [B, 1, T, sum(r)]: head h at a column offset
     elif src.dim() != 4 or src.stride(3) != 1:
         raise StarKVError("src must be [B, Hkv, T, r] with a contiguous last dim")
+    elif src.shape[1] < k.n_kv_heads or src.shape[3] < max(k.ranks):
+        raise StarKVError(f"src {tuple(src.shape)} holds fewer than {k.n_kv_heads} heads or "
+                          f"{max(k.ranks)} ranks")
+    if src.shape[0] > _cache_batch(k.data):
+        raise StarKVError(f"src batch {src.shape[0]} exceeds the cache's {_cache_batch(k.data)}")
     _require_cuda(src, *[t for t in (k.data, k.scale, k.data2, k.scale2) if t is not None])
     keep: list = []
     d = KAppendDesc()
@@ -505,6 +542,7 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
         keep.append(offs)
         d.src_head_offset = offs
     d.pos0_device = _pos_ptr(pos0_device)
+    d.error_flag = _flag_ptr(error_flag)
     check(_lib.lib().starkv_k_append(ctypes.byref(d), _stream(src.device)), "starkv_k_append")
 
 
@@ -517,16 +555,22 @@ def _pos_ptr(t: Optional[torch.Tensor]):
 
 
 def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int,
-             pos0_device: Optional[torch.Tensor] = None) -> None:
+             pos0_device: Optional[torch.Tensor] = None, error_flag: Optional[torch.Tensor] = None) -> None:
     """Write the new V latent rows src [B, T, Rv] (act dtype, last dim
     contiguous) into the cache described by ``v`` at positions
-    [pos0, pos0 + T), quantising to its format (starkv_v_append)."""
+    [pos0, pos0 + T), quantising to its format (starkv_v_append);
+    ``pos0_device`` / ``error_flag`` as in ``k_append``."""
     if src.dim() != 3 or src.stride(2) != 1:
         raise StarKVError("src must be [B, T, Rv] with a contiguous last dim")
+    if src.shape[2] < v.rank:
+        raise StarKVError(f"src rows hold {src.shape[2]} ranks, the cache stores {v.rank}")
+    if src.shape[0] > _cache_batch(v.data):
+        raise StarKVError(f"src batch {src.shape[0]} exceeds the cache's {_cache_batch(v.data)}")
     _require_cuda(src, *v.tensors)
     d = VAppendDesc()
     d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[1], int(pos0), int(capacity), _dt(src)
     d.src, d.src_stride_b, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1)
     d.v = v.c_struct()
     d.pos0_device = _pos_ptr(pos0_device)
+    d.error_flag = _flag_ptr(error_flag)
     check(_lib.lib().starkv_v_append(ctypes.byref(d), _stream(src.device)), "starkv_v_append")

@@ -72,18 +72,24 @@ class RopeConfig:
 
 
 _TABLES: dict = {}
+_RETIRED: list = []
 _LOCK = threading.Lock()
 
 
 def rope_table(cfg: RopeConfig, positions: int, device: torch.device):
     """Device rotation table covering at least `positions` positions, built
-    once per (config, device) by starkv_rope_build and grown by doubling."""
+    once per (config, device) by starkv_rope_build and grown by doubling.  An
+    outgrown table is retired, not freed: a captured graph keeps its address."""
     device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())    # one table per physical device
     key = (cfg, device)
     with _LOCK:
         ent = _TABLES.get(key)
         if ent is not None and ent[1] >= positions:
             return ent
+        if ent is not None:
+            _RETIRED.append(ent)
         cap = max(4096, 1 << max(0, (positions - 1)).bit_length())
         L = _lib.lib()
         nbytes = L.starkv_rope_table_bytes(cap)

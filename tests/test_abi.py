@@ -40,7 +40,11 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_status_strings():
     lib = L.lib()
-    assert lib.starkv_abi_version() == 1
+    m = re.search(r"#define\s+STARKV_ABI_VERSION\s+(\d+)", open(HEADER).read())
+    header_version = int(m.group(1))
+    # the library, the header and the ctypes mirrors must agree: a struct
+    # layout change bumps all three together
+    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 2
     for code in (OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_RANK, ERR_WORKSPACE, ERR_LIMIT, ERR_FORMAT):
         s = lib.starkv_status_string(code).decode()
         assert s and s != "unknown error"
@@ -64,8 +68,11 @@ int main(void) {
   F(starkv_decode_desc, rope_table) F(starkv_decode_desc, scale) F(starkv_decode_desc, mask) F(starkv_decode_desc, out_dtype)
   F(starkv_decode_desc, out_stride_h)
   S(starkv_k_append_desc) F(starkv_k_append_desc, k) F(starkv_k_append_desc, src_head_offset)
-  F(starkv_k_append_desc, pos0_device)
+  F(starkv_k_append_desc, pos0_device) F(starkv_k_append_desc, error_flag)
   S(starkv_v_append_desc) F(starkv_v_append_desc, v) F(starkv_v_append_desc, pos0_device)
+  F(starkv_v_append_desc, error_flag)
+  S(starkv_rope_apply_desc) F(starkv_rope_apply_desc, x) F(starkv_rope_apply_desc, rope_table)
+  F(starkv_rope_apply_desc, pos0) F(starkv_rope_apply_desc, pos0_device) F(starkv_rope_apply_desc, error_flag)
   S(starkv_prefill_desc) F(starkv_prefill_desc, pos0) F(starkv_prefill_desc, dtype) F(starkv_prefill_desc, q)
   F(starkv_prefill_desc, q_stride_t) F(starkv_prefill_desc, k) F(starkv_prefill_desc, v) F(starkv_prefill_desc, uv)
   F(starkv_prefill_desc, rope_table) F(starkv_prefill_desc, scale) F(starkv_prefill_desc, out)
@@ -77,7 +84,7 @@ int main(void) {
 _PY = {"starkv_klatent": L.KLatent, "starkv_klogits_desc": L.KLogitsDesc, "starkv_vlatent": L.VLatent,
        "starkv_pv_desc": L.PVDesc, "starkv_decode_desc": L.DecodeDesc,
        "starkv_prefill_desc": L.PrefillDesc, "starkv_k_append_desc": L.KAppendDesc,
-       "starkv_v_append_desc": L.VAppendDesc}
+       "starkv_v_append_desc": L.VAppendDesc, "starkv_rope_apply_desc": L.RopeApplyDesc}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
@@ -143,7 +150,7 @@ def test_valid_descriptor_sizes_a_workspace_and_asks_for_it():
     ("head_dim", 64, ERR_SHAPE),
     ("dtype", L.F32, ERR_DTYPE),
     ("n_q_heads", 12, ERR_SHAPE),          # not a multiple of n_kv_heads
-    ("n_q_heads", 40, ERR_LIMIT),          # P.V kernel handles up to 32 query heads
+    ("n_q_heads", 72, ERR_LIMIT),          # up to 64 query heads (two P.V head groups)
     ("q", None, ERR_NULL),
     ("uv", None, ERR_NULL),
     ("out", None, ERR_NULL),
@@ -209,8 +216,13 @@ def test_rope_build_and_pv_validation():
     need = lib.starkv_pv_latent_workspace_bytes(ctypes.byref(p))
     assert need > 0
     assert lib.starkv_pv_latent(ctypes.byref(p), None, 0, None) == ERR_WORKSPACE
-    p.n_heads = 33
-    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_LIMIT
+    # 33..64 heads take two head groups: a larger workspace; more than 64 are refused
+    p.n_heads = 40
+    need40 = lib.starkv_pv_latent_workspace_bytes(ctypes.byref(p))
+    assert need40 > need
+    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_WORKSPACE
+    p.n_heads = 65
+    assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need40, None) == ERR_LIMIT
     p.n_heads, p.p = 32, None
     assert lib.starkv_pv_latent(ctypes.byref(p), FAKE, need, None) == ERR_NULL
     # group-64 int4 rows are addressed with a 24-bit row multiply: pitches of
@@ -366,4 +378,28 @@ def test_rope_apply_validation():
     assert lib.starkv_rope_apply(ctypes.byref(d), None) == ERR_NULL
     d.x, d.dtype = FAKE, L.F32
     assert lib.starkv_rope_apply(ctypes.byref(d), None) == ERR_DTYPE
+    # one thread per (row, frequency): grids of 2^32 threads or more are refused
+    # before any launch (a device position lifts the host-side table check)
+    d.dtype, d.pos0_device = L.F16, FAKE
+    d.batch, d.n_heads, d.n_tokens = 1 << 16, 64, 1 << 10          # 2^32 * 64 / 64 threads
+    assert lib.starkv_rope_apply(ctypes.byref(d), None) == ERR_LIMIT
+
+
+def test_cache_writer_limits_and_device_positions():
+    lib = L.lib()
+    keep = []
+    # one wave per row: B * Hkv * T * 64 threads must stay below 2^32
+    d = L.KAppendDesc(batch=1 << 14, n_tokens=1 << 12, pos0=0, capacity=1 << 20, dtype=L.F16, src=FAKE,
+                      src_stride_b=0, src_stride_h=0, src_stride_t=0, k=_klatent([32] * 8, keep))
+    d.pos0_device = FAKE
+    assert lib.starkv_k_append(ctypes.byref(d), None) == ERR_LIMIT
+    v = L.VAppendDesc(batch=1 << 14, n_tokens=1 << 12, pos0=0, capacity=1 << 20, dtype=L.F16, src=FAKE,
+                      src_stride_b=0, src_stride_t=0,
+                      v=L.VLatent(rank=1024, format=L.FMT_INT4_G64, data=FAKE, stride_b=0, stride_s=512,
+                                  scale=FAKE, scale_stride_b=0, scale_stride_s=16, zero=FAKE))
+    v.pos0_device = FAKE
+    assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_LIMIT      # 2^26 rows x 16 groups x 64
+    # without a device position the host checks the capacity itself
+    v.pos0_device, v.batch, v.n_tokens, v.capacity = None, 1, 9, 8
+    assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_SHAPE
 

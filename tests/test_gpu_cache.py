@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import cfg2_ranks, errors
+from _util import cfg2_ranks, check_output, errors
 
 HEAD = 128
 
@@ -187,9 +187,9 @@ def test_quant_module_decode_matches_dequantised_history():
             core, _, _ = o.decode_attention(q, [bk[h] for h in range(Hkv)], [torch.from_numpy(kx[:, h]).double() for h in range(Hkv)],
                                             torch.from_numpy(vx).double(), m.v_proj.U.weight.double().cpu(), cos.double(), sin.double())
             ref = core.reshape(B, 1, -1) @ m.o_proj.weight.double().cpu().T
-            mx, mr = errors(out.float(), ref)
-            _flush(f"   decode t={t} S={S} max_abs={mx:.3e} mean_rel={mr:.3e}")
-            assert mr <= 1e-2
+            # o_proj is linear: the core's gates carry over to its output (the
+            # fp16 projection rounds at 2^-11, well inside them)
+            check_output(out, ref, f"decode t={t} S={S} (o_proj output): ")
 
 
 @pytest.mark.gpu

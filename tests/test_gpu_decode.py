@@ -48,6 +48,11 @@ def _check(case, ref, rope=None, mask=None):
 
 CASES = [
     # name, B, Hq, Hkv, S, ranks, Rv, dtype, layout
+    # config 1 (the CPU-baseline layer: B1, 32 x 128, S1024, r32 per head,
+    # Rv1024, seeded N(0,1) latents, B_k ~N(0,1/32), B_v ~N(0,1/1024), theta
+    # 10000) on the HIP path, its fp32 inputs cast to fp16 and to bf16
+    ("cfg1_f16", 1, 32, 32, 1024, [32] * 32, 1024, torch.float16, "reference"),
+    ("cfg1_bf16", 1, 32, 32, 1024, [32] * 32, 1024, torch.bfloat16, "reference"),
     ("mha_uniform_ref", 2, 32, 32, 1000, [32] * 32, 256, torch.float16, "reference"),
     ("mha_ragged_cfg2ranks", 2, 32, 32, 777, None, 1640, torch.float16, "ragged"),
     ("gqa4_ragged", 2, 32, 8, 1500, [32, 128, 32, 80, 32, 64, 80, 64], 512, torch.float16, "ragged"),
@@ -59,6 +64,10 @@ CASES = [
     # V wider than one P.V workgroup's 52 column tiles: several column blocks
     ("rv2048_two_blocks", 2, 32, 32, 700, [32] * 32, 2048, torch.float16, "ragged"),
     ("rv8192_max_bf16", 1, 32, 8, 300, [64] * 8, 8192, torch.bfloat16, "ragged"),
+    # more than 32 query heads: two P.V head groups (Llama-2-13B has 40 heads)
+    ("mha_hq40", 2, 40, 40, 700, [96, 56, 48, 32, 16, 88, 56, 48] * 5, 1280, torch.float16, "ragged"),
+    ("gqa_hq64_bf16", 1, 64, 8, 900, [32, 128, 32, 80, 32, 64, 80, 64], 512, torch.bfloat16, "ragged"),
+    ("mha_hq64_s33", 2, 64, 64, 33, [16, 32] * 32, 200, torch.float16, "ragged"),
 ]
 
 

@@ -9,7 +9,7 @@ import sys
 import pytest
 import torch
 
-from _util import errors
+from _util import check_logits, check_output, errors
 
 HEAD = 128
 
@@ -46,10 +46,14 @@ def test_abx_matches_oracle(dtype, Hq, Hkv, S, r, theta):
     cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), rope.attention_scaling)
     ref = o.k_logits(a[:, :, 0].cpu(), [b[h].cpu() for h in range(Hkv)], [x[:, h].cpu() for h in range(Hkv)],
                      cos, sin, scale=1.0)
-    mx, mr = errors(out[:, :, 0].float(), ref)
-    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e} ref_rms={ref.pow(2).mean().sqrt().item():.3f}")
-    tol = 8e-3 if dtype == torch.float16 else 1.6e-2     # output rounded to the act dtype
-    assert mr <= tol
+    _flush(f"   ref_rms={ref.pow(2).mean().sqrt().item():.3f}")
+    # abx returns unscaled logits in the act dtype (abx_rope_batched.py:157): gated
+    # at the softmax input's scale (bf16 against the bf16-rounded oracle) ...
+    check_logits(out[:, :, 0], ref, 1.0, "act-dtype out: ")
+    # ... and the same kernel's fp32 logits, which bf16 storage would otherwise mask
+    from starkv import KLatentSpec, k_logits
+    out32 = k_logits(a, KLatentSpec.from_reference(x, b), S, rope=rope, scale=1.0, out_dtype=torch.float32)
+    check_logits(out32, ref, 1.0, "fp32 out: ")
 
 
 # ---------------------------------------------------------------- attention module
@@ -114,8 +118,18 @@ def _module_reference(m, cfg, hidden_all, n_prefill):
 @pytest.mark.gpu
 @pytest.mark.parametrize("Hq,Hkv,r,Rv,dtype", [(4, 4, 48, 200, torch.float16), (8, 2, 64, 256, torch.bfloat16)])
 def test_attention_module_prefill_then_decode(Hq, Hkv, r, Rv, dtype):
+    """The module's attention cores (its HIP prefill and decode calls) against
+    the fp64 oracle on the same inputs -- the rotated queries and the caches
+    as the module stored them -- at max-abs 2e-2 / mean-rel 1e-3 (bf16 against
+    the bf16-rounded oracle).  For fp16 the module output (after o_proj) is
+    also held to the same gates against an fp64 re-computation of the whole
+    module from its weights (the fp16 projections round at 2^-11, well inside
+    them); in bf16 the projections' own rounding (2^-9) sets that error, so
+    only the attention cores are gated."""
+    import starkv.LlamaLoRaAttention_headwise as mod
     from transformers.cache_utils import DynamicCache
     from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    from _util import KernelRecorder
     _flush(f"[module] Hq={Hq} Hkv={Hkv} r={r} Rv={Rv} {dtype}")
     cfg, m = _module(Hq, Hkv, r, Rv, dtype)
     rot = LlamaRotaryEmbedding(config=cfg).to("cuda")
@@ -124,18 +138,18 @@ def test_attention_module_prefill_then_decode(Hq, Hkv, r, Rv, dtype):
     hidden_all = (torch.randn(B, P + n_dec, cfg.hidden_size, generator=g, device="cuda") * 0.5).to(dtype)
     ref = _module_reference(m, cfg, hidden_all, P)
     cache = DynamicCache()
-    with torch.no_grad():
+    outs = []
+    with torch.no_grad(), KernelRecorder(mod) as rec:
         pos = torch.arange(P, device="cuda")[None].expand(B, P)
         pe = rot(hidden_all[:, :P], pos)
-        out, _ = m(hidden_all[:, :P], pe, None, pos, past_key_values=cache)
-        mx, mr = errors(out.float(), ref[:, :P])
-        _flush(f"   prefill max_abs={mx:.3e} mean_rel={mr:.3e}")
-        assert mr <= 1e-2
+        outs.append(m(hidden_all[:, :P], pe, None, pos, past_key_values=cache)[0])
         for t in range(P, P + n_dec):
             pos = torch.full((B, 1), t, device="cuda")
             pe = rot(hidden_all[:, t:t + 1], pos)
-            out, _ = m(hidden_all[:, t:t + 1], pe, None, pos, past_key_values=cache)
-            torch.cuda.synchronize()
-            mx, mr = errors(out.float(), ref[:, t:t + 1])
-            _flush(f"   decode t={t} max_abs={mx:.3e} mean_rel={mr:.3e}")
-            assert mr <= 1e-2
+            outs.append(m(hidden_all[:, t:t + 1], pe, None, pos, past_key_values=cache)[0])
+    assert [c["kind"] for c in rec.calls] == ["prefill"] + ["decode"] * n_dec
+    assert rec.check() == 1 + n_dec
+    if dtype == torch.float16:
+        check_output(outs[0], ref[:, :P], "module prefill output: ")
+        for i, t in enumerate(range(P, P + n_dec)):
+            check_output(outs[1 + i], ref[:, t:t + 1], f"module decode t={t} output: ")

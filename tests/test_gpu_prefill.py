@@ -4,9 +4,11 @@ under a causal mask) against the CPU oracle's prefill_attention.
 
 Inputs are rounded to the act dtype first and the oracle runs in float64 on
 those values (quantised latents: on the oracle-dequantised fp16 values,
-rounded to bf16 for bf16 cases, as the kernel dequantises).  Tolerances:
-fp16 max-abs 2e-2 and mean-rel 1e-3; bf16 (K, V and the output each stored in
-bf16, unit roundoff 2^-9) max-abs 4e-2 and mean-rel 6e-3.
+rounded to bf16 for bf16 cases, as the kernel dequantises).  The reference
+materialises K and V in the act dtype (model.py:431-442); the kernel holds
+them in fp16 for both act dtypes (finer than bf16): the oracle rounds its
+fp64 K (after RoPE) and V once to fp16, then attends in fp64.  Gates: max-abs
+2e-2 and mean-rel 1e-3 (bf16 outputs against the bf16-rounded oracle).
 """
 import math
 import sys
@@ -15,10 +17,9 @@ import numpy as np
 import pytest
 import torch
 
-from _util import errors
+from _util import check_output, errors
 
 HEAD = 128
-TOL = {torch.float16: (2e-2, 1e-3), torch.bfloat16: (4e-2, 6e-3)}
 
 
 def _flush(msg):
@@ -86,12 +87,8 @@ def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0, r
     torch.cuda.synchronize()
     cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), rope.attention_scaling)
     ref = o.prefill_attention(q.double().cpu(), [b.double().cpu() for b in bk_heads], xk, xv, uv.double().cpu(),
-                              cos.double(), sin.double(), pos0=pos0)
-    assert torch.isfinite(out).all()
-    mx, mr = errors(out, ref)
-    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
-    tmx, tmr = TOL[dtype]
-    assert mx <= tmx and mr <= tmr, (mx, mr)
+                              cos.double(), sin.double(), pos0=pos0, kv_dtype=torch.float16)
+    check_output(out, ref)
     return out
 
 
@@ -161,3 +158,45 @@ def test_prefill_rejects_unsupported_formats():
     q = torch.zeros(1, 1, 64, HEAD, dtype=torch.float16, device="cuda")
     with pytest.raises(StarKVError, match="format"):
         prefill_attention(q, kspec, xv, uv)
+
+
+@pytest.mark.gpu
+def test_prefill_e2e_shape_sampled_rows():
+    """The e2e workload's prefill layer at full prompt length: 8192 tokens,
+    MHA 32 x 128, the cfg2 ragged K ranks (sum 1640) as int8 per (b, h, s),
+    V rank 1640 as int4 group-64, fp16, batch 2.  The whole prompt runs on the
+    GPU; sampled query rows are checked against the oracle's decode step over
+    the first t + 1 positions (a prefill row is that decode step: pinned on
+    the CPU by the oracle's chunk / last-row identities)."""
+    from oracle import starkv_oracle as o
+    from starkv import KLatentSpec, RopeConfig, prefill_attention
+    from starkv._lib import FMT_INT8_SYM
+    from test_gpu_quant import make_quant_v
+    from test_gpu_quant_k import ragged_int8_k
+    from _util import cfg2_ranks
+    B, T, Rv = 2, 8192, 1640
+    ranks = cfg2_ranks()
+    Hkv = Hq = len(ranks)
+    _flush(f"[prefill e2e shape] B={B} T={T} Hq={Hq} ranks sum {sum(ranks)} int8 K, Rv={Rv} g64 V")
+    g = torch.Generator(device="cuda").manual_seed(21)
+    bk_all, bko, bk_heads = _bk(ranks, torch.float16, g)
+    kb, scales, offs, deq_k = ragged_int8_k(B, T, ranks, seed=22)
+    sc = torch.from_numpy(scales).cuda()
+    kspec = KLatentSpec(torch.from_numpy(kb).cuda(), ranks, offs, ranks, kb.shape[1], bk_all, bko, HEAD,
+                        fmt=FMT_INT8_SYM, scale=sc, scale_stride_b=sc.stride(0), scale_stride_h=sc.stride(1))
+    vspec, deq_v, _ = make_quant_v("g64", B, T, Rv, seed=23)
+    uv = (torch.randn(Hkv * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).half()
+    q = torch.randn(B, Hq, T, HEAD, generator=g, device="cuda").half()
+    rope = RopeConfig()
+    out = prefill_attention(q, kspec, vspec, uv, rope=rope)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(T), rope.attention_scaling)
+    xv = torch.from_numpy(deq_v.astype(np.float64))
+    bk = [b.double().cpu() for b in bk_heads]
+    uvd = uv.double().cpu()
+    for b, t in [(0, 0), (1, 1), (0, 777), (1, 4095), (0, 6000), (1, T - 1)]:
+        S = t + 1
+        ref, _, _ = o.decode_attention(q[b:b + 1, :, t].double().cpu(), bk, [x[b:b + 1, :S] for x in deq_k],
+                                       xv[b:b + 1, :S], uvd, cos.double(), sin.double())
+        check_output(out[b:b + 1, :, t], ref, f"b={b} t={t}: ")

@@ -152,4 +152,4 @@ def test_bx_dropin(upper):
     ref = p.double().cpu() @ torch.from_numpy(deq).double()
     mx, mr = errors(out.float(), ref)
     _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
-    assert mr <= 1e-3
+    assert mr <= 1e-3 and mx <= 2e-2

@@ -209,6 +209,27 @@ def test_prefill_matches_causal_sdpa():
     torch.testing.assert_close(out, ref, atol=1e-10, rtol=1e-10)
 
 
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float16])
+def test_prefill_with_act_dtype_kv_matches_sdpa_on_rounded_kv(kv_dtype):
+    """kv_dtype: K and V materialised per query head by the decode pin's route,
+    rounded to the act dtype, then causal SDPA in fp64 -- and different from
+    the unrounded result by about the rounding (it does round)."""
+    q, bk, xk, xv, uv, cos, sin = _prefill_case(13)
+    B, Hq, S, _ = q.shape
+    gs = Hq // len(bk)
+    U = uv.view(len(bk), D, -1)
+    rnd = lambda t: t.to(kv_dtype).double()
+    ref = torch.stack([torch.nn.functional.scaled_dot_product_attention(
+        q[:, qh], rnd(o.apply_rope(xk[qh // gs] @ bk[qh // gs], cos, sin)), rnd(xv @ U[qh // gs].t()),
+        is_causal=True) for qh in range(Hq)], dim=1)
+    out = o.prefill_attention(q, bk, xk, xv, uv, cos, sin, kv_dtype=kv_dtype)
+    torch.testing.assert_close(out, ref, atol=1e-10, rtol=1e-10)
+    exact = o.prefill_attention(q, bk, xk, xv, uv, cos, sin)
+    rel = float((out - exact).abs().mean() / exact.abs().mean())
+    unit = 2.0 ** -9 if kv_dtype == torch.bfloat16 else 2.0 ** -12
+    assert unit / 50 < rel < unit * 4, rel
+
+
 def test_prefill_chunk_and_last_query_agree_with_full_and_decode():
     """Queries at positions pos0.. see what they see in a full prefill
     (chunked prefill), and the last query's row is the decode step."""
