@@ -13,8 +13,11 @@ B_v up-projection -- the scope of the reference's "attention us/layer"
 Prints ONE JSON line.  value = algorithmic HBM bytes of the step / step time
 (GB/s); roofline = the dominant kernel against MI355X's 8 TB/s HBM;
 cpu_baseline = the reference's eager PyTorch decode path restated op for op
-(oracle/starkv_oracle.py), timed on this host's cores on batch 1 of the same
-workload.
+(oracle/starkv_oracle.py), timed on this host's cores at config 1 (the
+CPU-baseline layer), with the same restatement on batch 1 of the cfg2
+workload as an extra key.  The default run then measures the metric's second
+half, e2e decode tok/s (the e2e workload below), and adds it to the line
+(``e2e_decode_tok_s`` and ``e2e``; ``--no-e2e`` skips it).
 """
 import argparse
 import json
@@ -45,23 +48,70 @@ def algorithmic_bytes(case):
     return {"k_logits": xk + bk + q, "pv_latent": xv, "up_proj": uv + out, "total": xk + xv + bk + uv + q + out}
 
 
-def cpu_baseline(case_cpu_fn, reps):
-    """Time the oracle's eager restatement of the reference decode path."""
+def cpu_baseline(case_cpu_fn, reps, warmup=3, min_reps=20, budget_s=15.0):
+    """Time the oracle's eager restatement of the reference decode path on
+    this host's cores: ``warmup`` untimed calls, then at least ``min_reps``
+    timed ones (more while the time budget lasts, up to ``reps``); returns
+    (median seconds, os.cpu_count(), torch.get_num_threads(), reps timed)."""
     import torch
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     fn = case_cpu_fn()
-    for _ in range(2):
+    for _ in range(warmup):
         fn()
     ts = []
-    t_end = time.perf_counter() + 15.0
-    for _ in range(reps):
+    t_end = time.perf_counter() + budget_s
+    for _ in range(max(reps, min_reps)):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end:
+        if len(ts) >= min_reps and time.perf_counter() > t_end:
             break
     return statistics.median(ts), threads, torch.get_num_threads(), len(ts)
+
+
+def cfg1_inputs():
+    """Config 1, the CPU-baseline layer: batch 1, 32
+    heads x 128, context 1024, K rank 32 per head, V rank 1024, fp32, seed 0.
+    Latents and q ~N(0,1), B_k [32 x 128] per head ~N(0,1/32), B_v
+    [1024 x 4096] ~N(0,1/1024) (U_v = v_proj.U.weight = B_v^T), theta 10000.
+    Returns the oracle's decode arguments and the algorithmic bytes."""
+    import torch
+    from oracle import starkv_oracle as o
+    g = torch.Generator().manual_seed(0)
+    B, H, S, r, Rv = 1, 32, 1024, 32, 1024
+    q = torch.randn(B, H, HEAD_DIM, generator=g)
+    xk = [torch.randn(B, S, r, generator=g) for _ in range(H)]
+    bk = [torch.randn(r, HEAD_DIM, generator=g) / math.sqrt(r) for _ in range(H)]
+    xv = torch.randn(B, S, Rv, generator=g)
+    bv = torch.randn(Rv, H * HEAD_DIM, generator=g) / math.sqrt(Rv)
+    uv = bv.t().contiguous()
+    cos, sin = o.rope_cos_sin(o.rope_inv_freq(10000.0), torch.arange(S))
+    nbytes = 4 * (B * S * H * r + B * S * Rv + H * r * HEAD_DIM + Rv * H * HEAD_DIM + 2 * B * H * HEAD_DIM)
+    return (q, bk, xk, xv, uv, cos, sin), nbytes
+
+
+def cfg1_cpu_baseline(reps):
+    """The reference's eager decode path (abx_rope_batched.py:189-202 with
+    per-position RoPE, model.py:458-487) restated op for op by the oracle,
+    fp32 on this host, at config 1."""
+    import torch
+    from oracle import starkv_oracle as o
+    args, nbytes = cfg1_inputs()
+
+    def make_fn():
+        def fn():
+            with torch.no_grad():
+                o.decode_attention(*args, dtype=torch.float32)
+        return fn
+
+    med, cores, nthreads, n = cpu_baseline(make_fn, reps)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "host_cpus": cores, "torch_threads": nthreads, "us_per_layer": round(med * 1e6, 1),
+            "sample": f"config 1 (B1, 32 heads x 128, S1024, K rank 32/head, V rank 1024, fp32, seed 0): the "
+                      f"reference eager decode path restated op for op (oracle.starkv_oracle.decode_attention: "
+                      f"X_k B_k, per-position RoPE, q K^T / sqrt(128), fp32 softmax, P X_v, U_v), 3 warm-ups, "
+                      f"median of {n} reps; value = algorithmic bytes ({nbytes}) / median time"}
 
 
 def build_workload(name, dev):
@@ -162,7 +212,7 @@ def build_workload(name, dev):
     raise SystemExit(f"unknown workload {name!r}")
 
 
-def run_e2e(args):
+def run_e2e(args, emit=True):
     """End-to-end decode (the e2e configuration): random-init 32-layer
     Llama-2-7B-shaped model (vocab 32000, MLP 11008, fp16), every attention on
     the latent cache (cfg3 ranks and formats: K int8, V int4-g64), prefill 8192
@@ -230,7 +280,10 @@ def run_e2e(args):
         "eager_attention_share": round(attn_s / (eager_wall / n_eager), 4),
         "prefill_s": round(t_prefill, 3), "build_s": round(t_build, 1),
     }
-    print(json.dumps(rec), flush=True)
+    del model
+    if emit:
+        print(json.dumps(rec), flush=True)
+    return rec
 
 
 MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 / bf16 MFMA
@@ -404,6 +457,8 @@ def main():
                          "prefill (one layer's 8192-token causal prefill at batch 8 over the int8 / int4-g64 "
                          "latent cache; prints TFLOP/s against the MFMA roofline)")
     ap.add_argument("--e2e-steps", type=int, default=256)
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="default workload: skip the e2e decode measurement that follows the layer measurement")
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run three 1 GiB device-to-device copies (the known-size reference for rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE per dispatch) and exit")
@@ -502,9 +557,10 @@ def main():
         except torch.cuda.OutOfMemoryError:
             torch_ref_us = None
 
-    cpu = None
+    cpu = cpu_b1 = None
     if not args.no_cpu_baseline and args.workload == "cfg2":
         from oracle import starkv_oracle as o
+        cpu = cfg1_cpu_baseline(10 * args.cpu_reps)      # ~10 ms per rep: about 10 s of CPU work
 
         def make_fn():
             c = {
@@ -523,7 +579,7 @@ def main():
 
         med, cores, nthreads, n = cpu_baseline(make_fn, args.cpu_reps)
         cpu_bytes = nbytes["total"] / B
-        cpu = {"value": round(cpu_bytes / med / 1e9, 3), "unit": "GB/s", "cores": nthreads,
+        cpu_b1 = {"value": round(cpu_bytes / med / 1e9, 3), "unit": "GB/s", "cores": nthreads,
                "kind": "port", "host_cpus": cores, "us_per_layer_b1": round(med * 1e6, 1),
                "sample": f"cfg2 workload batch 1 of {B} (S={S}), fp32 torch eager restatement of the reference "
                          f"decode path (oracle.starkv_oracle.decode_attention), median of {n} reps"}
@@ -552,7 +608,20 @@ def main():
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "torch_reference_gpu_us": round(torch_ref_us, 1) if torch_ref_us else None,
         "cpu_baseline": cpu,
+        "cpu_baseline_cfg2_b1": cpu_b1,
     }
+    if args.workload == "cfg2" and not args.no_e2e:
+        # the metric's second half: e2e decode tok/s (the e2e workload), in the
+        # same process after the layer measurement
+        del case, wl, step
+        import gc
+        gc.collect()
+        torch.cuda.empty_cache()
+        e2e = run_e2e(args, emit=False)
+        rec["e2e_decode_tok_s"] = e2e["value"]
+        rec["e2e"] = {k: e2e[k] for k in ("ms_per_decode_step", "eager_ms_per_decode_step",
+                                          "eager_attention_ms_per_decode_step", "eager_attention_share",
+                                          "prefill_s", "steps", "config")}
     print(json.dumps(rec), flush=True)
 
 

@@ -263,6 +263,7 @@ int starkv_decode_attention(const starkv_decode_desc* d, void* workspace, size_t
 int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes,
                                   void* stream, void* const* events);
 
+
 /* ---------------------------------------------------------------------
  * Latent-cache writers.  Quantise (or copy) n_tokens new latent rows into a
  * preallocated cache at positions [pos0, pos0 + n_tokens), in place.

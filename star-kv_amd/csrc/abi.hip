@@ -328,9 +328,9 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
 int head_groups(int H) { return (int)ceil_div(H, 32); }   // P.V passes of 32 heads
 
 struct DecodeLayout {
-  int S_pad, n_c1, tiles_per_chunk, n_hg, n_sl;
+  int S_pad, n_c1, tiles_per_chunk, n_hg, sw, n_sl;
   PVGeom pv;
-  size_t off_logits, off_cmax, off_part, off_psum, off_ctr, off_ypart, total;
+  size_t off_logits, off_cmax, off_part, off_psum, off_ypart, total;
 };
 
 DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes) {
@@ -342,7 +342,8 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
   L.n_hg = head_groups(Hq);
   L.pv = pv_geometry(B * L.n_hg, S, Rv, true, vq, v_row_bytes);
-  L.n_sl = (int)ceil_div(Rv, UP_SW);
+  L.sw = up_slice_width(Hkv, Rv);
+  L.n_sl = (int)ceil_div(Rv, L.sw);
   const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
   const size_t BQ = (size_t)B * L.n_hg;
   size_t o = 0;
@@ -350,7 +351,6 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
   L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * 4);
   L.off_psum = o; o = a256(o + BQ * n_c2 * 32 * 4);
-  L.off_ctr = o; o = a256(o + (size_t)Hkv * 4);
   L.off_ypart = o; o = a256(o + (size_t)Hkv * L.n_sl * ((size_t)B * (Hq / Hkv)) * HEAD_DIM * 4);
   L.total = o;
   return L;
@@ -645,7 +645,6 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = ka.o_sb; pa.l_st = ka.o_st; pa.l_sh = ka.o_sh;
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
-  pa.ctr = (int*)(ws + L.off_ctr); pa.n_ctr = d->k.n_kv_heads;
   pa.S = d->seq_len; pa.H = Hq; pa.n_hg = L.n_hg; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
   pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;
   if ((st = launch_pv(pa, d->dtype, vq, true, v_fast(d->v), B, s))) return st;
@@ -656,7 +655,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   ua.uv = d->uv; ua.uv_rs = d->uv_row_stride;
   ua.out = d->out; ua.o_sb = d->out_stride_b; ua.o_sh = d->out_stride_h;
   ua.B = B; ua.Hq = Hq; ua.gs = gs; ua.Rv = d->v.rank;
-  ua.n_sl = L.n_sl; ua.ypart = (float*)(ws + L.off_ypart); ua.ctr = pa.ctr;
+  ua.sw = L.sw; ua.n_sl = L.n_sl; ua.ypart = (float*)(ws + L.off_ypart);
   ua.out_f32 = d->out_dtype == STARKV_F32;
   const bool ufast = al(d->uv, 16) && al64(d->uv_row_stride * 2, 16);
   if ((st = launch_up_proj(ua, d->dtype, ufast, s))) return st;
@@ -673,6 +672,7 @@ int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, 
   if (!events || !events[0] || !events[1] || !events[2] || !events[3]) return STARKV_ERR_NULL;
   return decode_impl(d, workspace, workspace_bytes, stream, events);
 }
+
 
 int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
   if (!d) return STARKV_ERR_NULL;

@@ -91,12 +91,11 @@ struct PVArgs {
   const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
   int p_vec;                                       // drop-in: P rows allow 16-byte loads
-  // bq = b * n_hg + head group (32 heads each) indexes the partials
-  float* part;                                     // [B*n_hg][n_c2][32][Rvp] fp32
+  // bq = b * n_hg + head group (32 heads each)
+  float* part;                                     // [bq][n_c2][32][Rvp] fp32
   float* psum;                                     // fused: [B*n_hg][n_c2][32] softmax partial sums
   float* part2; int n_grp;                         // drop-in two-level reduction: [B*n_hg][n_grp][32][Rvp]
   void* out; int64_t o_sb, o_sh;                   // drop-in: act-dtype [B][H][Rv]
-  int* ctr; int n_ctr;                             // fused: the up-projection's arrival counters, zeroed here
   int S, H, n_hg, Rv, Rvp, n_cb, n_c2, c2_len;
 };
 
@@ -143,12 +142,10 @@ struct UPArgs {
   const void* uv; int64_t uv_rs;                   // [Hkv*128][Rv]
   void* out; int64_t o_sb, o_sh;                   // [B][Hq][128]
   int B, Hq, gs, Rv;
-  int n_sl;                                        // column slices of the V rank (UP_SW columns each)
+  int sw, n_sl;                                    // column slices of the V rank (sw columns each)
   float* ypart;                                    // [Hkv][n_sl][B*gs][128] partial up-projections
-  int* ctr;                                        // [Hkv] arrival counters, zero on entry
   int out_f32;                                     // 1: fp32 output, 0: weight dtype
 };
-constexpr int UP_SW = 64;                          // V-rank columns per up-projection workgroup
 
 // ---------------------------------------------------------------------------
 // In-place RoPE of query rows (rope.hip).
@@ -285,6 +282,7 @@ int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ran
 // dense variants (8 and 13 tiles) take one, the others two
 constexpr int pv_wg_per_cu(int ntw, int vq) { return ntw >= 8 && vq == VQ_DENSE ? 1 : 2; }
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
+int up_slice_width(int n_kv, int Rv);                 // V-rank columns per up-projection workgroup
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);

@@ -168,8 +168,6 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
     if (j == 0) Ms[q] = h0 + q < H ? m : 0.f;
-    // the up-projection's arrival counters start at zero (it runs after this kernel)
-    if (a.ctr != nullptr && blockIdx.x == 0 && bq == 0 && tid < a.n_ctr) a.ctr[tid] = 0;
     __syncthreads();
   }
   const float Mq = FUSED ? Ms[n] : 0.f;
@@ -423,7 +421,8 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     }
   }
 
-  // ---- this chunk's partial sums: D[row q][col] -> part[b][c2][q][col]
+  // ---- this chunk's partial sums: D[row q][col] -> part[bq][c2][q][col] (one
+  // contiguous 32 x Rvp block per workgroup row of the grid)
   const int Rvp = a.Rvp;
   float* part = a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
 #pragma unroll

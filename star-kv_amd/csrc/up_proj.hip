@@ -1,87 +1,124 @@
 // K3: split-S reduction, softmax normalisation and per-head up-projection on
-// gfx950, in one launch.
+// gfx950.
 //
 // Replaces model.py:485-487 (v_u.weight viewed [Hkv, 128, Rv], repeated per
 // query-head group, out = prob_v @ U^T) together with the sum over the P.V
 // kernel's position chunks:
 //     out[b, q, d] = (1 / L[b,q]) * sum_j U_v[kv*128 + d][j] * sum_c part_c[b, q, j]
 //     L[b, q] = sum_c psum_c[b, q]
-// Workgroup = (slice of UP_SW V-rank columns, KV head kv).  Its rows are the
-// M = B * gs (batch, query head of kv's group) pairs.  It sums the chunk
-// partials of its columns in fixed chunk order into LDS, multiplies them by
-// its U_v columns (fp32, the weights converted exactly) and writes the
-// [M][128] partial up-projection of its slice.  The workgroup that completes
-// a KV head last (an arrival counter per KV head, zeroed by the P.V kernel
-// that runs before) adds the slices in slice order and divides by L, so the
-// result does not depend on which workgroup arrives last: the output is
-// deterministic, with no float atomics and no second launch.  Nothing waits
-// on another workgroup.
+// up_proj_kernel: workgroup = (slice of SW V-rank columns, KV head kv); its
+// rows are the M = B * gs (batch, query head of kv's group) pairs.  It sums
+// the chunk partials of its columns in fixed chunk order into LDS, multiplies
+// them by its U_v columns (fp32; the weights convert exactly) and writes the
+// [M][128] partial up-projection of its slice.  up_finish_kernel adds the
+// slices in slice order and divides by L, one thread per output element.
+// Every sum runs in a fixed order: the output is deterministic, with no
+// atomics.
+//
+// Both kernels move a few MB and are latency-bound, so each thread issues
+// its loads in batches of up to 64 independent addresses and adds them
+// afterwards in their fixed order.
 #include "common.hpp"
 
 namespace starkv {
 
-constexpr int UP_MB = 64;          // rows per LDS block
+constexpr int UP_MB = 32;          // rows per LDS block
+constexpr int UP_CB = 16;          // chunk partials loaded per row and batch
+constexpr int UP_RB = 4;           // rows per thread and batch
 
-template <typename WT, typename OT, bool FAST>
+// sum of n values p[0], p[stride], ... in index order, UP_CB loads in flight
+__device__ inline float sum_strided(const float* p, int64_t stride, int n) {
+  float s = 0.f;
+  for (int c = 0; c < n; c += UP_CB) {
+    float v[UP_CB];
+#pragma unroll
+    for (int k = 0; k < UP_CB; ++k) v[k] = p[min(c + k, n - 1) * stride];
+#pragma unroll
+    for (int k = 0; k < UP_CB; ++k)
+      if (c + k < n) s += v[k];
+  }
+  return s;
+}
+
+template <typename WT, int SW, bool FAST>
 __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
-  __shared__ float os[UP_MB][UP_SW + 4];
-  __shared__ float Ls[UP_MB];
-  __shared__ int is_last;
+  constexpr int JT = 256 / SW;                     // rows summed side by side
+  __shared__ float os[UP_MB][SW + 4];
   const int tid = threadIdx.x;
   const int sl = blockIdx.x, kv = blockIdx.y;
   const int gs = a.gs, M = a.B * gs;
-  const int j0 = sl * UP_SW, nj = min(UP_SW, a.Rv - j0);   // valid columns of the slice
+  const int j0 = sl * SW, nj = min(SW, a.Rv - j0);        // valid columns of the slice
   const int64_t cstr = (int64_t)32 * a.Rvp;               // next chunk's partials
 
-  // this thread's U_v row (d) over the slice, in fp32
+  // this thread's U_v row (d) over the slice, raw; converted to fp32 after
+  // the first batch of chunk partials is in flight
   const int d = tid & (HEAD_DIM - 1), mh = tid >> 7;
-  float u[UP_SW];
   const WT* urow = (const WT*)a.uv + (int64_t)(kv * HEAD_DIM + d) * a.uv_rs + j0;
-  if (FAST && nj == UP_SW) {
+  uint4 uraw[SW / 8];
+  if (FAST && nj == SW) {
 #pragma unroll
-    for (int k = 0; k < UP_SW / 8; ++k) {
-      const uint4 w = *(const uint4*)(urow + 8 * k);
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        u[8 * k + 2 * e] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] & 0xffffu)));
-        u[8 * k + 2 * e + 1] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] >> 16)));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < UP_SW; ++j) u[j] = j < nj ? to_f32(urow[j]) : 0.f;
+    for (int k = 0; k < SW / 8; ++k) uraw[k] = *(const uint4*)(urow + 8 * k);
   }
+  float u[SW];
+  bool u_ready = false;
+  auto load_u = [&]() __attribute__((always_inline)) {
+    if (u_ready) return;
+    u_ready = true;
+    if (FAST && nj == SW) {
+#pragma unroll
+      for (int k = 0; k < SW / 8; ++k) {
+        const uint32_t ww[4] = {uraw[k].x, uraw[k].y, uraw[k].z, uraw[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          u[8 * k + 2 * e] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] & 0xffffu)));
+          u[8 * k + 2 * e + 1] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] >> 16)));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < SW; ++j) u[j] = j < nj ? to_f32(urow[j]) : 0.f;
+    }
+  };
 
   float* yp = a.ypart + ((int64_t)kv * a.n_sl + sl) * M * HEAD_DIM;
+  const int jj = tid % SW, mr = tid / SW;
+  const int jc = j0 + min(jj, nj - 1);                    // columns past the slice re-read its last
   for (int m0 = 0; m0 < M; m0 += UP_MB) {
     const int mb = min(UP_MB, M - m0);
-    // chunk sums of rows m0 .. m0+mb over the slice's columns
-    for (int e = tid; e < mb * UP_SW; e += 256) {
-      const int mm = e / UP_SW, jj = e % UP_SW;
-      const int m = m0 + mm, q = kv * gs + m % gs;
-      const int bq = (m / gs) * a.n_hg + (q >> 5);
-      float s = 0.f;
-      if (jj < nj) {
-        const float* p = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + j0 + jj;
-        int c = 0;
-        for (; c + 8 <= a.n_c2; c += 8) {
-          float v[8];
+    // chunk sums of rows m0 .. m0+mb over the slice's columns: UP_RB rows
+    // per thread at a time, UP_CB chunks each (rows past mb re-read row mb-1)
+    for (int mm0 = mr; mm0 < mb; mm0 += JT * UP_RB) {
+      const float* p[UP_RB];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) v[k] = p[(c + k) * cstr];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) s += v[k];
-        }
-        for (; c < a.n_c2; ++c) s += p[c * cstr];
+      for (int r = 0; r < UP_RB; ++r) {
+        const int m = m0 + min(mm0 + JT * r, mb - 1), q = kv * gs + m % gs;
+        const int bq = (m / gs) * a.n_hg + (q >> 5);
+        p[r] = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
       }
-      os[mm][jj] = s;
+      float s[UP_RB] = {};
+      for (int c = 0; c < a.n_c2; c += UP_CB) {
+        float v[UP_RB][UP_CB];
+#pragma unroll
+        for (int r = 0; r < UP_RB; ++r)
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k) v[r][k] = p[r][min(c + k, a.n_c2 - 1) * cstr];
+#pragma unroll
+        for (int r = 0; r < UP_RB; ++r)
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k)
+            if (c + k < a.n_c2) s[r] += v[r][k];
+      }
+#pragma unroll
+      for (int r = 0; r < UP_RB; ++r)
+        if (mm0 + JT * r < mb) os[mm0 + JT * r][jj] = jj < nj ? s[r] : 0.f;
     }
+    load_u();
     __syncthreads();
     // partial up-projection of the slice: two rows per pass (one per half block)
     for (int mm = mh; mm < mb; mm += 2) {
       float y[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < UP_SW; j += 4) {
+      for (int j = 0; j < SW; j += 4) {
         const float4 o4 = *(const float4*)&os[mm][j];
         y[0] = fmaf(u[j], o4.x, y[0]);
         y[1] = fmaf(u[j + 1], o4.y, y[1]);
@@ -92,62 +129,50 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
     }
     __syncthreads();
   }
-
-  // arrival: the last slice of this KV head finishes the head
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&a.ctr[kv], 1) == a.n_sl - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const float* y0 = a.ypart + (int64_t)kv * a.n_sl * M * HEAD_DIM;
-  const int64_t sstr = (int64_t)M * HEAD_DIM;             // next slice
-  for (int m0 = 0; m0 < M; m0 += UP_MB) {
-    const int mb = min(UP_MB, M - m0);
-    if (tid < mb) {
-      const int m = m0 + tid, q = kv * gs + m % gs;
-      const int bq = (m / gs) * a.n_hg + (q >> 5);
-      const float* ps = a.psum + (int64_t)bq * a.n_c2 * 32 + (q & 31);
-      float L = 0.f;
-      for (int c = 0; c < a.n_c2; ++c) L += ps[c * 32];
-      Ls[tid] = 1.0f / L;
-    }
-    __syncthreads();
-    for (int mm = mh; mm < mb; mm += 2) {
-      const float* yr = y0 + (int64_t)(m0 + mm) * HEAD_DIM + d;
-      float s = 0.f;
-      int k = 0;
-      for (; k + 8 <= a.n_sl; k += 8) {
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = yr[(k + e) * sstr];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s += v[e];
-      }
-      for (; k < a.n_sl; ++k) s += yr[k * sstr];
-      const int m = m0 + mm, b = m / gs, q = kv * gs + m % gs;
-      ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s * Ls[mm]);
-    }
-    __syncthreads();
-  }
-  if (tid == 0) a.ctr[kv] = 0;
 }
 
-template <typename WT, typename OT>
-static void launch_up_t(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
-  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, OT, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((up_proj_kernel<WT, OT, false>), grid, dim3(256), 0, st, a);
+// Sum of the slices' partial up-projections in slice order, times 1 / L.
+// One thread per output element (row m of KV head kv, dim d).
+template <typename OT>
+__global__ __launch_bounds__(256) void up_finish_kernel(const UPArgs a) {
+  const int gs = a.gs, M = a.B * gs;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int n_kv = a.Hq / gs;
+  if (e >= (int64_t)n_kv * M * HEAD_DIM) return;
+  const int d = (int)(e % HEAD_DIM), m = (int)((e / HEAD_DIM) % M), kv = (int)(e / ((int64_t)HEAD_DIM * M));
+  const int q = kv * gs + m % gs, b = m / gs;
+  const int bq = b * a.n_hg + (q >> 5);
+  const float L = sum_strided(a.psum + (int64_t)bq * a.n_c2 * 32 + (q & 31), 32, a.n_c2);
+  const float s = sum_strided(a.ypart + ((int64_t)kv * a.n_sl * M + m) * HEAD_DIM + d, (int64_t)M * HEAD_DIM, a.n_sl);
+  ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s / L);
 }
+
+template <typename WT, int SW>
+static void launch_up_sw(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
+  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false>), grid, dim3(256), 0, st, a);
+}
+
+template <typename WT>
+static void launch_up_t(const UPArgs& a, bool fast, hipStream_t st) {
+  const dim3 grid(a.n_sl, a.Hq / a.gs);
+  if (a.sw == 64) launch_up_sw<WT, 64>(a, fast, grid, st);
+  else launch_up_sw<WT, 32>(a, fast, grid, st);
+}
+
+// slice width: 64 columns when that still gives >= 256 workgroups, else 32
+int up_slice_width(int n_kv, int Rv) { return (int64_t)n_kv * ceil_div(Rv, 64) >= 256 ? 64 : 32; }
 
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st) {
-  const dim3 grid(a.n_sl, a.Hq / a.gs);
-  if (dtype == STARKV_F16) {
-    if (a.out_f32) launch_up_t<_Float16, float>(a, fast, grid, st);
-    else launch_up_t<_Float16, _Float16>(a, fast, grid, st);
-  } else {
-    if (a.out_f32) launch_up_t<__bf16, float>(a, fast, grid, st);
-    else launch_up_t<__bf16, __bf16>(a, fast, grid, st);
-  }
+  if (dtype == STARKV_F16) launch_up_t<_Float16>(a, fast, st);
+  else launch_up_t<__bf16>(a, fast, st);
+  int e = (int)hipGetLastError();
+  if (e) return e;
+  const int64_t n = (int64_t)(a.Hq / a.gs) * a.B * a.gs * HEAD_DIM;
+  const dim3 grid((unsigned)ceil_div(n, 256));
+  if (a.out_f32) hipLaunchKernelGGL(up_finish_kernel<float>, grid, dim3(256), 0, st, a);
+  else if (dtype == STARKV_F16) hipLaunchKernelGGL(up_finish_kernel<_Float16>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(up_finish_kernel<__bf16>, grid, dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 
