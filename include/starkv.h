@@ -263,6 +263,20 @@ int starkv_decode_attention(const starkv_decode_desc* d, void* workspace, size_t
 int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes,
                                   void* stream, void* const* events);
 
+/* ---------------------------------------------------------------------
+ * starkv_decode_attention_noalloc — no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the same decode as
+ * starkv_decode_attention with the same descriptor and results, but its
+ * workspace is a device array of STARKV_NOALLOC_SCRATCH_BYTES inside the
+ * library, which each GPU the library runs on holds until the process ends.
+ * Descriptors whose starkv_decode_workspace_bytes exceeds that size return
+ * STARKV_ERR_LIMIT (B16 S32768 with the Llama-2-7B shape needs 123 MiB).
+ * Runs on the current device (the stream must belong to it); calls that
+ * overlap on one GPU share the array and race -- order them on one stream.
+ * ------------------------------------------------------------------- */
+#define STARKV_NOALLOC_SCRATCH_BYTES (128u << 20)
+int starkv_decode_attention_noalloc(const starkv_decode_desc* d, void* stream);
 
 /* ---------------------------------------------------------------------
  * Latent-cache writers.  Quantise (or copy) n_tokens new latent rows into a

@@ -4,6 +4,7 @@
 // before any HIP call so that every argument error is reported without a GPU.
 #include <algorithm>
 #include <climits>
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
@@ -673,6 +674,55 @@ int starkv_decode_attention_timed(const starkv_decode_desc* d, void* workspace, 
   return decode_impl(d, workspace, workspace_bytes, stream, events);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the workspace is a file-scope device array of
+// STARKV_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds until
+// the process ends.  Its device address is looked up once per device (the
+// array's name is only a host-side stand-in) and kept; calls on one GPU share
+// it, so calls that overlap on one GPU race.  The decode kernels write every
+// workspace element they read (nothing needs clearing between calls).
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __align__(256) char scratch[STARKV_NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// the current device's address of `scratch` (looked up on its first use)
+int scratch_address(void** out) {
+  int dev = 0;
+  int st = (int)hipGetDevice(&dev);
+  if (st) return st;
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return STARKV_ERR_LIMIT;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if ((st = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))) return st;
+    if (!p) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return STARKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int starkv_decode_attention_noalloc(const starkv_decode_desc* d, void* stream) {
+  int gs = 0, n_wg = 0, vq = 0, st;
+  if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
+  const size_t need =
+      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v)).total;
+  if (need > (size_t)STARKV_NOALLOC_SCRATCH_BYTES) return STARKV_ERR_LIMIT;
+  void* ws = nullptr;
+  if ((st = scratch_address(&ws))) return st;
+  return decode_impl(d, ws, STARKV_NOALLOC_SCRATCH_BYTES, stream, nullptr);
+}
 
 int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
   if (!d) return STARKV_ERR_NULL;

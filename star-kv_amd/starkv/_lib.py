@@ -158,11 +158,13 @@ EXPORTS = (
     "starkv_k_logits_workspace_bytes", "starkv_k_logits",
     "starkv_pv_latent_workspace_bytes", "starkv_pv_latent",
     "starkv_decode_workspace_bytes", "starkv_decode_attention", "starkv_decode_attention_timed",
+    "starkv_decode_attention_noalloc",
     "starkv_k_append", "starkv_v_append",
     "starkv_prefill_workspace_bytes", "starkv_prefill_attention", "starkv_prefill_attention_timed",
 )
 
 ABI_VERSION = 2          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
+NOALLOC_SCRATCH_BYTES = 128 << 20   # STARKV_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 
@@ -200,6 +202,8 @@ def lib() -> ctypes.CDLL:
     L.starkv_prefill_attention_timed.restype = ctypes.c_int
     L.starkv_prefill_attention_timed.argtypes = [ctypes.POINTER(PrefillDesc), ctypes.c_void_p, ctypes.c_size_t,
                                                  ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    L.starkv_decode_attention_noalloc.restype = ctypes.c_int
+    L.starkv_decode_attention_noalloc.argtypes = [ctypes.POINTER(DecodeDesc), ctypes.c_void_p]
     L.starkv_rope_apply.restype = ctypes.c_int
     L.starkv_rope_apply.argtypes = [ctypes.POINTER(RopeApplyDesc), ctypes.c_void_p]
     L.starkv_k_append.restype = ctypes.c_int

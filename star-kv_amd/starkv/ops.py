@@ -361,10 +361,13 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
                      rope: RopeConfig = RopeConfig(), seq_len: Optional[int] = None,
                      mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                      out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
-                     events: Optional[Sequence] = None) -> torch.Tensor:
+                     events: Optional[Sequence] = None, noalloc: bool = False) -> torch.Tensor:
     """Fused decode attention core (model.py:450-487): [B, Hq, 128] in q's dtype
     (or float32 with out_dtype=torch.float32).  ``events``: four
     torch.cuda.Event recorded around the three kernels (timing).
+    ``noalloc``: run starkv_decode_attention_noalloc, whose workspace is the
+    library's own device array (no workspace allocation; with ``out`` given
+    the call allocates nothing at all).
 
     q: rotated query [B, Hq, 128]; k: key-latent spec; xv: V latent [B, S, Rv]
     (dense tensor) or a VLatentSpec; uv_weight: v_proj.U.weight [Hkv*128, Rv];
@@ -399,6 +402,11 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     d.out, d.out_stride_b, d.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
     d.out_dtype = F32 if out.dtype == torch.float32 else 0
     L = _lib.lib()
+    if noalloc:
+        if events is not None:
+            raise StarKVError("the allocation-free decode has no timed form")
+        check(L.starkv_decode_attention_noalloc(ctypes.byref(d), _stream(q.device)), "starkv_decode_attention_noalloc")
+        return out
     nb = L.starkv_decode_workspace_bytes(ctypes.byref(d))
     if nb == 0:
         # re-run validation through the call itself to surface the status code

@@ -133,6 +133,24 @@ def _call(d, ws=None, nbytes=0):
     return L.lib().starkv_decode_attention(ctypes.byref(d), ws, nbytes, None)
 
 
+def test_noalloc_decode_refuses_workspaces_beyond_its_array():
+    """starkv_decode_attention_noalloc validates like the workspace entry point
+    and refuses, before touching a device, any descriptor whose workspace
+    would not fit its fixed device array."""
+    lib = L.lib()
+    assert lib.starkv_decode_attention_noalloc(None, None) == ERR_NULL
+    keep = []
+    d = _decode_desc(keep, B=32, Hq=32, Hkv=32, S=32768, Rv=1640)
+    d.rope_max_positions = 1 << 16
+    need = lib.starkv_decode_workspace_bytes(ctypes.byref(d))
+    assert need > L.NOALLOC_SCRATCH_BYTES
+    assert lib.starkv_decode_attention_noalloc(ctypes.byref(d), None) == ERR_LIMIT
+    d.head_dim = 64
+    assert lib.starkv_decode_attention_noalloc(ctypes.byref(d), None) == ERR_SHAPE
+    m = re.search(r"#define\s+STARKV_NOALLOC_SCRATCH_BYTES\s+\((\d+)u << (\d+)\)", open(HEADER).read())
+    assert int(m.group(1)) << int(m.group(2)) == L.NOALLOC_SCRATCH_BYTES
+
+
 def test_valid_descriptor_sizes_a_workspace_and_asks_for_it():
     keep = []
     d = _decode_desc(keep)
