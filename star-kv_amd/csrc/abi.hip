@@ -147,24 +147,133 @@ int ws_row_chunks(const starkv_klatent& k, int h) {
   return k.format == STARKV_FMT_INT8_SYM ? (int)ceil_div(k.rank[h], 16) : k.rank[h] / 8;
 }
 
+// First-fit decreasing of heads hs (u[h] units each) into at most nb bins of
+// cap units; false if they do not fit.
+static bool ffd_bins(std::vector<int> hs, const std::vector<int>& u, int nb, int cap,
+                     std::vector<std::vector<int>>* out) {
+  std::stable_sort(hs.begin(), hs.end(), [&](int x, int y) { return u[x] > u[y]; });
+  std::vector<std::vector<int>> bins;
+  std::vector<int> load;
+  for (int h : hs) {
+    size_t i = 0;
+    while (i < bins.size() && load[i] + u[h] > cap) ++i;
+    if (i == bins.size()) {
+      if ((int)bins.size() == nb) return false;
+      bins.emplace_back();
+      load.push_back(0);
+    }
+    bins[i].push_back(h);
+    load[i] += u[h];
+  }
+  if (out) *out = bins;
+  return true;
+}
+
+// MHA query heads over workgroups of up to nw bins of cap units each, so that
+// the largest workgroup stages as few 16-byte chunks per tile as possible (a
+// single round of workgroups runs at the pace of the heaviest): longest first
+// into the least loaded workgroup where its heads still pack, then single
+// moves and pairwise swaps off the heaviest workgroup while they lower its
+// load.  Starts from n_min workgroups, one more while the greedy pass does not
+// fit.  Results are cached per (rank vector, geometry).
+static bool ws_balance(const starkv_klatent& k, int Hq, int unit, int nw, int cap, int n_min,
+                       std::vector<std::vector<int>>& parts) {
+  std::vector<int> u(Hq), c(Hq), order(Hq);
+  std::vector<int> key = {Hq, unit, nw, cap, n_min};
+  for (int h = 0; h < Hq; ++h) {
+    u[h] = (int)ceil_div(k.rank[h], unit);
+    c[h] = ws_row_chunks(k, h);
+    order[h] = h;
+    key.push_back(c[h]);
+    key.push_back(u[h]);
+  }
+  static std::mutex mu;
+  static std::vector<std::pair<std::vector<int>, std::vector<std::vector<int>>>> cache;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& e : cache)
+      if (e.first == key) { parts = e.second; return true; }
+  }
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return c[x] > c[y]; });
+  auto fits = [&](const std::vector<int>& hs) { return ffd_bins(hs, u, nw, cap, nullptr); };
+  for (int n = std::max(n_min, 1); n * nw <= K_MAX_WAVES; ++n) {
+    parts.assign(n, {});
+    std::vector<int> load(n, 0);
+    bool ok = true;
+    for (int h : order) {
+      int best = -1;
+      for (int g = 0; g < n; ++g) {
+        if (best >= 0 && load[g] >= load[best]) continue;
+        std::vector<int> t = parts[g];
+        t.push_back(h);
+        if (fits(t)) best = g;
+      }
+      if (best < 0) { ok = false; break; }
+      parts[best].push_back(h);
+      load[best] += c[h];
+    }
+    if (!ok) continue;
+    for (int iter = 0; iter < 256; ++iter) {
+      const int g = (int)(std::max_element(load.begin(), load.end()) - load.begin());
+      bool moved = false;
+      for (int o = 0; o < n && !moved; ++o) {
+        if (o == g) continue;
+        for (size_t i = 0; i < parts[g].size() && !moved; ++i) {
+          const int h = parts[g][i];
+          std::vector<int> rest = parts[g];
+          rest.erase(rest.begin() + i);
+          std::vector<int> grown = parts[o];
+          grown.push_back(h);
+          if (load[o] + c[h] < load[g] && fits(grown)) {           // move h to o
+            parts[g] = rest; parts[o] = grown;
+            load[g] -= c[h]; load[o] += c[h];
+            moved = true;
+            break;
+          }
+          for (size_t j = 0; j < parts[o].size(); ++j) {           // swap h with a lighter head of o
+            const int h2 = parts[o][j], d = c[h] - c[h2];
+            if (d <= 0 || load[o] + d >= load[g]) continue;
+            std::vector<int> a2 = rest, b2 = parts[o];
+            a2.push_back(h2);
+            b2[j] = h;
+            if (fits(a2) && fits(b2)) {
+              parts[g] = a2; parts[o] = b2;
+              load[g] -= d; load[o] += d;
+              moved = true;
+              break;
+            }
+          }
+        }
+      }
+      if (!moved) break;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (cache.size() >= 64) cache.erase(cache.begin());
+    cache.emplace_back(key, parts);
+    return true;
+  }
+  return false;
+}
+
 // Pack (query head, 32-rank M-tile) items into waves of up to 2 or 4 items
 // (first fit decreasing, whole heads per wave; 4 once any head has rank > 64)
 // and deal the waves round-robin over workgroups of 8 waves (2-item waves) or
 // 4 waves (4-item waves).
 int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArgs& a, KPlan& plan) {
-  struct QH { int qh, kv, ni; };
+  const bool ws = k_ws(k, dtype, S);
+  const int unit = 32;                        // ranks per item
+  struct QH { int qh, kv, ni; };              // ni: items of the head
   std::vector<QH> heads;
-  int max_ni = 1;
+  int max_items = 1;
   for (int qh = 0; qh < Hq; ++qh) {
     const int kv = qh / gs;
-    const int ni = (int)ceil_div(k.rank[kv], 32);
-    max_ni = std::max(max_ni, ni);
-    heads.push_back({qh, kv, ni});
+    max_items = std::max(max_items, (int)ceil_div(k.rank[kv], 32));
+    heads.push_back({qh, kv, (int)ceil_div(k.rank[kv], unit)});
   }
-  const bool ws = k_ws(k, dtype, S);
-  const int maxi = ws || max_ni > 2 ? 4 : 2;   // whole heads per (consumer) wave
+  const int maxi = ws || max_items > 2 ? 4 : 2;   // items per (consumer) wave
   const int nw = maxi == 2 ? 8 : 4;
-  // Bins of up to maxi items (whole query heads), first-fit decreasing.  With
+  const int cap = maxi * 32 / unit;               // units per wave
+  // Bins of up to cap units (whole query heads), first-fit decreasing.  With
   // GQA the query heads of one KV head are packed together (KV-major), so the
   // workgroup that stages or streams that head's latent serves all of them.
   std::vector<std::vector<QH>> bins;
@@ -173,7 +282,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
     const size_t first = bins.size();
     for (const QH& h : hs) {
       size_t i = first;
-      for (; i < bins.size(); ++i) if (load[i] + h.ni <= maxi) break;
+      for (; i < bins.size(); ++i) if (load[i] + h.ni <= cap) break;
       if (i == bins.size()) { bins.emplace_back(); load.push_back(0); }
       bins[i].push_back(h);
       load[i] += h.ni;
@@ -189,14 +298,36 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
       pack(grp);
     }
   }
-  const int n_waves = (int)bins.size();
+  int n_waves = (int)bins.size();
   plan.n_wg = (int)ceil_div(n_waves, nw);
   if (plan.n_wg * nw > K_MAX_WAVES) return STARKV_ERR_LIMIT;
   // bin -> (workgroup, wave).  MHA: the heaviest bins (latent rank sum) first,
   // each into the least loaded workgroup with a free wave, so workgroups
   // stream similar byte counts.  GQA: consecutive bins share a workgroup.
+  // Warp-specialised MHA: heads are partitioned over the workgroups first
+  // (ws_balance), then packed into bins per workgroup.
   std::vector<int> wg_of(n_waves), wave_of(n_waves);
-  if (gs == 1) {
+  std::vector<std::vector<int>> parts;
+  if (ws && gs == 1 && ws_balance(k, Hq, unit, nw, cap, plan.n_wg, parts)) {
+    bins.clear();
+    wg_of.clear();
+    wave_of.clear();
+    for (int g = 0; g < (int)parts.size(); ++g) {
+      std::vector<int> u(Hq, 0);
+      for (int h : parts[g]) u[h] = (int)ceil_div(k.rank[h], unit);
+      std::vector<std::vector<int>> wb;
+      ffd_bins(parts[g], u, nw, cap, &wb);
+      for (int w = 0; w < (int)wb.size(); ++w) {
+        std::vector<QH> bin;
+        for (int h : wb[w]) bin.push_back({h, h, u[h]});
+        bins.push_back(bin);
+        wg_of.push_back(g);
+        wave_of.push_back(w);
+      }
+    }
+    n_waves = (int)bins.size();
+    plan.n_wg = (int)parts.size();
+  } else if (gs == 1) {
     std::vector<int> order(n_waves), rsum(n_waves, 0);
     for (int bi = 0; bi < n_waves; ++bi) {
       order[bi] = bi;
@@ -221,14 +352,11 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
   for (int bi = 0; bi < n_waves; ++bi) {
     std::vector<QH> v = bins[bi];
     std::sort(v.begin(), v.end(), [](const QH& x, const QH& y) { return x.qh < y.qh; });
-    const int g = wg_of[bi], w = wave_of[bi];
+    uint32_t* row = a.items[wg_of[bi] * nw + wave_of[bi]];
     int i = 0;
     for (const QH& h : v) {
       const int r = k.rank[h.kv];
-      for (int mt = 0; mt < h.ni; ++mt) {
-        const int nv = std::min(32, r - 32 * mt);
-        a.items[g * nw + w][i++] = item_pack(h.qh, h.kv, mt, nv, mt == h.ni - 1);
-      }
+      for (int mt = 0; mt < h.ni; ++mt) row[i++] = item_pack(h.qh, h.kv, mt, std::min(32, r - 32 * mt), mt == h.ni - 1);
     }
   }
   const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
