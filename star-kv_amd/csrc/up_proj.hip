@@ -10,8 +10,11 @@
 // rows are the M = B * gs (batch, query head of kv's group) pairs.  It sums
 // the chunk partials of its columns in fixed chunk order into LDS, multiplies
 // them by its U_v columns (fp32; the weights convert exactly) and writes the
-// [M][128] partial up-projection of its slice.  up_finish_kernel adds the
-// slices in slice order and divides by L, one thread per output element.
+// [M][128] partial up-projection of its slice.  When a row block has fewer
+// rows than the workgroup has thread rows (small batch), the chunk range is
+// cut into P contiguous parts summed side by side and added in part order.
+// up_finish_kernel adds the slices in slice order and divides by L, one
+// thread per output element; the 128 threads of a row share L's chunk sum.
 // Every sum runs in a fixed order: the output is deterministic, with no
 // atomics.
 //
@@ -44,6 +47,7 @@ template <typename WT, int SW, bool FAST>
 __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   constexpr int JT = 256 / SW;                     // rows summed side by side
   __shared__ float os[UP_MB][SW + 4];
+  __shared__ float osp[JT][SW + 4];                // chunk-part sums (P > 1)
   const int tid = threadIdx.x;
   const int sl = blockIdx.x, kv = blockIdx.y;
   const int gs = a.gs, M = a.B * gs;
@@ -85,9 +89,36 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   const int jc = j0 + min(jj, nj - 1);                    // columns past the slice re-read its last
   for (int m0 = 0; m0 < M; m0 += UP_MB) {
     const int mb = min(UP_MB, M - m0);
+    const int P = mb < JT ? JT / mb : 1;           // chunk parts per row
+    if (P > 1) {
+      // thread row mr = part * mb + row sums chunks [c_lo, c_hi) of its row
+      if (mr < P * mb) {
+        const int part = mr / mb, m = m0 + mr % mb, q = kv * gs + m % gs;
+        const int bq = (m / gs) * a.n_hg + (q >> 5);
+        const int c_lo = (int)((int64_t)part * a.n_c2 / P), c_hi = (int)((int64_t)(part + 1) * a.n_c2 / P);
+        const float* p = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
+        float sp = 0.f;
+        for (int c = c_lo; c < c_hi; c += UP_CB) {
+          float v[UP_CB];
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k) v[k] = p[min(c + k, c_hi - 1) * cstr];
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k)
+            if (c + k < c_hi) sp += v[k];
+        }
+        osp[mr][jj] = sp;
+      }
+      __syncthreads();
+      if (tid < mb * SW) {
+        const int row = tid / SW, col = tid % SW;
+        float sr = 0.f;
+        for (int part = 0; part < P; ++part) sr += osp[part * mb + row][col];
+        os[row][col] = col < nj ? sr : 0.f;
+      }
+    }
     // chunk sums of rows m0 .. m0+mb over the slice's columns: UP_RB rows
     // per thread at a time, UP_CB chunks each (rows past mb re-read row mb-1)
-    for (int mm0 = mr; mm0 < mb; mm0 += JT * UP_RB) {
+    for (int mm0 = mr; P == 1 && mm0 < mb; mm0 += JT * UP_RB) {
       const float* p[UP_RB];
 #pragma unroll
       for (int r = 0; r < UP_RB; ++r) {
@@ -132,17 +163,34 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
 }
 
 // Sum of the slices' partial up-projections in slice order, times 1 / L.
-// One thread per output element (row m of KV head kv, dim d).
+// One thread per output element (row m of KV head kv, dim d); a workgroup
+// holds two whole rows, and the 128 threads of a row sum L's chunk partials
+// in contiguous parts, added in a fixed tree.
 template <typename OT>
 __global__ __launch_bounds__(256) void up_finish_kernel(const UPArgs a) {
+  __shared__ float red[256];
   const int gs = a.gs, M = a.B * gs;
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t e = (int64_t)blockIdx.x * 256 + tid;
   const int n_kv = a.Hq / gs;
-  if (e >= (int64_t)n_kv * M * HEAD_DIM) return;
+  const bool valid = e < (int64_t)n_kv * M * HEAD_DIM;   // whole rows: a row is valid or not as a whole
   const int d = (int)(e % HEAD_DIM), m = (int)((e / HEAD_DIM) % M), kv = (int)(e / ((int64_t)HEAD_DIM * M));
   const int q = kv * gs + m % gs, b = m / gs;
   const int bq = b * a.n_hg + (q >> 5);
-  const float L = sum_strided(a.psum + (int64_t)bq * a.n_c2 * 32 + (q & 31), 32, a.n_c2);
+  float lp = 0.f;
+  if (valid) {
+    const int c_lo = (int)((int64_t)d * a.n_c2 / HEAD_DIM), c_hi = (int)((int64_t)(d + 1) * a.n_c2 / HEAD_DIM);
+    if (c_hi > c_lo) lp = sum_strided(a.psum + ((int64_t)bq * a.n_c2 + c_lo) * 32 + (q & 31), 32, c_hi - c_lo);
+  }
+  red[tid] = lp;
+  __syncthreads();
+#pragma unroll
+  for (int w = HEAD_DIM / 2; w >= 1; w >>= 1) {
+    if (d < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (!valid) return;
+  const float L = red[tid - d];
   const float s = sum_strided(a.ypart + ((int64_t)kv * a.n_sl * M + m) * HEAD_DIM + d, (int64_t)M * HEAD_DIM, a.n_sl);
   ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s / L);
 }
@@ -157,11 +205,18 @@ template <typename WT>
 static void launch_up_t(const UPArgs& a, bool fast, hipStream_t st) {
   const dim3 grid(a.n_sl, a.Hq / a.gs);
   if (a.sw == 64) launch_up_sw<WT, 64>(a, fast, grid, st);
-  else launch_up_sw<WT, 32>(a, fast, grid, st);
+  else if (a.sw == 32) launch_up_sw<WT, 32>(a, fast, grid, st);
+  else if (a.sw == 16) launch_up_sw<WT, 16>(a, fast, grid, st);
+  else launch_up_sw<WT, 8>(a, fast, grid, st);
 }
 
-// slice width: 64 columns when that still gives >= 256 workgroups, else 32
-int up_slice_width(int n_kv, int Rv) { return (int64_t)n_kv * ceil_div(Rv, 64) >= 256 ? 64 : 32; }
+// slice width: the widest of 64, 32, 16 columns that still gives >= 512
+// workgroups (two per CU), else 8
+int up_slice_width(int n_kv, int Rv) {
+  for (int sw = 64; sw >= 16; sw >>= 1)
+    if ((int64_t)n_kv * ceil_div(Rv, sw) >= 512) return sw;
+  return 8;
+}
 
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st) {
   if (dtype == STARKV_F16) launch_up_t<_Float16>(a, fast, st);
