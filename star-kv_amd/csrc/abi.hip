@@ -359,6 +359,30 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
       for (int mt = 0; mt < h.ni; ++mt) row[i++] = item_pack(h.qh, h.kv, mt, std::min(32, r - 32 * mt), mt == h.ni - 1);
     }
   }
+  // grouped-query heads (k_logits_gqa.hip): K reconstructed once per KV
+  // head; two KV heads per workgroup (the largest rank with the smallest),
+  // each run by two consumer waves (dims halves p = 0, 1)
+  const bool gqa = ws && gs > 1 && gs <= 8 && k.format == STARKV_FMT_DENSE;
+  if (gqa) {
+    const int n = k.n_kv_heads;
+    std::vector<int> order(n);
+    for (int h = 0; h < n; ++h) order[h] = h;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return k.rank[x] > k.rank[y]; });
+    plan.n_wg = (int)ceil_div(n, 2);
+    if (plan.n_wg * 4 > K_MAX_WAVES) return STARKV_ERR_LIMIT;
+    for (int w = 0; w < K_MAX_WAVES; ++w)
+      for (int i = 0; i < K_MAXI; ++i) a.items[w][i] = 0;
+    for (int g = 0; g < plan.n_wg; ++g) {
+      const int h0 = order[g], h1 = n - 1 - g > g ? order[n - 1 - g] : -1;
+      for (int p = 0; p < 2; ++p) {
+        a.items[g * 4 + p][0] = item_pack(h0 * gs, h0, p, 0, 1);
+        if (h1 >= 0) a.items[g * 4 + 2 + p][0] = item_pack(h1 * gs, h1, p, 0, 1);
+      }
+    }
+  }
+  a.gqa = gqa;
+  a.gs = gs;
+  for (int h = 0; h < K_MAX_KV; ++h) a.krank[h] = (int16_t)(h < k.n_kv_heads ? k.rank[h] : 0);
   const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
   a.ksplit = two ? k.split : 128;
   a.k_a_int8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
@@ -396,7 +420,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
       max_chunks = std::max(max_chunks, chunks);
     }
     a.ws_stage = (int)round_up(max_chunks, 64) * 16 + 8192 + (a.ws_i8 ? 1024 : 0);
-    a.ws_nst = std::min(4, K1_WS_RING_BYTES / a.ws_stage);
+    a.ws_nst = std::min(4, (gqa ? K1_GQ_RING_BYTES : K1_WS_RING_BYTES) / a.ws_stage);
   }
   return STARKV_OK;
 }

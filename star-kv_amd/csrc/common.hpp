@@ -69,7 +69,13 @@ struct KArgs {
   int xpitch2[K_MAX_KV];
   int64_t bkoff[K_MAX_KV];
   uint32_t items[K_MAX_WAVES][K_MAXI];             // [workgroup plan * waves + wave][item]
+  // grouped-query variant (k_logits_gqa.hip, 2 <= gs <= 8): K reconstructed
+  // once per KV head; item 0 of consumer wave w = item_pack(kv * gs, kv, dim half, 0, 1)
+  int gqa, gs;
+  int16_t krank[K_MAX_KV];
 };
+constexpr int K1_GQ_CARRY_BYTES = 2 * 2 * 64 * 4 * 4;          // GQA: dim-half partial logits, 2 tiles x 2 heads
+constexpr int K1_GQ_RING_BYTES = 163840 - K1_GQ_CARRY_BYTES;   // its LDS ring
 
 // ---------------------------------------------------------------------------
 // P.V launch arguments.
@@ -276,6 +282,7 @@ int launch_rope_table(const float* inv_freq_host, int max_positions, float scali
 int launch_rope_apply(const RopeApplyArgs& a, int dtype, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
 int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
+int launch_k_logits_gqa(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
 int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st);
 int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ranks) per P.V wave
 // P.V workgroups resident per CU (the kernel's register budget): the wide

@@ -372,6 +372,7 @@ static int launch_o(const KArgs& a, int outk, bool fast, int B, hipStream_t st) 
 }
 
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st) {
+  if (a.gqa) return launch_k_logits_gqa(a, dtype, out_f32, out_dtype, B, st);
   if (a.ws) return launch_k_logits_ws(a, dtype, out_f32, out_dtype, B, st);
   const int outk = out_f32 ? 0 : (out_dtype == STARKV_F16 ? 1 : 2);
   const bool q = fmt != STARKV_FMT_DENSE;
