@@ -138,6 +138,7 @@ bool k_ws(const starkv_klatent& k, int dtype, int S) {
   for (int h = 0; h < k.n_kv_heads; ++h) {
     if (k.rank[h] % 8) return false;
     if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
+    if ((int64_t)TILE * k.pos_stride[h] * xe >= ((int64_t)1 << 31)) return false;   // 32-bit per-tile DMA step
   }
   return true;
 }

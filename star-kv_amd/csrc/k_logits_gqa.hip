@@ -150,15 +150,34 @@ __global__ __launch_bounds__((GQ_CONSUMERS + GQ_PRODUCERS) * 64, 1) void k_logit
       pmax[k] = S - 1;
       dst[k] = m * 1024;
     }
+    // full tiles (all 32 positions below S): first-tile address plus
+    // (tile - tile0) times a fixed per-lane step; the tail tile is clamped
+    const char* base[GQ_MAXK];     // lane address at tile0
+    uint32_t lstep[GQ_MAXK];       // bytes per tile (< 2^31, checked on the host)
+#pragma unroll
+    for (int k = 0; k < GQ_MAXK; ++k) {
+      base[k] = src[k] + (int64_t)(tile0 * tmul[k] + rowpos[k]) * adv[k];
+      lstep[k] = (uint32_t)(tmul[k] * adv[k]);
+    }
     auto issue = [&](int i) __attribute__((always_inline)) {
       const int tl = min(tile0 + i, last);
       char* st = ring + (i % nst) * stage;
+      if ((tl + 1) * TILE <= S) {
+        const uint32_t ti = (uint32_t)(tl - tile0);
 #pragma unroll
-      for (int k = 0; k < GQ_MAXK; ++k) {
-        const int m = pw + GQ_PRODUCERS * k;
-        if (m >= nI) break;
-        const int64_t pos = min(tl * tmul[k] + rowpos[k], pmax[k]);
-        __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+        for (int k = 0; k < GQ_MAXK; ++k) {
+          const int m = pw + GQ_PRODUCERS * k;
+          if (m >= nI) break;
+          __builtin_amdgcn_global_load_lds((const void*)(base[k] + (uint64_t)ti * lstep[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < GQ_MAXK; ++k) {
+          const int m = pw + GQ_PRODUCERS * k;
+          if (m >= nI) break;
+          const int64_t pos = min(tl * tmul[k] + rowpos[k], pmax[k]);
+          __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+        }
       }
     };
     for (int i = 0; i < ahead; ++i) issue(i);

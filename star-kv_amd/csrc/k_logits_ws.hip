@@ -249,15 +249,38 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
       pmax[k] = S - 1;
       dst[k] = m * 1024;
     }
+    // A tile whose 32 positions all lie below S needs no clamping: there each
+    // lane's address is its first tile's address plus (tile - tile0) times a
+    // fixed per-lane step (latent rows and scales: 32 positions; RoPE operand:
+    // 8 KB), one 32x32->64-bit multiply-add instead of the clamped form.  The
+    // producers share their SIMDs with the consumers, so this VALU work is
+    // taken from the consumers' issue slots.
+    const char* base[WS_MAXK];     // lane address at tile0
+    uint32_t lstep[WS_MAXK];       // bytes per tile (< 2^31, checked on the host)
+#pragma unroll
+    for (int k = 0; k < WS_MAXK; ++k) {
+      base[k] = src[k] + (int64_t)(tile0 * tmul[k] + rowpos[k]) * adv[k];
+      lstep[k] = (uint32_t)(tmul[k] * adv[k]);
+    }
     auto issue = [&](int i) __attribute__((always_inline)) {
       const int tl = min(tile0 + i, last);
       char* st = ring + (i % nst) * stage;
+      if ((tl + 1) * TILE <= S) {
+        const uint32_t ti = (uint32_t)(tl - tile0);
 #pragma unroll
-      for (int k = 0; k < WS_MAXK; ++k) {
-        const int m = pw + WS_PRODUCERS * k;
-        if (m >= nI) break;
-        const int64_t pos = min(tl * tmul[k] + rowpos[k], pmax[k]);
-        __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+        for (int k = 0; k < WS_MAXK; ++k) {
+          const int m = pw + WS_PRODUCERS * k;
+          if (m >= nI) break;
+          __builtin_amdgcn_global_load_lds((const void*)(base[k] + (uint64_t)ti * lstep[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < WS_MAXK; ++k) {
+          const int m = pw + WS_PRODUCERS * k;
+          if (m >= nI) break;
+          const int64_t pos = min(tl * tmul[k] + rowpos[k], pmax[k]);
+          __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
+        }
       }
     };
     for (int i = 0; i < ahead; ++i) issue(i);
