@@ -482,7 +482,7 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
 int head_groups(int H) { return (int)ceil_div(H, 32); }   // P.V passes of 32 heads
 
 struct DecodeLayout {
-  int S_pad, n_c1, tiles_per_chunk, n_hg, sw, n_sl;
+  int S_pad, n_c1, tiles_per_chunk, n_hg, sw, n_sl, n_cs;
   PVGeom pv;
   size_t off_logits, off_cmax, off_part, off_psum, off_ypart, total;
 };
@@ -498,6 +498,7 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   L.pv = pv_geometry(B * L.n_hg, S, Rv, true, vq, v_row_bytes);
   L.sw = up_slice_width(Hkv, Rv);
   L.n_sl = (int)ceil_div(Rv, L.sw);
+  L.n_cs = up_chunk_sets(Hkv, L.n_sl, L.pv.n_c2);
   const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
   const size_t BQ = (size_t)B * L.n_hg;
   size_t o = 0;
@@ -505,7 +506,7 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
   L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * 4);
   L.off_psum = o; o = a256(o + BQ * n_c2 * 32 * 4);
-  L.off_ypart = o; o = a256(o + (size_t)Hkv * L.n_sl * ((size_t)B * (Hq / Hkv)) * HEAD_DIM * 4);
+  L.off_ypart = o; o = a256(o + (size_t)Hkv * L.n_sl * L.n_cs * ((size_t)B * (Hq / Hkv)) * HEAD_DIM * 4);
   L.total = o;
   return L;
 }
@@ -809,7 +810,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   ua.uv = d->uv; ua.uv_rs = d->uv_row_stride;
   ua.out = d->out; ua.o_sb = d->out_stride_b; ua.o_sh = d->out_stride_h;
   ua.B = B; ua.Hq = Hq; ua.gs = gs; ua.Rv = d->v.rank;
-  ua.sw = L.sw; ua.n_sl = L.n_sl; ua.ypart = (float*)(ws + L.off_ypart);
+  ua.sw = L.sw; ua.n_sl = L.n_sl; ua.n_cs = L.n_cs; ua.ypart = (float*)(ws + L.off_ypart);
   ua.out_f32 = d->out_dtype == STARKV_F32;
   const bool ufast = al(d->uv, 16) && al64(d->uv_row_stride * 2, 16);
   if ((st = launch_up_proj(ua, d->dtype, ufast, s))) return st;

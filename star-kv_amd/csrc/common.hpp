@@ -149,7 +149,8 @@ struct UPArgs {
   void* out; int64_t o_sb, o_sh;                   // [B][Hq][128]
   int B, Hq, gs, Rv;
   int sw, n_sl;                                    // column slices of the V rank (sw columns each)
-  float* ypart;                                    // [Hkv][n_sl][B*gs][128] partial up-projections
+  int n_cs;                                        // chunk sets (contiguous ranges of the n_c2 chunks)
+  float* ypart;                                    // [Hkv][n_sl][n_cs][B*gs][128] partial up-projections
   int out_f32;                                     // 1: fp32 output, 0: weight dtype
 };
 
@@ -290,6 +291,7 @@ int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ran
 constexpr int pv_wg_per_cu(int ntw, int vq) { return ntw >= 8 && vq == VQ_DENSE ? 1 : 2; }
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
 int up_slice_width(int n_kv, int Rv);                 // V-rank columns per up-projection workgroup
+int up_chunk_sets(int n_kv, int n_sl, int n_c2);      // chunk sets per (slice, KV head)
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);

@@ -13,14 +13,20 @@
 // [M][128] partial up-projection of its slice.  When a row block has fewer
 // rows than the workgroup has thread rows (small batch), the chunk range is
 // cut into P contiguous parts summed side by side and added in part order.
-// up_finish_kernel adds the slices in slice order and divides by L, one
-// thread per output element; the 128 threads of a row share L's chunk sum.
+// With few workgroups (small batch, few KV heads) the chunks are also cut
+// into n_cs contiguous sets, one workgroup each (grid z): the up-projection
+// is linear, so each set's projection is a partial of its own.
+// up_finish_kernel adds the n_sl * n_cs partials in order and divides by L,
+// one thread per output element; the 128 threads of a row share L's chunk
+// sum.
 // Every sum runs in a fixed order: the output is deterministic, with no
 // atomics.
 //
 // Both kernels move a few MB and are latency-bound, so each thread issues
 // its loads in batches of up to 64 independent addresses and adds them
 // afterwards in their fixed order.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace starkv {
@@ -49,7 +55,9 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   __shared__ float os[UP_MB][SW + 4];
   __shared__ float osp[JT][SW + 4];                // chunk-part sums (P > 1)
   const int tid = threadIdx.x;
-  const int sl = blockIdx.x, kv = blockIdx.y;
+  const int sl = blockIdx.x, kv = blockIdx.y, cs = blockIdx.z;
+  const int cb0 = (int)((int64_t)cs * a.n_c2 / a.n_cs), cb1 = (int)((int64_t)(cs + 1) * a.n_c2 / a.n_cs);
+  const int nc = cb1 - cb0;                               // this workgroup's chunks
   const int gs = a.gs, M = a.B * gs;
   const int j0 = sl * SW, nj = min(SW, a.Rv - j0);        // valid columns of the slice
   const int64_t cstr = (int64_t)32 * a.Rvp;               // next chunk's partials
@@ -84,7 +92,7 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
     }
   };
 
-  float* yp = a.ypart + ((int64_t)kv * a.n_sl + sl) * M * HEAD_DIM;
+  float* yp = a.ypart + (((int64_t)kv * a.n_sl + sl) * a.n_cs + cs) * M * HEAD_DIM;
   const int jj = tid % SW, mr = tid / SW;
   const int jc = j0 + min(jj, nj - 1);                    // columns past the slice re-read its last
   for (int m0 = 0; m0 < M; m0 += UP_MB) {
@@ -95,7 +103,7 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
       if (mr < P * mb) {
         const int part = mr / mb, m = m0 + mr % mb, q = kv * gs + m % gs;
         const int bq = (m / gs) * a.n_hg + (q >> 5);
-        const int c_lo = (int)((int64_t)part * a.n_c2 / P), c_hi = (int)((int64_t)(part + 1) * a.n_c2 / P);
+        const int c_lo = cb0 + (int)((int64_t)part * nc / P), c_hi = cb0 + (int)((int64_t)(part + 1) * nc / P);
         const float* p = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
         float sp = 0.f;
         for (int c = c_lo; c < c_hi; c += UP_CB) {
@@ -124,20 +132,20 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
       for (int r = 0; r < UP_RB; ++r) {
         const int m = m0 + min(mm0 + JT * r, mb - 1), q = kv * gs + m % gs;
         const int bq = (m / gs) * a.n_hg + (q >> 5);
-        p[r] = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
+        p[r] = a.part + (((int64_t)bq * a.n_c2 + cb0) * 32 + (q & 31)) * a.Rvp + jc;
       }
       float s[UP_RB] = {};
-      for (int c = 0; c < a.n_c2; c += UP_CB) {
+      for (int c = 0; c < nc; c += UP_CB) {
         float v[UP_RB][UP_CB];
 #pragma unroll
         for (int r = 0; r < UP_RB; ++r)
 #pragma unroll
-          for (int k = 0; k < UP_CB; ++k) v[r][k] = p[r][min(c + k, a.n_c2 - 1) * cstr];
+          for (int k = 0; k < UP_CB; ++k) v[r][k] = p[r][min(c + k, nc - 1) * cstr];
 #pragma unroll
         for (int r = 0; r < UP_RB; ++r)
 #pragma unroll
           for (int k = 0; k < UP_CB; ++k)
-            if (c + k < a.n_c2) s[r] += v[r][k];
+            if (c + k < nc) s[r] += v[r][k];
       }
 #pragma unroll
       for (int r = 0; r < UP_RB; ++r)
@@ -191,7 +199,8 @@ __global__ __launch_bounds__(256) void up_finish_kernel(const UPArgs a) {
   }
   if (!valid) return;
   const float L = red[tid - d];
-  const float s = sum_strided(a.ypart + ((int64_t)kv * a.n_sl * M + m) * HEAD_DIM + d, (int64_t)M * HEAD_DIM, a.n_sl);
+  const int np = a.n_sl * a.n_cs;                         // partial up-projections of the row
+  const float s = sum_strided(a.ypart + ((int64_t)kv * np * M + m) * HEAD_DIM + d, (int64_t)M * HEAD_DIM, np);
   ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s / L);
 }
 
@@ -203,19 +212,19 @@ static void launch_up_sw(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) 
 
 template <typename WT>
 static void launch_up_t(const UPArgs& a, bool fast, hipStream_t st) {
-  const dim3 grid(a.n_sl, a.Hq / a.gs);
+  const dim3 grid(a.n_sl, a.Hq / a.gs, a.n_cs);
   if (a.sw == 64) launch_up_sw<WT, 64>(a, fast, grid, st);
-  else if (a.sw == 32) launch_up_sw<WT, 32>(a, fast, grid, st);
-  else if (a.sw == 16) launch_up_sw<WT, 16>(a, fast, grid, st);
-  else launch_up_sw<WT, 8>(a, fast, grid, st);
+  else launch_up_sw<WT, 32>(a, fast, grid, st);
 }
 
-// slice width: the widest of 64, 32, 16 columns that still gives >= 512
-// workgroups (two per CU), else 8
-int up_slice_width(int n_kv, int Rv) {
-  for (int sw = 64; sw >= 16; sw >>= 1)
-    if ((int64_t)n_kv * ceil_div(Rv, sw) >= 512) return sw;
-  return 8;
+// slice width: 64 columns when that still gives >= 256 workgroups, else 32
+// (whole 128-byte lines of the partials either way)
+int up_slice_width(int n_kv, int Rv) { return (int64_t)n_kv * ceil_div(Rv, 64) >= 256 ? 64 : 32; }
+
+// chunk sets: enough workgroups for two per CU, with at least 16 chunks each
+int up_chunk_sets(int n_kv, int n_sl, int n_c2) {
+  const int64_t wg = (int64_t)n_kv * n_sl;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(512, wg), n_c2 / 16));
 }
 
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st) {
