@@ -338,9 +338,12 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream);
  * q + b*q_stride_b + q*q_stride_h + t*q_stride_t + d (16-byte aligned, strides
  * multiples of 8).  out likewise with out_stride_*, act dtype.
  * K latent: STARKV_FMT_DENSE (ranks, offsets and pitches multiples of 8,
- * data 16-byte aligned) or STARKV_FMT_INT8_SYM; V latent: STARKV_FMT_DENSE
- * (rank and strides multiples of 8, data 16-byte aligned) or
- * STARKV_FMT_INT4_G64; other formats STARKV_ERR_FORMAT.  uv: 16-byte aligned,
+ * data 16-byte aligned), STARKV_FMT_INT8_SYM or STARKV_FMT_INT4_REF (the
+ * reference module's split cache, either upper-block format; ranks multiples
+ * of 8); V latent: STARKV_FMT_DENSE (rank and strides multiples of 8, data
+ * 16-byte aligned), STARKV_FMT_INT4_G64, STARKV_FMT_INT8_SYM or
+ * STARKV_FMT_INT4_REF (with or without its upper block; rank a multiple of
+ * 8); each under the same layout rules as in decode.  uv: 16-byte aligned,
  * row stride a multiple of 8.  Quantised latents are dequantised bit-exactly
  * as in decode.  The workspace holds the reconstructed K and V
  * (2 x batch x Hkv x round_up(pos0 + n_tokens, 64) x 128 fp16 elements, for

@@ -605,9 +605,11 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
   return STARKV_OK;
 }
 
-// Prefill: dense (16-byte rows) or int8 K latents, dense (16-byte rows) or
-// group-64 int4 V latents; q, U_v 16-byte aligned.  Positions reconstructed:
-// pos0 + n_tokens, padded to 64 in the workspace.
+// Prefill: dense (16-byte rows), int8 or reference split-format K latents;
+// dense (16-byte rows), group-64 int4 or per-token block (reference int4 with
+// an optional int8 / int4 upper block, or int8) V latents; q, U_v 16-byte
+// aligned.  Positions reconstructed: pos0 + n_tokens, padded to 64 in the
+// workspace.
 int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->batch > 65535 || d->n_tokens < 1 || d->pos0 < 0) return STARKV_ERR_SHAPE;
@@ -617,7 +619,6 @@ int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
   int st = validate_klatent(d->k, d->n_q_heads, d->dtype, gs);
   if (st) return st;
   const starkv_klatent& k = d->k;
-  if (k.format != STARKV_FMT_DENSE && k.format != STARKV_FMT_INT8_SYM) return STARKV_ERR_FORMAT;
   for (int h = 0; h < k.n_kv_heads; ++h) {
     if (k.rank[h] % 8) return STARKV_ERR_SHAPE;
     if (k.format == STARKV_FMT_DENSE && (!al64(k.head_offset[h], 8) || !al64(k.pos_stride[h], 8)))
@@ -627,7 +628,6 @@ int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
   PVArgs vtmp = {};
   int vq = 0;
   if ((st = validate_v(d->v, vtmp, &vq))) return st;
-  if (vq != VQ_DENSE && vq != VQ_G64) return STARKV_ERR_FORMAT;
   if (d->v.rank % 8) return STARKV_ERR_SHAPE;
   if (vq == VQ_DENSE && (!al(d->v.data, 16) || !al64(d->v.stride_s, 8) || !al64(d->v.stride_b, 8)))
     return STARKV_ERR_ALIGN;
@@ -980,9 +980,18 @@ static int prefill_impl(const starkv_prefill_desc* d, void* workspace, size_t wo
   a.Hkv = k.n_kv_heads; a.Hq = d->n_q_heads; a.gs = gs; a.T = d->n_tokens; a.pos0 = d->pos0;
   a.kx = k.data; a.kx_sb = k.stride_b; a.k_i8 = k.format == STARKV_FMT_INT8_SYM;
   a.kscale = k.scale; a.ks_sb = k.scale_stride_b; a.ks_sh = k.scale_stride_h;
+  // reference split format: ranks [0, ksplit) int8 or int4 in data, the rest int4 in data2
+  const bool ktwo = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+  a.k_ref = k.format == STARKV_FMT_INT4_REF;
+  a.ksplit = ktwo ? k.split : 128;
+  a.k_a8 = ktwo && k.split_format == STARKV_FMT_INT8_SYM;
+  a.kx2 = k.data2; a.kx2_sb = k.stride2_b;
+  a.kscale2 = k.scale2; a.ks2_sb = k.scale2_stride_b; a.ks2_sh = k.scale2_stride_h;
   for (int h = 0; h < k.n_kv_heads; ++h) {
     a.krank[h] = k.rank[h];
     a.kxoff[h] = k.head_offset[h]; a.kxpitch[h] = k.pos_stride[h];
+    const bool lo = ktwo && k.rank[h] > k.split;
+    a.kxoff2[h] = lo ? k.head_offset2[h] : 0; a.kxpitch2[h] = lo ? k.pos_stride2[h] : 0;
     a.bkoff[h] = k.bk_head_offset[h];
   }
   a.bk = k.bk; a.bk_rs = k.bk_row_stride;
@@ -990,6 +999,16 @@ static int prefill_impl(const starkv_prefill_desc* d, void* workspace, size_t wo
   a.vx = v.data; a.vx_sb = v.stride_b; a.vx_ss = v.stride_s;
   a.v_g64 = v.format == STARKV_FMT_INT4_G64; a.Rv = v.rank;
   a.vscale = v.scale; a.vzero = v.zero; a.vs_sb = v.scale_stride_b; a.vs_ss = v.scale_stride_s;
+  {
+    // per-token blocks: the split and block formats as validate_v reads them
+    PVArgs vb = {};
+    int vq = 0;
+    if ((st = validate_v(v, vb, &vq))) return st;
+    a.v_blk = vq == VQ_BLOCK;
+    a.vsplit = vb.split; a.v_a8 = vb.a_int8;
+    a.vx2 = vb.x2; a.vx2_sb = vb.x2_sb; a.vx2_ss = vb.x2_ss;
+    a.vscale2 = vb.xs2; a.vs2_sb = vb.xs2_sb; a.vs2_ss = vb.xs2_ss;
+  }
   a.uv = d->uv; a.uv_rs = d->uv_row_stride;
   a.rope = d->rope_table;
   a.kbuf = workspace; a.vbuf = (char*)workspace + kvb;

@@ -184,9 +184,23 @@ struct PFArgs {
   int64_t kxpitch[K_MAX_KV];
   const void* bk; int64_t bk_rs;
   int64_t bkoff[K_MAX_KV];
+  // K latent in the reference split format (k_ref): ranks [0, ksplit) in kx (int8 if k_a8, else
+  // int4 nibbles), ranks [ksplit, r) int4 nibbles in kx2 (bytes); fp16 scales per (b, h, s) in
+  // kscale / kscale2
+  int k_ref, ksplit, k_a8;
+  const void* kx2; int64_t kx2_sb;
+  const void* kscale2; int64_t ks2_sb, ks2_sh;
+  int64_t kxoff2[K_MAX_KV];
+  int64_t kxpitch2[K_MAX_KV];
   // V latent: dense act dtype (elements) or group-64 int4 (bytes) with fp16 scale / zero (b, s, g)
   const void* vx; int64_t vx_sb, vx_ss; int v_g64, Rv;
   const void* vscale; const void* vzero; int64_t vs_sb, vs_ss;
+  // ... or per-token blocks (v_blk: the reference int4 format with an optional int8 / int4 upper
+  // block, or int8): ranks [0, vsplit) in vx (int8 if v_a8, else int4), [vsplit, Rv) int4 in vx2;
+  // fp16 scales per (b, s) in vscale / vscale2
+  int v_blk, vsplit, v_a8;
+  const void* vx2; int64_t vx2_sb, vx2_ss;
+  const void* vscale2; int64_t vs2_sb, vs2_ss;
   const void* uv; int64_t uv_rs;                   // [Hkv*128][Rv]
   const void* rope;                                // RoPE table (rope.hip layout)
   void* kbuf; void* vbuf;                          // [B][Hkv][S_pad][128] act dtype
@@ -194,6 +208,8 @@ struct PFArgs {
   float scale_log2;                                // softmax scale * log2(e)
   void* out; int64_t o_sb, o_sh, o_st;             // (b, qh, t), act dtype
 };
+// both are passed by value as kernel arguments (at most 4 KiB)
+static_assert(sizeof(KArgs) <= 4096 && sizeof(PFArgs) <= 4096, "kernel argument size");
 
 // ---------------------------------------------------------------------------
 // small helpers

@@ -11,8 +11,9 @@
 //    K and V in the activation dtype, model.py:431-442; fp16 holds bf16
 //    models' K and V with 2^-12 instead of 2^-9 unit roundoff).  Quantised
 //    latents are dequantised on the way in, bit-exactly as everywhere else
-//    (int8: fp16(q s); group-64 int4: fp16(n s + z)), then rounded once more
-//    to bf16 for bf16 activations.  Rows in [S, S_pad) are written as zeros.
+//    (int8: fp16(q s); the reference int4 format: fp16((nibble - 8) s);
+//    group-64 int4: fp16(n s + z)), then rounded once more to bf16 for bf16
+//    activations.  Rows in [S, S_pad) are written as zeros.
 // 2. fa_causal_kernel: flash attention over those buffers, one workgroup per
 //    (b, query head, 256 queries), 8 waves of 32 queries, fp16 MFMAs (bf16
 //    queries converted to fp16 on load).  Per 64-key block it forms
@@ -92,6 +93,37 @@ __device__ inline uint4 pf_dq_int8(uint2 q, uint16_t s16) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// 8 int4 nibbles of the reference format (rank 2k in the low nibble of byte k,
+// value nibble - 8) -> fp16((nibble - 8) * s), ranks in order, bit-exact
+// (1024 + nibble - 1032 is exact in fp16; one rounding in the multiply)
+__device__ inline uint4 pf_dq_int4ref(uint32_t w, uint16_t s16) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  const kh2 s = __builtin_bit_cast(kh2, (uint32_t)s16 * 0x10001u);
+  const kh2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t p = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u + 0x00010001u * k) | 0x64006400u;
+    o[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(kh2, p) + bias) * s);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// 8 ranks of a per-token block latent (the reference split format): the chunk
+// of ranks j .. j+7 lies wholly in the upper block (j < split; int8 or int4)
+// or the lower one (int4); the raw words hold 8 bytes (int8) or 4 (int4, .x)
+__device__ inline uint2 pf_ld_block(const uint8_t* up, const uint8_t* lo, int j, int split, bool a8) {
+  if (j < split) {
+    if (a8) return *(const uint2*)(up + j);
+    return make_uint2(*(const uint32_t*)(up + j / 2), 0u);
+  }
+  return make_uint2(*(const uint32_t*)(lo + (j - split) / 2), 0u);
+}
+__device__ inline uint4 pf_dq_block(uint2 w, int j, int split, bool a8, uint16_t s_up, uint16_t s_lo) {
+  if (j < split) return a8 ? pf_dq_int8(w, s_up) : pf_dq_int4ref(w.x, s_up);
+  return pf_dq_int4ref(w.x, s_lo);
+}
+
 // 8 int4 nibbles (rank 2k in the low nibble of byte k) -> fp16(n * s + z), ranks in order
 __device__ inline uint4 pf_dq_g64(uint32_t w, uint16_t s16, uint16_t z16) {
   const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
@@ -131,11 +163,13 @@ constexpr int C_PITCH = 136;                     // halves per epilogue row
 constexpr int RC_LDS = 4 * RC_WAVE_POS * C_PITCH;
 
 // raw K latent data of one K-step for this lane: [N-tile][K-chunk]
-template <bool Q> struct RkRaw { uint4 d[4][4]; };                        // dense: 8 ranks per chunk
-template <> struct RkRaw<true> { uint2 d[4][4]; };                        // int8
+template <int Q> struct RkRaw { uint2 d[4][4]; };                         // int8 / reference split: <= 8 bytes per chunk
+template <> struct RkRaw<0> { uint4 d[4][4]; };                           // dense: 8 ranks per chunk
 
-// Q: int8 latents (else dense act dtype)
-template <typename XT, bool Q>
+// Q: 0 dense act dtype, 1 int8 with one scale per (b, h, s), 2 the reference
+// split format (ranks below ksplit int8 or int4, the rest int4, each block
+// with its scale per (b, h, s))
+template <typename XT, int Q>
 __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -152,15 +186,22 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   const int R = a.krank[h];                         // multiple of 8 (host-checked)
   const int nks = (R + RC_KS - 1) / RC_KS;
 
-  // per N-tile latent row (clamped position) and int8 scales
+  // per N-tile latent row (clamped position) and scales
   const uint8_t* xrow[4];
-  uint16_t ksc[4] = {0, 0, 0, 0};
+  const uint8_t* xrow2[4];                           // reference split: the lower (int4) block
+  uint16_t ksc[4] = {0, 0, 0, 0}, ksc2[4] = {0, 0, 0, 0};
+  const bool klo = Q == 2 && R > a.ksplit;           // this head has a lower block
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     const int pc = min(pw + nt * 32 + n, S - 1);
-    constexpr int64_t es = Q ? 1 : 2;                // latent offsets: bytes (int8) or elements
+    constexpr int64_t es = Q ? 1 : 2;                // latent offsets: bytes (quantised) or elements
     xrow[nt] = (const uint8_t*)a.kx + (b * a.kx_sb + a.kxoff[h] + (int64_t)pc * a.kxpitch[h]) * es;
+    xrow2[nt] = xrow[nt];
     if constexpr (Q) ksc[nt] = ((const uint16_t*)a.kscale)[b * a.ks_sb + h * a.ks_sh + pc];
+    if (klo) {
+      xrow2[nt] = (const uint8_t*)a.kx2 + b * a.kx2_sb + a.kxoff2[h] + (int64_t)pc * a.kxpitch2[h];
+      ksc2[nt] = ((const uint16_t*)a.kscale2)[b * a.ks2_sb + h * a.ks2_sh + pc];
+    }
   }
 
   // Ranks past R (the last step only) read a valid chunk instead (address
@@ -174,16 +215,23 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int j = min(j0 + 8 * kk, R - 8);
-        if constexpr (!Q) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * j);
-        else r.d[nt][kk] = *(const uint2*)(xrow[nt] + j);
+        if constexpr (Q == 0) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * j);
+        else if constexpr (Q == 1) r.d[nt][kk] = *(const uint2*)(xrow[nt] + j);
+        else r.d[nt][kk] = pf_ld_block(xrow[nt], xrow2[nt], j, a.ksplit, a.k_a8);
       }
   };
-  // raw -> B fragment (act dtype)
-  auto frag = [&](const RkRaw<Q>& r, int nt, int kk) -> uint4 {
-    if constexpr (!Q) {
+  // raw -> B fragment (act dtype) of K-step ks
+  auto frag = [&](const RkRaw<Q>& r, int ks, int nt, int kk) -> uint4 {
+    if constexpr (Q == 0) {
       return r.d[nt][kk];
     } else {
-      uint4 f = pf_dq_int8(r.d[nt][kk], ksc[nt]);
+      uint4 f;
+      if constexpr (Q == 1) {
+        f = pf_dq_int8(r.d[nt][kk], ksc[nt]);
+      } else {
+        const int j = min(ks * RC_KS + 32 * hh + 8 * kk, R - 8);
+        f = pf_dq_block(r.d[nt][kk], j, a.ksplit, a.k_a8, ksc[nt], ksc2[nt]);
+      }
       if constexpr (!__is_same(XT, _Float16)) f = pf_f16_to_bf16(f);
       return f;
     }
@@ -224,7 +272,7 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
     for (int kk = 0; kk < 4; ++kk) {
       uint4 bf[4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) bf[nt] = frag(cur, nt, kk);
+      for (int nt = 0; nt < 4; ++nt) bf[nt] = frag(cur, ks, nt, kk);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const uint16_t* sb = lds + (ks * RC_KS + 8 * kk) * BK_PITCH + tr_off + 32 * mt;
@@ -300,10 +348,14 @@ constexpr int RV_SZ_OFF = 2 * RV_UVBUF;              // halves: chunk [position]
 static_assert(RV_SZ_OFF + RV_POS * RV_SZG * 2 <= RC_LDS, "V reconstruction LDS");
 static_assert(8 * RV_WAVE_POS * C_PITCH <= RC_LDS, "V reconstruction epilogue LDS");
 
-template <bool Q> struct RvRaw { uint4 d[2][4]; };                       // dense: [N-tile][K-chunk]
-template <> struct RvRaw<true> { uint4 d[2]; };                          // group-64 int4: word kk = chunk kk
+template <int Q> struct RvRaw { uint4 d[2][4]; };                        // dense: [N-tile][K-chunk]
+template <> struct RvRaw<1> { uint4 d[2]; };                             // group-64 int4: word kk = chunk kk
+template <> struct RvRaw<2> { uint2 d[2][4]; };                          // per-token blocks: <= 8 bytes per chunk
 
-template <typename XT, bool Q>
+// Q: 0 dense act dtype, 1 group-64 int4 (scale and zero per (b, s, group)),
+// 2 per-token blocks (the reference int4 format with an optional int8 / int4
+// upper block, or int8; one scale per (b, s) and block)
+template <typename XT, int Q>
 __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -325,11 +377,20 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
   const int nks = (R + RC_KS - 1) / RC_KS;
 
   const uint8_t* xrow[2];
+  const uint8_t* xrow2[2];                           // per-token blocks: the lower (int4) block
+  uint16_t vsc[2] = {0, 0}, vsc2[2] = {0, 0};
+  const bool vlo = Q == 2 && R > a.vsplit;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int pc = min(pw + nt * 32 + n, S - 1);
     constexpr int64_t es = Q ? 1 : 2;
     xrow[nt] = (const uint8_t*)a.vx + (b * a.vx_sb + (int64_t)pc * a.vx_ss) * es;
+    xrow2[nt] = xrow[nt];
+    if constexpr (Q == 2) vsc[nt] = ((const uint16_t*)a.vscale)[b * a.vs_sb + (int64_t)pc * a.vs_ss];
+    if (vlo) {
+      xrow2[nt] = (const uint8_t*)a.vx2 + b * a.vx2_sb + (int64_t)pc * a.vx2_ss;
+      vsc2[nt] = ((const uint16_t*)a.vscale2)[b * a.vs2_sb + (int64_t)pc * a.vs2_ss];
+    }
   }
   uint32_t* szl = (uint32_t*)(lds + RV_SZ_OFF);
   auto sz_stage = [&](int ks) {                      // groups ks .. ks + RV_SZG - 1 of every position
@@ -351,7 +412,11 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
     const int j0 = ks * RC_KS + 32 * hh;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      if constexpr (Q) {
+      if constexpr (Q == 2) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          r.d[nt][kk] = pf_ld_block(xrow[nt], xrow2[nt], min(j0 + 8 * kk, R - 8), a.vsplit, a.v_a8);
+      } else if constexpr (Q == 1) {
         if (ks * RC_KS + RC_KS <= R) {
           r.d[nt] = *(const uint4*)(xrow[nt] + j0 / 2);
         } else {
@@ -393,7 +458,7 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
   auto step = [&](int ks, const Raw& cur) {
     const bool more = ks + 1 < nks;
     uint32_t sz[2] = {0, 0};
-    if constexpr (Q) {
+    if constexpr (Q == 1) {
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) sz[nt] = szl[(pl0 + nt * 32 + n) * RV_SZG + ks % RV_SZG];
     }
@@ -402,9 +467,13 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
       uint4 bf[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        if constexpr (Q) {
+        if constexpr (Q == 1) {
           const uint32_t w = kk == 0 ? cur.d[nt].x : kk == 1 ? cur.d[nt].y : kk == 2 ? cur.d[nt].z : cur.d[nt].w;
           bf[nt] = pf_dq_g64(w, (uint16_t)(sz[nt] & 0xffff), (uint16_t)(sz[nt] >> 16));
+          if constexpr (!__is_same(XT, _Float16)) bf[nt] = pf_f16_to_bf16(bf[nt]);
+        } else if constexpr (Q == 2) {
+          const int j = min(ks * RC_KS + 32 * hh + 8 * kk, R - 8);
+          bf[nt] = pf_dq_block(cur.d[nt][kk], j, a.vsplit, a.v_a8, vsc[nt], vsc2[nt]);
           if constexpr (!__is_same(XT, _Float16)) bf[nt] = pf_f16_to_bf16(bf[nt]);
         } else {
           bf[nt] = cur.d[nt][kk];
@@ -418,7 +487,7 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
       }
     }
     if (more) uv_store((ks + 1) & 1, ks + 1);
-    if constexpr (Q) {
+    if constexpr (Q == 1) {
       if (more && (ks + 1) % RV_SZG == 0) {
         __syncthreads();                             // everyone done with the old chunk
         sz_stage(ks + 1);
@@ -429,8 +498,8 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
 
   uv_load(0);
   uv_store(0, 0);
-  if constexpr (Q) sz_stage(0);
-  if constexpr (!Q) {
+  if constexpr (Q == 1) sz_stage(0);
+  if constexpr (Q == 0) {
     // dense latents: one step ahead (a step's fragments take 32 registers)
     Raw cur, nxt;
     load(0, cur);
@@ -688,13 +757,15 @@ static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t m
   r.rc_nb = (int)ceil_div(a.S, RC_POS);
   r.rc_blocks = r.rc_nb * B;
   const dim3 rg((unsigned)(ceil_div(r.rc_blocks, 8) * 8 * a.Hkv));
-  if (a.k_i8) hipLaunchKernelGGL((recon_kernel<XT, true>), rg, dim3(256), 0, st, r);
-  else hipLaunchKernelGGL((recon_kernel<XT, false>), rg, dim3(256), 0, st, r);
+  if (a.k_ref) hipLaunchKernelGGL((recon_kernel<XT, 2>), rg, dim3(256), 0, st, r);
+  else if (a.k_i8) hipLaunchKernelGGL((recon_kernel<XT, 1>), rg, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL((recon_kernel<XT, 0>), rg, dim3(256), 0, st, r);
   r.rv_nb = (int)ceil_div(a.S, RV_POS);
   r.rv_blocks = r.rv_nb * B;
   const dim3 vg((unsigned)(ceil_div(r.rv_blocks, 8) * 8 * ((a.Hkv + 1) / 2)));
-  if (a.v_g64) hipLaunchKernelGGL((recon_v_kernel<XT, true>), vg, dim3(512), 0, st, r);
-  else hipLaunchKernelGGL((recon_v_kernel<XT, false>), vg, dim3(512), 0, st, r);
+  if (a.v_blk) hipLaunchKernelGGL((recon_v_kernel<XT, 2>), vg, dim3(512), 0, st, r);
+  else if (a.v_g64) hipLaunchKernelGGL((recon_v_kernel<XT, 1>), vg, dim3(512), 0, st, r);
+  else hipLaunchKernelGGL((recon_v_kernel<XT, 0>), vg, dim3(512), 0, st, r);
   int e = (int)hipGetLastError();
   if (e) return e;
   if (mid && (e = (int)hipEventRecord(mid, st))) return e;

@@ -14,7 +14,10 @@ fp16 scale per block and token (22-25, 107-127).
   RoPE, softmax, P.V and the per-KV-head up-projection.  The caches are not
   repeated per query head (the reference repeats them, 146-147); GQA is
   handled by the kernels.
-* Prefill dequantises the caches and runs causal SDPA.
+* Causal prefill (no explicit mask) runs ``starkv_prefill_attention`` on the
+  same split caches: the kernels dequantise them bit-exactly while
+  reconstructing K (with RoPE) and V on MFMA, then flash attention.  With an
+  explicit mask, prefill dequantises the caches and runs masked SDPA.
 
 Keys are rotated by their own positions (the reference's no-kernel branch
 uses the last position for all keys, 28-35, 142).
@@ -29,7 +32,7 @@ import torch.nn.functional as F
 
 from ._lib import StarKVError
 from .LlamaLoRaAttention_headwise import _additive, _rotate_half
-from .ops import KLatentSpec, VLatentSpec, decode_attention
+from .ops import KLatentSpec, VLatentSpec, decode_attention, prefill_attention
 from .quant_utils import quantize_r_split_int8_int4_packed, unpack_uint8_to_int4_signed
 from .rope import RopeConfig
 
@@ -42,7 +45,7 @@ UPPER_RANKS_V = 256
 
 
 class LlamaCustomAttention(nn.Module):
-    """Llama attention over a quantised low-rank latent KV cache (decode on MI355X HIP kernels)."""
+    """Llama attention over a quantised low-rank latent KV cache (decode and causal prefill on MI355X HIP kernels)."""
 
     def __init__(self, config, layer_idx: Optional[int] = None, decomp_goup_num: Optional[int] = 1):
         super().__init__()
@@ -101,7 +104,16 @@ class LlamaCustomAttention(nn.Module):
         S = ku_q.shape[-2]
         mask = _additive(attention_mask, q.dtype)
 
-        if query_len > 1:
+        def specs():
+            kspec = KLatentSpec.from_reference_quant(ku_q, sku, self._k_basis(k_u), rk, x2=kl_q, s2=skl,
+                                                     split=UPPER_RANKS_K)
+            return kspec, VLatentSpec.int4_ref(vu_q, svu, rv, split=UPPER_RANKS_V, x2=vl_q, scale2=svl)
+
+        if query_len > 1 and mask is None and rk % 8 == 0 and rv % 8 == 0:
+            kspec, vspec = specs()
+            out = prefill_attention(q, kspec, vspec, v_u.weight, rope=self.rope, pos0=S - query_len,
+                                    scale=self.scaling)
+        elif query_len > 1:
             dt = q.dtype
             kx = torch.cat([(ku_q.to(torch.float32) * sku.float()).to(torch.float16),
                             (unpack_uint8_to_int4_signed(kl_q, r4_k).float() * skl.float()).to(torch.float16)], -1)
@@ -117,9 +129,7 @@ class LlamaCustomAttention(nn.Module):
                 torch.ones(query_len, S, dtype=torch.bool, device=q.device).tril(S - query_len)
             out = F.scaled_dot_product_attention(q, K, V, attn_mask=am, scale=self.scaling)
         else:
-            kspec = KLatentSpec.from_reference_quant(ku_q, sku, self._k_basis(k_u), rk, x2=kl_q, s2=skl,
-                                                     split=UPPER_RANKS_K)
-            vspec = VLatentSpec.int4_ref(vu_q, svu, rv, split=UPPER_RANKS_V, x2=vl_q, scale2=svl)
+            kspec, vspec = specs()
             m = mask[:, :, :, :S] if mask is not None else None
             out = decode_attention(q, kspec, vspec, v_u.weight, rope=self.rope, seq_len=S, mask=m,
                                    scale=self.scaling).unsqueeze(2)

@@ -434,8 +434,9 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
 
     q: rotated queries [B, Hq, T, 128] (last dim contiguous) at positions
     pos0 .. pos0 + T - 1; k / xv: the K and V latent caches holding at least
-    pos0 + T positions (K dense or int8, V dense [B, S, Rv] or a group-64 int4
-    VLatentSpec); uv_weight: v_proj.U.weight [Hkv*128, Rv].  ``events``:
+    pos0 + T positions (K dense, int8 or the reference split format; V dense
+    [B, S, Rv] or a quantised VLatentSpec: group-64 int4, int8 or the
+    reference split format); uv_weight: v_proj.U.weight [Hkv*128, Rv].  ``events``:
     three torch.cuda.Event recorded before the K / V reconstruction, after it
     and after the attention kernel (timing)."""
     if q.dim() != 4 or q.shape[-1] != HEAD_DIM or q.stride(-1) != 1:

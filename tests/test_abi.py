@@ -349,7 +349,7 @@ def test_prefill_workspace_holds_the_reconstructed_k_and_v():
 
 @pytest.mark.parametrize("what,code", [
     ("n_tokens0", ERR_SHAPE), ("pos0_neg", ERR_SHAPE), ("rope_short", ERR_SHAPE), ("head_dim", ERR_SHAPE),
-    ("k_int4", ERR_FORMAT), ("v_int8", ERR_FORMAT), ("k_rank_odd", ERR_SHAPE), ("v_rank_odd", ERR_SHAPE),
+    ("k_format", ERR_FORMAT), ("v_format", ERR_FORMAT), ("k_split_format", ERR_FORMAT), ("k_rank_odd", ERR_SHAPE), ("v_rank_odd", ERR_SHAPE),
     ("q_stride", ERR_ALIGN), ("q_null", ERR_NULL), ("uv_stride", ERR_ALIGN), ("gqa", ERR_SHAPE),
     ("dtype", ERR_DTYPE),
 ])
@@ -364,10 +364,12 @@ def test_prefill_rejects(what, code):
         d.rope_max_positions = 119
     elif what == "head_dim":
         d.head_dim = 64
-    elif what == "k_int4":
-        d.k.format, d.k.scale = L.FMT_INT4_REF, FAKE
-    elif what == "v_int8":
-        d.v.format, d.v.scale = L.FMT_INT8_SYM, FAKE
+    elif what == "k_format":
+        d.k.format, d.k.scale = 77, FAKE
+    elif what == "v_format":
+        d.v.format, d.v.scale = 77, FAKE
+    elif what == "k_split_format":
+        d.k.format, d.k.scale, d.k.split, d.k.split_format = L.FMT_INT4_REF, FAKE, 16, L.FMT_INT4_G64
     elif what == "k_rank_odd":
         d.k.rank[2] = 20
     elif what == "v_rank_odd":

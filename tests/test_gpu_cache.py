@@ -142,13 +142,13 @@ class _VProj(torch.nn.Module):
 
 
 @pytest.mark.gpu
-def test_quant_module_decode_matches_dequantised_history():
+def test_quant_module_prefill_and_decode_match_dequantised_history():
     from oracle import starkv_oracle as o
     from transformers import LlamaConfig
     from transformers.cache_utils import DynamicCache
     from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
     from starkv.LlamaLoRaAttention_headwise_quant import LlamaCustomAttention
-    _flush("[quant module] Hq=8 Hkv=2 r=80 Rv=512, prefill 33 + 3 decode steps")
+    _flush("[quant module] Hq=8 Hkv=2 r=80 Rv=512, prefill 33 (checked) + 3 decode steps")
     Hq, Hkv, r, Rv = 8, 2, 80, 512
     torch.manual_seed(0)
     cfg = LlamaConfig(hidden_size=Hq * HEAD, num_attention_heads=Hq, num_key_value_heads=Hkv,
@@ -162,28 +162,47 @@ def test_quant_module_decode_matches_dequantised_history():
     g = torch.Generator(device="cuda").manual_seed(4)
     hid = (torch.randn(B, P + 3, cfg.hidden_size, generator=g, device="cuda") * 0.5).half()
     caches = [DynamicCache() for _ in range(4)]
+
+    def dequantised():
+        """The module's own caches, dequantised: K [B, Hkv, S, r], V [B, S, Rv]."""
+        ku, vu = caches[0].layers[0].keys, caches[0].layers[0].values
+        kl, vl = caches[1].layers[0].keys, caches[1].layers[0].values
+        sku, svu = caches[2].layers[0].keys, caches[2].layers[0].values
+        skl, svl = caches[3].layers[0].keys, caches[3].layers[0].values
+        kx = np.concatenate([o.dequant_int8_sym(ku.cpu().numpy(), sku.cpu().numpy()),
+                             o.dequant_int4_ref(kl.cpu().numpy(), skl.cpu().numpy(), r - 16)], -1)
+        vx = np.concatenate([o.dequant_int8_sym(vu.cpu().numpy(), svu.cpu().numpy()),
+                             o.dequant_int4_ref(vl.cpu().numpy(), svl.cpu().numpy(), Rv - 256)], -1)
+        return kx, vx
+
+    bk = m.k_proj.U.double().cpu().transpose(-1, -2)
     with torch.no_grad():
         pos = torch.arange(P, device="cuda")[None].expand(B, P)
-        m(hid[:, :P], rot(hid[:, :P], pos), None, pos, *caches)
+        pre, _ = m(hid[:, :P], rot(hid[:, :P], pos), None, pos, *caches)
+        torch.cuda.synchronize()
+        # causal prefill (the HIP prefill kernels): fp64 causal attention over
+        # the dequantised caches, K and V rounded once to fp16 as the module
+        # materialises them in its dtype
+        kx, vx = dequantised()
+        q = (hid[:, :P].double().cpu() @ m.q_proj.weight.double().cpu().T).view(B, P, Hq, HEAD).transpose(1, 2)
+        cos, sin = o.rope_cos_sin(m.rope.inv_freq(), torch.arange(P))
+        q = o.apply_rope(q, cos.double(), sin.double())
+        core = o.prefill_attention(q, [bk[h] for h in range(Hkv)], [torch.from_numpy(kx[:, h]).double() for h in range(Hkv)],
+                                   torch.from_numpy(vx).double(), m.v_proj.U.weight.double().cpu(), cos.double(),
+                                   sin.double(), kv_dtype=torch.float16)
+        ref = core.transpose(1, 2).reshape(B, P, -1) @ m.o_proj.weight.double().cpu().T
+        check_output(pre, ref, f"prefill P={P} (o_proj output): ")
         for t in range(P, P + 3):
             pos = torch.full((B, 1), t, device="cuda")
             out, _ = m(hid[:, t:t + 1], rot(hid[:, t:t + 1], pos), None, pos, *caches)
             torch.cuda.synchronize()
             # fp64 attention over the module's own (dequantised) caches
-            ku, vu = caches[0].layers[0].keys, caches[0].layers[0].values
-            kl, vl = caches[1].layers[0].keys, caches[1].layers[0].values
-            sku, svu = caches[2].layers[0].keys, caches[2].layers[0].values
-            skl, svl = caches[3].layers[0].keys, caches[3].layers[0].values
-            kx = np.concatenate([o.dequant_int8_sym(ku.cpu().numpy(), sku.cpu().numpy()),
-                                 o.dequant_int4_ref(kl.cpu().numpy(), skl.cpu().numpy(), r - 16)], -1)
-            vx = np.concatenate([o.dequant_int8_sym(vu.cpu().numpy(), svu.cpu().numpy()),
-                                 o.dequant_int4_ref(vl.cpu().numpy(), svl.cpu().numpy(), Rv - 256)], -1)
+            kx, vx = dequantised()
             S = kx.shape[2]
             q = (hid[:, t:t + 1].double().cpu() @ m.q_proj.weight.double().cpu().T).view(B, 1, Hq, HEAD).transpose(1, 2)
             cos, sin = o.rope_cos_sin(m.rope.inv_freq(), torch.arange(t, t + 1))
             q = o.apply_rope(q[:, :, 0], cos.double(), sin.double())
             cos, sin = o.rope_cos_sin(m.rope.inv_freq(), torch.arange(S))
-            bk = m.k_proj.U.double().cpu().transpose(-1, -2)
             core, _, _ = o.decode_attention(q, [bk[h] for h in range(Hkv)], [torch.from_numpy(kx[:, h]).double() for h in range(Hkv)],
                                             torch.from_numpy(vx).double(), m.v_proj.U.weight.double().cpu(), cos.double(), sin.double())
             ref = core.reshape(B, 1, -1) @ m.o_proj.weight.double().cpu().T

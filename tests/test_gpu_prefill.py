@@ -65,6 +65,23 @@ def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0, r
         buf, offs, xk_dev = _dense_k(B, S, ranks, dtype, g)
         kspec = KLatentSpec(buf, ranks, offs, ranks, buf.stride(0), bk_all, bko, HEAD)
         xk = [x.double().cpu() for x in xk_dev]
+    elif kfmt.startswith("ref"):
+        # the reference module's split K cache (uniform rank): "ref8_U" / "ref4_U" = an int8 / int4
+        # upper block of U ranks over an int4 lower one, "ref4w" = all ranks int4
+        from test_gpu_quant_k import reference_split_k
+        r = ranks[0]
+        assert ranks == [r] * Hkv
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        bk = bk_all.view(Hkv, r, HEAD)
+        if kfmt == "ref4w":
+            q1, s1, _, _, deq = reference_split_k(B, Hkv, S, r, 0, "int4", seed=seed + 1)
+            kspec = KLatentSpec.from_reference_quant(dev(q1), dev(s1), bk, r)
+        else:
+            up = int(kfmt.split("_")[1])
+            q1, s1, q2, s2, deq = reference_split_k(B, Hkv, S, up, r - up, "int8" if kfmt[3] == "8" else "int4",
+                                                    seed=seed + 1)
+            kspec = KLatentSpec.from_reference_quant(dev(q1), dev(s1), bk, r, x2=dev(q2), s2=dev(s2), split=up)
+        xk = [torch.from_numpy(deq[:, h]).to(dtype).double() for h in range(Hkv)]
     else:
         from test_gpu_quant_k import ragged_int8_k
         kb, scales, offs, deq = ragged_int8_k(B, S, ranks, seed=seed + 1)
@@ -77,8 +94,11 @@ def _run(B, Hq, ranks, Rv, T, pos0, dtype, kfmt="dense", vfmt="dense", seed=0, r
         v = xv_dev
         xv = xv_dev.double().cpu()
     else:
+        # "g64", or a per-token block kind of make_quant_v ("ref_int4" / "ref_int8" with the upper
+        # block's width after a colon, "int8", "int4_whole")
         from test_gpu_quant import make_quant_v
-        v, dq, _ = make_quant_v("g64", B, S, Rv, seed=seed + 2)
+        kind, _, split = vfmt.partition(":")
+        v, dq, _ = make_quant_v(kind, B, S, Rv, split=int(split or 256), seed=seed + 2)
         xv = torch.from_numpy(dq.astype(np.float64)).to(dtype).double()
     uv = (torch.randn(Hkv * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).to(dtype)
     q = torch.randn(B, Hq, T, HEAD, generator=g, device="cuda").to(dtype)
@@ -104,6 +124,13 @@ CASES = [
     # an odd KV-head count leaves the last V head pair half empty; MQA has one KV head
     ("odd_hkv3_gqa2", 2, 6, [24, 64, 40], 72, 130, 5, torch.float16, "dense", "dense"),
     ("mqa_int8_g64", 1, 8, [96], 136, 300, 0, torch.float16, "int8", "g64"),
+    # the reference module's quantised caches: split K (int8 / int4 upper block over int4) and
+    # per-token block V (int8 / int4 upper block over int4, whole int8, whole int4)
+    ("ref8k_ref8v_f16", 2, 8, [80, 80], 512, 150, 0, torch.float16, "ref8_16", "ref_int8:256"),
+    ("ref8k_ref4v_bf16_chunk", 1, 8, [128] * 4, 384, 100, 37, torch.bfloat16, "ref8_16", "ref_int4:256"),
+    ("ref4k_int8v_mha", 2, 4, [64] * 4, 264, 129, 0, torch.float16, "ref4_32", "int8"),
+    ("ref4w_k_int4w_v", 1, 4, [48] * 2, 512, 257, 3, torch.bfloat16, "ref4w", "int4_whole"),
+    ("ref8k_ref8v_cfg_ranks", 1, 32, [128] * 8, 1640, 64, 200, torch.float16, "ref8_16", "ref_int8:256"),
 ]
 
 
@@ -141,23 +168,6 @@ def test_prefill_last_row_matches_decode():
     mx, mr = errors(pre[:, :, -1], dec)
     _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
     assert mx <= 2e-2 and mr <= 2e-3, (mx, mr)
-
-
-@pytest.mark.gpu
-def test_prefill_rejects_unsupported_formats():
-    from starkv import KLatentSpec, StarKVError, VLatentSpec, prefill_attention
-    from starkv._lib import FMT_INT4_REF
-    g = torch.Generator(device="cuda").manual_seed(3)
-    bk_all, bko, _ = _bk([16], torch.float16, g)
-    kb = torch.zeros(1, 64 * 8, dtype=torch.uint8, device="cuda")
-    sc = torch.ones(1, 1, 64, dtype=torch.float16, device="cuda")
-    kspec = KLatentSpec(kb, [16], [0], [8], kb.stride(0), bk_all, bko, HEAD, fmt=FMT_INT4_REF, scale=sc,
-                        scale_stride_b=64, scale_stride_h=64)
-    xv = torch.zeros(1, 64, 16, dtype=torch.float16, device="cuda")
-    uv = torch.zeros(HEAD, 16, dtype=torch.float16, device="cuda")
-    q = torch.zeros(1, 1, 64, HEAD, dtype=torch.float16, device="cuda")
-    with pytest.raises(StarKVError, match="format"):
-        prefill_attention(q, kspec, xv, uv)
 
 
 @pytest.mark.gpu
