@@ -24,7 +24,7 @@ extern "C" {
 
 /* Bumped on every change of a struct layout or of an entry point's meaning;
  * the Python binding refuses a library of another version. */
-#define STARKV_ABI_VERSION 2
+#define STARKV_ABI_VERSION 3
 
 /* element types */
 enum {
@@ -370,6 +370,49 @@ int starkv_prefill_attention(const starkv_prefill_desc* d, void* workspace, size
  * attention kernel (per-kernel timing, as starkv_decode_attention_timed). */
 int starkv_prefill_attention_timed(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes,
                                    void* stream, void* const* events);
+
+/* ---------------------------------------------------------------------
+ * The e2e decoder layer's own elementwise work.  No counterpart in the
+ * reference's attention path: these replace, in the end-to-end harness, the
+ * HF layers the reference's latency.py runs around the attention
+ * (transformers models/llama/modeling_llama.py: LlamaRMSNorm.forward, the
+ * residual adds of LlamaDecoderLayer.forward, LlamaMLP's act_fn(gate) * up),
+ * one launch each instead of torch's several.  act() below rounds to the
+ * activation dtype, as torch does after each fp16 / bf16 operation.
+ *
+ * starkv_rms_norm: for each of `rows` rows of `hidden` values,
+ *   x' = act(x + residual)   (when residual is given; stored to residual_out when that is given)
+ *   out = act(weight * act(x' * rsqrt(sum(x'^2) / hidden + eps)))   (sum and rsqrt in fp32)
+ * Row r of x at x + r * x_stride (elements), likewise residual, residual_out
+ * and out; weight [hidden].  hidden a multiple of 8 and <= 16384
+ * (STARKV_ERR_LIMIT); every pointer 16-byte aligned and every stride a
+ * multiple of 8 (STARKV_ERR_ALIGN).  out may alias x; residual_out may alias
+ * x or residual.
+ * ------------------------------------------------------------------- */
+typedef struct {
+  int rows, hidden, dtype;
+  const void* x; int64_t x_stride;
+  const void* residual; int64_t residual_stride;       /* optional */
+  void* residual_out; int64_t residual_out_stride;     /* optional (requires residual) */
+  const void* weight;
+  float eps;
+  void* out; int64_t out_stride;
+} starkv_rms_norm_desc;
+
+int starkv_rms_norm(const starkv_rms_norm_desc* d, void* stream);
+
+/* starkv_silu_mul: out = act(act(g / (1 + exp(-g))) * u) elementwise over
+ * `rows` rows of `width` values (gate row r at gate + r * gate_stride, up and
+ * out likewise; fp32 inside).  width a multiple of 8; pointers 16-byte
+ * aligned, strides multiples of 8 (STARKV_ERR_ALIGN). */
+typedef struct {
+  int rows, width, dtype;
+  const void* gate; int64_t gate_stride;
+  const void* up; int64_t up_stride;
+  void* out; int64_t out_stride;
+} starkv_silu_mul_desc;
+
+int starkv_silu_mul(const starkv_silu_mul_desc* d, void* stream);
 
 #ifdef __cplusplus
 }

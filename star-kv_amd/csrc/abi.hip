@@ -955,6 +955,43 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   return launch_v_append(a, d->dtype, (hipStream_t)stream);
 }
 
+// rows of act-dtype values: data 16-byte aligned, strides multiples of 8 elements
+static bool rows16(const void* p, int64_t stride) { return al(p, 16) && stride >= 0 && stride % 8 == 0; }
+
+int starkv_rms_norm(const starkv_rms_norm_desc* d, void* stream) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->rows < 0 || d->hidden < 8 || d->hidden % 8) return STARKV_ERR_SHAPE;
+  if (d->hidden > NORM_MAX_HIDDEN) return STARKV_ERR_LIMIT;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  if (!d->x || !d->weight || !d->out || (d->residual_out && !d->residual)) return STARKV_ERR_NULL;
+  if (!(d->eps >= 0.f)) return STARKV_ERR_SHAPE;
+  if (!rows16(d->x, d->x_stride) || !rows16(d->out, d->out_stride) || !al(d->weight, 16) ||
+      (d->residual && !rows16(d->residual, d->residual_stride)) ||
+      (d->residual_out && !rows16(d->residual_out, d->residual_out_stride)))
+    return STARKV_ERR_ALIGN;
+  NormArgs a = {};
+  a.x = d->x; a.xs = d->x_stride;
+  a.res = d->residual; a.rs = d->residual_stride;
+  a.res_out = d->residual_out; a.ros = d->residual_out_stride;
+  a.w = d->weight; a.out = d->out; a.os = d->out_stride;
+  a.rows = d->rows; a.H = d->hidden; a.eps = d->eps;
+  return launch_rms_norm(a, d->dtype, (hipStream_t)stream);
+}
+
+int starkv_silu_mul(const starkv_silu_mul_desc* d, void* stream) {
+  if (!d) return STARKV_ERR_NULL;
+  if (d->rows < 0 || d->width < 8 || d->width % 8) return STARKV_ERR_SHAPE;
+  if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
+  if (!d->gate || !d->up || !d->out) return STARKV_ERR_NULL;
+  if (!rows16(d->gate, d->gate_stride) || !rows16(d->up, d->up_stride) || !rows16(d->out, d->out_stride))
+    return STARKV_ERR_ALIGN;
+  if ((int64_t)d->rows * (d->width / 8) > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
+  SiluMulArgs a = {};
+  a.g = d->gate; a.gs = d->gate_stride; a.u = d->up; a.us = d->up_stride;
+  a.out = d->out; a.os = d->out_stride; a.rows = d->rows; a.W = d->width;
+  return launch_silu_mul(a, d->dtype, (hipStream_t)stream);
+}
+
 }  // extern "C"
 
 extern "C" {

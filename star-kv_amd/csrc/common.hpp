@@ -208,6 +208,26 @@ struct PFArgs {
   float scale_log2;                                // softmax scale * log2(e)
   void* out; int64_t o_sb, o_sh, o_st;             // (b, qh, t), act dtype
 };
+// ---------------------------------------------------------------------------
+// The e2e decoder layer's RMSNorm and SiLU-multiply (layer_ops.hip).
+// ---------------------------------------------------------------------------
+constexpr int NORM_MAX_HIDDEN = 16384;
+struct NormArgs {
+  const void* x; int64_t xs;                       // rows of H act-dtype values, strides in elements
+  const void* res; int64_t rs;                     // optional residual added first
+  void* res_out; int64_t ros;                      // optional: the sum x + res
+  const void* w;                                   // [H] weight
+  void* out; int64_t os;
+  int rows, H;
+  float eps;
+};
+struct SiluMulArgs {
+  const void* g; int64_t gs;
+  const void* u; int64_t us;
+  void* out; int64_t os;
+  int rows, W;
+};
+
 // both are passed by value as kernel arguments (at most 4 KiB)
 static_assert(sizeof(KArgs) <= 4096 && sizeof(PFArgs) <= 4096, "kernel argument size");
 
@@ -297,6 +317,8 @@ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 int rope_table_tiles(int max_positions);
 int launch_rope_table(const float* inv_freq_host, int max_positions, float scaling, void* table, hipStream_t st);
 int launch_rope_apply(const RopeApplyArgs& a, int dtype, hipStream_t st);
+int launch_rms_norm(const NormArgs& a, int dtype, hipStream_t st);
+int launch_silu_mul(const SiluMulArgs& a, int dtype, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
 int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
 int launch_k_logits_gqa(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);

@@ -152,6 +152,27 @@ class RopeApplyDesc(ctypes.Structure):
     ]
 
 
+class RmsNormDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int), ("hidden", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int64),
+        ("residual", ctypes.c_void_p), ("residual_stride", ctypes.c_int64),
+        ("residual_out", ctypes.c_void_p), ("residual_out_stride", ctypes.c_int64),
+        ("weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int64),
+    ]
+
+
+class SiluMulDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int), ("width", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("gate", ctypes.c_void_p), ("gate_stride", ctypes.c_int64),
+        ("up", ctypes.c_void_p), ("up_stride", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int64),
+    ]
+
+
 EXPORTS = (
     "starkv_abi_version", "starkv_status_string",
     "starkv_rope_table_bytes", "starkv_rope_build", "starkv_rope_apply",
@@ -161,9 +182,10 @@ EXPORTS = (
     "starkv_decode_attention_noalloc",
     "starkv_k_append", "starkv_v_append",
     "starkv_prefill_workspace_bytes", "starkv_prefill_attention", "starkv_prefill_attention_timed",
+    "starkv_rms_norm", "starkv_silu_mul",
 )
 
-ABI_VERSION = 2          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
+ABI_VERSION = 3          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
 NOALLOC_SCRATCH_BYTES = 128 << 20   # STARKV_NOALLOC_SCRATCH_BYTES
 
 _lib = None
@@ -213,6 +235,10 @@ def lib() -> ctypes.CDLL:
     if L.starkv_abi_version() != ABI_VERSION:
         raise StarKVError(f"{LIB_PATH} has ABI version {L.starkv_abi_version()}, this binding needs "
                           f"{ABI_VERSION}: rebuild it with `make -C star-kv_amd`")
+    L.starkv_rms_norm.restype = ctypes.c_int
+    L.starkv_rms_norm.argtypes = [ctypes.POINTER(RmsNormDesc), ctypes.c_void_p]
+    L.starkv_silu_mul.restype = ctypes.c_int
+    L.starkv_silu_mul.argtypes = [ctypes.POINTER(SiluMulDesc), ctypes.c_void_p]
     _lib = L
     return L
 

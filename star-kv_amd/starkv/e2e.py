@@ -28,7 +28,8 @@ from .cache import LatentCache
 from .ops import decode_attention, prefill_attention, rope_apply
 from .rope import RopeConfig
 
-__all__ = ["LatentAttention", "DecodeGraphState", "build_model", "generate", "generate_graphed", "decode_graphed"]
+__all__ = ["LatentAttention", "DecodeGraphState", "build_model", "fuse_layers_", "generate", "generate_graphed",
+           "decode_graphed"]
 
 HEAD_DIM = 128
 
@@ -153,10 +154,42 @@ class LatentAttention(nn.Module):
             o = F.scaled_dot_product_attention(qf, Kf, Vf, attn_mask=m, scale=self.scaling)
         return o.to(q.dtype)
 
+    def merge_projections_(self) -> None:
+        """Hold q_proj, k_vs and v_vs as row blocks of one weight ``qkv_weight``
+        (the three Linear weights become views of it), so the projections of
+        the layer input run as one GEMM; the Linear modules keep working."""
+        with torch.no_grad():
+            w = torch.cat([self.q_proj.weight, self.k_vs.weight, self.v_vs.weight], 0).contiguous()
+        self.register_buffer("qkv_weight", w, persistent=False)
+        rows = [self.q_proj.weight.shape[0], self.k_vs.weight.shape[0], self.v_vs.weight.shape[0]]
+        off = 0
+        for lin, n in zip((self.q_proj, self.k_vs, self.v_vs), rows):
+            lin.weight = nn.Parameter(w[off:off + n], requires_grad=False)
+            off += n
+
+    def _project(self, hidden_states: torch.Tensor):
+        """(q [B, Hq, T, 128], new K latent rows [B, T, sum(r)], new V latent rows [B, T, Rv])."""
+        B, T, _ = hidden_states.shape
+        w = getattr(self, "qkv_weight", None)
+        if w is None or self.reference:
+            q = self.q_proj(hidden_states)
+            return (q.view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2), self.k_vs(hidden_states),
+                    self.v_vs(hidden_states))
+        nq, nk = self.n_heads * HEAD_DIM, sum(self.ranks)
+        qkv = F.linear(hidden_states, w)
+        return (qkv[..., :nq].view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2), qkv[..., nq:nq + nk],
+                qkv[..., nq + nk:])
+
     def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None, past_key_values=None,
                 use_cache=False, position_embeddings=None, **kwargs):
         B, T, _ = hidden_states.shape
-        q = self.q_proj(hidden_states).view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2)
+        o = self.core(hidden_states, position_embeddings)
+        return self.o_proj(o), None
+
+    def core(self, hidden_states: torch.Tensor, position_embeddings=None) -> torch.Tensor:
+        """The attention of the layer input without the output projection: [B, T, Hq*128]."""
+        B, T, _ = hidden_states.shape
+        q, k_new, v_new = self._project(hidden_states)
         if self.reference:
             cos, sin = position_embeddings
             q = q * cos.unsqueeze(1) + _rotate_half(q) * sin.unsqueeze(1)
@@ -165,14 +198,13 @@ class LatentAttention(nn.Module):
                        error_flag=self.graph.error)
         else:
             rope_apply(q, self.rope, pos0=self.cache.length)     # positions continue the cache
-        k_new = self.k_vs(hidden_states)                    # [B, T, sum(r)]: the writer takes the heads packed
+        # k_new [B, T, sum(r)]: the writer takes the heads packed
         if self.graph is not None and T == 1 and not self.reference:
-            kspec, vspec = self.cache.append_at(k_new, self.v_vs(hidden_states), self.bk, self.graph.pos,
-                                                error_flag=self.graph.error)
+            kspec, vspec = self.cache.append_at(k_new, v_new, self.bk, self.graph.pos, error_flag=self.graph.error)
             o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope,
                                  seq_len=self.graph.capacity, scale=self.scaling, mask=self.graph.mask)
-            return self.o_proj(o.unsqueeze(1).reshape(B, T, self.n_heads * HEAD_DIM)), None
-        kspec, vspec, S = self.cache.append(k_new, self.v_vs(hidden_states), self.bk)
+            return o.unsqueeze(1).reshape(B, T, self.n_heads * HEAD_DIM)
+        kspec, vspec, S = self.cache.append(k_new, v_new, self.bk)
         if T > 1 and not self.reference:
             o = prefill_attention(q, kspec, vspec, self.v_u.weight, rope=self.rope, pos0=S - T,
                                   scale=self.scaling).transpose(1, 2)               # [B, T, Hq, 128]
@@ -188,16 +220,71 @@ class LatentAttention(nn.Module):
             o = o.unsqueeze(1)                                                      # [B, 1, Hq, 128]
         else:
             o = self._attend_torch(q, S, T).transpose(1, 2)                         # [B, T, Hq, 128]
-        return self.o_proj(o.reshape(B, T, self.n_heads * HEAD_DIM)), None
+        return o.reshape(B, T, self.n_heads * HEAD_DIM)
+
+
+def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None,
+                           past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
+    """LlamaDecoderLayer.forward (transformers models/llama/modeling_llama.py)
+    with the layer's own elementwise work in single launches: RMSNorm on
+    ``starkv_rms_norm``, the residual adds folded into the o_proj and down_proj
+    GEMMs (addmm: one rounding instead of two), gate and up projections as one
+    GEMM and SiLU(gate) * up on ``starkv_silu_mul``.  The reference path
+    (``self_attn.reference``) runs HF's own forward."""
+    from .ops import rms_norm, silu_mul
+    att = self.self_attn
+    if att.reference:
+        return type(self).forward(self, hidden_states, attention_mask=attention_mask, position_ids=position_ids,
+                                  past_key_values=past_key_values, use_cache=use_cache,
+                                  position_embeddings=position_embeddings, **kwargs)
+    B, T, Hd = hidden_states.shape
+    x = rms_norm(hidden_states, self.input_layernorm.weight, self.input_layernorm.variance_epsilon)
+    o = att.core(x, position_embeddings)
+    h = torch.addmm(hidden_states.reshape(-1, Hd), o.reshape(B * T, -1), att.o_proj.weight.t())
+    n = rms_norm(h, self.post_attention_layernorm.weight, self.post_attention_layernorm.variance_epsilon)
+    m = silu_mul(F.linear(n, self.mlp.gate_up_weight))
+    return torch.addmm(h, m, self.mlp.down_proj.weight.t()).view(B, T, Hd)
+
+
+def _fused_norm_forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+    """LlamaRMSNorm.forward in one launch (``starkv_rms_norm``); HF's own
+    forward while ``starkv_reference`` is set (``generate(reference=True)``)."""
+    from .ops import rms_norm
+    if getattr(self, "starkv_reference", False):
+        return type(self).forward(self, hidden_states)
+    return rms_norm(hidden_states, self.weight, self.variance_epsilon)
+
+
+def fuse_layers_(model) -> None:
+    """Run every decoder layer of ``model`` (and the final norm) through
+    ``_fused_decoder_forward``: q / k / v latent projections and the MLP's
+    gate / up projections merged into one weight each (the HF Linear weights
+    become views of them, so nothing is duplicated and HF's forward still
+    works), the norms and activation on the library's kernels."""
+    import types
+    for layer in model.model.layers:
+        layer.self_attn.merge_projections_()
+        mlp = layer.mlp
+        with torch.no_grad():
+            w = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).contiguous()
+        mlp.register_buffer("gate_up_weight", w, persistent=False)
+        n = mlp.gate_proj.weight.shape[0]
+        mlp.gate_proj.weight = nn.Parameter(w[:n], requires_grad=False)
+        mlp.up_proj.weight = nn.Parameter(w[n:], requires_grad=False)
+        layer.forward = types.MethodType(_fused_decoder_forward, layer)
+    model.model.norm.forward = types.MethodType(_fused_norm_forward, model.model.norm)
 
 
 def build_model(n_layers: int, hidden: int, heads: int, kv_heads: int, intermediate: int, vocab: int,
                 ranks: Sequence[int], v_rank: int, batch: int, capacity: int, fmt: str = "int8_g64",
-                seed: int = 0, device="cuda", dtype=torch.float16, projections: Optional[Sequence] = None):
+                seed: int = 0, device="cuda", dtype=torch.float16, projections: Optional[Sequence] = None,
+                fused: bool = True):
     """Random-init LlamaForCausalLM with every attention replaced by LatentAttention.
 
     `projections`: per layer, an exported `LatentProjections` whose ranks and
-    weights replace `ranks`, `v_rank` and the random latent projections."""
+    weights replace `ranks`, `v_rank` and the random latent projections.
+    `fused`: run the decoder layers through ``fuse_layers_`` (HF's own layer
+    forward otherwise; the reference path always uses HF's)."""
     from transformers import LlamaConfig, LlamaForCausalLM
     cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=intermediate,
                       num_hidden_layers=n_layers, num_attention_heads=heads, num_key_value_heads=kv_heads,
@@ -220,6 +307,8 @@ def build_model(n_layers: int, hidden: int, heads: int, kv_heads: int, intermedi
         if p is not None:
             att.load_projections(p)
         layer.self_attn = att
+    if fused:
+        fuse_layers_(model)
     return model
 
 
@@ -236,6 +325,7 @@ def generate(model, prompt: torch.Tensor, steps: int, reference: bool = False,
     Returns (tokens [B, steps + 1], logits of the last position per forward)."""
     for att in attention_layers(model):
         att.reference = reference
+    model.model.norm.starkv_reference = reference
     B, P = prompt.shape
     dev = prompt.device
     out = model(input_ids=prompt, position_ids=torch.arange(P, device=dev)[None].expand(B, P),
@@ -260,6 +350,7 @@ def generate_graphed(model, prompt: torch.Tensor, steps: int, keep_logits: bool 
     position per forward, or [] when ``keep_logits`` is False)."""
     for att in attention_layers(model):
         att.reference = False
+    model.model.norm.starkv_reference = False
     B, P = prompt.shape
     dev = prompt.device
     out = model(input_ids=prompt, position_ids=torch.arange(P, device=dev)[None].expand(B, P),

@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KAppendDesc,
-                   PrefillDesc, RopeApplyDesc,
+                   PrefillDesc, RmsNormDesc, RopeApplyDesc, SiluMulDesc,
                    KLatent, KLogitsDesc, PVDesc, StarKVError, VAppendDesc, VLatent, check, i64_array, int_array)
 from .rope import RopeConfig, rope_table
 
@@ -583,3 +583,75 @@ def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int,
     d.pos0_device = _pos_ptr(pos0_device)
     d.error_flag = _flag_ptr(error_flag)
     check(_lib.lib().starkv_v_append(ctypes.byref(d), _stream(src.device)), "starkv_v_append")
+
+
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    """t viewed as [rows, width] rows with a contiguous last dim (a copy-free view or an error)."""
+    if t.stride(-1) != 1:
+        raise StarKVError(f"{name} must have a contiguous last dim")
+    try:
+        return t.view(-1, t.shape[-1])
+    except RuntimeError:
+        raise StarKVError(f"{name} rows must be addressable with one row stride") from None
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: Optional[torch.Tensor] = None,
+             out: Optional[torch.Tensor] = None, residual_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """HF LlamaRMSNorm over the last dim in one launch (starkv_rms_norm),
+    optionally after the residual add that precedes it in the decoder layer:
+    x' = x + residual (stored to ``residual_out`` when given), then
+    weight * (x' * rsqrt(mean(x'^2) + eps)) with HF's roundings.  Returns out."""
+    _require_cuda(x, weight)
+    xr = _rows(x, "x")
+    H = x.shape[-1]
+    if weight.shape != (H,) or weight.dtype != x.dtype or not weight.is_contiguous():
+        raise StarKVError("weight must be a contiguous [hidden] tensor of x's dtype")
+    if out is None:
+        out = torch.empty_like(x)
+    d = RmsNormDesc()
+    d.rows, d.hidden, d.dtype = xr.shape[0], H, _dt(x)
+    d.x, d.x_stride = xr.data_ptr(), xr.stride(0)
+    for name, t in (("out", out), ("residual", residual), ("residual_out", residual_out)):
+        if t is not None and (t.shape != x.shape or t.dtype != x.dtype or t.device != x.device):
+            raise StarKVError(f"{name} must match x's shape, dtype and device")
+    if residual_out is not None and residual is None:
+        raise StarKVError("residual_out needs residual")
+    orr = _rows(out, "out")
+    d.out, d.out_stride = orr.data_ptr(), orr.stride(0)
+    if residual is not None:
+        rr = _rows(residual, "residual")
+        d.residual, d.residual_stride = rr.data_ptr(), rr.stride(0)
+    if residual_out is not None:
+        ro = _rows(residual_out, "residual_out")
+        d.residual_out, d.residual_out_stride = ro.data_ptr(), ro.stride(0)
+    d.weight, d.eps = weight.data_ptr(), float(eps)
+    check(_lib.lib().starkv_rms_norm(ctypes.byref(d), _stream(x.device)), "starkv_rms_norm")
+    return out
+
+
+def silu_mul(gate: torch.Tensor, up: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """LlamaMLP's SiLU(gate) * up in one launch (starkv_silu_mul).  With
+    ``up`` None, ``gate`` holds [..., 2 I] = the gate and up halves of one
+    merged projection.  Returns [..., I] in gate's dtype."""
+    _require_cuda(gate)
+    if up is None:
+        if gate.shape[-1] % 2:
+            raise StarKVError("a merged gate/up tensor has an even last dim")
+        W = gate.shape[-1] // 2
+        g, u = gate[..., :W], gate[..., W:]
+    else:
+        if up.shape != gate.shape or up.dtype != gate.dtype:
+            raise StarKVError("gate and up must match in shape and dtype")
+        W, g, u = gate.shape[-1], gate, up
+    if out is None:
+        out = torch.empty(*g.shape, dtype=gate.dtype, device=gate.device)
+    if out.shape != g.shape or out.dtype != gate.dtype:
+        raise StarKVError("out must be [..., I] of gate's dtype")
+    gr, ur, orr = _rows(g, "gate"), _rows(u, "up"), _rows(out, "out")
+    d = SiluMulDesc()
+    d.rows, d.width, d.dtype = gr.shape[0], W, _dt(gate)
+    d.gate, d.gate_stride = gr.data_ptr(), gr.stride(0)
+    d.up, d.up_stride = ur.data_ptr(), ur.stride(0)
+    d.out, d.out_stride = orr.data_ptr(), orr.stride(0)
+    check(_lib.lib().starkv_silu_mul(ctypes.byref(d), _stream(gate.device)), "starkv_silu_mul")
+    return out

@@ -44,7 +44,7 @@ def test_version_and_status_strings():
     header_version = int(m.group(1))
     # the library, the header and the ctypes mirrors must agree: a struct
     # layout change bumps all three together
-    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 2
+    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 3
     for code in (OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_RANK, ERR_WORKSPACE, ERR_LIMIT, ERR_FORMAT):
         s = lib.starkv_status_string(code).decode()
         assert s and s != "unknown error"
@@ -77,6 +77,9 @@ int main(void) {
   F(starkv_prefill_desc, q_stride_t) F(starkv_prefill_desc, k) F(starkv_prefill_desc, v) F(starkv_prefill_desc, uv)
   F(starkv_prefill_desc, rope_table) F(starkv_prefill_desc, scale) F(starkv_prefill_desc, out)
   F(starkv_prefill_desc, out_stride_t)
+  S(starkv_rms_norm_desc) F(starkv_rms_norm_desc, x) F(starkv_rms_norm_desc, residual_out_stride)
+  F(starkv_rms_norm_desc, weight) F(starkv_rms_norm_desc, eps) F(starkv_rms_norm_desc, out_stride)
+  S(starkv_silu_mul_desc) F(starkv_silu_mul_desc, gate) F(starkv_silu_mul_desc, up_stride) F(starkv_silu_mul_desc, out)
   return 0;
 }
 """
@@ -84,7 +87,8 @@ int main(void) {
 _PY = {"starkv_klatent": L.KLatent, "starkv_klogits_desc": L.KLogitsDesc, "starkv_vlatent": L.VLatent,
        "starkv_pv_desc": L.PVDesc, "starkv_decode_desc": L.DecodeDesc,
        "starkv_prefill_desc": L.PrefillDesc, "starkv_k_append_desc": L.KAppendDesc,
-       "starkv_v_append_desc": L.VAppendDesc, "starkv_rope_apply_desc": L.RopeApplyDesc}
+       "starkv_v_append_desc": L.VAppendDesc, "starkv_rope_apply_desc": L.RopeApplyDesc,
+       "starkv_rms_norm_desc": L.RmsNormDesc, "starkv_silu_mul_desc": L.SiluMulDesc}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
@@ -423,3 +427,37 @@ def test_cache_writer_limits_and_device_positions():
     v.pos0_device, v.batch, v.n_tokens, v.capacity = None, 1, 9, 8
     assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_SHAPE
 
+
+
+# ---------------------------------------------------------------- e2e layer ops
+
+def _norm_desc(**kw):
+    d = L.RmsNormDesc()
+    d.rows, d.hidden, d.dtype = 8, 4096, L.F16
+    d.x, d.x_stride, d.weight, d.eps, d.out, d.out_stride = FAKE, 4096, FAKE, 1e-6, FAKE, 4096
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(hidden=4100), ERR_SHAPE), (dict(hidden=16392), ERR_LIMIT), (dict(rows=-1), ERR_SHAPE),
+    (dict(dtype=L.F32), ERR_DTYPE), (dict(weight=None), ERR_NULL), (dict(residual_out=FAKE), ERR_NULL),
+    (dict(x_stride=4100), ERR_ALIGN), (dict(out=FAKE + 8), ERR_ALIGN), (dict(eps=-1.0), ERR_SHAPE),
+    (dict(residual=FAKE, residual_stride=12), ERR_ALIGN),
+])
+def test_rms_norm_rejects(kw, code):
+    assert L.lib().starkv_rms_norm(ctypes.byref(_norm_desc(**kw)), None) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(width=12), ERR_SHAPE), (dict(dtype=L.F32), ERR_DTYPE), (dict(up=None), ERR_NULL),
+    (dict(gate_stride=22020), ERR_ALIGN), (dict(out=FAKE + 2), ERR_ALIGN),
+])
+def test_silu_mul_rejects(kw, code):
+    d = L.SiluMulDesc()
+    d.rows, d.width, d.dtype = 8, 11008, L.F16
+    d.gate, d.gate_stride, d.up, d.up_stride, d.out, d.out_stride = FAKE, 22016, FAKE + 22016, 22016, FAKE, 11008
+    for k, v in kw.items():
+        setattr(d, k, v)
+    assert L.lib().starkv_silu_mul(ctypes.byref(d), None) == code
