@@ -414,6 +414,27 @@ typedef struct {
 
 int starkv_silu_mul(const starkv_silu_mul_desc* d, void* stream);
 
+/* starkv_skinny_gemm: the decode-batch projections of the e2e decoder layer
+ * (nn.Linear y = x W^T with m <= 16 rows, where the weight stream bounds the
+ * time), fp32 accumulation, one rounding:
+ *   epilogue 0: out[i][j]  = act(sum_k x[i][k] w[j][k])              (j < n)
+ *   epilogue 1: out[i][j]  = act(sum_k x[i][k] w[j][k] + out[i][j])  (the residual add, in place)
+ *   epilogue 2: g = act(x . w[j]), u = act(x . w[j + n/2]):
+ *               out[i][j]  = act(act(g / (1 + exp(-g))) * u)        (j < n/2; LlamaMLP over the
+ *               gate rows followed by the up rows of one merged weight)
+ * x [m][k] row stride x_stride, w [n][k] row stride w_stride, out row stride
+ * out_stride (elements).  k a multiple of 32, n a multiple of 16 (32 for
+ * epilogue 2), m <= 16 (STARKV_ERR_LIMIT); x and w 16-byte aligned with
+ * strides multiples of 8 (STARKV_ERR_ALIGN). */
+typedef struct {
+  int m, n, k, dtype, epilogue;
+  const void* x; int64_t x_stride;
+  const void* w; int64_t w_stride;
+  void* out; int64_t out_stride;
+} starkv_skinny_gemm_desc;
+
+int starkv_skinny_gemm(const starkv_skinny_gemm_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

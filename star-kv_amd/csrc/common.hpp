@@ -228,6 +228,15 @@ struct SiluMulArgs {
   int rows, W;
 };
 
+constexpr int GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SILU_MUL = 2;
+constexpr int GEMM_MAX_M = 16, GEMM_MAX_WAVES = 16, GEMM_TARGET_WAVES = 4096;
+struct GemmArgs {
+  const void* x; int64_t xs;                       // [M][K] activations, row stride (elements)
+  const void* w; int64_t ws;                       // [N][K] weight (nn.Linear layout), row stride
+  void* out; int64_t os;                           // [M][N] (SILU_MUL: [M][half_rows])
+  int M, N, K, half_rows;
+};
+
 // both are passed by value as kernel arguments (at most 4 KiB)
 static_assert(sizeof(KArgs) <= 4096 && sizeof(PFArgs) <= 4096, "kernel argument size");
 
@@ -319,6 +328,7 @@ int launch_rope_table(const float* inv_freq_host, int max_positions, float scali
 int launch_rope_apply(const RopeApplyArgs& a, int dtype, hipStream_t st);
 int launch_rms_norm(const NormArgs& a, int dtype, hipStream_t st);
 int launch_silu_mul(const SiluMulArgs& a, int dtype, hipStream_t st);
+int launch_skinny_gemm(const GemmArgs& a, int dtype, int epi, hipStream_t st);
 int launch_k_logits(const KArgs& a, int dtype, int fmt, bool out_f32, int out_dtype, bool fast, int B, hipStream_t st);
 int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
 int launch_k_logits_gqa(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);

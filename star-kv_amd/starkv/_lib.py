@@ -173,6 +173,16 @@ class SiluMulDesc(ctypes.Structure):
     ]
 
 
+class SkinnyGemmDesc(ctypes.Structure):
+    _fields_ = [
+        ("m", ctypes.c_int), ("n", ctypes.c_int), ("k", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("epilogue", ctypes.c_int),
+        ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int64),
+        ("w", ctypes.c_void_p), ("w_stride", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int64),
+    ]
+
+
 EXPORTS = (
     "starkv_abi_version", "starkv_status_string",
     "starkv_rope_table_bytes", "starkv_rope_build", "starkv_rope_apply",
@@ -182,7 +192,7 @@ EXPORTS = (
     "starkv_decode_attention_noalloc",
     "starkv_k_append", "starkv_v_append",
     "starkv_prefill_workspace_bytes", "starkv_prefill_attention", "starkv_prefill_attention_timed",
-    "starkv_rms_norm", "starkv_silu_mul",
+    "starkv_rms_norm", "starkv_silu_mul", "starkv_skinny_gemm",
 )
 
 ABI_VERSION = 3          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
@@ -239,6 +249,8 @@ def lib() -> ctypes.CDLL:
     L.starkv_rms_norm.argtypes = [ctypes.POINTER(RmsNormDesc), ctypes.c_void_p]
     L.starkv_silu_mul.restype = ctypes.c_int
     L.starkv_silu_mul.argtypes = [ctypes.POINTER(SiluMulDesc), ctypes.c_void_p]
+    L.starkv_skinny_gemm.restype = ctypes.c_int
+    L.starkv_skinny_gemm.argtypes = [ctypes.POINTER(SkinnyGemmDesc), ctypes.c_void_p]
     _lib = L
     return L
 

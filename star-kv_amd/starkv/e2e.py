@@ -25,7 +25,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .cache import LatentCache
-from .ops import decode_attention, prefill_attention, rope_apply
+from .ops import (GEMM_ADD, GEMM_SILU_MUL, SKINNY_MAX_ROWS, decode_attention, prefill_attention, rope_apply,
+                  skinny_linear)
 from .rope import RopeConfig
 
 __all__ = ["LatentAttention", "DecodeGraphState", "build_model", "fuse_layers_", "generate", "generate_graphed",
@@ -176,7 +177,10 @@ class LatentAttention(nn.Module):
             return (q.view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2), self.k_vs(hidden_states),
                     self.v_vs(hidden_states))
         nq, nk = self.n_heads * HEAD_DIM, sum(self.ranks)
-        qkv = F.linear(hidden_states, w)
+        if B * T <= SKINNY_MAX_ROWS and hidden_states.shape[-1] % 32 == 0 and w.shape[0] % 16 == 0:
+            qkv = skinny_linear(hidden_states, w)                 # decode: one weight stream
+        else:
+            qkv = F.linear(hidden_states, w)
         return (qkv[..., :nq].view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2), qkv[..., nq:nq + nk],
                 qkv[..., nq + nk:])
 
@@ -228,9 +232,12 @@ def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=Non
     """LlamaDecoderLayer.forward (transformers models/llama/modeling_llama.py)
     with the layer's own elementwise work in single launches: RMSNorm on
     ``starkv_rms_norm``, the residual adds folded into the o_proj and down_proj
-    GEMMs (addmm: one rounding instead of two), gate and up projections as one
-    GEMM and SiLU(gate) * up on ``starkv_silu_mul``.  The reference path
-    (``self_attn.reference``) runs HF's own forward."""
+    GEMMs (one rounding instead of two), gate and up projections as one GEMM
+    followed by SiLU(gate) * up.  Decode batches (at most 16 rows) run the
+    projections on ``starkv_skinny_gemm`` (the residual add and the SiLU
+    product in its epilogue); larger ones on torch's GEMMs (addmm) and
+    ``starkv_silu_mul``.  The reference path (``self_attn.reference``) runs
+    HF's own forward."""
     from .ops import rms_norm, silu_mul
     att = self.self_attn
     if att.reference:
@@ -240,10 +247,26 @@ def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=Non
     B, T, Hd = hidden_states.shape
     x = rms_norm(hidden_states, self.input_layernorm.weight, self.input_layernorm.variance_epsilon)
     o = att.core(x, position_embeddings)
-    h = torch.addmm(hidden_states.reshape(-1, Hd), o.reshape(B * T, -1), att.o_proj.weight.t())
+    # the residual stream is updated in place (an out-of-place addmm first
+    # copies its input): the layer input is the previous layer's output or
+    # the embedding lookup, which nothing reads after this layer
+    h = hidden_states.reshape(-1, Hd)
+    if h.data_ptr() != hidden_states.data_ptr() or not h.is_contiguous():
+        h = h.clone()
+    o = o.reshape(B * T, -1)
+    w_o, w_gu, w_d = att.o_proj.weight, self.mlp.gate_up_weight, self.mlp.down_proj.weight
+    skinny = (B * T <= SKINNY_MAX_ROWS and all(t.shape[1] % 32 == 0 and t.shape[0] % 32 == 0 and t.stride(1) == 1
+                                                 for t in (w_o, w_gu, w_d)))
+    if skinny:
+        skinny_linear(o, w_o, out=h, epilogue=GEMM_ADD)
+    else:
+        h.addmm_(o, w_o.t())
     n = rms_norm(h, self.post_attention_layernorm.weight, self.post_attention_layernorm.variance_epsilon)
-    m = silu_mul(F.linear(n, self.mlp.gate_up_weight))
-    return torch.addmm(h, m, self.mlp.down_proj.weight.t()).view(B, T, Hd)
+    if skinny:
+        skinny_linear(skinny_linear(n, w_gu, epilogue=GEMM_SILU_MUL), w_d, out=h, epilogue=GEMM_ADD)
+    else:
+        h.addmm_(silu_mul(F.linear(n, w_gu)), w_d.t())
+    return h.view(B, T, Hd)
 
 
 def _fused_norm_forward(self, hidden_states: torch.Tensor) -> torch.Tensor:

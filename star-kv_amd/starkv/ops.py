@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import (BF16, F16, F32, FMT_DENSE, FMT_INT4_G64, FMT_INT4_REF, FMT_INT8_SYM, DecodeDesc, KAppendDesc,
-                   PrefillDesc, RmsNormDesc, RopeApplyDesc, SiluMulDesc,
+                   PrefillDesc, RmsNormDesc, RopeApplyDesc, SiluMulDesc, SkinnyGemmDesc,
                    KLatent, KLogitsDesc, PVDesc, StarKVError, VAppendDesc, VLatent, check, i64_array, int_array)
 from .rope import RopeConfig, rope_table
 
@@ -654,4 +654,37 @@ def silu_mul(gate: torch.Tensor, up: Optional[torch.Tensor] = None, out: Optiona
     d.up, d.up_stride = ur.data_ptr(), ur.stride(0)
     d.out, d.out_stride = orr.data_ptr(), orr.stride(0)
     check(_lib.lib().starkv_silu_mul(ctypes.byref(d), _stream(gate.device)), "starkv_silu_mul")
+    return out
+
+
+SKINNY_MAX_ROWS = 16
+GEMM_STORE, GEMM_ADD, GEMM_SILU_MUL = 0, 1, 2
+
+
+def skinny_linear(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None,
+                  epilogue: int = GEMM_STORE) -> torch.Tensor:
+    """nn.Linear x W^T for decode batches (at most 16 rows of x over its
+    leading dims) on starkv_skinny_gemm.  ``epilogue``: GEMM_STORE (out =
+    x W^T), GEMM_ADD (out += x W^T, in place: the residual add) or
+    GEMM_SILU_MUL (weight = gate rows then up rows: out = SiLU(x Wg^T) *
+    (x Wu^T)).  Returns out [..., n] (n/2 for GEMM_SILU_MUL)."""
+    _require_cuda(x, weight)
+    xr = _rows(x, "x")
+    if weight.dim() != 2 or weight.stride(1) != 1 or weight.shape[1] != x.shape[-1] or weight.dtype != x.dtype:
+        raise StarKVError("weight must be [n, k] of x's dtype with a contiguous last dim, k = x.shape[-1]")
+    n = weight.shape[0]
+    n_out = n // 2 if epilogue == GEMM_SILU_MUL else n
+    if out is None:
+        if epilogue == GEMM_ADD:
+            raise StarKVError("GEMM_ADD accumulates into a given out")
+        out = torch.empty(*x.shape[:-1], n_out, dtype=x.dtype, device=x.device)
+    if out.shape != (*x.shape[:-1], n_out) or out.dtype != x.dtype:
+        raise StarKVError(f"out must be [..., {n_out}] of x's dtype")
+    orr = _rows(out, "out")
+    d = SkinnyGemmDesc()
+    d.m, d.n, d.k, d.dtype, d.epilogue = xr.shape[0], n, x.shape[-1], _dt(x), int(epilogue)
+    d.x, d.x_stride = xr.data_ptr(), xr.stride(0)
+    d.w, d.w_stride = weight.data_ptr(), weight.stride(0)
+    d.out, d.out_stride = orr.data_ptr(), orr.stride(0)
+    check(_lib.lib().starkv_skinny_gemm(ctypes.byref(d), _stream(x.device)), "starkv_skinny_gemm")
     return out

@@ -80,6 +80,8 @@ int main(void) {
   S(starkv_rms_norm_desc) F(starkv_rms_norm_desc, x) F(starkv_rms_norm_desc, residual_out_stride)
   F(starkv_rms_norm_desc, weight) F(starkv_rms_norm_desc, eps) F(starkv_rms_norm_desc, out_stride)
   S(starkv_silu_mul_desc) F(starkv_silu_mul_desc, gate) F(starkv_silu_mul_desc, up_stride) F(starkv_silu_mul_desc, out)
+  S(starkv_skinny_gemm_desc) F(starkv_skinny_gemm_desc, epilogue) F(starkv_skinny_gemm_desc, x)
+  F(starkv_skinny_gemm_desc, w_stride) F(starkv_skinny_gemm_desc, out_stride)
   return 0;
 }
 """
@@ -88,7 +90,8 @@ _PY = {"starkv_klatent": L.KLatent, "starkv_klogits_desc": L.KLogitsDesc, "stark
        "starkv_pv_desc": L.PVDesc, "starkv_decode_desc": L.DecodeDesc,
        "starkv_prefill_desc": L.PrefillDesc, "starkv_k_append_desc": L.KAppendDesc,
        "starkv_v_append_desc": L.VAppendDesc, "starkv_rope_apply_desc": L.RopeApplyDesc,
-       "starkv_rms_norm_desc": L.RmsNormDesc, "starkv_silu_mul_desc": L.SiluMulDesc}
+       "starkv_rms_norm_desc": L.RmsNormDesc, "starkv_silu_mul_desc": L.SiluMulDesc,
+       "starkv_skinny_gemm_desc": L.SkinnyGemmDesc}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
@@ -461,3 +464,18 @@ def test_silu_mul_rejects(kw, code):
     for k, v in kw.items():
         setattr(d, k, v)
     assert L.lib().starkv_silu_mul(ctypes.byref(d), None) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(m=17), ERR_LIMIT), (dict(m=0), ERR_SHAPE), (dict(k=4100), ERR_SHAPE), (dict(n=4104), ERR_SHAPE),
+    (dict(epilogue=3), ERR_SHAPE), (dict(epilogue=2, n=4112), ERR_SHAPE), (dict(dtype=L.F32), ERR_DTYPE),
+    (dict(w=None), ERR_NULL), (dict(x_stride=4000), ERR_SHAPE), (dict(out_stride=100), ERR_SHAPE),
+    (dict(w_stride=4100), ERR_ALIGN), (dict(x=FAKE + 8), ERR_ALIGN), (dict(out=FAKE + 1), ERR_ALIGN),
+])
+def test_skinny_gemm_rejects(kw, code):
+    d = L.SkinnyGemmDesc()
+    d.m, d.n, d.k, d.dtype, d.epilogue = 8, 4096, 4096, L.F16, 0
+    d.x, d.x_stride, d.w, d.w_stride, d.out, d.out_stride = FAKE, 4096, FAKE, 4096, FAKE, 4096
+    for k, v in kw.items():
+        setattr(d, k, v)
+    assert L.lib().starkv_skinny_gemm(ctypes.byref(d), None) == code

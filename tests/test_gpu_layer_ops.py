@@ -97,6 +97,52 @@ def test_silu_mul_matches_torch(dtype, rows, width):
     assert u <= 2.0
 
 
+GEMM_CASES = [
+    # m, n, k, epilogue, dtype
+    (8, 7376, 4096, 0, torch.float16), (8, 4096, 4096, 1, torch.float16), (8, 22016, 4096, 2, torch.float16),
+    (8, 4096, 11008, 1, torch.float16), (1, 256, 32, 0, torch.float16), (16, 512, 1056, 0, torch.bfloat16),
+    (3, 1024, 2048, 2, torch.bfloat16), (13, 2048, 736, 1, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=[f"m{c[0]}n{c[1]}k{c[2]}e{c[3]}{str(c[4])[-4:]}" for c in GEMM_CASES])
+def test_skinny_gemm_matches_fp32(case):
+    """starkv_skinny_gemm against the fp32 product rounded as torch rounds it:
+    epilogue 0 act(x W^T); 1 act(x W^T + out); 2 act(act(silu(act(g))) act(u)).
+    The fp32 sums run in another order than the reference's, so the gate is
+    one rounding of the output plus the fp32 accumulation error
+    (k 2^-24 sum |x||w|)."""
+    from starkv.ops import skinny_linear
+    m, n, k, epi, dtype = case
+    _flush(f"[skinny gemm] m={m} n={n} k={k} epilogue={epi} {dtype}")
+    g = torch.Generator(device="cuda").manual_seed(m * 31 + n + k)
+    x = torch.randn(m, k, generator=g, device="cuda").to(dtype)
+    w = (torch.randn(n, k, generator=g, device="cuda") / k ** 0.5).to(dtype)
+    acc = x.double() @ w.double().t()
+    bound = k * 2.0 ** -24 * (x.double().abs() @ w.double().abs().t())
+    if epi == 2:
+        h = n // 2
+        gt, up = acc[:, :h].to(dtype), acc[:, h:].to(dtype)
+        ref = (F.silu(gt.float()).to(dtype).double() * up.double())
+        out = skinny_linear(x, w, epilogue=2)
+        bound = 4 * bound[:, :h] + 2.0 ** -8 * ref.abs()          # two roundings of the inputs feed the product
+    elif epi == 1:
+        res = torch.randn(m, n, generator=g, device="cuda").to(dtype)
+        ref = acc + res.double()
+        out = res.clone()
+        skinny_linear(x, w, out=out, epilogue=1)
+    else:
+        ref = acc
+        out = skinny_linear(x, w)
+    torch.cuda.synchronize()
+    ulp = 2.0 ** -(10 if dtype == torch.float16 else 7)
+    err = (out.double() - ref).abs()
+    lim = bound + ulp * ref.abs() + 2.0 ** -24
+    worst = float((err / lim).max())
+    _flush(f"   worst error / bound = {worst:.3f}")
+    assert worst <= 1.0
+
+
 @pytest.mark.parametrize("T", [1, 37])
 def test_fused_decoder_layer_matches_hf_forward(T):
     """One decoder layer of the e2e model through the fused forward against
@@ -119,7 +165,8 @@ def test_fused_decoder_layer_matches_hf_forward(T):
         pos = torch.arange(T, device="cuda")[None].expand(2, T)
         pe = m.model.rotary_emb(h, pos)
         with torch.no_grad():
-            outs.append(layer(h, attention_mask=None, position_ids=pos, position_embeddings=pe))
+            # the fused forward updates its input (the residual stream) in place
+            outs.append(layer(h.clone(), attention_mask=None, position_ids=pos, position_embeddings=pe))
     torch.cuda.synchronize()
     mx, mr = errors(outs[0], outs[1])
     _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
