@@ -423,7 +423,7 @@ int starkv_silu_mul(const starkv_silu_mul_desc* d, void* stream);
  *               out[i][j]  = act(act(g / (1 + exp(-g))) * u)        (j < n/2; LlamaMLP over the
  *               gate rows followed by the up rows of one merged weight)
  * x [m][k] row stride x_stride, w [n][k] row stride w_stride, out row stride
- * out_stride (elements).  k a multiple of 32, n a multiple of 16 (32 for
+ * out_stride (elements).  k a multiple of 64, n a multiple of 16 (32 for
  * epilogue 2), m <= 16 (STARKV_ERR_LIMIT); x and w 16-byte aligned with
  * strides multiples of 8 (STARKV_ERR_ALIGN). */
 typedef struct {

@@ -994,7 +994,7 @@ int starkv_silu_mul(const starkv_silu_mul_desc* d, void* stream) {
 
 int starkv_skinny_gemm(const starkv_skinny_gemm_desc* d, void* stream) {
   if (!d) return STARKV_ERR_NULL;
-  if (d->m < 1 || d->k < 32 || d->k % 32 || d->n < 16 || d->n % 16) return STARKV_ERR_SHAPE;
+  if (d->m < 1 || d->k < 64 || d->k % 64 || d->n < 16 || d->n % 16) return STARKV_ERR_SHAPE;
   if (d->m > GEMM_MAX_M) return STARKV_ERR_LIMIT;
   if (d->epilogue < GEMM_STORE || d->epilogue > GEMM_SILU_MUL) return STARKV_ERR_SHAPE;
   if (d->epilogue == GEMM_SILU_MUL && d->n % 32) return STARKV_ERR_SHAPE;

@@ -229,12 +229,13 @@ struct SiluMulArgs {
 };
 
 constexpr int GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SILU_MUL = 2;
-constexpr int GEMM_MAX_M = 16, GEMM_MAX_WAVES = 16, GEMM_TARGET_WAVES = 4096;
-struct GemmArgs {
+constexpr int GEMM_MAX_M = 16, GEMM_MAX_WAVES = 8, GEMM_MAX_STAGES = 8, GEMM_PAIRS_PER_STAGE = 4;
+struct GemmArgs {                                  // skinny_gemm.hip
   const void* x; int64_t xs;                       // [M][K] activations, row stride (elements)
   const void* w; int64_t ws;                       // [N][K] weight (nn.Linear layout), row stride
   void* out; int64_t os;                           // [M][N] (SILU_MUL: [M][half_rows])
   int M, N, K, half_rows;
+  int nst, pps;                                    // LDS ring stages per wave, 64-k pairs per stage (launcher)
 };
 
 // both are passed by value as kernel arguments (at most 4 KiB)

@@ -19,8 +19,6 @@
 // Both are HBM-bound (2-3 bytes moved per element and a handful of VALU
 // operations); at decode batch sizes they are latency-bound single waves of
 // small workgroups, which is the point: one launch instead of several.
-#include <algorithm>
-
 #include "common.hpp"
 
 namespace starkv {
@@ -130,125 +128,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const SiluMulArgs a) {
     o[e] = s * elem_f32<T>(u, e);
   }
   *(uint4*)((uint8_t*)a.out + (row * a.os + (int64_t)c * 8) * 2) = pack8<T>(o);
-}
-
-// ---------------------------------------------------------------------------
-// Skinny GEMM for decode batches (M <= 16 activation rows):
-//   out[m][n] (=|+=) sum_k x[m][k] W[n][k]      (nn.Linear: y = x W^T)
-// The weight is streamed once, so the kernel is an HBM weight stream with
-// 8-16 flops per weight byte.  A workgroup owns NT tiles of 16 output columns
-// (16 weight rows each) and its waves split the K range; wave w runs
-// v_mfma_f32_16x16x32 over its steps of 32 k: B operand = 16 weight rows x
-// 32 k (lane (c, g) holds row c, k 8g..8g+7: one 16-byte load; cached, as a
-// non-temporal load of half a 128-byte line measured 10-25 % slower),
-// A operand = the activation rows (lane (c, g) holds row min(c, M-1), same k;
-// rows >= M are never stored), eight steps of loads in flight per wave.  The
-// waves' 16x16 fp32 partials meet in LDS and wave 0 applies the epilogue:
-//   GEMM_STORE     out = act(acc)
-//   GEMM_ADD       out = act(acc + out)        (the residual add, in place)
-//   GEMM_SILU_MUL  tile 0 = gate rows n, tile 1 = up rows n + half_rows:
-//                  out = act(act(silu(act(acc_g))) * act(acc_u))   (LlamaMLP's
-//                  act_fn(gate_proj(x)) * up_proj(x) with torch's roundings)
-// ---------------------------------------------------------------------------
-constexpr int GEMM_UNROLL = 8;
-
-__device__ inline floatx4 mfma16(uint4 a, uint4 b, floatx4 c, _Float16*) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0, 0, 0);
-}
-__device__ inline floatx4 mfma16(uint4 a, uint4 b, floatx4 c, __bf16*) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
-                                                 0);
-}
-
-
-template <typename T, int NT, int EPI>
-__global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const GemmArgs a) {
-  __shared__ floatx4 red[GEMM_MAX_WAVES - 1][NT][64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int c = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16 * (EPI == GEMM_SILU_MUL ? 1 : NT);
-  const int steps = a.K >> 5;
-  const int s0 = (int)((int64_t)steps * w / nw), s1 = (int)((int64_t)steps * (w + 1) / nw);
-  const uint8_t* xr = (const uint8_t*)a.x + ((int64_t)min(c, a.M - 1) * a.xs + 8 * g) * 2;
-  const uint8_t* wr[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int64_t row = n0 + c + (EPI == GEMM_SILU_MUL ? t * (int64_t)a.half_rows : 16 * t);
-    wr[t] = (const uint8_t*)a.w + (row * a.ws + 8 * g) * 2;
-  }
-  floatx4 acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  int s = s0;
-  for (; s + GEMM_UNROLL <= s1; s += GEMM_UNROLL) {
-    uint4 xa[GEMM_UNROLL], wb[GEMM_UNROLL][NT];
-#pragma unroll
-    for (int u = 0; u < GEMM_UNROLL; ++u) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) wb[u][t] = *(const uint4*)(wr[t] + (int64_t)(s + u) * 64);
-      xa[u] = *(const uint4*)(xr + (int64_t)(s + u) * 64);
-    }
-#pragma unroll
-    for (int u = 0; u < GEMM_UNROLL; ++u)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] = mfma16(xa[u], wb[u][t], acc[t], (T*)nullptr);
-  }
-  for (; s < s1; ++s) {
-    const uint4 xa = *(const uint4*)(xr + (int64_t)s * 64);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = mfma16(xa, *(const uint4*)(wr[t] + (int64_t)s * 64), acc[t], (T*)nullptr);
-  }
-
-  if (w > 0) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) red[w - 1][t][lane] = acc[t];
-  }
-  __syncthreads();
-  if (w > 0) return;
-  for (int v = 0; v < nw - 1; ++v)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] += red[v][t][lane];
-  // lane (c, g) holds rows 4g .. 4g+3 of column c
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int m = 4 * g + e;
-    if (m >= a.M) break;
-    if constexpr (EPI == GEMM_SILU_MUL) {
-      const float gt = round_act<T>(acc[0][e]), up = round_act<T>(acc[1][e]);
-      const float sl = round_act<T>(gt / (1.0f + expf(-gt)));
-      ((T*)a.out)[m * a.os + n0 + c] = (T)(sl * up);
-    } else {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        T* o = (T*)a.out + m * a.os + n0 + 16 * t + c;
-        float v = acc[t][e];
-        if constexpr (EPI == GEMM_ADD) v += (float)*o;
-        *o = (T)v;
-      }
-    }
-  }
-}
-
-template <typename T>
-static int launch_gemm_t(const GemmArgs& a, int epi, int nw, hipStream_t st) {
-  const dim3 block(64 * nw);
-  if (epi == GEMM_SILU_MUL) {
-    hipLaunchKernelGGL((skinny_gemm_kernel<T, 2, GEMM_SILU_MUL>), dim3(a.half_rows / 16), block, 0, st, a);
-  } else if (epi == GEMM_ADD) {
-    hipLaunchKernelGGL((skinny_gemm_kernel<T, 1, GEMM_ADD>), dim3(a.N / 16), block, 0, st, a);
-  } else {
-    hipLaunchKernelGGL((skinny_gemm_kernel<T, 1, GEMM_STORE>), dim3(a.N / 16), block, 0, st, a);
-  }
-  return (int)hipGetLastError();
-}
-
-int launch_skinny_gemm(const GemmArgs& a, int dtype, int epi, hipStream_t st) {
-  if (a.M == 0) return 0;
-  // waves per workgroup: split K so that about GEMM_TARGET_WAVES stream the weight
-  const int n_wg = epi == GEMM_SILU_MUL ? a.half_rows / 16 : a.N / 16;
-  const int nw = std::max(1, std::min({GEMM_MAX_WAVES, GEMM_TARGET_WAVES / n_wg, a.K / 32}));
-  return dtype == STARKV_F16 ? launch_gemm_t<_Float16>(a, epi, nw, st) : launch_gemm_t<__bf16>(a, epi, nw, st);
 }
 
 int launch_rms_norm(const NormArgs& a, int dtype, hipStream_t st) {

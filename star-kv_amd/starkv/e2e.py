@@ -177,7 +177,7 @@ class LatentAttention(nn.Module):
             return (q.view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2), self.k_vs(hidden_states),
                     self.v_vs(hidden_states))
         nq, nk = self.n_heads * HEAD_DIM, sum(self.ranks)
-        if B * T <= SKINNY_MAX_ROWS and hidden_states.shape[-1] % 32 == 0 and w.shape[0] % 16 == 0:
+        if B * T <= SKINNY_MAX_ROWS and hidden_states.shape[-1] % 64 == 0 and w.shape[0] % 16 == 0:
             qkv = skinny_linear(hidden_states, w)                 # decode: one weight stream
         else:
             qkv = F.linear(hidden_states, w)
@@ -255,7 +255,7 @@ def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=Non
         h = h.clone()
     o = o.reshape(B * T, -1)
     w_o, w_gu, w_d = att.o_proj.weight, self.mlp.gate_up_weight, self.mlp.down_proj.weight
-    skinny = (B * T <= SKINNY_MAX_ROWS and all(t.shape[1] % 32 == 0 and t.shape[0] % 32 == 0 and t.stride(1) == 1
+    skinny = (B * T <= SKINNY_MAX_ROWS and all(t.shape[1] % 64 == 0 and t.shape[0] % 32 == 0 and t.stride(1) == 1
                                                  for t in (w_o, w_gu, w_d)))
     if skinny:
         skinny_linear(o, w_o, out=h, epilogue=GEMM_ADD)

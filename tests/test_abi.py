@@ -467,7 +467,7 @@ def test_silu_mul_rejects(kw, code):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(m=17), ERR_LIMIT), (dict(m=0), ERR_SHAPE), (dict(k=4100), ERR_SHAPE), (dict(n=4104), ERR_SHAPE),
+    (dict(m=17), ERR_LIMIT), (dict(m=0), ERR_SHAPE), (dict(k=4100), ERR_SHAPE), (dict(k=4128), ERR_SHAPE), (dict(n=4104), ERR_SHAPE),
     (dict(epilogue=3), ERR_SHAPE), (dict(epilogue=2, n=4112), ERR_SHAPE), (dict(dtype=L.F32), ERR_DTYPE),
     (dict(w=None), ERR_NULL), (dict(x_stride=4000), ERR_SHAPE), (dict(out_stride=100), ERR_SHAPE),
     (dict(w_stride=4100), ERR_ALIGN), (dict(x=FAKE + 8), ERR_ALIGN), (dict(out=FAKE + 1), ERR_ALIGN),

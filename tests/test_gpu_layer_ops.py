@@ -100,8 +100,9 @@ def test_silu_mul_matches_torch(dtype, rows, width):
 GEMM_CASES = [
     # m, n, k, epilogue, dtype
     (8, 7376, 4096, 0, torch.float16), (8, 4096, 4096, 1, torch.float16), (8, 22016, 4096, 2, torch.float16),
-    (8, 4096, 11008, 1, torch.float16), (1, 256, 32, 0, torch.float16), (16, 512, 1056, 0, torch.bfloat16),
-    (3, 1024, 2048, 2, torch.bfloat16), (13, 2048, 736, 1, torch.bfloat16),
+    (8, 4096, 11008, 1, torch.float16), (1, 256, 64, 0, torch.float16), (16, 512, 1088, 0, torch.bfloat16),
+    (3, 1024, 2048, 2, torch.bfloat16), (13, 2048, 704, 1, torch.bfloat16), (8, 32000, 4096, 0, torch.float16),
+    (9, 96, 192, 2, torch.float16),
 ]
 
 
