@@ -323,6 +323,16 @@ typedef struct {
 int starkv_k_append(const starkv_k_append_desc* d, void* stream);
 int starkv_v_append(const starkv_v_append_desc* d, void* stream);
 
+/* starkv_decode_append: starkv_k_append(k), starkv_v_append(v) and, when q
+ * is not NULL, starkv_rope_apply(q) in one launch -- the three small writes
+ * before a decode step's attention (the reference's DynamicLayer.update,
+ * HF:cache_utils.py:127-146, and the query half of model.py:423), with the
+ * same results, validation and status codes as the three calls; all three
+ * descriptors must carry one dtype (STARKV_ERR_DTYPE).  For launch-bound
+ * decode loops: one kernel instead of three. */
+int starkv_decode_append(const starkv_k_append_desc* k, const starkv_v_append_desc* v,
+                         const starkv_rope_apply_desc* q, void* stream);
+
 /* ---------------------------------------------------------------------
  * starkv_prefill_attention — replaces the reference prefill branch
  * model.py:429-449 (materialise key_full = RoPE(X_k @ B_k) and

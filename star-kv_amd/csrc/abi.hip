@@ -878,7 +878,7 @@ int starkv_decode_attention_noalloc(const starkv_decode_desc* d, void* stream) {
   return decode_impl(d, ws, STARKV_NOALLOC_SCRATCH_BYTES, stream, nullptr);
 }
 
-int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
+static int build_rope_apply(const starkv_rope_apply_desc* d, RopeApplyArgs& a) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->n_heads < 1 || d->n_tokens < 0 || d->pos0 < 0) return STARKV_ERR_SHAPE;
   if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
@@ -887,14 +887,20 @@ int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
   if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->rope_max_positions) return STARKV_ERR_SHAPE;
   // one thread per (row, frequency); HIP keeps grid x block below 2^32
   if ((int64_t)d->batch * d->n_heads * d->n_tokens * 64 > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
-  RopeApplyArgs a;
+  a = RopeApplyArgs{};
   a.x = d->x; a.sb = d->stride_b; a.sh = d->stride_h; a.st = d->stride_t;
   a.B = d->batch; a.H = d->n_heads; a.T = d->n_tokens; a.pos0 = d->pos0; a.max_pos = d->rope_max_positions;
   a.pos0_dev = d->pos0_device; a.err = d->error_flag; a.table = d->rope_table;
-  return launch_rope_apply(a, d->dtype, (hipStream_t)stream);
+  return STARKV_OK;
 }
 
-int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
+int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream) {
+  RopeApplyArgs a;
+  const int st = build_rope_apply(d, a);
+  return st ? st : launch_rope_apply(a, d->dtype, (hipStream_t)stream);
+}
+
+static int build_k_append(const starkv_k_append_desc* d, KAppendArgs& a) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;
   if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
@@ -906,7 +912,7 @@ int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
   if (d->src_stride_b < 0 || d->src_stride_h < 0 || d->src_stride_t < 0) return STARKV_ERR_SHAPE;
   // one wave (64 threads) per row
   if ((int64_t)d->batch * k.n_kv_heads * d->n_tokens * 64 > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
-  KAppendArgs a = {};
+  a = KAppendArgs{};
   a.src = d->src; a.src_sb = d->src_stride_b; a.src_sh = d->src_stride_h; a.src_st = d->src_stride_t;
   a.B = d->batch; a.H = k.n_kv_heads; a.T = d->n_tokens; a.pos0 = d->pos0; a.cap = d->capacity;
   a.pos0_dev = d->pos0_device; a.err = d->error_flag;
@@ -926,10 +932,16 @@ int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
     a.src_off[h] = d->src_head_offset ? d->src_head_offset[h] : h * d->src_stride_h;
     if (a.src_off[h] < 0) return STARKV_ERR_SHAPE;
   }
-  return launch_k_append(a, d->dtype, (hipStream_t)stream);
+  return STARKV_OK;
 }
 
-int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
+int starkv_k_append(const starkv_k_append_desc* d, void* stream) {
+  KAppendArgs a;
+  const int st = build_k_append(d, a);
+  return st ? st : launch_k_append(a, d->dtype, (hipStream_t)stream);
+}
+
+static int build_v_append(const starkv_v_append_desc* d, VAppendArgs& a) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->n_tokens < 0 || d->pos0 < 0 || d->capacity < 1 || d->capacity > MAX_S) return STARKV_ERR_SHAPE;
   if (!d->pos0_device && (int64_t)d->pos0 + d->n_tokens > d->capacity) return STARKV_ERR_SHAPE;
@@ -942,7 +954,7 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   // one wave per row (group-64: per row and group of 64 ranks)
   const int64_t waves_per_row = vq == VQ_G64 ? ceil_div(d->v.rank, 64) : 1;
   if ((int64_t)d->batch * d->n_tokens * waves_per_row * 64 > MAX_THREADS_1D) return STARKV_ERR_LIMIT;
-  VAppendArgs a = {};
+  a = VAppendArgs{};
   a.src = d->src; a.src_sb = d->src_stride_b; a.src_st = d->src_stride_t;
   a.B = d->batch; a.T = d->n_tokens; a.pos0 = d->pos0; a.cap = d->capacity; a.R = d->v.rank; a.vq = vq;
   a.pos0_dev = d->pos0_device; a.err = d->error_flag;
@@ -952,7 +964,28 @@ int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
   a.split = pa.split; a.a_int8 = pa.a_int8;
   a.data2 = (void*)pa.x2; a.stride2_b = pa.x2_sb; a.stride2_s = pa.x2_ss;
   a.scale2 = (void*)pa.xs2; a.sc2_sb = pa.xs2_sb; a.sc2_ss = pa.xs2_ss;
-  return launch_v_append(a, d->dtype, (hipStream_t)stream);
+  return STARKV_OK;
+}
+
+int starkv_v_append(const starkv_v_append_desc* d, void* stream) {
+  VAppendArgs a;
+  const int st = build_v_append(d, a);
+  return st ? st : launch_v_append(a, d->dtype, (hipStream_t)stream);
+}
+
+int starkv_decode_append(const starkv_k_append_desc* k, const starkv_v_append_desc* v,
+                         const starkv_rope_apply_desc* q, void* stream) {
+  StepAppendArgs a = {};
+  int st;
+  if ((st = build_k_append(k, a.k)) || (st = build_v_append(v, a.v))) return st;
+  if (q && (st = build_rope_apply(q, a.r))) return st;
+  if (v->dtype != k->dtype || (q && q->dtype != k->dtype)) return STARKV_ERR_DTYPE;
+  a.has_rope = q != nullptr;
+  const int64_t nb = ceil_div((int64_t)k->batch * k->k.n_kv_heads * k->n_tokens, 4) +
+                     ceil_div((int64_t)v->batch * v->n_tokens * ceil_div(v->v.rank, 64), 4) +
+                     (q ? ceil_div((int64_t)q->batch * q->n_heads * q->n_tokens * 64, 256) : 0);
+  if (nb > INT32_MAX) return STARKV_ERR_LIMIT;
+  return launch_step_append(a, k->dtype, (hipStream_t)stream);
 }
 
 // rows of act-dtype values: data 16-byte aligned, strides multiples of 8 elements

@@ -165,6 +165,8 @@ struct RopeApplyArgs {
   const void* table;
 };
 
+// In-place rotation of [B][H][T][128] rows by the table: one thread per
+// (row, frequency i < 64), computing both halves in fp32 and rounding once.
 // ---------------------------------------------------------------------------
 // Prefill arguments (prefill.hip).
 // ---------------------------------------------------------------------------
@@ -238,8 +240,18 @@ struct GemmArgs {                                  // skinny_gemm.hip
   int nst, pps;                                    // LDS ring stages per wave, 64-k pairs per stage (launcher)
 };
 
-// both are passed by value as kernel arguments (at most 4 KiB)
-static_assert(sizeof(KArgs) <= 4096 && sizeof(PFArgs) <= 4096, "kernel argument size");
+// A decode step's cache writes and query rotation in one launch (quant.hip)
+struct StepAppendArgs {
+  KAppendArgs k;
+  VAppendArgs v;
+  RopeApplyArgs r;
+  int has_rope;
+  int64_t nbk, nbv;                                // workgroups of the K and V writes (set by the launcher)
+};
+
+// these are passed by value as kernel arguments (at most 4 KiB)
+static_assert(sizeof(KArgs) <= 4096 && sizeof(PFArgs) <= 4096 && sizeof(StepAppendArgs) <= 4096,
+              "kernel argument size");
 
 // ---------------------------------------------------------------------------
 // small helpers
@@ -344,6 +356,36 @@ int up_chunk_sets(int n_kv, int n_sl, int n_c2);      // chunk sets per (slice, 
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);
+int launch_step_append(const StepAppendArgs& a, int dtype, hipStream_t st);
 int launch_prefill(const PFArgs& a, int dtype, int B, hipStream_t st, hipEvent_t mid);   // mid: after K/V
+
+// In-place RoPE of one (query row, frequency i < 64) element pair by the
+// table, in fp32 and rounded once; rows whose run-time position falls outside
+// the table are left as they are and set the error flag.
+// The (cos, sin) pair of (position p, frequency i) is fp16 element pair
+// ((p/32*8 + i/8)*64 + (i%8)/4*32 + p%32)*8 + 2*(i%4) of the table.
+template <typename T>
+__device__ inline void rope_apply_row(const RopeApplyArgs& a, int64_t idx) {
+  const int64_t rows = (int64_t)a.B * a.H * a.T;
+  if (idx >= rows * 64) return;
+  const int i = (int)(idx & 63);
+  const int64_t row = idx >> 6;
+  const int t = (int)(row % a.T);
+  const int h = (int)((row / a.T) % a.H);
+  const int b = (int)(row / ((int64_t)a.T * a.H));
+  const int p = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t;
+  if (p < 0 || p >= a.max_pos) {                 // only a run-time position can land here
+    if (a.err != nullptr) *a.err = 1;
+    return;
+  }
+  T* x = (T*)a.x + b * a.sb + h * a.sh + (int64_t)t * a.st;
+  const int64_t te = ((int64_t)((p >> 5) * 8 + (i >> 3)) * 64 + ((i & 7) >> 2) * 32 + (p & 31)) * 8 + 2 * (i & 3);
+  const uint32_t cs = ((const uint32_t*)a.table)[te >> 1];
+  const kh2 c2 = __builtin_bit_cast(kh2, cs);
+  const float c = (float)c2[0], sn = (float)c2[1];
+  const float x0 = to_f32(x[i]), x1 = to_f32(x[i + 64]);
+  x[i] = (T)(x0 * c - x1 * sn);
+  x[i + 64] = (T)(x1 * c + x0 * sn);
+}
 
 }  // namespace starkv

@@ -87,11 +87,11 @@ __device__ void quant_g64(const T* x, int R, int g0, uint8_t* q, uint16_t* sp, u
   }
 }
 
-// one row per wave; 4 waves per workgroup
+// one row per wave; 4 waves per workgroup (blk: the workgroup's index)
 template <typename T>
-__global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
+__device__ inline void k_append_rows(const KAppendArgs& a, int64_t blk) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = blk * 4 + (threadIdx.x >> 6);
   if (row >= (int64_t)a.B * a.H * a.T) return;
   const int t = (int)(row % a.T), h = (int)((row / a.T) % a.H), b = (int)(row / ((int64_t)a.T * a.H));
   const int s = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t, r = a.rank[h];
@@ -118,9 +118,9 @@ __global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
 
 // one row per wave; group-64 int4: one (row, group) per wave
 template <typename T>
-__global__ __launch_bounds__(256) void v_append_kernel(const VAppendArgs a) {
+__device__ inline void v_append_rows(const VAppendArgs& a, int64_t blk) {
   const int lane = threadIdx.x & 63;
-  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t wid = blk * 4 + (threadIdx.x >> 6);
   const int64_t row = wid / a.gw;
   const int grp = (int)(wid - row * a.gw);
   if (row >= (int64_t)a.B * a.T) return;
@@ -148,6 +148,47 @@ __global__ __launch_bounds__(256) void v_append_kernel(const VAppendArgs a) {
     uint16_t* s2 = (uint16_t*)a.scale2 + b * a.sc2_sb + (int64_t)s * a.sc2_ss;
     quant_block(x, a.split, R, false, q2, s2, lane);
   }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_append_kernel(const KAppendArgs a) {
+  k_append_rows<T>(a, blockIdx.x);
+}
+template <typename T>
+__global__ __launch_bounds__(256) void v_append_kernel(const VAppendArgs a) {
+  v_append_rows<T>(a, blockIdx.x);
+}
+
+// A decode step's three small writes in one launch: workgroups [0, nbk) write
+// the K rows, [nbk, nbk + nbv) the V rows, the rest rotate the query rows
+// (64 threads per row, as rope_apply_kernel).
+template <typename T>
+__global__ __launch_bounds__(256) void step_append_kernel(const StepAppendArgs a) {
+  int64_t blk = blockIdx.x;
+  if (blk < a.nbk) {
+    k_append_rows<T>(a.k, blk);
+    return;
+  }
+  blk -= a.nbk;
+  if (blk < a.nbv) {
+    v_append_rows<T>(a.v, blk);
+    return;
+  }
+  blk -= a.nbv;
+  rope_apply_row<T>(a.r, blk * 256 + threadIdx.x);
+}
+
+int launch_step_append(const StepAppendArgs& a0, int dtype, hipStream_t st) {
+  StepAppendArgs a = a0;
+  a.v.gw = a.v.vq == VQ_G64 ? (int)ceil_div(a.v.R, 64) : 1;
+  a.nbk = ceil_div((int64_t)a.k.B * a.k.H * a.k.T, 4);
+  a.nbv = ceil_div((int64_t)a.v.B * a.v.T * a.v.gw, 4);
+  const int64_t nbr = a.has_rope ? ceil_div((int64_t)a.r.B * a.r.H * a.r.T * 64, 256) : 0;
+  const int64_t n = a.nbk + a.nbv + nbr;
+  if (n == 0) return 0;
+  if (dtype == STARKV_F16) hipLaunchKernelGGL(step_append_kernel<_Float16>, dim3((unsigned)n), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(step_append_kernel<__bf16>, dim3((unsigned)n), dim3(256), 0, st, a);
+  return (int)hipGetLastError();
 }
 
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st) {

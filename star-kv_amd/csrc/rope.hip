@@ -38,33 +38,11 @@ __global__ void rope_table_kernel(InvFreq f, float scaling, int n_tiles, uint4* 
   table[idx] = __builtin_bit_cast(uint4, h);
 }
 
-// In-place rotation of [B][H][T][128] rows by the table: one thread per
-// (row, frequency i < 64), computing both halves in fp32 and rounding once.
-// The (cos, sin) pair of (position p, frequency i) is fp16 element pair
-// ((p/32*8 + i/8)*64 + (i%8)/4*32 + p%32)*8 + 2*(i%4) of the table.
+// In-place rotation of [B][H][T][128] rows by the table (rope_apply_row):
+// one thread per (row, frequency i < 64).
 template <typename T>
 __global__ void rope_apply_kernel(RopeApplyArgs a) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t rows = (int64_t)a.B * a.H * a.T;
-  if (idx >= rows * 64) return;
-  const int i = (int)(idx & 63);
-  const int64_t row = idx >> 6;
-  const int t = (int)(row % a.T);
-  const int h = (int)((row / a.T) % a.H);
-  const int b = (int)(row / ((int64_t)a.T * a.H));
-  const int p = (a.pos0_dev ? *a.pos0_dev : a.pos0) + t;
-  if (p < 0 || p >= a.max_pos) {                 // only a run-time position can land here
-    if (a.err != nullptr) *a.err = 1;
-    return;
-  }
-  T* x = (T*)a.x + b * a.sb + h * a.sh + (int64_t)t * a.st;
-  const int64_t te = ((int64_t)((p >> 5) * 8 + (i >> 3)) * 64 + ((i & 7) >> 2) * 32 + (p & 31)) * 8 + 2 * (i & 3);
-  const uint32_t cs = ((const uint32_t*)a.table)[te >> 1];
-  const kh2 c2 = __builtin_bit_cast(kh2, cs);
-  const float c = (float)c2[0], sn = (float)c2[1];
-  const float x0 = to_f32(x[i]), x1 = to_f32(x[i + 64]);
-  x[i] = (T)(x0 * c - x1 * sn);
-  x[i + 64] = (T)(x1 * c + x0 * sn);
+  rope_apply_row<T>(a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 int launch_rope_apply(const RopeApplyArgs& a, int dtype, hipStream_t st) {

@@ -33,7 +33,6 @@ namespace starkv {
 
 constexpr int UP_MB = 32;          // rows per LDS block
 constexpr int UP_CB = 16;          // chunk partials loaded per row and batch
-constexpr int UP_RB = 4;           // rows per thread and batch
 
 // sum of n values p[0], p[stride], ... in index order, UP_CB loads in flight
 __device__ inline float sum_strided(const float* p, int64_t stride, int n) {
@@ -49,7 +48,21 @@ __device__ inline float sum_strided(const float* p, int64_t stride, int n) {
   return s;
 }
 
-template <typename WT, int SW, bool FAST>
+// U_v element e of a row held as packed 16-bit words, in fp32
+__device__ inline float uv_elem(const uint4* w, int e, _Float16*) {
+  const uint4 q = w[e >> 3];
+  const uint32_t x = (e & 7) < 2 ? q.x : (e & 7) < 4 ? q.y : (e & 7) < 6 ? q.z : q.w;
+  return (float)__builtin_bit_cast(kh2, x)[e & 1];
+}
+__device__ inline float uv_elem(const uint4* w, int e, __bf16*) {
+  const uint4 q = w[e >> 3];
+  const uint32_t x = (e & 7) < 2 ? q.x : (e & 7) < 4 ? q.y : (e & 7) < 6 ? q.z : q.w;
+  return __uint_as_float((e & 1) ? (x & 0xffff0000u) : (x << 16));
+}
+
+// RB: rows per thread and batch of the chunk sums (the row block's rows over
+// the JT thread rows, rounded up: 2 or 4)
+template <typename WT, int SW, bool FAST, int RB>
 __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   constexpr int JT = 256 / SW;                     // rows summed side by side
   __shared__ float os[UP_MB][SW + 4];
@@ -62,35 +75,28 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   const int j0 = sl * SW, nj = min(SW, a.Rv - j0);        // valid columns of the slice
   const int64_t cstr = (int64_t)32 * a.Rvp;               // next chunk's partials
 
-  // this thread's U_v row (d) over the slice, raw; converted to fp32 after
-  // the first batch of chunk partials is in flight
+  // this thread's U_v row (d) over the slice, kept as packed 16-bit words
+  // (converted inside the multiply-adds); columns past the slice are zero
   const int d = tid & (HEAD_DIM - 1), mh = tid >> 7;
   const WT* urow = (const WT*)a.uv + (int64_t)(kv * HEAD_DIM + d) * a.uv_rs + j0;
   uint4 uraw[SW / 8];
   if (FAST && nj == SW) {
 #pragma unroll
     for (int k = 0; k < SW / 8; ++k) uraw[k] = *(const uint4*)(urow + 8 * k);
-  }
-  float u[SW];
-  bool u_ready = false;
-  auto load_u = [&]() __attribute__((always_inline)) {
-    if (u_ready) return;
-    u_ready = true;
-    if (FAST && nj == SW) {
+  } else {
 #pragma unroll
-      for (int k = 0; k < SW / 8; ++k) {
-        const uint32_t ww[4] = {uraw[k].x, uraw[k].y, uraw[k].z, uraw[k].w};
+    for (int k = 0; k < SW / 8; ++k) {
+      uint32_t w4[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          u[8 * k + 2 * e] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] & 0xffffu)));
-          u[8 * k + 2 * e + 1] = to_f32(__builtin_bit_cast(WT, (uint16_t)(ww[e] >> 16)));
-        }
+      for (int e = 0; e < 4; ++e) {
+        const int j = 8 * k + 2 * e;
+        const uint32_t lo = j < nj ? __builtin_bit_cast(uint16_t, urow[j]) : 0u;
+        const uint32_t hi = j + 1 < nj ? __builtin_bit_cast(uint16_t, urow[j + 1]) : 0u;
+        w4[e] = lo | (hi << 16);
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < SW; ++j) u[j] = j < nj ? to_f32(urow[j]) : 0.f;
+      uraw[k] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     }
-  };
+  }
 
   float* yp = a.ypart + (((int64_t)kv * a.n_sl + sl) * a.n_cs + cs) * M * HEAD_DIM;
   const int jj = tid % SW, mr = tid / SW;
@@ -126,32 +132,31 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
     }
     // chunk sums of rows m0 .. m0+mb over the slice's columns: UP_RB rows
     // per thread at a time, UP_CB chunks each (rows past mb re-read row mb-1)
-    for (int mm0 = mr; P == 1 && mm0 < mb; mm0 += JT * UP_RB) {
-      const float* p[UP_RB];
+    for (int mm0 = mr; P == 1 && mm0 < mb; mm0 += JT * RB) {
+      const float* p[RB];
 #pragma unroll
-      for (int r = 0; r < UP_RB; ++r) {
+      for (int r = 0; r < RB; ++r) {
         const int m = m0 + min(mm0 + JT * r, mb - 1), q = kv * gs + m % gs;
         const int bq = (m / gs) * a.n_hg + (q >> 5);
         p[r] = a.part + (((int64_t)bq * a.n_c2 + cb0) * 32 + (q & 31)) * a.Rvp + jc;
       }
-      float s[UP_RB] = {};
+      float s[RB] = {};
       for (int c = 0; c < nc; c += UP_CB) {
-        float v[UP_RB][UP_CB];
+        float v[RB][UP_CB];
 #pragma unroll
-        for (int r = 0; r < UP_RB; ++r)
+        for (int r = 0; r < RB; ++r)
 #pragma unroll
           for (int k = 0; k < UP_CB; ++k) v[r][k] = p[r][min(c + k, nc - 1) * cstr];
 #pragma unroll
-        for (int r = 0; r < UP_RB; ++r)
+        for (int r = 0; r < RB; ++r)
 #pragma unroll
           for (int k = 0; k < UP_CB; ++k)
             if (c + k < nc) s[r] += v[r][k];
       }
 #pragma unroll
-      for (int r = 0; r < UP_RB; ++r)
+      for (int r = 0; r < RB; ++r)
         if (mm0 + JT * r < mb) os[mm0 + JT * r][jj] = jj < nj ? s[r] : 0.f;
     }
-    load_u();
     __syncthreads();
     // partial up-projection of the slice: two rows per pass (one per half block)
     for (int mm = mh; mm < mb; mm += 2) {
@@ -159,10 +164,10 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
 #pragma unroll
       for (int j = 0; j < SW; j += 4) {
         const float4 o4 = *(const float4*)&os[mm][j];
-        y[0] = fmaf(u[j], o4.x, y[0]);
-        y[1] = fmaf(u[j + 1], o4.y, y[1]);
-        y[2] = fmaf(u[j + 2], o4.z, y[2]);
-        y[3] = fmaf(u[j + 3], o4.w, y[3]);
+        y[0] = fmaf(uv_elem(uraw, j, (WT*)nullptr), o4.x, y[0]);
+        y[1] = fmaf(uv_elem(uraw, j + 1, (WT*)nullptr), o4.y, y[1]);
+        y[2] = fmaf(uv_elem(uraw, j + 2, (WT*)nullptr), o4.z, y[2]);
+        y[3] = fmaf(uv_elem(uraw, j + 3, (WT*)nullptr), o4.w, y[3]);
       }
       yp[(int64_t)(m0 + mm) * HEAD_DIM + d] = (y[0] + y[1]) + (y[2] + y[3]);
     }
@@ -204,10 +209,18 @@ __global__ __launch_bounds__(256) void up_finish_kernel(const UPArgs a) {
   ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s / L);
 }
 
+template <typename WT, int SW, int RB>
+static void launch_up_rb(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
+  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, RB>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, RB>), grid, dim3(256), 0, st, a);
+}
+
 template <typename WT, int SW>
 static void launch_up_sw(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
-  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false>), grid, dim3(256), 0, st, a);
+  // rows of the largest row block per thread row: two per batch suffice up to 2 * JT
+  const int mb = std::min(UP_MB, a.B * a.gs);
+  if (mb > 2 * (256 / SW)) launch_up_rb<WT, SW, 4>(a, fast, grid, st);
+  else launch_up_rb<WT, SW, 2>(a, fast, grid, st);
 }
 
 template <typename WT>

@@ -190,7 +190,7 @@ EXPORTS = (
     "starkv_pv_latent_workspace_bytes", "starkv_pv_latent",
     "starkv_decode_workspace_bytes", "starkv_decode_attention", "starkv_decode_attention_timed",
     "starkv_decode_attention_noalloc",
-    "starkv_k_append", "starkv_v_append",
+    "starkv_k_append", "starkv_v_append", "starkv_decode_append",
     "starkv_prefill_workspace_bytes", "starkv_prefill_attention", "starkv_prefill_attention_timed",
     "starkv_rms_norm", "starkv_silu_mul", "starkv_skinny_gemm",
 )
@@ -242,6 +242,9 @@ def lib() -> ctypes.CDLL:
     L.starkv_k_append.argtypes = [ctypes.POINTER(KAppendDesc), ctypes.c_void_p]
     L.starkv_v_append.restype = ctypes.c_int
     L.starkv_v_append.argtypes = [ctypes.POINTER(VAppendDesc), ctypes.c_void_p]
+    L.starkv_decode_append.restype = ctypes.c_int
+    L.starkv_decode_append.argtypes = [ctypes.POINTER(KAppendDesc), ctypes.POINTER(VAppendDesc),
+                                       ctypes.POINTER(RopeApplyDesc), ctypes.c_void_p]
     if L.starkv_abi_version() != ABI_VERSION:
         raise StarKVError(f"{LIB_PATH} has ABI version {L.starkv_abi_version()}, this binding needs "
                           f"{ABI_VERSION}: rebuild it with `make -C star-kv_amd`")

@@ -4,8 +4,9 @@ The reference grows its latent caches by ``torch.cat`` every decode step (HF
 ``DynamicLayer.update``, HF:cache_utils.py:127-146, reached from
 model.py:411-419), re-copying the whole cache per token.  ``LatentCache``
 preallocates one layer's caches for ``capacity`` positions and writes each new
-token in place with the HIP cache writer (``starkv_k_append`` /
-``starkv_v_append``), quantising on the fly when the format asks for it.
+token in place with the HIP cache writer (``starkv_decode_append``: the K and
+V writes, with the query rotation when asked, in one launch), quantising on
+the fly when the format asks for it.
 
 Formats (K / V):
   "dense"       act dtype / act dtype
@@ -27,7 +28,8 @@ from typing import List, Optional, Sequence
 import torch
 
 from ._lib import FMT_DENSE, FMT_INT4_REF, FMT_INT8_SYM, StarKVError
-from .ops import KLatentSpec, VLatentSpec, k_append, v_append
+from .ops import KLatentSpec, VLatentSpec, decode_append
+from .rope import RopeConfig
 
 __all__ = ["LatentCache"]
 
@@ -186,33 +188,37 @@ class LatentCache:
         return (k_new if k_new.stride(3) == 1 else k_new.contiguous()), k_new.shape[2]
 
     def append_at(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor, pos: torch.Tensor,
-                  error_flag: Optional[torch.Tensor] = None):
+                  error_flag: Optional[torch.Tensor] = None, q: Optional[torch.Tensor] = None,
+                  rope: Optional[RopeConfig] = None):
         """Write k_new / v_new at the position held by the int32 device tensor
         ``pos`` (read when the writer kernels run, so the call can be captured in
         a CUDA/HIP graph and replayed at advancing positions); the host-side
         ``length`` is left to the caller.  Rows that would land past the
         capacity are skipped and set ``error_flag`` (int32 device tensor) to 1.
-        Returns the (K spec, V spec)."""
+        With ``q`` [B, H, T, 128], its rows are rotated in place by ``rope`` at
+        the same positions, in the same launch.  Returns the (K spec, V spec)."""
         src, T = self._k_src(k_new)
         if v_new.shape[1] != T:
             raise StarKVError("k_new and v_new must hold the same number of positions")
         ks = self.k_spec(bk)
-        k_append(src, ks, 0, self.cap, pos0_device=pos, error_flag=error_flag)
-        v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, 0, self.cap, pos0_device=pos,
-                 error_flag=error_flag)
+        vsrc = v_new.contiguous() if v_new.stride(2) != 1 else v_new
+        decode_append(src, ks, vsrc, self.v_spec, 0, self.cap, q=q, rope=rope or RopeConfig(), pos0_device=pos,
+                      error_flag=error_flag)
         return ks, self.v_spec
 
-    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor):
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, bk: torch.Tensor, q: Optional[torch.Tensor] = None,
+               rope: Optional[RopeConfig] = None):
         """Write T new positions (k_new [B, Hkv, T, r_max] or [B, T, sum(ranks)],
-        v_new [B, T, Rv]) in place; returns (K spec, V spec, length) for the
-        attention kernels."""
+        v_new [B, T, Rv]) in place; with ``q`` [B, H, T, 128], its rows are
+        rotated in place by ``rope`` at the new positions in the same launch.
+        Returns (K spec, V spec, length) for the attention kernels."""
         src, T = self._k_src(k_new)
         if v_new.shape[1] != T:
             raise StarKVError("k_new and v_new must hold the same number of positions")
         if self.length + T > self.cap:
             raise StarKVError(f"cache full: {self.length} + {T} > capacity {self.cap}")
         ks = self.k_spec(bk)
-        k_append(src, ks, self.length, self.cap)
-        v_append(v_new.contiguous() if v_new.stride(2) != 1 else v_new, self.v_spec, self.length, self.cap)
+        vsrc = v_new.contiguous() if v_new.stride(2) != 1 else v_new
+        decode_append(src, ks, vsrc, self.v_spec, self.length, self.cap, q=q, rope=rope or RopeConfig())
         self.length += T
         return ks, self.v_spec, self.length

@@ -25,8 +25,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .cache import LatentCache
-from .ops import (GEMM_ADD, GEMM_SILU_MUL, SKINNY_MAX_ROWS, decode_attention, prefill_attention, rope_apply,
-                  skinny_linear)
+from .ops import GEMM_ADD, GEMM_SILU_MUL, SKINNY_MAX_ROWS, decode_attention, prefill_attention, skinny_linear
 from .rope import RopeConfig
 
 __all__ = ["LatentAttention", "DecodeGraphState", "build_model", "fuse_layers_", "generate", "generate_graphed",
@@ -194,21 +193,22 @@ class LatentAttention(nn.Module):
         """The attention of the layer input without the output projection: [B, T, Hq*128]."""
         B, T, _ = hidden_states.shape
         q, k_new, v_new = self._project(hidden_states)
+        # k_new [B, T, sum(r)]: the writer takes the heads packed.  The cache
+        # writes and the query rotation (positions continuing the cache) run as
+        # one launch
         if self.reference:
             cos, sin = position_embeddings
             q = q * cos.unsqueeze(1) + _rotate_half(q) * sin.unsqueeze(1)
         elif self.graph is not None and T == 1:
-            rope_apply(q, self.rope, pos0_device=self.graph.pos, max_positions=self.graph.capacity,
-                       error_flag=self.graph.error)
-        else:
-            rope_apply(q, self.rope, pos0=self.cache.length)     # positions continue the cache
-        # k_new [B, T, sum(r)]: the writer takes the heads packed
-        if self.graph is not None and T == 1 and not self.reference:
-            kspec, vspec = self.cache.append_at(k_new, v_new, self.bk, self.graph.pos, error_flag=self.graph.error)
+            kspec, vspec = self.cache.append_at(k_new, v_new, self.bk, self.graph.pos, error_flag=self.graph.error,
+                                                q=q, rope=self.rope)
             o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope,
                                  seq_len=self.graph.capacity, scale=self.scaling, mask=self.graph.mask)
             return o.unsqueeze(1).reshape(B, T, self.n_heads * HEAD_DIM)
-        kspec, vspec, S = self.cache.append(k_new, v_new, self.bk)
+        if self.reference:
+            kspec, vspec, S = self.cache.append(k_new, v_new, self.bk)
+        else:
+            kspec, vspec, S = self.cache.append(k_new, v_new, self.bk, q=q, rope=self.rope)
         if T > 1 and not self.reference:
             o = prefill_attention(q, kspec, vspec, self.v_u.weight, rope=self.rope, pos0=S - T,
                                   scale=self.scaling).transpose(1, 2)               # [B, T, Hq, 128]

@@ -490,6 +490,12 @@ def rope_apply(x: torch.Tensor, rope: RopeConfig = RopeConfig(), pos0: int = 0,
     ``max_positions`` bounding the positions it may hold; a row whose run-time
     position falls outside them is left as it is and sets ``error_flag`` (an
     int32 device tensor the caller zeroes and checks) to 1.  Returns x."""
+    d = _rope_apply_desc(x, rope, pos0, pos0_device, max_positions, error_flag)
+    check(_lib.lib().starkv_rope_apply(ctypes.byref(d), _stream(x.device)), "starkv_rope_apply")
+    return x
+
+
+def _rope_apply_desc(x, rope, pos0, pos0_device, max_positions, error_flag) -> RopeApplyDesc:
     if x.dim() != 4 or x.shape[-1] != HEAD_DIM or x.stride(-1) != 1:
         raise StarKVError("x must be [B, H, T, 128] with a contiguous last dim")
     _require_cuda(x)
@@ -502,8 +508,7 @@ def rope_apply(x: torch.Tensor, rope: RopeConfig = RopeConfig(), pos0: int = 0,
     d.pos0 = int(pos0)
     d.pos0_device = _pos_ptr(pos0_device)
     d.error_flag = _flag_ptr(error_flag)
-    check(_lib.lib().starkv_rope_apply(ctypes.byref(d), _stream(x.device)), "starkv_rope_apply")
-    return x
+    return d
 
 
 def _flag_ptr(t: Optional[torch.Tensor]):
@@ -528,6 +533,12 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
     ``pos0_device``: an int32 device tensor holding the position, read when
     the kernel runs (graph capture / replay); rows it would place outside the
     capacity are skipped and set ``error_flag`` (int32 device tensor) to 1."""
+    keep: list = []
+    d = _k_append_desc(src, k, pos0, capacity, pos0_device, error_flag, keep)
+    check(_lib.lib().starkv_k_append(ctypes.byref(d), _stream(src.device)), "starkv_k_append")
+
+
+def _k_append_desc(src, k, pos0, capacity, pos0_device, error_flag, keep) -> KAppendDesc:
     packed = src.dim() == 3
     if packed:
         if src.stride(2) != 1 or src.shape[2] < sum(k.ranks):
@@ -541,7 +552,6 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
     if src.shape[0] > _cache_batch(k.data):
         raise StarKVError(f"src batch {src.shape[0]} exceeds the cache's {_cache_batch(k.data)}")
     _require_cuda(src, *[t for t in (k.data, k.scale, k.data2, k.scale2) if t is not None])
-    keep: list = []
     d = KAppendDesc()
     d.batch, d.n_tokens, d.pos0, d.capacity, d.dtype = src.shape[0], src.shape[2], int(pos0), int(capacity), _dt(src)
     d.src, d.src_stride_b, d.src_stride_h, d.src_stride_t = src.data_ptr(), src.stride(0), src.stride(1), src.stride(2)
@@ -552,7 +562,7 @@ def k_append(src: torch.Tensor, k: KLatentSpec, pos0: int, capacity: int,
         d.src_head_offset = offs
     d.pos0_device = _pos_ptr(pos0_device)
     d.error_flag = _flag_ptr(error_flag)
-    check(_lib.lib().starkv_k_append(ctypes.byref(d), _stream(src.device)), "starkv_k_append")
+    return d
 
 
 def _pos_ptr(t: Optional[torch.Tensor]):
@@ -569,6 +579,11 @@ def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int,
     contiguous) into the cache described by ``v`` at positions
     [pos0, pos0 + T), quantising to its format (starkv_v_append);
     ``pos0_device`` / ``error_flag`` as in ``k_append``."""
+    d = _v_append_desc(src, v, pos0, capacity, pos0_device, error_flag)
+    check(_lib.lib().starkv_v_append(ctypes.byref(d), _stream(src.device)), "starkv_v_append")
+
+
+def _v_append_desc(src, v, pos0, capacity, pos0_device, error_flag) -> VAppendDesc:
     if src.dim() != 3 or src.stride(2) != 1:
         raise StarKVError("src must be [B, T, Rv] with a contiguous last dim")
     if src.shape[2] < v.rank:
@@ -582,7 +597,23 @@ def v_append(src: torch.Tensor, v: VLatentSpec, pos0: int, capacity: int,
     d.v = v.c_struct()
     d.pos0_device = _pos_ptr(pos0_device)
     d.error_flag = _flag_ptr(error_flag)
-    check(_lib.lib().starkv_v_append(ctypes.byref(d), _stream(src.device)), "starkv_v_append")
+    return d
+
+
+def decode_append(k_src: torch.Tensor, k: KLatentSpec, v_src: torch.Tensor, v: "VLatentSpec", pos0: int,
+                  capacity: int, q: Optional[torch.Tensor] = None, rope: RopeConfig = RopeConfig(),
+                  pos0_device: Optional[torch.Tensor] = None, error_flag: Optional[torch.Tensor] = None) -> None:
+    """``k_append``, ``v_append`` and (when ``q`` is given) ``rope_apply`` of
+    the query rows q [B, H, T, 128] at the same positions, in one launch
+    (starkv_decode_append)."""
+    keep: list = []
+    kd = _k_append_desc(k_src, k, pos0, capacity, pos0_device, error_flag, keep)
+    vd = _v_append_desc(v_src, v, pos0, capacity, pos0_device, error_flag)
+    qd = (_rope_apply_desc(q, rope, pos0, pos0_device, capacity if pos0_device is not None else None, error_flag)
+          if q is not None else None)
+    check(_lib.lib().starkv_decode_append(ctypes.byref(kd), ctypes.byref(vd),
+                                          ctypes.byref(qd) if qd is not None else None, _stream(k_src.device)),
+          "starkv_decode_append")
 
 
 def _rows(t: torch.Tensor, name: str) -> torch.Tensor:

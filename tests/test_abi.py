@@ -324,6 +324,16 @@ def test_cache_writer_validation():
     v.v.stride_s, v.v.data = 32, FAKE + 2
     assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_ALIGN
     assert lib.starkv_v_append(None, None) == ERR_NULL
+    # the combined writer reports each description's own status, and a dtype mismatch
+    d.k.format = L.FMT_DENSE
+    assert lib.starkv_decode_append(ctypes.byref(d), ctypes.byref(v), None, None) == ERR_ALIGN
+    assert lib.starkv_decode_append(None, ctypes.byref(v), None, None) == ERR_NULL
+    v.v.data = FAKE
+    q = L.RopeApplyDesc(batch=2, n_heads=8, n_tokens=4, dtype=L.BF16, x=FAKE, stride_b=8 * 4 * 128,
+                        stride_h=4 * 128, stride_t=128, rope_table=FAKE, rope_max_positions=16, pos0=10)
+    assert lib.starkv_decode_append(ctypes.byref(d), ctypes.byref(v), ctypes.byref(q), None) == ERR_DTYPE
+    q.rope_max_positions = 12
+    assert lib.starkv_decode_append(ctypes.byref(d), ctypes.byref(v), ctypes.byref(q), None) == ERR_SHAPE
 
 
 # ---------------------------------------------------------------- prefill validation

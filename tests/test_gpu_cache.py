@@ -239,3 +239,48 @@ def test_k_append_packed_heads_equals_padded_layout(fmt):
     assert torch.equal(caches[0].k_data, caches[1].k_data)
     if fmt != "dense":
         assert torch.equal(caches[0].k_scale, caches[1].k_scale)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["dense", "int8_g64", "reference"])
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_decode_append_equals_the_three_writes(fmt, device_pos):
+    """starkv_decode_append (K write, V write and query rotation in one launch)
+    stores exactly what starkv_k_append, starkv_v_append and starkv_rope_apply
+    store one by one, for each cache format, at a host or a device position."""
+    from starkv import RopeConfig
+    from starkv.cache import LatentCache
+    from starkv.ops import k_append, rope_apply, v_append
+    print(f"[cache] decode_append fmt={fmt} device_pos={device_pos}", flush=True)
+    ranks, Rv, B, T, cap, pos = [24, 8, 40, 16], 264, 2, 3, 32, 9
+    g = torch.Generator(device="cuda").manual_seed(17)
+    k_new = torch.randn(B, T, sum(ranks), generator=g, device="cuda").half()
+    v_new = torch.randn(B, T, Rv, generator=g, device="cuda").half()
+    bk = torch.randn(len(ranks), max(ranks), HEAD, generator=g, device="cuda").half()
+    q0 = torch.randn(B, 8, T, HEAD, generator=g, device="cuda").half()
+    rope = RopeConfig(theta=500000.0)
+    a, b = (LatentCache(B, ranks, Rv, cap, torch.float16, "cuda", fmt=fmt) for _ in range(2))
+    qa, qb = q0.clone(), q0.clone()
+    if device_pos:
+        p = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        a.append_at(k_new, v_new, bk, p, error_flag=err, q=qa, rope=rope)
+        ks = b.k_spec(bk)
+        k_append(k_new, ks, 0, cap, pos0_device=p, error_flag=err)
+        v_append(v_new, b.v_spec, 0, cap, pos0_device=p, error_flag=err)
+        rope_apply(qb, rope, pos0_device=p, max_positions=cap, error_flag=err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+    else:
+        a.length = b.length = pos
+        a.append(k_new, v_new, bk, q=qa, rope=rope)
+        ks = b.k_spec(bk)
+        k_append(k_new, ks, pos, cap)
+        v_append(v_new, b.v_spec, pos, cap)
+        rope_apply(qb, rope, pos0=pos)
+        torch.cuda.synchronize()
+    assert torch.equal(qa, qb) and not torch.equal(qa, q0)
+    for name in ("k_data", "k_scale", "k_data2", "k_scale2", "v_data", "v_scale", "v_zero", "v_data2", "v_scale2"):
+        ta, tb = getattr(a, name, None), getattr(b, name, None)
+        if ta is not None:
+            assert torch.equal(ta, tb), name
