@@ -24,7 +24,7 @@ extern "C" {
 
 /* Bumped on every change of a struct layout or of an entry point's meaning;
  * the Python binding refuses a library of another version. */
-#define STARKV_ABI_VERSION 3
+#define STARKV_ABI_VERSION 4
 
 /* element types */
 enum {
@@ -433,14 +433,23 @@ int starkv_silu_mul(const starkv_silu_mul_desc* d, void* stream);
  *               out[i][j]  = act(act(g / (1 + exp(-g))) * u)        (j < n/2; LlamaMLP over the
  *               gate rows followed by the up rows of one merged weight)
  * x [m][k] row stride x_stride, w [n][k] row stride w_stride, out row stride
- * out_stride (elements).  k a multiple of 64, n a multiple of 16 (32 for
- * epilogue 2), m <= 16 (STARKV_ERR_LIMIT); x and w 16-byte aligned with
- * strides multiples of 8 (STARKV_ERR_ALIGN). */
+ * out_stride (elements).  With w_packed, w holds the weight packed as
+ * [n/16][k/64][16][64] (element (j, kk) at ((j/16 * k/64 + kk/64) * 16 +
+ * j%16) * 64 + kk%64; w_stride unused): each tile's range then streams
+ * linearly.  With rms, x is the raw input of an RMSNorm whose weight the
+ * caller folded into w (w[j][kk] = act(W[j][kk] * norm_weight[kk])): the sums
+ * above are scaled by rsqrt(sum_kk x[i][kk]^2 / k + rms_eps) per row before
+ * the epilogue (HF LlamaRMSNorm followed by the projection, without rounding
+ * the normalised input).  k a multiple of 64, n a multiple of 16 (32 for
+ * epilogue 2), m <= 16 (STARKV_ERR_LIMIT); x and w 16-byte aligned, strides
+ * multiples of 8 (STARKV_ERR_ALIGN). */
 typedef struct {
   int m, n, k, dtype, epilogue;
   const void* x; int64_t x_stride;
   const void* w; int64_t w_stride;
   void* out; int64_t out_stride;
+  int w_packed;
+  int rms; float rms_eps;
 } starkv_skinny_gemm_desc;
 
 int starkv_skinny_gemm(const starkv_skinny_gemm_desc* d, void* stream);

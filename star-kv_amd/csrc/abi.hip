@@ -1033,12 +1033,16 @@ int starkv_skinny_gemm(const starkv_skinny_gemm_desc* d, void* stream) {
   if (d->epilogue == GEMM_SILU_MUL && d->n % 32) return STARKV_ERR_SHAPE;
   if (d->dtype != STARKV_F16 && d->dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
   if (!d->x || !d->w || !d->out) return STARKV_ERR_NULL;
-  if (d->x_stride < d->k || d->w_stride < d->k) return STARKV_ERR_SHAPE;
+  if (d->x_stride < d->k || (!d->w_packed && d->w_stride < d->k)) return STARKV_ERR_SHAPE;
   const int n_out = d->epilogue == GEMM_SILU_MUL ? d->n / 2 : d->n;
   if (d->out_stride < n_out) return STARKV_ERR_SHAPE;
-  if (!rows16(d->x, d->x_stride) || !rows16(d->w, d->w_stride) || !al(d->out, 2)) return STARKV_ERR_ALIGN;
+  if (!rows16(d->x, d->x_stride) || !al(d->w, 16) || (!d->w_packed && !rows16(d->w, d->w_stride)) || !al(d->out, 2))
+    return STARKV_ERR_ALIGN;
   GemmArgs a = {};
   a.x = d->x; a.xs = d->x_stride; a.w = d->w; a.ws = d->w_stride; a.out = d->out; a.os = d->out_stride;
+  a.wpk = d->w_packed != 0;
+  if (d->rms && !(d->rms_eps >= 0.f)) return STARKV_ERR_SHAPE;
+  a.rms = d->rms != 0; a.rms_eps = d->rms_eps;
   a.M = d->m; a.N = d->n; a.K = d->k; a.half_rows = d->n / 2;
   return launch_skinny_gemm(a, d->dtype, d->epilogue, (hipStream_t)stream);
 }

@@ -237,6 +237,8 @@ struct GemmArgs {                                  // skinny_gemm.hip
   const void* w; int64_t ws;                       // [N][K] weight (nn.Linear layout), row stride
   void* out; int64_t os;                           // [M][N] (SILU_MUL: [M][half_rows])
   int M, N, K, half_rows;
+  int wpk;                                         // w packed [N / 16][K / 64][16][64]
+  int rms; float rms_eps;                          // x is an RMSNorm's raw input (weight folded into w)
   int nst, pps;                                    // LDS ring stages per wave, 64-k pairs per stage (launcher)
 };
 

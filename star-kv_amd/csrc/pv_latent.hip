@@ -41,6 +41,8 @@ namespace starkv {
 
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_fp16x4;
 
+constexpr int PV_QDEPTH = 2;   // quantised latents: K-steps loaded ahead
+
 __device__ inline uint2 lds_read_tr16(const uint16_t* p) {
   auto r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) lds_fp16x4*)(p));
   return __builtin_bit_cast(uint2, r);
@@ -134,6 +136,8 @@ __device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
 
 template <typename VT, int NTW, bool FUSED, bool FAST, int VQ>
 __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PVArgs a) {
+  // K-steps of loads in flight per wave (register stages)
+  constexpr int DEPTH = VQ == VQ_DENSE ? 2 : PV_QDEPTH;
   constexpr int PITCH = NTW * 32 + 8;            // elements per staged row (16-byte pad)
   constexpr int STAGE = 16 * PITCH;              // elements per staged K-step
   constexpr int CPR = NTW * 4;                   // 16-byte chunks per staged row
@@ -347,7 +351,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
     } else {
       praw = st.praw;
     }
-    load(st, ks + 2);                       // clamped past the chunk
+    load(st, ks + DEPTH);                   // clamped past the chunk
     if constexpr (COOP) {
       // every wave's chunks of this K-step are in LDS (and every wave has
       // consumed the buffer's previous K-step, two steps ago)
@@ -410,14 +414,15 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   };
 
   if ((COOP || nvt > 0) && nks > 0) {       // cooperative: every wave takes part in the barriers
-    // K-steps in pairs; an odd chunk's last pair computes one K-step past the
-    // chunk with P = 0 (no branch in the loop body)
-    PVStage<NTW, VQ> st0, st1;
-    load(st0, 0);
-    load(st1, 1);
-    for (int ks = 0; ks < nks; ks += 2) {
-      compute(st0, ks, 0);
-      compute(st1, ks + 1, 1);
+    // K-steps in groups of DEPTH, each stage loaded DEPTH steps ahead; the
+    // last group computes up to DEPTH - 1 K-steps past the chunk with P = 0
+    // (no branch in the loop body)
+    PVStage<NTW, VQ> st[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(st[d], d);
+    for (int ks = 0; ks < nks; ks += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) compute(st[d], ks + d, (ks + d) & 1);
     }
   }
 

@@ -6,7 +6,11 @@
 // the CU's LDS holds, in whole 128-byte lines:
 //
 // * A workgroup owns one tile of 16 output columns = 16 weight rows (two
-//   tiles for GEMM_SILU_MUL: the gate rows n and the up rows n + half_rows);
+//   tiles for GEMM_SILU_MUL: the gate rows n and the up rows n + half_rows).
+//   The weight is row-major or packed [N/16][K/64][16][64]: packed, each
+//   wave's range of a tile is one contiguous, linearly streamed region (a
+//   row-major tile is 16 streams one row pitch apart, which HBM serves
+//   measurably slower);
 //   its waves split the K range in pairs of 32-k MFMA steps and run
 //   independently until the final reduction.
 // * Each wave streams its range through its own LDS ring of `nst` stages
@@ -30,7 +34,11 @@
 //     GEMM_ADD       out = act(acc + out)           (the residual add, in place)
 //     GEMM_SILU_MUL  out = act(act(silu(act(acc_g))) * act(acc_u))
 //                    (LlamaMLP's act_fn(gate_proj(x)) * up_proj(x) with torch's roundings)
-//   act() rounds to the activation dtype.
+//   act() rounds to the activation dtype.  With `rms`, x is the raw input of
+//   an RMSNorm whose weight the caller folded into W: every wave also sums
+//   x^2 over its range (from the A operands it reads anyway), and acc is
+//   scaled by rsqrt(sum / K + eps) per row before the epilogue -- the norm
+//   without a launch of its own.
 #include <algorithm>
 
 #include "common.hpp"
@@ -67,6 +75,13 @@ __device__ inline floatx4 mfma16(uint4 a, uint4 b, floatx4 c, __bf16*) {
 
 template <typename T> __device__ inline float round_act(float f) { return (float)(T)f; }
 
+// element e of 8 packed activation values, in fp32
+__device__ inline float act_elem(uint4 v, int e, _Float16*) { return (float)__builtin_bit_cast(half8, v)[e]; }
+__device__ inline float act_elem(uint4 v, int e, __bf16*) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+
 // LDS byte offset, within an 8-row block, of 16-byte chunk k of row r (block i)
 __device__ inline int sg_slot(int r, int k, int i) { return r * 128 + ((k ^ ((r >> 1) + 4 * i)) << 4); }
 
@@ -93,13 +108,18 @@ __global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const 
   const int rs = lane >> 3, q = lane & 7;
   const uint8_t* wsrc[NT][2];
   const uint8_t* xsrc[2];
+  // weight rows: row-major [N][ws] (pairs 128 bytes apart), or packed
+  // [N / 16][K / 64][16 rows][64 k] (a tile's pair = one contiguous 2 KB block)
+  const int64_t pstep = a.wpk ? 2048 : 128;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t row = EPI == GEMM_SILU_MUL ? n0 + 8 * i + rs + t * (int64_t)a.half_rows
                                                : std::min(n0 + 8 * i + rs, (int64_t)a.N - 1);
-      wsrc[t][i] = (const uint8_t*)a.w + row * a.ws * 2 + ((q ^ ((rs >> 1) + 4 * i)) << 4) + (int64_t)p0 * 128;
+      const int64_t chunk = (q ^ ((rs >> 1) + 4 * i)) << 4;
+      wsrc[t][i] = a.wpk ? (const uint8_t*)a.w + ((row >> 4) * pairs + p0) * 2048 + (row & 15) * 128 + chunk
+                         : (const uint8_t*)a.w + row * a.ws * 2 + chunk + (int64_t)p0 * 128;
     }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -112,22 +132,25 @@ __global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const 
   auto issue = [&](int j) __attribute__((always_inline)) {
     uint8_t* st = ring + (j % nst) * sb;
     for (int sp = 0; sp < pps; ++sp) {
-      const int64_t off = (int64_t)std::min(j * pps + sp, np - 1) * 128;
+      const int64_t pj = std::min(j * pps + sp, np - 1);
       uint8_t* sq = st + sp * pb;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          __builtin_amdgcn_global_load_lds((const void*)(wsrc[t][i] + off), (lds_void*)(sq + (t * 2 + i) * 1024), 16, 0,
-                                           0);
+          __builtin_amdgcn_global_load_lds((const void*)(wsrc[t][i] + pj * pstep), (lds_void*)(sq + (t * 2 + i) * 1024),
+                                           16, 0, 0);
       for (int i = 0; i < xr; ++i)
-        __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + off), (lds_void*)(sq + NT * 2048 + i * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + pj * 128), (lds_void*)(sq + NT * 2048 + i * 1024), 16,
+                                         0, 0);
     }
   };
 
   floatx4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.f;                              // RMS-normalised input: this lane's sum of x^2 (row c)
+  const bool rms = a.rms != 0;
   if (np > 0) {
     for (int j = 0; j < nst - 1; ++j) issue(j);
     const int xrow = xr == 2 ? c : (c & 7);
@@ -141,6 +164,13 @@ __global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint4 av = *(const uint4*)(sq + NT * 2048 + (xrow >> 3) * 1024 + sg_slot(xrow & 7, 4 * h + g, xrow >> 3));
+          if (rms) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float v = act_elem(av, e, (T*)nullptr);
+              ss = fmaf(v, v, ss);
+            }
+          }
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
             const uint4 bv = *(const uint4*)(sq + (t * 2 + (c >> 3)) * 1024 + sg_slot(c & 7, 4 * h + g, c >> 3));
@@ -153,6 +183,13 @@ __global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const 
   }
   __syncthreads();
   floatx4* red = (floatx4*)lds;
+  float* red_ss = (float*)(red + (nw - 1) * NT * 64);    // [wave][16 rows]
+  if (rms) {
+    // the four k-chunk lanes of row c, then the waves through LDS
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (g == 0) red_ss[w * 16 + c] = ss;
+  }
   if (w > 0) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) red[((w - 1) * NT + t) * 64 + lane] = acc[t];
@@ -162,6 +199,16 @@ __global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const 
   for (int v = 0; v < nw - 1; ++v)
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] += red[(v * NT + t) * 64 + lane];
+  // per-row scale of the RMS-normalised input: rsqrt(mean(x^2) + eps)
+  float rscale[4] = {1.f, 1.f, 1.f, 1.f};
+  if (rms) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float tot = 0.f;
+      for (int v = 0; v < nw; ++v) tot += red_ss[v * 16 + 4 * g + e];
+      rscale[e] = rsqrtf(tot * (1.0f / (float)a.K) + a.rms_eps);
+    }
+  }
   // lane (c, g) holds rows 4g .. 4g+3 of column n0 + c
   const int64_t col = n0 + c;
   if (EPI != GEMM_SILU_MUL && col >= a.N) return;
@@ -171,10 +218,10 @@ __global__ __launch_bounds__(64 * GEMM_MAX_WAVES) void skinny_gemm_kernel(const 
     if (m >= a.M) break;
     T* o = (T*)a.out + m * a.os + col;
     if constexpr (EPI == GEMM_SILU_MUL) {
-      const float gt = round_act<T>(acc[0][e]), up = round_act<T>(acc[1][e]);
+      const float gt = round_act<T>(rscale[e] * acc[0][e]), up = round_act<T>(rscale[e] * acc[1][e]);
       *o = (T)(round_act<T>(gt / (1.0f + expf(-gt))) * up);
     } else {
-      float v = acc[0][e];
+      float v = rscale[e] * acc[0][e];
       if constexpr (EPI == GEMM_ADD) v += (float)*o;
       *o = (T)v;
     }
@@ -228,7 +275,7 @@ int launch_skinny_gemm(const GemmArgs& a0, int dtype, int epi, hipStream_t st) {
   a.pps = pps;
   a.nst = nst;
   const int sbf = pps * pb;
-  const size_t lds = std::max((size_t)nw * a.nst * sbf, (size_t)(nw - 1) * nt * 1024);
+  const size_t lds = std::max((size_t)nw * a.nst * sbf, (size_t)(nw - 1) * nt * 1024 + nw * 16 * 4);
   return dtype == STARKV_F16 ? launch_gemm_epi<_Float16>(a, epi, n_wg, nw, lds, st)
                              : launch_gemm_epi<__bf16>(a, epi, n_wg, nw, lds, st);
 }

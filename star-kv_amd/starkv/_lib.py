@@ -180,6 +180,8 @@ class SkinnyGemmDesc(ctypes.Structure):
         ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int64),
         ("w", ctypes.c_void_p), ("w_stride", ctypes.c_int64),
         ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int64),
+        ("w_packed", ctypes.c_int),
+        ("rms", ctypes.c_int), ("rms_eps", ctypes.c_float),
     ]
 
 
@@ -195,7 +197,7 @@ EXPORTS = (
     "starkv_rms_norm", "starkv_silu_mul", "starkv_skinny_gemm",
 )
 
-ABI_VERSION = 3          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
+ABI_VERSION = 4          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
 NOALLOC_SCRATCH_BYTES = 128 << 20   # STARKV_NOALLOC_SCRATCH_BYTES
 
 _lib = None

@@ -167,9 +167,16 @@ class LatentAttention(nn.Module):
             lin.weight = nn.Parameter(w[off:off + n], requires_grad=False)
             off += n
 
-    def _project(self, hidden_states: torch.Tensor):
-        """(q [B, Hq, T, 128], new K latent rows [B, T, sum(r)], new V latent rows [B, T, Rv])."""
+    def _project(self, hidden_states: torch.Tensor, rms_eps: Optional[float] = None):
+        """(q [B, Hq, T, 128], new K latent rows [B, T, sum(r)], new V latent rows [B, T, Rv]).
+        ``rms_eps``: hidden_states is the raw layer input and the input RMSNorm
+        is folded into the packed projection (``qkv_packed``)."""
         B, T, _ = hidden_states.shape
+        if rms_eps is not None:
+            nq, nk = self.n_heads * HEAD_DIM, sum(self.ranks)
+            qkv = skinny_linear(hidden_states, self.qkv_packed, rms_eps=rms_eps)
+            return (qkv[..., :nq].view(B, T, self.n_heads, HEAD_DIM).transpose(1, 2), qkv[..., nq:nq + nk],
+                    qkv[..., nq + nk:])
         w = getattr(self, "qkv_weight", None)
         if w is None or self.reference:
             q = self.q_proj(hidden_states)
@@ -189,10 +196,12 @@ class LatentAttention(nn.Module):
         o = self.core(hidden_states, position_embeddings)
         return self.o_proj(o), None
 
-    def core(self, hidden_states: torch.Tensor, position_embeddings=None) -> torch.Tensor:
-        """The attention of the layer input without the output projection: [B, T, Hq*128]."""
+    def core(self, hidden_states: torch.Tensor, position_embeddings=None,
+             rms_eps: Optional[float] = None) -> torch.Tensor:
+        """The attention of the layer input without the output projection: [B, T, Hq*128]
+        (``rms_eps``: as in ``_project``)."""
         B, T, _ = hidden_states.shape
-        q, k_new, v_new = self._project(hidden_states)
+        q, k_new, v_new = self._project(hidden_states, rms_eps)
         # k_new [B, T, sum(r)]: the writer takes the heads packed.  The cache
         # writes and the query rotation (positions continuing the cache) run as
         # one launch
@@ -245,7 +254,19 @@ def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=Non
                                   past_key_values=past_key_values, use_cache=use_cache,
                                   position_embeddings=position_embeddings, **kwargs)
     B, T, Hd = hidden_states.shape
-    x = rms_norm(hidden_states, self.input_layernorm.weight, self.input_layernorm.variance_epsilon)
+    eps_in, eps_post = self.input_layernorm.variance_epsilon, self.post_attention_layernorm.variance_epsilon
+    if B * T <= SKINNY_MAX_ROWS and getattr(self.mlp, "gate_up_packed", None) is not None:
+        # decode: four weight streams, the norms folded into the projections
+        # that follow them, the residual adds and SiLU(gate) * up in epilogues
+        if not hidden_states.is_contiguous():
+            hidden_states = hidden_states.contiguous()
+        o = att.core(hidden_states, position_embeddings, rms_eps=eps_in)
+        h = hidden_states.view(-1, Hd)
+        skinny_linear(o.reshape(B * T, -1), att.o_packed, out=h, epilogue=GEMM_ADD)
+        m = skinny_linear(h, self.mlp.gate_up_packed, epilogue=GEMM_SILU_MUL, rms_eps=eps_post)
+        skinny_linear(m, self.mlp.down_packed, out=h, epilogue=GEMM_ADD)
+        return h.view(B, T, Hd)
+    x = rms_norm(hidden_states, self.input_layernorm.weight, eps_in)
     o = att.core(x, position_embeddings)
     # the residual stream is updated in place (an out-of-place addmm first
     # copies its input): the layer input is the previous layer's output or
@@ -261,7 +282,7 @@ def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=Non
         skinny_linear(o, w_o, out=h, epilogue=GEMM_ADD)
     else:
         h.addmm_(o, w_o.t())
-    n = rms_norm(h, self.post_attention_layernorm.weight, self.post_attention_layernorm.variance_epsilon)
+    n = rms_norm(h, self.post_attention_layernorm.weight, eps_post)
     if skinny:
         skinny_linear(skinny_linear(n, w_gu, epilogue=GEMM_SILU_MUL), w_d, out=h, epilogue=GEMM_ADD)
     else:
@@ -278,15 +299,33 @@ def _fused_norm_forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
     return rms_norm(hidden_states, self.weight, self.variance_epsilon)
 
 
+def _fused_lm_head_forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+    """nn.Linear forward of the output projection on ``starkv_skinny_gemm``
+    (packed weight) for decode batches, torch's GEMM otherwise."""
+    rows = hidden_states.numel() // hidden_states.shape[-1]
+    if rows <= SKINNY_MAX_ROWS and getattr(self, "packed", None) is not None:
+        return skinny_linear(hidden_states.contiguous(), self.packed)
+    return F.linear(hidden_states, self.weight, self.bias)
+
+
+def _packable(w: torch.Tensor) -> bool:
+    return w.dim() == 2 and w.shape[0] % 32 == 0 and w.shape[1] % 64 == 0
+
+
 def fuse_layers_(model) -> None:
     """Run every decoder layer of ``model`` (and the final norm) through
     ``_fused_decoder_forward``: q / k / v latent projections and the MLP's
     gate / up projections merged into one weight each (the HF Linear weights
-    become views of them, so nothing is duplicated and HF's forward still
-    works), the norms and activation on the library's kernels."""
+    become views of them, so HF's forward still works), the norms and
+    activation on the library's kernels.  For decode batches each layer's
+    four projections also get a packed copy for ``starkv_skinny_gemm``
+    (``pack_weight``), the input and post-attention RMSNorm weights folded
+    into the q/k/v and gate/up copies."""
     import types
+    from .ops import pack_weight
     for layer in model.model.layers:
-        layer.self_attn.merge_projections_()
+        att = layer.self_attn
+        att.merge_projections_()
         mlp = layer.mlp
         with torch.no_grad():
             w = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).contiguous()
@@ -294,8 +333,23 @@ def fuse_layers_(model) -> None:
         n = mlp.gate_proj.weight.shape[0]
         mlp.gate_proj.weight = nn.Parameter(w[:n], requires_grad=False)
         mlp.up_proj.weight = nn.Parameter(w[n:], requires_grad=False)
+        mlp.gate_up_packed = None
+        # qkv rows need 16 (tiles), the others 32 (gate/up halves), k 64
+        if (att.qkv_weight.shape[0] % 16 == 0 and att.qkv_weight.shape[1] % 64 == 0
+                and all(_packable(t) for t in (att.o_proj.weight, w, mlp.down_proj.weight))):
+            with torch.no_grad():
+                att.qkv_packed = pack_weight(att.qkv_weight, layer.input_layernorm.weight)
+                att.o_packed = pack_weight(att.o_proj.weight)
+                mlp.gate_up_packed = pack_weight(w, layer.post_attention_layernorm.weight)
+                mlp.down_packed = pack_weight(mlp.down_proj.weight)
         layer.forward = types.MethodType(_fused_decoder_forward, layer)
     model.model.norm.forward = types.MethodType(_fused_norm_forward, model.model.norm)
+    head = model.lm_head
+    head.packed = None
+    if _packable(head.weight) and head.bias is None:
+        with torch.no_grad():
+            head.packed = pack_weight(head.weight)
+        head.forward = types.MethodType(_fused_lm_head_forward, head)
 
 
 def build_model(n_layers: int, hidden: int, heads: int, kv_heads: int, intermediate: int, vocab: int,

@@ -693,17 +693,28 @@ GEMM_STORE, GEMM_ADD, GEMM_SILU_MUL = 0, 1, 2
 
 
 def skinny_linear(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None,
-                  epilogue: int = GEMM_STORE) -> torch.Tensor:
+                  epilogue: int = GEMM_STORE, rms_eps: Optional[float] = None) -> torch.Tensor:
     """nn.Linear x W^T for decode batches (at most 16 rows of x over its
-    leading dims) on starkv_skinny_gemm.  ``epilogue``: GEMM_STORE (out =
+    leading dims) on starkv_skinny_gemm; ``weight`` [n, k] or packed by
+    ``pack_weight`` (faster: streamed linearly).  ``epilogue``: GEMM_STORE (out =
     x W^T), GEMM_ADD (out += x W^T, in place: the residual add) or
     GEMM_SILU_MUL (weight = gate rows then up rows: out = SiLU(x Wg^T) *
-    (x Wu^T)).  Returns out [..., n] (n/2 for GEMM_SILU_MUL)."""
+    (x Wu^T)).  ``rms_eps``: x is the raw input of an RMSNorm whose weight
+    is folded into ``weight`` (``pack_weight(w, norm_weight)``); the products
+    are scaled by rsqrt(mean(x^2) + rms_eps) per row.  Returns out [..., n]
+    (n/2 for GEMM_SILU_MUL)."""
     _require_cuda(x, weight)
     xr = _rows(x, "x")
-    if weight.dim() != 2 or weight.stride(1) != 1 or weight.shape[1] != x.shape[-1] or weight.dtype != x.dtype:
+    packed = weight.dim() == 4
+    if packed:
+        if (weight.shape[2:] != (16, 64) or not weight.is_contiguous() or weight.shape[1] * 64 != x.shape[-1]
+                or weight.dtype != x.dtype):
+            raise StarKVError("a packed weight must be pack_weight's contiguous [n/16, k/64, 16, 64] of x's dtype")
+        n = weight.shape[0] * 16
+    elif weight.dim() != 2 or weight.stride(1) != 1 or weight.shape[1] != x.shape[-1] or weight.dtype != x.dtype:
         raise StarKVError("weight must be [n, k] of x's dtype with a contiguous last dim, k = x.shape[-1]")
-    n = weight.shape[0]
+    else:
+        n = weight.shape[0]
     n_out = n // 2 if epilogue == GEMM_SILU_MUL else n
     if out is None:
         if epilogue == GEMM_ADD:
@@ -715,7 +726,25 @@ def skinny_linear(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Ten
     d = SkinnyGemmDesc()
     d.m, d.n, d.k, d.dtype, d.epilogue = xr.shape[0], n, x.shape[-1], _dt(x), int(epilogue)
     d.x, d.x_stride = xr.data_ptr(), xr.stride(0)
-    d.w, d.w_stride = weight.data_ptr(), weight.stride(0)
+    d.w, d.w_stride, d.w_packed = weight.data_ptr(), (0 if packed else weight.stride(0)), int(packed)
+    d.rms, d.rms_eps = int(rms_eps is not None), float(rms_eps or 0.0)
     d.out, d.out_stride = orr.data_ptr(), orr.stride(0)
     check(_lib.lib().starkv_skinny_gemm(ctypes.byref(d), _stream(x.device)), "starkv_skinny_gemm")
     return out
+
+
+def pack_weight(w: torch.Tensor, norm_weight: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """An nn.Linear weight [n, k] (n a multiple of 16, k of 64) in the layout
+    starkv_skinny_gemm streams linearly: [n/16, k/64, 16, 64], each 16-row
+    tile's 64-column block contiguous (a copy).  ``norm_weight`` [k]: the
+    weight of an RMSNorm applied to the input first, folded in (w * norm_weight
+    per column, rounded once to w's dtype) for ``skinny_linear(...,
+    rms_eps=...)``."""
+    n, k = w.shape
+    if n % 16 or k % 64:
+        raise StarKVError("pack_weight needs n a multiple of 16 and k of 64")
+    if norm_weight is not None:
+        if norm_weight.shape != (k,):
+            raise StarKVError("norm_weight must be [k]")
+        w = (w.float() * norm_weight.float()).to(w.dtype)
+    return w.reshape(n // 16, 16, k // 64, 64).permute(0, 2, 1, 3).contiguous()

@@ -44,7 +44,7 @@ def test_version_and_status_strings():
     header_version = int(m.group(1))
     # the library, the header and the ctypes mirrors must agree: a struct
     # layout change bumps all three together
-    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 3
+    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 4
     for code in (OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_RANK, ERR_WORKSPACE, ERR_LIMIT, ERR_FORMAT):
         s = lib.starkv_status_string(code).decode()
         assert s and s != "unknown error"
@@ -81,7 +81,8 @@ int main(void) {
   F(starkv_rms_norm_desc, weight) F(starkv_rms_norm_desc, eps) F(starkv_rms_norm_desc, out_stride)
   S(starkv_silu_mul_desc) F(starkv_silu_mul_desc, gate) F(starkv_silu_mul_desc, up_stride) F(starkv_silu_mul_desc, out)
   S(starkv_skinny_gemm_desc) F(starkv_skinny_gemm_desc, epilogue) F(starkv_skinny_gemm_desc, x)
-  F(starkv_skinny_gemm_desc, w_stride) F(starkv_skinny_gemm_desc, out_stride)
+  F(starkv_skinny_gemm_desc, w_stride) F(starkv_skinny_gemm_desc, out_stride) F(starkv_skinny_gemm_desc, w_packed)
+  F(starkv_skinny_gemm_desc, rms_eps)
   return 0;
 }
 """

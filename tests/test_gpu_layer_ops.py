@@ -106,35 +106,49 @@ GEMM_CASES = [
 ]
 
 
+@pytest.mark.parametrize("mode", ["rowmajor", "packed", "packed_rms"])
 @pytest.mark.parametrize("case", GEMM_CASES, ids=[f"m{c[0]}n{c[1]}k{c[2]}e{c[3]}{str(c[4])[-4:]}" for c in GEMM_CASES])
-def test_skinny_gemm_matches_fp32(case):
+def test_skinny_gemm_matches_fp32(case, mode):
     """starkv_skinny_gemm against the fp32 product rounded as torch rounds it:
     epilogue 0 act(x W^T); 1 act(x W^T + out); 2 act(act(silu(act(g))) act(u)).
     The fp32 sums run in another order than the reference's, so the gate is
     one rounding of the output plus the fp32 accumulation error
-    (k 2^-24 sum |x||w|)."""
-    from starkv.ops import skinny_linear
+    (k 2^-24 sum |x||w|).  "packed": the weight in pack_weight's layout (the
+    same results); "packed_rms": x is an RMSNorm's raw input, the norm
+    weight folded into the packed weight, and the reference product is
+    (x rsqrt(mean(x^2) + eps)) act(W nw)^T."""
+    from starkv.ops import pack_weight, skinny_linear
     m, n, k, epi, dtype = case
-    _flush(f"[skinny gemm] m={m} n={n} k={k} epilogue={epi} {dtype}")
+    _flush(f"[skinny gemm] m={m} n={n} k={k} epilogue={epi} {dtype} {mode}")
     g = torch.Generator(device="cuda").manual_seed(m * 31 + n + k)
     x = torch.randn(m, k, generator=g, device="cuda").to(dtype)
     w = (torch.randn(n, k, generator=g, device="cuda") / k ** 0.5).to(dtype)
-    acc = x.double() @ w.double().t()
-    bound = k * 2.0 ** -24 * (x.double().abs() @ w.double().abs().t())
+    eps = 1e-5
+    if mode == "packed_rms":
+        nw = (1.0 + 0.2 * torch.randn(k, generator=g, device="cuda")).to(dtype)
+        wk = pack_weight(w, nw)
+        wf = (w.float() * nw.float()).to(dtype).double()
+        xd = x.double() * torch.rsqrt(x.double().pow(2).mean(-1, keepdim=True) + eps)
+    else:
+        wk = pack_weight(w) if mode == "packed" else w
+        wf, xd = w.double(), x.double()
+    acc = xd @ wf.t()
+    bound = k * 2.0 ** -24 * (xd.abs() @ wf.abs().t())
+    lin = (lambda xx, **kw: skinny_linear(xx, wk, rms_eps=eps if mode == "packed_rms" else None, **kw))
     if epi == 2:
         h = n // 2
         gt, up = acc[:, :h].to(dtype), acc[:, h:].to(dtype)
         ref = (F.silu(gt.float()).to(dtype).double() * up.double())
-        out = skinny_linear(x, w, epilogue=2)
+        out = lin(x, epilogue=2)
         bound = 4 * bound[:, :h] + 2.0 ** -8 * ref.abs()          # two roundings of the inputs feed the product
     elif epi == 1:
         res = torch.randn(m, n, generator=g, device="cuda").to(dtype)
         ref = acc + res.double()
         out = res.clone()
-        skinny_linear(x, w, out=out, epilogue=1)
+        lin(x, out=out, epilogue=1)
     else:
         ref = acc
-        out = skinny_linear(x, w)
+        out = lin(x)
     torch.cuda.synchronize()
     ulp = 2.0 ** -(10 if dtype == torch.float16 else 7)
     err = (out.double() - ref).abs()
@@ -149,12 +163,15 @@ def test_fused_decoder_layer_matches_hf_forward(T):
     """One decoder layer of the e2e model through the fused forward against
     HF's own LlamaDecoderLayer.forward on the same weights and caches: the
     layer outputs within max-abs 2e-2 and mean-rel 1e-3 (the residual adds
-    round once inside the GEMMs instead of twice)."""
+    round once inside the GEMMs instead of twice; at T = 1 the RMSNorms are
+    folded into the projections, so the normalised input is not rounded).
+    Dense latent caches: quantising the new latents would turn last-place
+    differences of the projections into whole quantisation steps."""
     import starkv.e2e as e2e
     from _util import errors
     _flush(f"[fused layer] T={T}")
     kw = dict(n_layers=1, hidden=1024, heads=8, kv_heads=2, intermediate=2048, vocab=1000, ranks=[48, 96],
-              v_rank=256, batch=2, capacity=64, fmt="int8_g64", seed=7)
+              v_rank=256, batch=2, capacity=64, fmt="dense", seed=7)
     fused, plain = e2e.build_model(**kw), e2e.build_model(**kw, fused=False)
     for a, b in zip(fused.state_dict().values(), plain.state_dict().values()):
         assert torch.equal(a, b)
