@@ -484,10 +484,18 @@ int head_groups(int H) { return (int)ceil_div(H, 32); }   // P.V passes of 32 he
 struct DecodeLayout {
   int S_pad, n_c1, tiles_per_chunk, n_hg, sw, n_sl, n_cs;
   PVGeom pv;
+  bool part16;
   size_t off_logits, off_cmax, off_part, off_psum, off_ypart, total;
 };
 
-DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes) {
+// f16: fp16 model.  Short P.V chunks (<= 512 positions) then keep their
+// partials in fp16, each divided by its chunk's softmax sum (a convex
+// combination of V rows: bounded by max |V|): there the partials are a large
+// share of the P.V traffic (at 272 positions about as many bytes as the
+// int4 V latent) and halving them pays for the per-chunk rescale in the
+// up-projection; with long chunks it does not (measured).
+DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes,
+                           bool f16) {
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
@@ -504,7 +512,9 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
-  L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * 4);
+  const bool part16 = f16 && L.pv.c2_len <= 512;
+  L.part16 = part16;
+  L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * (part16 ? 2 : 4));
   L.off_psum = o; o = a256(o + BQ * n_c2 * 32 * 4);
   L.off_ypart = o; o = a256(o + (size_t)Hkv * L.n_sl * L.n_cs * ((size_t)B * (Hq / Hkv)) * HEAD_DIM * 4);
   L.total = o;
@@ -760,7 +770,8 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
   int gs = 0, n_wg = 0, vq = 0;
   if (validate_decode(d, &gs, &n_wg, &vq)) return 0;
-  return decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v)).total;
+  return decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v),
+                    d->dtype == STARKV_F16).total;
 }
 
 static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream,
@@ -768,7 +779,8 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   int gs = 0, n_wg = 0, vq = 0, st;
   if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
   const DecodeLayout L =
-      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v));
+      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v),
+                    d->dtype == STARKV_F16);
   if (!workspace || workspace_bytes < L.total) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   char* ws = (char*)workspace;
@@ -799,14 +811,15 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   if ((st = validate_v(d->v, pa, &vq))) return st;
   pa.logits = (const float*)(ws + L.off_logits); pa.l_sb = ka.o_sb; pa.l_st = ka.o_st; pa.l_sh = ka.o_sh;
   pa.chunkmax = (const float*)(ws + L.off_cmax); pa.n_chunk1 = L.n_c1;
-  pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum);
+  pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum); pa.part16 = L.part16;
   pa.S = d->seq_len; pa.H = Hq; pa.n_hg = L.n_hg; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
   pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;
   if ((st = launch_pv(pa, d->dtype, vq, true, v_fast(d->v), B, s))) return st;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
 
   UPArgs ua;
-  ua.part = pa.part; ua.psum = pa.psum; ua.n_c2 = L.pv.n_c2; ua.Rvp = L.pv.Rvp; ua.n_hg = L.n_hg;
+  ua.part = pa.part; ua.psum = pa.psum; ua.part16 = L.part16; ua.n_c2 = L.pv.n_c2; ua.Rvp = L.pv.Rvp;
+  ua.n_hg = L.n_hg;
   ua.uv = d->uv; ua.uv_rs = d->uv_row_stride;
   ua.out = d->out; ua.o_sb = d->out_stride_b; ua.o_sh = d->out_stride_h;
   ua.B = B; ua.Hq = Hq; ua.gs = gs; ua.Rv = d->v.rank;
@@ -871,7 +884,8 @@ int starkv_decode_attention_noalloc(const starkv_decode_desc* d, void* stream) {
   int gs = 0, n_wg = 0, vq = 0, st;
   if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
   const size_t need =
-      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v)).total;
+      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v),
+                    d->dtype == STARKV_F16).total;
   if (need > (size_t)STARKV_NOALLOC_SCRATCH_BYTES) return STARKV_ERR_LIMIT;
   void* ws = nullptr;
   if ((st = scratch_address(&ws))) return st;

@@ -98,7 +98,8 @@ struct PVArgs {
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
   int p_vec;                                       // drop-in: P rows allow 16-byte loads
   // bq = b * n_hg + head group (32 heads each)
-  float* part;                                     // [bq][n_c2][32][Rvp] fp32
+  float* part;                                     // [bq][n_c2][32][Rvp] fp32, or fp16 when part16
+  int part16;                                      // fused: fp16 partials divided by their chunk's softmax sum
   float* psum;                                     // fused: [B*n_hg][n_c2][32] softmax partial sums
   float* part2; int n_grp;                         // drop-in two-level reduction: [B*n_hg][n_grp][32][Rvp]
   void* out; int64_t o_sb, o_sh;                   // drop-in: act-dtype [B][H][Rv]
@@ -144,6 +145,7 @@ struct VAppendArgs {
 // ---------------------------------------------------------------------------
 struct UPArgs {
   const float* part; const float* psum;            // P.V split partials and softmax sums (PVArgs layout)
+  int part16;                                      // partials fp16, divided by their psum
   int n_c2, Rvp, n_hg;
   const void* uv; int64_t uv_rs;                   // [Hkv*128][Rv]
   void* out; int64_t o_sb, o_sh;                   // [B][Hq][128]

@@ -427,8 +427,31 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   }
 
   // ---- this chunk's partial sums: D[row q][col] -> part[bq][c2][q][col] (one
-  // contiguous 32 x Rvp block per workgroup row of the grid)
+  // contiguous 32 x Rvp block per workgroup row of the grid).  Fused fp16
+  // partials are divided by the head's softmax sum over the chunk (the same
+  // in every wave: all waves form the same P): a convex combination of V
+  // rows, so fp16 holds it without overflow or underflow into subnormals.
   const int Rvp = a.Rvp;
+  if constexpr (FUSED) {
+    const float ps = add_halves(psum);
+    if (hh == 0) Ps[wave][n] = ps;
+    __syncthreads();
+    if (cb == 0 && tid < 32) a.psum[((int64_t)bq * a.n_c2 + c2) * 32 + tid] = Ps[0][tid];
+  }
+  if (FUSED && a.part16) {
+    _Float16* part = (_Float16*)a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
+      const float sq = Ps[wave][q];
+      const float inv = sq > 0.f ? 1.0f / sq : 0.f;
+#pragma unroll
+      for (int j = 0; j < NTW; ++j)
+        if (j < nvt)
+          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = (_Float16)(acc[j][v] * inv);
+    }
+    return;
+  }
   float* part = a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
@@ -439,12 +462,6 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
         part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = acc[j][v];
       }
     }
-  }
-  if constexpr (FUSED) {
-    const float ps = add_halves(psum);
-    if (hh == 0) Ps[wave][n] = ps;
-    __syncthreads();
-    if (cb == 0 && tid < 32) a.psum[((int64_t)bq * a.n_c2 + c2) * 32 + tid] = Ps[0][tid];
   }
 }
 

@@ -26,6 +26,7 @@
 // its loads in batches of up to 64 independent addresses and adds them
 // afterwards in their fixed order.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -61,9 +62,12 @@ __device__ inline float uv_elem(const uint4* w, int e, __bf16*) {
 }
 
 // RB: rows per thread and batch of the chunk sums (the row block's rows over
-// the JT thread rows, rounded up: 2 or 4)
-template <typename WT, int SW, bool FAST, int RB>
+// the JT thread rows, rounded up: 2 or 4).  P16: the partials are fp16,
+// each divided by its chunk's softmax sum, which multiplies it back here
+// (the sum's address is the same for every column of a row).
+template <typename WT, int SW, bool FAST, int RB, bool P16>
 __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
+  typedef typename std::conditional<P16, _Float16, float>::type PT;
   constexpr int JT = 256 / SW;                     // rows summed side by side
   __shared__ float os[UP_MB][SW + 4];
   __shared__ float osp[JT][SW + 4];                // chunk-part sums (P > 1)
@@ -98,6 +102,12 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
     }
   }
 
+  // P16: softmax sum of row m's chunk c (c relative to cb0)
+  auto psum_of = [&](int m, int c) -> float {
+    const int q = kv * gs + m % gs, bq = (m / gs) * a.n_hg + (q >> 5);
+    return a.psum[((int64_t)bq * a.n_c2 + cb0 + c) * 32 + (q & 31)];
+  };
+
   float* yp = a.ypart + (((int64_t)kv * a.n_sl + sl) * a.n_cs + cs) * M * HEAD_DIM;
   const int jj = tid % SW, mr = tid / SW;
   const int jc = j0 + min(jj, nj - 1);                    // columns past the slice re-read its last
@@ -110,12 +120,16 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
         const int part = mr / mb, m = m0 + mr % mb, q = kv * gs + m % gs;
         const int bq = (m / gs) * a.n_hg + (q >> 5);
         const int c_lo = cb0 + (int)((int64_t)part * nc / P), c_hi = cb0 + (int)((int64_t)(part + 1) * nc / P);
-        const float* p = a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
+        const PT* p = (const PT*)a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
         float sp = 0.f;
         for (int c = c_lo; c < c_hi; c += UP_CB) {
           float v[UP_CB];
 #pragma unroll
-          for (int k = 0; k < UP_CB; ++k) v[k] = p[min(c + k, c_hi - 1) * cstr];
+          for (int k = 0; k < UP_CB; ++k) {
+            const int cc = min(c + k, c_hi - 1);
+            v[k] = (float)p[cc * cstr];
+            if constexpr (P16) v[k] *= psum_of(m, cc - cb0);
+          }
 #pragma unroll
           for (int k = 0; k < UP_CB; ++k)
             if (c + k < c_hi) sp += v[k];
@@ -133,12 +147,14 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
     // chunk sums of rows m0 .. m0+mb over the slice's columns: UP_RB rows
     // per thread at a time, UP_CB chunks each (rows past mb re-read row mb-1)
     for (int mm0 = mr; P == 1 && mm0 < mb; mm0 += JT * RB) {
-      const float* p[RB];
+      const PT* p[RB];
+      int mrow[RB];
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int m = m0 + min(mm0 + JT * r, mb - 1), q = kv * gs + m % gs;
         const int bq = (m / gs) * a.n_hg + (q >> 5);
-        p[r] = a.part + (((int64_t)bq * a.n_c2 + cb0) * 32 + (q & 31)) * a.Rvp + jc;
+        p[r] = (const PT*)a.part + (((int64_t)bq * a.n_c2 + cb0) * 32 + (q & 31)) * a.Rvp + jc;
+        mrow[r] = m;
       }
       float s[RB] = {};
       for (int c = 0; c < nc; c += UP_CB) {
@@ -146,7 +162,11 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
 #pragma unroll
         for (int r = 0; r < RB; ++r)
 #pragma unroll
-          for (int k = 0; k < UP_CB; ++k) v[r][k] = p[r][min(c + k, nc - 1) * cstr];
+          for (int k = 0; k < UP_CB; ++k) {
+            const int cc = min(c + k, nc - 1);
+            v[r][k] = (float)p[r][cc * cstr];
+            if constexpr (P16) v[r][k] *= psum_of(mrow[r], cc);
+          }
 #pragma unroll
         for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -211,8 +231,13 @@ __global__ __launch_bounds__(256) void up_finish_kernel(const UPArgs a) {
 
 template <typename WT, int SW, int RB>
 static void launch_up_rb(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
-  if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, RB>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, RB>), grid, dim3(256), 0, st, a);
+  if (a.part16) {
+    if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, RB, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, RB, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, RB, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, RB, false>), grid, dim3(256), 0, st, a);
+  }
 }
 
 template <typename WT, int SW>
