@@ -464,13 +464,21 @@ def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = Tru
     toks, logits = [], []
 
     def step():
+        # the decode forward of LlamaForCausalLM (embedding, decoder layers,
+        # final norm, output projection of the last position) without HF's
+        # per-forward position, mask and rotary bookkeeping: the latent
+        # attentions take their positions from the graph state
         nonlocal logit_buf
         state.open_position()
-        o = model(input_ids=tok_buf, position_ids=pos_buf, use_cache=False, logits_to_keep=1)
-        if logit_buf is None:
-            logit_buf = torch.empty(B, o.logits.shape[-1], device=dev, dtype=torch.float32)
-        logit_buf.copy_(o.logits[:, -1])
-        tok_buf.copy_(logit_buf.argmax(-1, keepdim=True))
+        h = model.model.embed_tokens(tok_buf)
+        for layer in model.model.layers:
+            h = layer(h, attention_mask=None, position_ids=pos_buf, position_embeddings=None)
+        last = model.lm_head(model.model.norm(h)[:, -1])
+        if keep_logits:
+            if logit_buf is None:
+                logit_buf = torch.empty(B, last.shape[-1], device=dev, dtype=torch.float32)
+            logit_buf.copy_(last)
+        tok_buf.copy_(last.argmax(-1, keepdim=True))   # fp16 -> fp32 is exact: the same argmax
         state.advance()
         pos_buf.add_(1)
 
