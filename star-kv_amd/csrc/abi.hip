@@ -652,7 +652,9 @@ int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
   // one-dimensional grids of the three launches (workgroup counts, ints in the kernels)
   const int64_t S = (int64_t)d->pos0 + d->n_tokens, Hkv = d->k.n_kv_heads;
   const int64_t g_k = round_up((int64_t)d->batch * ceil_div(S, PF_K_POS), 8) * Hkv;
-  const int64_t g_v = round_up((int64_t)d->batch * ceil_div(S, PF_V_POS), 8) * ((Hkv + 1) / 2);
+  const int64_t nhp = (Hkv + 1) / 2;
+  const int64_t g_v = nhp >= 8 ? 8 * ceil_div(nhp, 8) * d->batch * ceil_div(S, PF_V_POS)
+                               : round_up((int64_t)d->batch * ceil_div(S, PF_V_POS), 8) * nhp;
   const int64_t g_a = round_up((int64_t)d->batch * Hkv, 8) * *gs * ceil_div(d->n_tokens, PF_Q_POS);
   if (std::max({g_k, g_v, g_a}) > INT32_MAX) return STARKV_ERR_LIMIT;
   *S_pad = round_up(S, 64);

@@ -179,6 +179,7 @@ struct PFArgs {
   int S, S_pad, Hkv, Hq, gs, T, pos0;              // S = pos0 + T positions reconstructed, S_pad = round_up(S, 64)
   int rc_nb, rc_blocks;                            // K reconstruction: position blocks per batch, times B
   int rv_nb, rv_blocks;                            // V reconstruction: the same for its blocks
+  int rv_hpx;                                      // V reconstruction: head pairs per XCD (0: blocks per XCD)
   int fa_nqb, fa_nkvi;                             // attention: query blocks per head, B * Hkv
   // K latent: dense act dtype (offsets / pitches in elements) or int8 (bytes) with fp16 scales (b, h, s)
   const void* kx; int64_t kx_sb; int k_i8;

@@ -331,85 +331,134 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// V reconstruction, two KV heads per workgroup of 8 waves: 256 positions x
-// 256 dims, wave w computing head 2 hp + (w & 1) for positions
-// 64 (w >> 1) .. + 63 as 4 x 2 MFMA tiles (128 accumulators, so two waves fit
-// a SIMD and hide each other's latencies; the two heads' waves read the same
-// latent rows, the second from L1).  Per 64-rank step the U_v rows of both
-// heads are staged in LDS; group-64 scale and zero of the workgroup's
-// positions are staged 16 groups at a time.  Same lane / K-chunk layout and
-// epilogue as recon_kernel.
+// V reconstruction, two KV heads per workgroup of 4 waves: 256 positions x
+// 256 dims (both heads), wave w computing all 256 dims of positions
+// 64 w .. + 63 as 8 x 2 MFMA tiles (256 fp32 accumulators, one wave per
+// SIMD), so each dequantised latent fragment feeds eight MFMAs.
+// * U_v rows of both heads stream through an LDS ring of NST stages of 64
+//   ranks with global_load_lds (no VGPRs held by loads in flight); each wave
+//   DMAs 64 of a stage's 256 rows.  In LDS, 16-byte chunk c of stage row r
+//   sits at slot c ^ ((r >> 1) & 7) of its 128-byte row, so an operand read
+//   (16 lanes = rows r .. r + 15 of one chunk per ds_read_b128 cycle)
+//   touches 16 distinct (bank half, slot) pairs.
+// * Each stage is an LDS array of its own and the step loop is unrolled by
+//   NST, so every access names its stage at compile time: the compiler then
+//   sees that an operand read of one stage cannot alias the DMA in flight
+//   into another, and waits only where the code says so.
+// * Latent words (and group-64 scale / zero) are loaded NST - 1 steps ahead
+//   into NST rotating register sets.  Per step the DMA of stage ks + NST - 1
+//   and the latents of step ks + NST - 1 are issued in that order, so fixed
+//   s_waitcnt vmcnt counts tell when this step's latents (top of the step)
+//   and the next stage (before the barrier) have landed.
+// * One barrier per step, before the step's last K-chunk: the next stage's
+//   first operand reads are then in flight while that chunk's MFMAs run, and
+//   the stage consumed in the previous step is refilled right after it.
+// * Ranks past Rv (the last stage only): the DMA copies a 16-byte zero line
+//   for those U_v chunks, against clamped valid latent chunks.
+// Same lane / K-chunk layout as recon_kernel; the epilogue stages each
+// wave's 64 x 256 tile in one stage array (16-byte chunks XOR-swizzled by
+// row) and writes whole 256-byte rows per head.
 // ---------------------------------------------------------------------------
 constexpr int RV_POS = PF_V_POS;                     // positions per workgroup
 constexpr int RV_WAVE_POS = 64;                      // positions per wave (2 N-tiles)
-constexpr int RV_UVBUF = 2 * HEAD_DIM * UV_PITCH;    // halves per U_v stage (two heads)
-constexpr int RV_SZG = 16;                           // scale / zero groups per LDS chunk
-constexpr int RV_SZ_OFF = 2 * RV_UVBUF;              // halves: chunk [position][RV_SZG] x (scale | zero << 16)
-static_assert(RV_SZ_OFF + RV_POS * RV_SZG * 2 <= RC_LDS, "V reconstruction LDS");
-static_assert(8 * RV_WAVE_POS * C_PITCH <= RC_LDS, "V reconstruction epilogue LDS");
+static_assert(4 * RV_WAVE_POS == RV_POS, "V reconstruction: 4 waves");
+constexpr int RV_STAGE = 2 * HEAD_DIM * 128;         // bytes per stage: 256 rows x 64 ranks x 2 bytes
+static_assert(RV_WAVE_POS * 2 * HEAD_DIM * 2 == RV_STAGE, "epilogue tile = one stage array");
 
 template <int Q> struct RvRaw { uint4 d[2][4]; };                        // dense: [N-tile][K-chunk]
-template <> struct RvRaw<1> { uint4 d[2]; };                             // group-64 int4: word kk = chunk kk
+template <> struct RvRaw<1> { uint4 d[2]; uint16_t sz[2]; };              // group-64 int4: word kk = chunk kk; scale (lanes
+                                                                         // 0-31) / zero (lanes 32-63) of the two positions
 template <> struct RvRaw<2> { uint2 d[2][4]; };                          // per-token blocks: <= 8 bytes per chunk
+// ring depth (= latent register sets): dense latents take 32 registers per
+// step, so they get one set less
+template <int Q> constexpr int rv_nst() { return Q == 0 ? 3 : 4; }
+// fewest vector-memory instructions one step's latent loads issue (the wait
+// counts assume no fewer; a step that issues more only waits longer)
+template <int Q> constexpr int rv_lat_ops() { return Q == 1 ? 4 : 8; }
+
+template <int N> __device__ inline void rv_vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+typedef __attribute__((address_space(3))) void pf_lds_void;
+
+// 16 zero bytes in global memory: the DMA source of U_v chunks past Rv
+__device__ __attribute__((aligned(16))) uint4 pf_zero_line = {0u, 0u, 0u, 0u};
 
 // Q: 0 dense act dtype, 1 group-64 int4 (scale and zero per (b, s, group)),
 // 2 per-token blocks (the reference int4 format with an optional int8 / int4
 // upper block, or int8; one scale per (b, s) and block)
-template <typename XT, int Q>
-__global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
+// NARROW (group-64 only): Rv < 32, rows shorter than one 16-byte load
+template <typename XT, int Q, bool NARROW>
+__global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t st0[RV_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st1[RV_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st2[RV_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t st3[RV_STAGE];
+  constexpr int NST = rv_nst<Q>();
+  constexpr int D = NST - 1;                         // prefetch distance (steps)
+  constexpr int NL = rv_lat_ops<Q>();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
-  // XCD-aware order as in recon_kernel: the head pairs of one (b, 256
-  // positions) share an XCD
+  // XCD-aware order (workgroup L runs on XCD L % 8).  With 8 or more head
+  // pairs each XCD owns rv_hpx of them and walks all position blocks, so its
+  // L2 holds those heads' U_v (2 x 128 x Rv x 2 bytes each) and only the
+  // latents are read by several XCDs; with fewer, the head pairs of one
+  // (b, 256 positions) share an XCD as in recon_kernel.
   const int L = blockIdx.x, t8 = L >> 3;
   const int nhp = (a.Hkv + 1) >> 1;
-  const int hp = t8 % nhp, blk = (t8 / nhp) * 8 + (L & 7);
+  int hp, blk;
+  if (a.rv_hpx) {
+    hp = (L & 7) * a.rv_hpx + t8 % a.rv_hpx;
+    blk = t8 / a.rv_hpx;
+    if (hp >= nhp) return;
+  } else {
+    hp = t8 % nhp;
+    blk = (t8 / nhp) * 8 + (L & 7);
+  }
   if (blk >= a.rv_blocks) return;
   const int b = blk / a.rv_nb;
-  const int p0 = (blk - b * a.rv_nb) * RV_POS;
-  const int hw = 2 * hp + (wave & 1);
-  const bool hlive = hw < a.Hkv;                     // an odd Hkv leaves the last pair's second head empty
-  const int pl0 = RV_WAVE_POS * (wave >> 1);         // first local position of this wave
-  const int pw = p0 + pl0;
+  const int pw = (blk - b * a.rv_nb) * RV_POS + RV_WAVE_POS * wave;   // this wave's first position
   const int S = a.S, R = a.Rv;
-  const int nks = (R + RC_KS - 1) / RC_KS;
+  const int nks = (R + 63) >> 6;
+
+  auto stage = [&](auto ic) __attribute__((always_inline)) -> uint8_t* {
+    constexpr int i = decltype(ic)::value % 4;
+    if constexpr (i == 0) return st0;
+    else if constexpr (i == 1) return st1;
+    else if constexpr (i == 2) return st2;
+    else return st3;
+  };
 
   const uint8_t* xrow[2];
   const uint8_t* xrow2[2];                           // per-token blocks: the lower (int4) block
   uint16_t vsc[2] = {0, 0}, vsc2[2] = {0, 0};
   const bool vlo = Q == 2 && R > a.vsplit;
+  const uint16_t* srow[2];                           // per-token blocks: scale rows of the two positions
+  const uint16_t* szrow[2];                          // group-64: scale (lane half 0) or zero (half 1) rows
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int pc = min(pw + nt * 32 + n, S - 1);
     constexpr int64_t es = Q ? 1 : 2;
     xrow[nt] = (const uint8_t*)a.vx + (b * a.vx_sb + (int64_t)pc * a.vx_ss) * es;
     xrow2[nt] = xrow[nt];
-    if constexpr (Q == 2) vsc[nt] = ((const uint16_t*)a.vscale)[b * a.vs_sb + (int64_t)pc * a.vs_ss];
+    srow[nt] = (const uint16_t*)a.vscale + b * a.vs_sb + (int64_t)pc * a.vs_ss;
+    szrow[nt] = (const uint16_t*)(hh ? a.vzero : a.vscale) + b * a.vs_sb + (int64_t)pc * a.vs_ss;
+    if constexpr (Q == 2) vsc[nt] = *srow[nt];
     if (vlo) {
       xrow2[nt] = (const uint8_t*)a.vx2 + b * a.vx2_sb + (int64_t)pc * a.vx2_ss;
       vsc2[nt] = ((const uint16_t*)a.vscale2)[b * a.vs2_sb + (int64_t)pc * a.vs2_ss];
     }
   }
-  uint32_t* szl = (uint32_t*)(lds + RV_SZ_OFF);
-  auto sz_stage = [&](int ks) {                      // groups ks .. ks + RV_SZG - 1 of every position
-    const int pl = tid >> 1, gh = (tid & 1) * (RV_SZG / 2);
-    const int pc = min(p0 + pl, S - 1);
-    const int64_t o = b * a.vs_sb + (int64_t)pc * a.vs_ss;
-    const int G = (R + 63) >> 6;
-#pragma unroll
-    for (int i = 0; i < RV_SZG / 2; ++i) {
-      const int g = min(ks + gh + i, G - 1);
-      szl[pl * RV_SZG + gh + i] = (uint32_t)((const uint16_t*)a.vscale)[o + g] |
-                                  ((uint32_t)((const uint16_t*)a.vzero)[o + g] << 16);
-    }
-  };
 
-  // latent loads: as in recon_kernel, clamped to rank R - 8 past the end
+  // latent loads of step ks (clamped to the last step; ranks past R read the
+  // chunk at rank R - 8, which meets zero U_v chunks)
   typedef RvRaw<Q> Raw;
-  auto load = [&](int ks, Raw& r) {
-    const int j0 = ks * RC_KS + 32 * hh;
+  auto load = [&](int ks_, Raw& r) __attribute__((always_inline)) {
+    const int ks = min(ks_, nks - 1);
+    const int j0 = ks * 64 + 32 * hh;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       if constexpr (Q == 2) {
@@ -417,161 +466,233 @@ __global__ __launch_bounds__(512, 1) void recon_v_kernel(const PFArgs a) {
         for (int kk = 0; kk < 4; ++kk)
           r.d[nt][kk] = pf_ld_block(xrow[nt], xrow2[nt], min(j0 + 8 * kk, R - 8), a.vsplit, a.v_a8);
       } else if constexpr (Q == 1) {
-        if (ks * RC_KS + RC_KS <= R) {
-          r.d[nt] = *(const uint4*)(xrow[nt] + j0 / 2);
+        // one 16-byte load per N-tile in every step (an equal instruction
+        // count keeps the compiler's own wait counts exact).  Where the lane's
+        // 32 ranks pass the row end (last step), it loads the row's last 16
+        // bytes and moves chunk kk + sh down to kk (the chunks left over are
+        // past R and meet zero U_v).  Rows shorter than 16 bytes take 4-byte
+        // loads (NARROW: more instructions, so the waits only wait longer).
+        if constexpr (!NARROW) {
+          r.d[nt] = *(const uint4*)(xrow[nt] + min(j0, R - 32) / 2);   // shifted by tail_fix
         } else {
           uint32_t w[4];
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) w[kk] = *(const uint32_t*)(xrow[nt] + min(j0 + 8 * kk, R - 8) / 2);
           r.d[nt] = make_uint4(w[0], w[1], w[2], w[3]);
         }
+        r.sz[nt] = szrow[nt][ks];
       } else {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * min(j0 + 8 * kk, R - 8));
       }
     }
   };
-
-  // U_v stage: thread row tid / 2 (head 2 hp + row / 128, dim row % 128), ranks 32 (tid % 2) .. + 31
-  const int ur = tid >> 1, uc = (tid & 1) * 32;
-  const int uh = min(2 * hp + (ur >> 7), a.Hkv - 1);
-  const XT* urow = (const XT*)a.uv + ((int64_t)uh * HEAD_DIM + (ur & 127)) * a.uv_rs;
-  uint4 un[4];
-  auto uv_load = [&](int ks) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) un[c] = *(const uint4*)(urow + min(ks * RC_KS + uc + 8 * c, R - 8));
-  };
-  auto uv_store = [&](int buf, int ks) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *(uint4*)&lds[buf * RV_UVBUF + ur * UV_PITCH + uc + 8 * c] =
-          ks * RC_KS + uc + 8 * c < R ? un[c] : make_uint4(0, 0, 0, 0);
-  };
-
-  floatx16 acc[4][2];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = floatx16{};
-  const int abase = (wave & 1) * HEAD_DIM * UV_PITCH;  // this wave's head within a U_v stage
-
-  auto step = [&](int ks, const Raw& cur) {
-    const bool more = ks + 1 < nks;
-    uint32_t sz[2] = {0, 0};
-    if constexpr (Q == 1) {
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) sz[nt] = szl[(pl0 + nt * 32 + n) * RV_SZG + ks % RV_SZG];
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      uint4 bf[2];
+  // the last step's 16-byte latent loads (group-64): a lane whose 32 ranks
+  // pass the row end loaded the row's last 16 bytes; move chunk kk + sh down
+  // to kk (the chunks left over are past R and meet zero U_v)
+  auto tail_fix = [&](Raw& r, int ks) __attribute__((always_inline)) {
+    if constexpr (Q == 1 && !NARROW) {
+      const int j0 = ks * 64 + 32 * hh;
+      const int sh = (j0 - min(j0, R - 32)) >> 3;   // 0 .. 3
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        if constexpr (Q == 1) {
-          const uint32_t w = kk == 0 ? cur.d[nt].x : kk == 1 ? cur.d[nt].y : kk == 2 ? cur.d[nt].z : cur.d[nt].w;
-          bf[nt] = pf_dq_g64(w, (uint16_t)(sz[nt] & 0xffff), (uint16_t)(sz[nt] >> 16));
-          if constexpr (!__is_same(XT, _Float16)) bf[nt] = pf_f16_to_bf16(bf[nt]);
-        } else if constexpr (Q == 2) {
-          const int j = min(ks * RC_KS + 32 * hh + 8 * kk, R - 8);
-          bf[nt] = pf_dq_block(cur.d[nt][kk], j, a.vsplit, a.v_a8, vsc[nt], vsc2[nt]);
-          if constexpr (!__is_same(XT, _Float16)) bf[nt] = pf_f16_to_bf16(bf[nt]);
-        } else {
-          bf[nt] = cur.d[nt][kk];
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const uint4 af = *(const uint4*)&lds[(ks & 1) * RV_UVBUF + abase + (mt * 32 + n) * UV_PITCH + 32 * hh + 8 * kk];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = pf_mfma<XT>(af, bf[nt], acc[mt][nt]);
+        const uint4 w = r.d[nt];
+        r.d[nt] = make_uint4(sh == 0 ? w.x : sh == 1 ? w.y : sh == 2 ? w.z : w.w,
+                             sh == 0 ? w.y : sh == 1 ? w.z : w.w, sh == 0 ? w.z : w.w, w.w);
       }
     }
-    if (more) uv_store((ks + 1) & 1, ks + 1);
+  };
+  // raw -> B fragment (act dtype) of N-tile nt, K-chunk kk of step ks
+  auto frag = [&](const Raw& r, int ks, int nt, int kk) __attribute__((always_inline)) -> uint4 {
+    uint4 f;
     if constexpr (Q == 1) {
-      if (more && (ks + 1) % RV_SZG == 0) {
-        __syncthreads();                             // everyone done with the old chunk
-        sz_stage(ks + 1);
-      }
+      const uint32_t w = kk == 0 ? r.d[nt].x : kk == 1 ? r.d[nt].y : kk == 2 ? r.d[nt].z : r.d[nt].w;
+      // the lane halves swap: every lane then holds the scale (first) and
+      // the zero (second) of its position
+      const auto sz = __builtin_amdgcn_permlane32_swap((uint32_t)r.sz[nt], (uint32_t)r.sz[nt], false, false);
+      f = pf_dq_g64(w, (uint16_t)sz[0], (uint16_t)sz[1]);
+    } else if constexpr (Q == 2) {
+      const int j = min(ks * 64 + 32 * hh + 8 * kk, R - 8);
+      f = pf_dq_block(r.d[nt][kk], j, a.vsplit, a.v_a8, vsc[nt], vsc2[nt]);
+    } else {
+      f = r.d[nt][kk];
     }
-    __syncthreads();
+    if constexpr (Q != 0 && !__is_same(XT, _Float16)) f = pf_f16_to_bf16(f);
+    return f;
   };
 
-  uv_load(0);
-  uv_store(0, 0);
-  if constexpr (Q == 1) sz_stage(0);
-  if constexpr (Q == 0) {
-    // dense latents: one step ahead (a step's fragments take 32 registers)
-    Raw cur, nxt;
-    load(0, cur);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int ks = 0; ks < nks; ++ks) {
-      const bool more = ks + 1 < nks;
-      if (more) {
-        uv_load(ks + 1);
-        load(ks + 1, nxt);
-      }
-      step(ks, cur);
-      if (more) cur = nxt;
-    }
-  } else {
-    // packed latents two steps ahead, the U_v stage one step ahead (requested
-    // first: loads complete in order, so storing it waits only for itself)
-    Raw r0, r1, r2;
-    load(0, r0);
-    if (nks > 1) load(1, r1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    int ks = 0;
-    for (; ks + 3 <= nks; ks += 3) {
-      uv_load(ks + 1);
-      load(ks + 2, r2);
-      step(ks, r0);
-      if (ks + 2 < nks) uv_load(ks + 2);
-      if (ks + 3 < nks) load(ks + 3, r0);
-      step(ks + 1, r1);
-      if (ks + 3 < nks) uv_load(ks + 3);
-      if (ks + 4 < nks) load(ks + 4, r1);
-      step(ks + 2, r2);
-    }
-    if (ks < nks) {
-      if (ks + 1 < nks) uv_load(ks + 1);
-      step(ks, r0);
-    }
-    if (ks + 1 < nks) {
-      if (ks + 2 < nks) uv_load(ks + 2);
-      step(ks + 1, r1);
-    }
-  }
+  // U_v DMA: this wave fills stage rows 64 wave .. + 63 (head 2 hp + wave / 2,
+  // dims 64 (wave % 2) .. + 63); instruction i covers rows 8 i + rs, and lane
+  // slot q receives chunk q ^ ((rs >> 1) + 4 (i & 1)) of its row
+  const int rs = lane >> 3, q = lane & 7;
+  const int uh = min(2 * hp + (wave >> 1), a.Hkv - 1);
+  const uint8_t* ug = (const uint8_t*)a.uv + ((int64_t)uh * HEAD_DIM + 64 * (wave & 1) + rs) * a.uv_rs * 2;
+  const int64_t urow8 = a.uv_rs * 16;                // bytes between rows 8 apart
+  const int uc0 = (q ^ (rs >> 1)) * 8, uc1 = (q ^ ((rs >> 1) + 4)) * 8;   // the lane's chunk (ranks), even / odd i
+  const int wrow = wave * 64 * 128;                  // this wave's rows within a stage
+  auto issue = [&](auto ic, int j) __attribute__((always_inline)) {   // stage j into array ic
+    const int r0 = min(j, nks - 1) * 64;
+    uint8_t* dst = stage(ic) + wrow;
+    // chunks of ranks >= Rv (the last stage when Rv is not a multiple of 64)
+    // copy a zero line, so those U_v rows are zero in LDS
+    const int c0 = r0 + uc0, c1 = r0 + uc1;
+    const uint8_t* src0 = c0 < R ? ug + c0 * 2 : (const uint8_t*)&pf_zero_line;
+    const uint8_t* src1 = c1 < R ? ug + c1 * 2 : (const uint8_t*)&pf_zero_line;
+    const int64_t st0 = c0 < R ? urow8 : 0, st1 = c1 < R ? urow8 : 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)((i & 1) ? src1 + i * st1 : src0 + i * st0),
+                                       (pf_lds_void*)(dst + i * 1024), 16, 0, 0);
+  };
+  // operand reads: lane (n, hh) reads row 32 mt + n, chunk 4 hh + kk
+  int rd[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) rd[kk] = n * 128 + (((4 * hh + kk) ^ ((n >> 1) & 7)) << 4);
+  auto read_a = [&](auto ic, int kk, uint4* af) __attribute__((always_inline)) {
+    const uint8_t* base = stage(ic) + rd[kk];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) af[mt] = *(const uint4*)(base + mt * 4096);
+  };
 
-  // epilogue (the last step ended with a barrier): stage 64 x 128 per wave, write whole rows
-  uint16_t* cw = lds + wave * RV_WAVE_POS * C_PITCH;
+  floatx16 acc[8][2];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = floatx16{};
+
+  uint4 afA[8], afB[8];                              // A fragments: chunks 0, 2 in afA, chunks 1, 3 in afB
+  uint4 bfA[2], bfB[2];                              // B fragments, alternating the same way
+  Raw raw[NST];
+  // One step: stage ks in array ic, its latents in raw[ic]; on entry the
+  // chunk-0 A fragments are in afA and (packed formats) the chunk-0 B
+  // fragments in bfA.  Each chunk is one scheduling region: the next chunk's
+  // operand reads are issued first, then this chunk's MFMAs interleave with
+  // the next chunk's dequantisation.  The last chunk also refills the array
+  // of stage ks - 1 with stage ks + D and loads the latents of ks + D.
+  auto step = [&](auto ic, int ks) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    const std::integral_constant<int, (i + 1) % NST> inext;
+    const std::integral_constant<int, (i + NST - 1) % NST> iprev;
+    if constexpr (Q == 0) rv_vm_wait<8 + NL>();      // this step's latents landed (issued two steps back)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4* afc = (kk & 1) ? afB : afA;
+      uint4* afn = (kk & 1) ? afA : afB;
+      uint4* bfc = (kk & 1) ? bfB : bfA;
+      uint4* bfn = (kk & 1) ? bfA : bfB;
+      if (kk < 3) {
+        // this chunk's operands (read a region ago) are in; with them retired
+        // the next chunk's 8 reads keep the LDS counter within its 15
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        read_a(ic, kk + 1, afn);
+      } else {
+        // this wave's part of stage ks + 1 landed (packed formats: and the
+        // latents of ks + 1, issued just after it)
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // chunk 3's operands in (as above)
+        if constexpr (Q == 0) rv_vm_wait<0>();
+        else rv_vm_wait<8 + NL>();
+        // stage ks + 1 complete for all waves; stage ks - 1 free.  A bare
+        // barrier: each wave has waited for its own DMA above, and a fence
+        // here would also wait for the refills still in flight into the
+        // other stages.  The memory clobber keeps the compiler from moving
+        // LDS accesses across it.
+        asm volatile("s_barrier" ::: "memory");
+        read_a(inext, 0, afn);                       // the next step's chunk 0, in flight under this chunk's MFMAs
+        if (ks + 2 == nks && (R & 63)) tail_fix(raw[(i + 1) % NST], ks + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (Q == 0) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) bfc[nt] = raw[i].d[nt][kk];
+      }
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = pf_mfma<XT>(afc[mt], bfc[nt], acc[mt][nt]);
+      if constexpr (Q != 0) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) bfn[nt] = kk < 3 ? frag(raw[i], ks, nt, kk + 1) : frag(raw[(i + 1) % NST], ks + 1, nt, 0);
+      }
+      if (kk == 3) {
+        issue(iprev, ks + D);
+        load(ks + D, raw[(i + D) % NST]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const std::integral_constant<int, 0> i0;
+  const std::integral_constant<int, 1> i1;
+  const std::integral_constant<int, 2> i2;
+  const std::integral_constant<int, 3> i3;
+
+  // prologue: stages 0 .. D - 1 and their latents, in the steady state's order
+  issue(i0, 0);
+  load(0, raw[0]);
+  issue(i1, 1);
+  load(1, raw[1]);
+  if constexpr (D == 3) {
+    issue(i2, 2);
+    load(2, raw[2]);
+  }
+  rv_vm_wait<(D - 1) * (8 + NL)>();                  // this wave's part of stage 0 and the latents of step 0
+  __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0): no scalar loads pending into the loop
+  __syncthreads();
+  read_a(i0, 0, afA);
+  if (nks == 1 && (R & 63)) tail_fix(raw[0], 0);
+  if constexpr (Q != 0) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) bfA[nt] = frag(raw[0], 0, nt, 0);
+  }
+  int ks = 0;
+  for (; ks + NST <= nks; ks += NST) {
+    step(i0, ks);
+    step(i1, ks + 1);
+    step(i2, ks + 2);
+    if constexpr (NST == 4) step(i3, ks + 3);
+  }
+  if (ks < nks) step(i0, ks);
+  if (ks + 1 < nks) step(i1, ks + 1);
+  if constexpr (NST == 4) {
+    if (ks + 2 < nks) step(i2, ks + 2);
+  }
+  rv_vm_wait<0>();                                   // the clamped refills past the last step, before LDS is reused
+  __syncthreads();
+
+  // epilogue: lane holds positions pw + 32 nt + n, dims 32 mt + 8 q + 4 hh + c
+  // (head mt / 4) in acc[mt][nt][4 q + c].  Wave w stages its 64 x 256 tile in
+  // array w: row = local position (512 bytes), 16-byte chunk c at c ^ (row & 31).
+  uint8_t* cw = wave == 0 ? st0 : wave == 1 ? st1 : wave == 2 ? st2 : st3;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const bool live = pw + nt * 32 + n < S;
-    uint16_t* crow = cw + (nt * 32 + n) * C_PITCH + 4 * hh;
+    const int row = nt * 32 + n;
+    const bool live = pw + row < S;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q4 = 0; q4 < 4; ++q4) {
         uint32_t w[2];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
-          const float v0 = live ? acc[mt][nt][4 * q + 2 * c2] : 0.f;
-          const float v1 = live ? acc[mt][nt][4 * q + 2 * c2 + 1] : 0.f;
+          const float v0 = live ? acc[mt][nt][4 * q4 + 2 * c2] : 0.f;
+          const float v1 = live ? acc[mt][nt][4 * q4 + 2 * c2 + 1] : 0.f;
           w[c2] = (uint32_t)pf_bits<KVT>(v0) | ((uint32_t)pf_bits<KVT>(v1) << 16);
         }
-        *(uint2*)(crow + mt * 32 + 8 * q) = make_uint2(w[0], w[1]);
+        const int c16 = (mt * 4 + q4) ^ (row & 31);
+        *(uint2*)(cw + row * 512 + c16 * 16 + hh * 8) = make_uint2(w[0], w[1]);
       }
   }
-  __syncthreads();
-  if (hlive) {
+  // each wave reads back only its own array: no barrier
+#pragma unroll
+  for (int hs = 0; hs < 2; ++hs) {
+    const int hw = 2 * hp + hs;
+    if (hw >= a.Hkv) break;                          // an odd Hkv leaves the last pair's second head empty
     KVT* dst = (KVT*)a.vbuf + (((int64_t)b * a.Hkv + hw) * a.S_pad) * HEAD_DIM;
 #pragma unroll 4
     for (int it = 0; it < RV_WAVE_POS * 16 / 64; ++it) {
       const int idx = it * 64 + lane, row = idx >> 4, ch = idx & 15;
       const int p = pw + row;
-      if (p < a.S_pad) *(uint4*)(dst + (int64_t)p * HEAD_DIM + ch * 8) = *(const uint4*)&cw[row * C_PITCH + ch * 8];
+      if (p < a.S_pad)
+        *(uint4*)(dst + (int64_t)p * HEAD_DIM + ch * 8) = *(const uint4*)(cw + row * 512 + (((hs * 16 + ch) ^ (row & 31)) << 4));
     }
   }
 }
@@ -762,10 +883,13 @@ static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t m
   else hipLaunchKernelGGL((recon_kernel<XT, 0>), rg, dim3(256), 0, st, r);
   r.rv_nb = (int)ceil_div(a.S, RV_POS);
   r.rv_blocks = r.rv_nb * B;
-  const dim3 vg((unsigned)(ceil_div(r.rv_blocks, 8) * 8 * ((a.Hkv + 1) / 2)));
-  if (a.v_blk) hipLaunchKernelGGL((recon_v_kernel<XT, 2>), vg, dim3(512), 0, st, r);
-  else if (a.v_g64) hipLaunchKernelGGL((recon_v_kernel<XT, 1>), vg, dim3(512), 0, st, r);
-  else hipLaunchKernelGGL((recon_v_kernel<XT, 0>), vg, dim3(512), 0, st, r);
+  const int nhp = (a.Hkv + 1) / 2;
+  r.rv_hpx = nhp >= 8 ? (int)ceil_div(nhp, 8) : 0;
+  const dim3 vg((unsigned)(r.rv_hpx ? 8 * r.rv_hpx * r.rv_blocks : ceil_div(r.rv_blocks, 8) * 8 * nhp));
+  if (a.v_blk) hipLaunchKernelGGL((recon_v_kernel<XT, 2, false>), vg, dim3(256), 0, st, r);
+  else if (a.v_g64 && a.Rv < 32) hipLaunchKernelGGL((recon_v_kernel<XT, 1, true>), vg, dim3(256), 0, st, r);
+  else if (a.v_g64) hipLaunchKernelGGL((recon_v_kernel<XT, 1, false>), vg, dim3(256), 0, st, r);
+  else hipLaunchKernelGGL((recon_v_kernel<XT, 0, false>), vg, dim3(256), 0, st, r);
   int e = (int)hipGetLastError();
   if (e) return e;
   if (mid && (e = (int)hipEventRecord(mid, st))) return e;
