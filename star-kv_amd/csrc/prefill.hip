@@ -399,6 +399,11 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
   constexpr int NST = rv_nst<Q>();
   constexpr int D = NST - 1;                         // prefetch distance (steps)
   constexpr int NL = rv_lat_ops<Q>();
+  // where a step's refill and latent loads are issued: packed formats (ring
+  // depth 4) in the first two regions of the next step, dense (depth 3, one
+  // step less lead) at the end of the step itself; either way the next
+  // stage's wait before the barrier counts one step's DMA + latent loads
+  constexpr bool EARLY = D == 3;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
@@ -573,6 +578,7 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
     constexpr int i = decltype(ic)::value;
     const std::integral_constant<int, (i + 1) % NST> inext;
     const std::integral_constant<int, (i + NST - 1) % NST> iprev;
+    const std::integral_constant<int, (i + NST - 2) % NST> ipre2;
     if constexpr (Q == 0) rv_vm_wait<8 + NL>();      // this step's latents landed (issued two steps back)
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -584,23 +590,24 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
         // this chunk's operands (read a region ago) are in; with them retired
         // the next chunk's 8 reads keep the LDS counter within its 15
         __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_sched_barrier(0);
         read_a(ic, kk + 1, afn);
       } else {
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // chunk 3's operands in (as above)
         // this wave's part of stage ks + 1 landed (packed formats: and the
         // latents of ks + 1, issued just after it)
-        __builtin_amdgcn_s_waitcnt(0xC07F);           // chunk 3's operands in (as above)
         if constexpr (Q == 0) rv_vm_wait<0>();
         else rv_vm_wait<8 + NL>();
+        if (ks + 2 == nks && (R & 63)) tail_fix(raw[(i + 1) % NST], ks + 1);
         // stage ks + 1 complete for all waves; stage ks - 1 free.  A bare
         // barrier: each wave has waited for its own DMA above, and a fence
         // here would also wait for the refills still in flight into the
         // other stages.  The memory clobber keeps the compiler from moving
         // LDS accesses across it.
         asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         read_a(inext, 0, afn);                       // the next step's chunk 0, in flight under this chunk's MFMAs
-        if (ks + 2 == nks && (R & 63)) tail_fix(raw[(i + 1) % NST], ks + 1);
       }
-      __builtin_amdgcn_sched_barrier(0);
       if constexpr (Q == 0) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) bfc[nt] = raw[i].d[nt][kk];
@@ -612,10 +619,40 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
       if constexpr (Q != 0) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) bfn[nt] = kk < 3 ? frag(raw[i], ks, nt, kk + 1) : frag(raw[(i + 1) % NST], ks + 1, nt, 0);
+        // an empty use here keeps the dequantisation in this region (under
+        // this chunk's MFMAs) instead of sunk past the next region's branch
+        asm volatile("" ::"v"(bfn[0].x), "v"(bfn[0].y), "v"(bfn[0].z), "v"(bfn[0].w), "v"(bfn[1].x), "v"(bfn[1].y),
+                     "v"(bfn[1].z), "v"(bfn[1].w));
       }
-      if (kk == 3) {
-        issue(iprev, ks + D);
-        load(ks + D, raw[(i + D) % NST]);
+      if constexpr (EARLY) {
+        // packed formats: stage ks + D - 1 into the array freed by the last
+        // barrier, and its latents, one region each
+        if (kk == 0) issue(ipre2, ks + D - 1);
+        if (kk == 1) load(ks + D - 1, raw[(i + D - 1) % NST]);
+      } else {
+        if (kk == 3) {
+          issue(iprev, ks + D);
+          load(ks + D, raw[(i + D) % NST]);
+        }
+      }
+      // one wave per SIMD issues in program order: spread the operand reads,
+      // loads and VALU work between the MFMAs so that they issue while the
+      // previous MFMA runs
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // 1 LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);          // 3 VALU
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // 1 MFMA
+        if (EARLY ? kk < 2 : kk == 3) {
+          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);        // 2 global loads (DMA, latents)
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);        // 5 VALU
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);        // 3 VALU
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -625,16 +662,13 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
   const std::integral_constant<int, 2> i2;
   const std::integral_constant<int, 3> i3;
 
-  // prologue: stages 0 .. D - 1 and their latents, in the steady state's order
+  // prologue: stages 0 and 1 and their latents, in the steady state's order
+  // (step 0 issues stage 2 with EARLY, and D = 2 needs no more)
   issue(i0, 0);
   load(0, raw[0]);
   issue(i1, 1);
   load(1, raw[1]);
-  if constexpr (D == 3) {
-    issue(i2, 2);
-    load(2, raw[2]);
-  }
-  rv_vm_wait<(D - 1) * (8 + NL)>();                  // this wave's part of stage 0 and the latents of step 0
+  rv_vm_wait<8 + NL>();                              // this wave's part of stage 0 and the latents of step 0
   __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0): no scalar loads pending into the loop
   __syncthreads();
   read_a(i0, 0, afA);
