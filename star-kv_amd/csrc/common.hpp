@@ -172,7 +172,7 @@ struct RopeApplyArgs {
 // ---------------------------------------------------------------------------
 // Prefill arguments (prefill.hip).
 // ---------------------------------------------------------------------------
-constexpr int PF_K_POS = 512;    // positions per K-reconstruction workgroup
+constexpr int PF_K_POS = 256;    // positions per K-reconstruction workgroup
 constexpr int PF_V_POS = 256;    // positions per V-reconstruction workgroup (two KV heads)
 constexpr int PF_Q_POS = 256;    // queries per attention workgroup
 struct PFArgs {

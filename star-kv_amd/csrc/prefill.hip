@@ -5,7 +5,7 @@
 //
 // 1. recon_kernel / recon_v_kernel: MFMA GEMM tiles computing
 //    K = RoPE(X_k[s] . B_k) (RoPE applied in the epilogue from the decode's
-//    RoPE table; per (KV head, b, 512 positions)) and V = X_v[s] . U_v[h]^T
+//    RoPE table; per (KV head, b, 256 positions)) and V = X_v[s] . U_v[h]^T
 //    (per (KV-head pair, b, 256 positions)), into [B][Hkv][S_pad][128]
 //    fp16 buffers (for either activation dtype: the reference materialises
 //    K and V in the activation dtype, model.py:431-442; fp16 holds bf16
@@ -142,18 +142,20 @@ __device__ inline uint4 pf_dq_g64(uint32_t w, uint16_t s16, uint16_t z16) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// K reconstruction: per (KV head h, b, 512 positions) one workgroup of 4
-// waves; wave w computes C^T[d][p] for all 128 dims d and its 128 positions
-// p as 4 x 4 MFMA tiles (A = B_k[h], dims as rows, staged whole in LDS as
+// K reconstruction: per (KV head h, b, 256 positions) one workgroup of 4
+// waves; wave w computes C^T[d][p] for all 128 dims d and its 64 positions
+// p as 4 x 2 MFMA tiles (128 accumulators: two workgroups share a CU, so one's
+// stores overlap the other's loads and MFMAs) (A = B_k[h], dims as rows, staged whole in LDS as
 // [j][d] and read with the transposed LDS load; B = latent rows, positions as
 // columns, loaded from global straight into registers one K-step ahead).  A
 // K-step is 64 ranks; within it lane half hh takes ranks [32 hh, 32 hh + 32)
 // (MFMA K-chunk kk: ranks 32 hh + 8 kk .. + 7) in both operands, so each lane
 // reads one contiguous 32-rank run of a latent row.  RoPE pairs (d, d + 64)
 // sit in M-tiles mt and mt + 2 of the same lane.  The epilogue stages each
-// wave's 128 x 128 tile in LDS and writes whole 256-byte rows.
+// wave's 64 x 128 tile in LDS and writes whole 256-byte rows.
 // ---------------------------------------------------------------------------
-constexpr int RC_WAVE_POS = 128;                 // positions per wave
+constexpr int RC_WAVE_POS = 64;                  // positions per wave
+constexpr int RC_NT = RC_WAVE_POS / 32;          // N-tiles per wave
 constexpr int RC_POS = 4 * RC_WAVE_POS;          // positions per workgroup
 static_assert(RC_POS == PF_K_POS, "host grid sizing");
 constexpr int RC_KS = 64;                        // ranks per K-step
@@ -163,20 +165,20 @@ constexpr int C_PITCH = 136;                     // halves per epilogue row
 constexpr int RC_LDS = 4 * RC_WAVE_POS * C_PITCH;
 
 // raw K latent data of one K-step for this lane: [N-tile][K-chunk]
-template <int Q> struct RkRaw { uint2 d[4][4]; };                         // int8 / reference split: <= 8 bytes per chunk
-template <> struct RkRaw<0> { uint4 d[4][4]; };                           // dense: 8 ranks per chunk
+template <int Q> struct RkRaw { uint2 d[RC_NT][4]; };                         // int8 / reference split: <= 8 bytes per chunk
+template <> struct RkRaw<0> { uint4 d[RC_NT][4]; };                          // dense: 8 ranks per chunk
 
 // Q: 0 dense act dtype, 1 int8 with one scale per (b, h, s), 2 the reference
 // split format (ranks below ksplit int8 or int4, the rest int4, each block
 // with its scale per (b, h, s))
 template <typename XT, int Q>
-__global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
+__global__ __launch_bounds__(256, 2) void recon_kernel(const PFArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[RC_LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
   // XCD-aware order: workgroup L runs on XCD L % 8, and the Hkv heads of one
-  // (batch, 512-position block) all land on one XCD
+  // (batch, 256-position block) all land on one XCD
   const int L = blockIdx.x, t8 = L >> 3;
   const int h = t8 % a.Hkv, blk = (t8 / a.Hkv) * 8 + (L & 7);
   if (blk >= a.rc_blocks) return;
@@ -187,12 +189,12 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   const int nks = (R + RC_KS - 1) / RC_KS;
 
   // per N-tile latent row (clamped position) and scales
-  const uint8_t* xrow[4];
-  const uint8_t* xrow2[4];                           // reference split: the lower (int4) block
-  uint16_t ksc[4] = {0, 0, 0, 0}, ksc2[4] = {0, 0, 0, 0};
+  const uint8_t* xrow[RC_NT];
+  const uint8_t* xrow2[RC_NT];                           // reference split: the lower (int4) block
+  uint16_t ksc[RC_NT] = {}, ksc2[RC_NT] = {};
   const bool klo = Q == 2 && R > a.ksplit;           // this head has a lower block
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
+  for (int nt = 0; nt < RC_NT; ++nt) {
     const int pc = min(pw + nt * 32 + n, S - 1);
     constexpr int64_t es = Q ? 1 : 2;                // latent offsets: bytes (quantised) or elements
     xrow[nt] = (const uint8_t*)a.kx + (b * a.kx_sb + a.kxoff[h] + (int64_t)pc * a.kxpitch[h]) * es;
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   auto load = [&](int ks, RkRaw<Q>& r) {
     const int j0 = ks * RC_KS + 32 * hh;             // this lane's first rank of the step
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < RC_NT; ++nt)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const int j = min(j0 + 8 * kk, R - 8);
@@ -256,11 +258,11 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
       *(uint4*)&lds[j * BK_PITCH + d8] = v;
     }
   }
-  floatx16 acc[4][4];
+  floatx16 acc[4][RC_NT];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = floatx16{};
+    for (int nt = 0; nt < RC_NT; ++nt) acc[mt][nt] = floatx16{};
 
   RkRaw<Q> cur, nxt;
   load(0, cur);
@@ -270,16 +272,16 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
     if (more) load(ks + 1, nxt);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      uint4 bf[4];
+      uint4 bf[RC_NT];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) bf[nt] = frag(cur, ks, nt, kk);
+      for (int nt = 0; nt < RC_NT; ++nt) bf[nt] = frag(cur, ks, nt, kk);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const uint16_t* sb = lds + (ks * RC_KS + 8 * kk) * BK_PITCH + tr_off + 32 * mt;
         const uint2 lo = pf_read_tr16(sb), hi = pf_read_tr16(sb + 4 * BK_PITCH);
         const uint4 af = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = pf_mfma<XT>(af, bf[nt], acc[mt][nt]);
+        for (int nt = 0; nt < RC_NT; ++nt) acc[mt][nt] = pf_mfma<XT>(af, bf[nt], acc[mt][nt]);
       }
     }
     if (more) cur = nxt;
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(256, 1) void recon_kernel(const PFArgs a) {
   // epilogue: lane holds positions pw + 32 nt + n, dims 32 mt + 8 q + 4 hh + c in acc[mt][nt][4q + c]
   uint16_t* cw = lds + wave * RC_WAVE_POS * C_PITCH;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
+  for (int nt = 0; nt < RC_NT; ++nt) {
     const int p = pw + nt * 32 + n;
     const bool live = p < S;
     uint16_t* crow = cw + (nt * 32 + n) * C_PITCH + 4 * hh;
