@@ -10,10 +10,9 @@
 // rows are the M = B * gs (batch, query head of kv's group) pairs.  It sums
 // the chunk partials of its columns in fixed chunk order into LDS, multiplies
 // them by its U_v columns (fp32; the weights convert exactly) and writes the
-// [M][128] partial up-projection of its slice.  Each thread sums one 16-byte
-// column group of one row over a contiguous part of the chunk range (up to
-// 16 loads in flight); with few rows the range is cut into more parts,
-// added in part order.
+// [M][128] partial up-projection of its slice.  When a row block has fewer
+// rows than the workgroup has thread rows (small batch), the chunk range is
+// cut into P contiguous parts summed side by side and added in part order.
 // With few workgroups (small batch, few KV heads) the chunks are also cut
 // into n_cs contiguous sets, one workgroup each (grid z): the up-projection
 // is linear, so each set's projection is a partial of its own.
@@ -24,8 +23,8 @@
 // atomics.
 //
 // Both kernels move a few MB and are latency-bound, so each thread issues
-// its loads in batches of independent addresses and adds them afterwards in
-// their fixed order.
+// its loads in batches of up to 64 independent addresses and adds them
+// afterwards in their fixed order.
 #include <algorithm>
 #include <type_traits>
 
@@ -62,14 +61,16 @@ __device__ inline float uv_elem(const uint4* w, int e, __bf16*) {
   return __uint_as_float((e & 1) ? (x & 0xffff0000u) : (x << 16));
 }
 
-// P16: the partials are fp16, each divided by its chunk's softmax sum, which
-// multiplies it back here (the sum's address is the same for every column
-// of a row).
-template <typename WT, int SW, bool FAST, bool P16>
+// RB: rows per thread and batch of the chunk sums (the row block's rows over
+// the JT thread rows, rounded up: 2 or 4).  P16: the partials are fp16,
+// each divided by its chunk's softmax sum, which multiplies it back here
+// (the sum's address is the same for every column of a row).
+template <typename WT, int SW, bool FAST, int RB, bool P16>
 __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   typedef typename std::conditional<P16, _Float16, float>::type PT;
+  constexpr int JT = 256 / SW;                     // rows summed side by side
   __shared__ float os[UP_MB][SW + 4];
-  __shared__ float ost[256 * 8 / SW][SW + 4];      // chunk-part sums, one row per (part, row) slot
+  __shared__ float osp[JT][SW + 4];                // chunk-part sums (P > 1)
   const int tid = threadIdx.x;
   const int sl = blockIdx.x, kv = blockIdx.y, cs = blockIdx.z;
   const int cb0 = (int)((int64_t)cs * a.n_c2 / a.n_cs), cb1 = (int)((int64_t)(cs + 1) * a.n_c2 / a.n_cs);
@@ -108,53 +109,73 @@ __global__ __launch_bounds__(256) void up_proj_kernel(const UPArgs a) {
   };
 
   float* yp = a.ypart + (((int64_t)kv * a.n_sl + sl) * a.n_cs + cs) * M * HEAD_DIM;
-  // chunk sums: thread (slot g, column group cg) sums VW columns of one row
-  // over one contiguous part of the chunk range with 16-byte loads, UP_CB
-  // chunks in flight; a row block of mb rows gets P = G / mb parts per row,
-  // which meet in LDS in part order
-  constexpr int VW = 16 / (int)sizeof(PT), CG = SW / VW, G = 256 / CG;
-  const int g = tid / CG, cg = tid % CG;
-  const int ng = (nj + VW - 1) / VW;                      // column groups of the slice
-  const int cgc = min(cg, ng - 1);                        // groups past the slice re-read its last
+  const int jj = tid % SW, mr = tid / SW;
+  const int jc = j0 + min(jj, nj - 1);                    // columns past the slice re-read its last
   for (int m0 = 0; m0 < M; m0 += UP_MB) {
     const int mb = min(UP_MB, M - m0);
-    const int P = mb < G ? G / mb : 1;
-    for (int rr = g; rr < P * mb; rr += G) {
-      const int part = rr / mb, m = m0 + rr % mb, q = kv * gs + m % gs;
-      const int bq = (m / gs) * a.n_hg + (q >> 5);
-      const int c_lo = (int)((int64_t)part * nc / P), c_hi = (int)((int64_t)(part + 1) * nc / P);
-      const PT* pp = (const PT*)a.part + (((int64_t)bq * a.n_c2 + cb0) * 32 + (q & 31)) * a.Rvp + j0 + cgc * VW;
-      float sv[VW] = {};
-      for (int c = c_lo; c < c_hi; c += UP_CB) {
-        uint4 raw[UP_CB];
-        float ps[UP_CB];
+    const int P = mb < JT ? JT / mb : 1;           // chunk parts per row
+    if (P > 1) {
+      // thread row mr = part * mb + row sums chunks [c_lo, c_hi) of its row
+      if (mr < P * mb) {
+        const int part = mr / mb, m = m0 + mr % mb, q = kv * gs + m % gs;
+        const int bq = (m / gs) * a.n_hg + (q >> 5);
+        const int c_lo = cb0 + (int)((int64_t)part * nc / P), c_hi = cb0 + (int)((int64_t)(part + 1) * nc / P);
+        const PT* p = (const PT*)a.part + ((int64_t)bq * a.n_c2 * 32 + (q & 31)) * a.Rvp + jc;
+        float sp = 0.f;
+        for (int c = c_lo; c < c_hi; c += UP_CB) {
+          float v[UP_CB];
 #pragma unroll
-        for (int k = 0; k < UP_CB; ++k) {
-          const int cc = min(c + k, c_hi - 1);
-          raw[k] = *(const uint4*)(pp + cc * cstr);
-          ps[k] = P16 ? psum_of(m, cc) : 1.f;
-        }
-#pragma unroll
-        for (int k = 0; k < UP_CB; ++k)
-          if (c + k < c_hi) {
-#pragma unroll
-            for (int e = 0; e < VW; ++e) {
-              float v;
-              if constexpr (P16) v = (float)__builtin_bit_cast(half8, raw[k])[e] * ps[k];
-              else v = __builtin_bit_cast(float4, raw[k])[e];
-              sv[e] += v;
-            }
+          for (int k = 0; k < UP_CB; ++k) {
+            const int cc = min(c + k, c_hi - 1);
+            v[k] = (float)p[cc * cstr];
+            if constexpr (P16) v[k] *= psum_of(m, cc - cb0);
           }
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k)
+            if (c + k < c_hi) sp += v[k];
+        }
+        osp[mr][jj] = sp;
+      }
+      __syncthreads();
+      if (tid < mb * SW) {
+        const int row = tid / SW, col = tid % SW;
+        float sr = 0.f;
+        for (int part = 0; part < P; ++part) sr += osp[part * mb + row][col];
+        os[row][col] = col < nj ? sr : 0.f;
+      }
+    }
+    // chunk sums of rows m0 .. m0+mb over the slice's columns: UP_RB rows
+    // per thread at a time, UP_CB chunks each (rows past mb re-read row mb-1)
+    for (int mm0 = mr; P == 1 && mm0 < mb; mm0 += JT * RB) {
+      const PT* p[RB];
+      int mrow[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int m = m0 + min(mm0 + JT * r, mb - 1), q = kv * gs + m % gs;
+        const int bq = (m / gs) * a.n_hg + (q >> 5);
+        p[r] = (const PT*)a.part + (((int64_t)bq * a.n_c2 + cb0) * 32 + (q & 31)) * a.Rvp + jc;
+        mrow[r] = m;
+      }
+      float s[RB] = {};
+      for (int c = 0; c < nc; c += UP_CB) {
+        float v[RB][UP_CB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k) {
+            const int cc = min(c + k, nc - 1);
+            v[r][k] = (float)p[r][cc * cstr];
+            if constexpr (P16) v[r][k] *= psum_of(mrow[r], cc);
+          }
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+          for (int k = 0; k < UP_CB; ++k)
+            if (c + k < nc) s[r] += v[r][k];
       }
 #pragma unroll
-      for (int e = 0; e < VW; ++e) ost[rr][cg * VW + e] = cg * VW + e < nj ? sv[e] : 0.f;
-    }
-    __syncthreads();
-    for (int idx = tid; idx < mb * SW; idx += 256) {
-      const int r = idx / SW, col = idx % SW;
-      float sr = 0.f;
-      for (int part = 0; part < P; ++part) sr += ost[part * mb + r][col];
-      os[r][col] = sr;
+      for (int r = 0; r < RB; ++r)
+        if (mm0 + JT * r < mb) os[mm0 + JT * r][jj] = jj < nj ? s[r] : 0.f;
     }
     __syncthreads();
     // partial up-projection of the slice: two rows per pass (one per half block)
@@ -208,15 +229,23 @@ __global__ __launch_bounds__(256) void up_finish_kernel(const UPArgs a) {
   ((OT*)a.out)[b * a.o_sb + q * a.o_sh + d] = (OT)(s / L);
 }
 
+template <typename WT, int SW, int RB>
+static void launch_up_rb(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
+  if (a.part16) {
+    if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, RB, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, RB, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, RB, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, RB, false>), grid, dim3(256), 0, st, a);
+  }
+}
+
 template <typename WT, int SW>
 static void launch_up_sw(const UPArgs& a, bool fast, dim3 grid, hipStream_t st) {
-  if (a.part16) {
-    if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, true>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, true>), grid, dim3(256), 0, st, a);
-  } else {
-    if (fast) hipLaunchKernelGGL((up_proj_kernel<WT, SW, true, false>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((up_proj_kernel<WT, SW, false, false>), grid, dim3(256), 0, st, a);
-  }
+  // rows of the largest row block per thread row: two per batch suffice up to 2 * JT
+  const int mb = std::min(UP_MB, a.B * a.gs);
+  if (mb > 2 * (256 / SW)) launch_up_rb<WT, SW, 4>(a, fast, grid, st);
+  else launch_up_rb<WT, SW, 2>(a, fast, grid, st);
 }
 
 template <typename WT>
