@@ -54,6 +54,7 @@ int choose_splits(int64_t groups, int slots, int n_units, int max_n, double c0, 
 
 struct KPlan {
   int n_wg = 0;
+  int per_cu = K1_WG_PER_CU;   // K1 workgroups resident per CU (the grouped-query kernel: two)
   bool fast = false;
 };
 
@@ -370,6 +371,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
     for (int h = 0; h < n; ++h) order[h] = h;
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return k.rank[x] > k.rank[y]; });
     plan.n_wg = (int)ceil_div(n, 2);
+    plan.per_cu = 2;
     if (plan.n_wg * 4 > K_MAX_WAVES) return STARKV_ERR_LIMIT;
     for (int w = 0; w < K_MAX_WAVES; ++w)
       for (int i = 0; i < K_MAXI; ++i) a.items[w][i] = 0;
@@ -421,7 +423,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
       max_chunks = std::max(max_chunks, chunks);
     }
     a.ws_stage = (int)round_up(max_chunks, 64) * 16 + 8192 + (a.ws_i8 ? 1024 : 0);
-    a.ws_nst = std::min(4, (gqa ? K1_GQ_RING_BYTES : K1_WS_RING_BYTES) / a.ws_stage);
+    a.ws_nst = gqa ? std::min(6, K1_GQ_RING_BYTES / a.ws_stage) : std::min(4, K1_WS_RING_BYTES / a.ws_stage);
   }
   return STARKV_OK;
 }
@@ -494,12 +496,12 @@ struct DecodeLayout {
 // share of the P.V traffic (at 272 positions about as many bytes as the
 // int4 V latent) and halving them pays for the per-chunk rescale in the
 // up-projection; with long chunks it does not (measured).
-DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int vq, int64_t v_row_bytes,
+DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int k1pc, int vq, int64_t v_row_bytes,
                            bool f16) {
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
-  L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 256, 3.0, 0.0);
+  L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * k1pc, n_tiles, 256, 3.0, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
   L.n_hg = head_groups(Hq);
@@ -593,7 +595,7 @@ int64_t v_row_bytes(const starkv_vlatent& v) {
   return std::max({v.stride_s, v.scale_stride_s * 2, v.stride2_s, v.scale2_stride_s * 2});
 }
 
-int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
+int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* k1pc, int* vq) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S) return STARKV_ERR_SHAPE;
   if (d->head_dim != HEAD_DIM) return STARKV_ERR_SHAPE;
@@ -612,6 +614,7 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* vq) {
   KPlan plan;
   if ((st = build_k_plan(d->k, d->n_q_heads, *gs, d->dtype, d->seq_len, tmp, plan))) return st;
   *n_wg = plan.n_wg;
+  *k1pc = plan.per_cu;
   return STARKV_OK;
 }
 
@@ -727,7 +730,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
   const int n_tiles = (int)ceil_div(d->seq_len, TILE);
-  int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * K1_WG_PER_CU, n_tiles, 256, 3.0, 0.0);
+  int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * plan.per_cu, n_tiles, 256, 3.0, 0.0);
   a.tiles_per_chunk = (int)ceil_div(n_tiles, nc);
   a.n_chunks = (int)ceil_div(n_tiles, a.tiles_per_chunk);
   const bool fast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
@@ -770,18 +773,18 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
 }
 
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
-  int gs = 0, n_wg = 0, vq = 0;
-  if (validate_decode(d, &gs, &n_wg, &vq)) return 0;
-  return decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v),
+  int gs = 0, n_wg = 0, k1pc = 1, vq = 0;
+  if (validate_decode(d, &gs, &n_wg, &k1pc, &vq)) return 0;
+  return decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, k1pc, vq, v_row_bytes(d->v),
                     d->dtype == STARKV_F16).total;
 }
 
 static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t workspace_bytes, void* stream,
                        void* const* events) {
-  int gs = 0, n_wg = 0, vq = 0, st;
-  if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
+  int gs = 0, n_wg = 0, k1pc = 1, vq = 0, st;
+  if ((st = validate_decode(d, &gs, &n_wg, &k1pc, &vq))) return st;
   const DecodeLayout L =
-      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v),
+      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, k1pc, vq, v_row_bytes(d->v),
                     d->dtype == STARKV_F16);
   if (!workspace || workspace_bytes < L.total) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
@@ -883,10 +886,10 @@ int scratch_address(void** out) {
 extern "C" {
 
 int starkv_decode_attention_noalloc(const starkv_decode_desc* d, void* stream) {
-  int gs = 0, n_wg = 0, vq = 0, st;
-  if ((st = validate_decode(d, &gs, &n_wg, &vq))) return st;
+  int gs = 0, n_wg = 0, k1pc = 1, vq = 0, st;
+  if ((st = validate_decode(d, &gs, &n_wg, &k1pc, &vq))) return st;
   const size_t need =
-      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, vq, v_row_bytes(d->v),
+      decode_layout(d->batch, d->n_q_heads, d->k.n_kv_heads, d->seq_len, d->v.rank, n_wg, k1pc, vq, v_row_bytes(d->v),
                     d->dtype == STARKV_F16).total;
   if (need > (size_t)STARKV_NOALLOC_SCRATCH_BYTES) return STARKV_ERR_LIMIT;
   void* ws = nullptr;

@@ -75,7 +75,7 @@ struct KArgs {
   int16_t krank[K_MAX_KV];
 };
 constexpr int K1_GQ_CARRY_BYTES = 2 * 2 * 64 * 4 * 4;          // GQA: dim-half partial logits, 2 tiles x 2 heads
-constexpr int K1_GQ_RING_BYTES = 163840 - K1_GQ_CARRY_BYTES;   // its LDS ring
+constexpr int K1_GQ_RING_BYTES = 81920 - K1_GQ_CARRY_BYTES;    // its LDS ring (two workgroups per CU)
 
 // ---------------------------------------------------------------------------
 // P.V launch arguments.

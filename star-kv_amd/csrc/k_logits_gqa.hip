@@ -23,26 +23,28 @@
 //   kappa = d with bits 2 and 3 swapped turns accumulator entries 8j..8j+7
 //   of M-tile m into the B operand of K-step 2m + j as they are.
 //
-// Workgroup: 4 producer waves (the warp-specialised DMA ring of
-// k_logits_ws.hip: each tile's latent rows of the workgroup's KV heads, rows
-// rotated for conflict-free reads, plus the 8 KB RoPE operand) and 4
-// consumer waves, two per KV head: wave (slot, p) reconstructs M-tiles p and
-// p+2 (dims 32p..32p+31 and their RoPE partners), so its B_k^T operands (r/2
-// registers per lane) stay resident.  The p = 0 wave leaves its partial
-// logits of tile i in LDS; the p = 1 wave adds its own one tile later (after
-// the next barrier) and stores.
+// Workgroup: 4 waves, two per KV head: wave (slot, p) reconstructs M-tiles
+// p and p+2 (dims 32p..32p+31 and their RoPE partners), so its B_k^T
+// operands (r/2 registers per lane) stay resident.  Every wave also issues
+// its share of each tile's DMA into an LDS ring (the tile's latent rows of
+// the workgroup's KV heads, rows rotated for conflict-free reads, plus the
+// 8 KB RoPE operand), `ahead` = stages - 1 tiles ahead, and waits for its
+// own share with an explicit vmcnt before the tile's barrier.  Two
+// workgroups share a CU (80 KB of LDS and <= 256 registers each), so each
+// SIMD interleaves two waves' per-tile chains (reconstruction MFMAs ->
+// rotation -> q.K MFMAs).  The p = 0 wave hands its partial logits of a
+// tile to the p = 1 wave through LDS one tile later; the p = 1 wave adds
+// its own and stores.
 #include "common.hpp"
 
 namespace starkv {
 
 namespace {
 
-constexpr int GQ_PRODUCERS = 4;
-constexpr int GQ_CONSUMERS = 4;                  // 2 KV heads x 2 dim halves
+constexpr int GQ_WAVES = 4;                      // 2 KV heads x 2 dim halves
 constexpr int GQ_MAXH = 2;                       // KV heads per workgroup
 constexpr int GQ_RING = K1_GQ_RING_BYTES;
-constexpr int GQ_MAXK = (GQ_MAXH * 32 * 16 / 64 + 8 + GQ_PRODUCERS - 1) / GQ_PRODUCERS;   // DMA instructions per producer
-typedef __attribute__((address_space(3))) void lds_void;
+constexpr int GQ_MAXK = (GQ_MAXH * 32 * 16 / 64 + 8 + GQ_WAVES - 1) / GQ_WAVES;   // DMA instructions per wave and tile
 
 // 16-byte chunk rotation of staged rows (see k_logits_ws.hip: conflict-free
 // ds_read_b128 of one chunk of 8 consecutive rows)
@@ -57,12 +59,21 @@ template <int N> __device__ inline void gq_wait_vm() {
 __device__ inline void gq_wait_vm_n(int n) {
   switch (n) {
 #define GQ_CASE(N) case N: gq_wait_vm<N>(); break;
-    GQ_CASE(0) GQ_CASE(1) GQ_CASE(2) GQ_CASE(3) GQ_CASE(4) GQ_CASE(5) GQ_CASE(6) GQ_CASE(7)
-    GQ_CASE(8) GQ_CASE(9) GQ_CASE(10) GQ_CASE(11) GQ_CASE(12) GQ_CASE(13) GQ_CASE(14) GQ_CASE(15)
-    GQ_CASE(16) GQ_CASE(17) GQ_CASE(18) GQ_CASE(19) GQ_CASE(20)
+#define GQ_CASE8(N) GQ_CASE(N) GQ_CASE(N + 1) GQ_CASE(N + 2) GQ_CASE(N + 3) GQ_CASE(N + 4) GQ_CASE(N + 5) \
+    GQ_CASE(N + 6) GQ_CASE(N + 7)
+    GQ_CASE8(0) GQ_CASE8(8) GQ_CASE8(16) GQ_CASE8(24) GQ_CASE8(32) GQ_CASE8(40) GQ_CASE8(48) GQ_CASE8(56)
+#undef GQ_CASE8
 #undef GQ_CASE
     default: gq_wait_vm<0>(); break;
   }
+}
+
+// One 1 KB global -> LDS DMA (16 bytes per lane, to LDS byte address `lds` +
+// 16 * lane).  Written as inline assembly so that the compiler, which does
+// not see it write LDS, adds no waits of its own before the reads of other
+// stages; the kernel orders it with explicit vmcnt waits and barriers.
+__device__ inline void gq_dma(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 
 template <typename XT> struct GqVec;
@@ -75,145 +86,64 @@ __device__ inline floatx16 gq_mfma(typename GqVec<XT>::T a, typename GqVec<XT>::
   else return mfma_bf16(a, b, c);
 }
 
+// this wave's share of every tile's DMA: instructions m = wave + 4k
+struct GqDma {
+  const char* base[GQ_MAXK];   // lane address at tile0
+  uint32_t lstep[GQ_MAXK];     // bytes per tile (< 2^31, checked on the host)
+  int rowp[GQ_MAXK];           // latent: the lane's row in a tile; RoPE operand: -2^30 (never clamped)
+  int adv[GQ_MAXK];            // latent row pitch in bytes
+  int dst[GQ_MAXK];            // byte offset in a stage
+  int cnt;                     // instructions per tile
+  uint32_t ring;               // LDS byte address of the ring
+  int stage, nst, tile0, S;
+
+  // tile tile0 + i into stage i % nst; rows past S re-read row S - 1
+  __device__ inline void issue(int i) const {
+    const int tl = tile0 + i;
+    const uint32_t lb = ring + (uint32_t)((i % nst) * stage);
+#pragma unroll
+    for (int k = 0; k < GQ_MAXK; ++k) {
+      if (k >= cnt) break;
+      const int over = max(tl * TILE + rowp[k] - (S - 1), 0);
+      gq_dma(base[k] + (uint64_t)(uint32_t)i * lstep[k] - (int64_t)over * adv[k], lb + (uint32_t)dst[k]);
+    }
+  }
+};
+
+// the workgroup's KV heads and where their rows sit in a stage
+struct GqHeads {
+  int hkv[GQ_MAXH], hrank[GQ_MAXH], hoff[GQ_MAXH];
+  int tot;                     // 16-byte chunks of one tile
+};
+
 }  // namespace
 
-// OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
-template <typename XT, int OUTK>
-__global__ __launch_bounds__((GQ_CONSUMERS + GQ_PRODUCERS) * 64, 1) void k_logits_gqa_kernel(const KArgs a) {
+// One consumer wave (KV head slot, dim half p) over its tiles; NK = rank
+// K-steps (16 ranks each) rounded up to even, the B_k^T rows past the rank
+// being zero.  MASKED: an additive mask is read in the epilogue (its loads,
+// which the compiler waits for with counts that do not see the DMA, drain
+// the ring once per tile; the unmasked kernel issues no waited-for load in
+// its loop).
+template <typename XT, int OUTK, int NK, bool MASKED>
+__device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a, const GqHeads& H, const GqDma& d,
+                                                                  char* ring, float (*carry)[GQ_MAXH][64][4],
+                                                                  int slot, int p, int kv, int b, int chunk, int ntl,
+                                                                  int ahead) {
   typedef typename GqVec<XT>::T XV;
-  __shared__ __attribute__((aligned(16))) char ring[GQ_RING];          // a.ws_nst stages of a.ws_stage bytes
-  __shared__ float carry[2][GQ_MAXH][64][4];                           // p = 0 partial logits, by tile parity
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int t = lane & 31, hh = lane >> 5;
-  const int chunk = blockIdx.x, wgp = blockIdx.y, b = blockIdx.z;
-  const int S = a.S;
-  const int n_tiles = (S + TILE - 1) / TILE;
-  const int tile0 = chunk * a.tiles_per_chunk;
-  const int tile1 = min(tile0 + a.tiles_per_chunk, n_tiles);
-  if (tile0 >= tile1) return;
-  const int last = tile1 - 1;
-  const int ntl = tile1 - tile0;
-
-  // ---- the workgroup's KV heads (items of consumer waves 0 and 2), their
-  // ranks and chunk offsets in a stage
-  int hkv[GQ_MAXH], hrank[GQ_MAXH], hoff[GQ_MAXH];
-  int tot = 0;
-#pragma unroll
-  for (int k = 0; k < GQ_MAXH; ++k) {
-    const uint32_t itm = a.items[wgp * GQ_CONSUMERS + 2 * k][0];
-    hkv[k] = 0; hrank[k] = 8; hoff[k] = 1 << 30;
-    if (!item_valid(itm)) continue;
-    hkv[k] = item_kv(itm);
-    hrank[k] = a.krank[hkv[k]];
-    hoff[k] = tot;
-    tot += 32 * (hrank[k] >> 3);
-  }
-  // stage: latent chunks [0, 64 * nX), the RoPE operand in the last 8 KB
-  const int nX = (tot + 63) / 64, stage = a.ws_stage, nst = a.ws_nst;
-  if (tot == 0 || nX * 1024 + 8192 > stage || nst < 2 || nst * stage > GQ_RING) return;   // uniform
-
-  if (wave >= GQ_CONSUMERS) {
-    // ================= producer (as in k_logits_ws.hip) =================
-    const int pw = wave - GQ_CONSUMERS;
-    const int nI = nX + 8, ahead = nst - 1;
-    const char* src[GQ_MAXK];
-    int64_t adv[GQ_MAXK];
-    int rowpos[GQ_MAXK], tmul[GQ_MAXK], pmax[GQ_MAXK], dst[GQ_MAXK];
-    int cnt = 0;
-#pragma unroll
-    for (int k = 0; k < GQ_MAXK; ++k) {
-      const int m = pw + GQ_PRODUCERS * k;
-      src[k] = (const char*)a.rope; adv[k] = 8192; rowpos[k] = 0; tmul[k] = 1; pmax[k] = 1 << 30; dst[k] = 0;
-      if (m >= nI) continue;
-      ++cnt;
-      if (m >= nX) {
-        const int j = m - nX;
-        src[k] = (const char*)a.rope + (j * 64 + lane) * 16;
-        dst[k] = stage - 8192 + j * 1024;
-        continue;
-      }
-      int q = m * 64 + lane;
-      if (q >= tot) q = tot - 1;            // lanes past the last chunk re-read it into an unused slot
-      int hb = hoff[0], hr = hrank[0], hk = hkv[0];
-#pragma unroll
-      for (int j = 1; j < GQ_MAXH; ++j)
-        if (hoff[j] <= q) { hb = hoff[j]; hr = hrank[j]; hk = hkv[j]; }
-      const int n16 = hr >> 3, loc = q - hb;
-      const int row = loc / n16, cr = loc % n16;
-      const int c = (cr - gq_shift(row, n16) % n16 + n16) % n16;
-      src[k] = (const char*)a.x + (b * a.x_sb + a.xoff[hk]) * 2 + (int64_t)c * 16;
-      adv[k] = (int64_t)a.xpitch[hk] * 2;
-      rowpos[k] = row;
-      tmul[k] = TILE;
-      pmax[k] = S - 1;
-      dst[k] = m * 1024;
-    }
-    // full tiles (all 32 positions below S): first-tile address plus
-    // (tile - tile0) times a fixed per-lane step; the tail tile is clamped
-    const char* base[GQ_MAXK];     // lane address at tile0
-    uint32_t lstep[GQ_MAXK];       // bytes per tile (< 2^31, checked on the host)
-#pragma unroll
-    for (int k = 0; k < GQ_MAXK; ++k) {
-      base[k] = src[k] + (int64_t)(tile0 * tmul[k] + rowpos[k]) * adv[k];
-      lstep[k] = (uint32_t)(tmul[k] * adv[k]);
-    }
-    auto issue = [&](int i) __attribute__((always_inline)) {
-      const int tl = min(tile0 + i, last);
-      char* st = ring + (i % nst) * stage;
-      if ((tl + 1) * TILE <= S) {
-        const uint32_t ti = (uint32_t)(tl - tile0);
-#pragma unroll
-        for (int k = 0; k < GQ_MAXK; ++k) {
-          const int m = pw + GQ_PRODUCERS * k;
-          if (m >= nI) break;
-          __builtin_amdgcn_global_load_lds((const void*)(base[k] + (uint64_t)ti * lstep[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < GQ_MAXK; ++k) {
-          const int m = pw + GQ_PRODUCERS * k;
-          if (m >= nI) break;
-          const int64_t pos = min(tl * tmul[k] + rowpos[k], pmax[k]);
-          __builtin_amdgcn_global_load_lds((const void*)(src[k] + pos * adv[k]), (lds_void*)(st + dst[k]), 16, 0, 0);
-        }
-      }
-    };
-    for (int i = 0; i < ahead; ++i) issue(i);
-    for (int i = 0; i < ntl; ++i) {
-      gq_wait_vm_n((ahead - 1) * cnt);
-      __builtin_amdgcn_s_barrier();
-      issue(i + ahead);
-    }
-    __builtin_amdgcn_s_barrier();           // the consumers' extra barrier
-    gq_wait_vm<0>();
-    return;
-  }
-
-  // ================= consumer: KV head slot, dim half p =================
-  const int slot = wave >> 1, p = wave & 1;
-  const uint32_t itm = a.items[wgp * GQ_CONSUMERS + wave][0];
-  if (!item_valid(itm)) {                    // keep the workgroup's barrier count
-    for (int i = 0; i <= ntl; ++i) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      __builtin_amdgcn_s_barrier();
-    }
-    return;
-  }
-  const int kv = item_kv(itm), gs = a.gs;
-  const int r = hrank[slot], hb = hoff[slot], n16 = r >> 3, nk = (r + 15) >> 4;
+  const int lane = threadIdx.x & 63, t = lane & 31, hh = lane >> 5;
+  const int gs = a.gs, S = a.S, tile0 = d.tile0, stage = d.stage, nst = d.nst;
+  const int r = H.hrank[slot], hb = H.hoff[slot], n16 = r >> 3;
 
   // B_k^T operands of M-tiles p and p+2: lane l holds dim 32m + l%32, ranks
   // 16kk + 8hh + 0..7 (zero past r)
-  XV bt[2][8];
+  XV bt[2][NK];
   {
     const XT* bk = (const XT*)a.bk + a.bkoff[kv];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
       const int dim = 32 * (p + 2 * mi) + t;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
+      for (int kk = 0; kk < NK; ++kk) {
         XV v;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -237,37 +167,44 @@ __global__ __launch_bounds__((GQ_CONSUMERS + GQ_PRODUCERS) * 64, 1) void k_logit
       half8 v;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int d = 32 * (kk2 >> 1) + 8 * (2 * (kk2 & 1) + (i >> 2)) + 4 * hh + (i & 3);
-        v[i] = h < gs ? (_Float16)to_f32(qrow[d]) : (_Float16)0.f;
+        const int dd = 32 * (kk2 >> 1) + 8 * (2 * (kk2 & 1) + (i >> 2)) + 4 * hh + (i & 3);
+        v[i] = h < gs ? (_Float16)to_f32(qrow[dd]) : (_Float16)0.f;
       }
       qa[n] = v;
     }
   }
   // LDS offsets of this lane's latent chunk per rank K-step: row t, chunk
-  // 2kk + hh (past the rank: chunk 2kk, against zero B_k^T rows)
-  int xo[8];
+  // 2kk + hh (past the rank: a chunk of the same row, against zero B_k^T rows)
+  int xo[NK];
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) {
+  for (int kk = 0; kk < NK; ++kk) {
     const int c = min(2 * kk + hh < n16 ? 2 * kk + hh : 2 * kk, n16 - 1);
     xo[kk] = (hb + t * n16 + (c + gq_shift(t, n16)) % n16) * 16;
   }
   // query rows h < gs <= 8 are accumulator entries v = h % 4 of lane half h / 4
+  // operands in before the ring fills: the compiler's waits for them, which
+  // do not see the DMA, then hold none
+  gq_wait_vm<0>();
+  for (int i = 0; i < min(ahead, ntl); ++i) d.issue(i);
+
   float mx[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) mx[v] = -INFINITY;
-  float prev[4] = {0.f, 0.f, 0.f, 0.f};      // p = 1: own partial logits of the previous tile
+  float prev[4] = {0.f, 0.f, 0.f, 0.f};      // this wave's partial logits of the tile before the current one
 
   // epilogue of tile `ti` (absolute tile index): scale, mask, store, maxima
+  // (one store instruction per v < min(gs, 4): lane t = 0 of lane half 0
+  // always stores, so none is skipped; the DMA waits count them)
   auto emit = [&](const float* sum, int ti) __attribute__((always_inline)) {
     const int s = ti * TILE + t;
-    if (s >= S) return;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
+      if (v >= gs) break;
       const int h = 4 * hh + v;
-      if (h >= gs) continue;
+      if (h >= gs || s >= S) continue;
       const int qh = kv * gs + h;
       float val = a.wscale * sum[v];
-      if (a.mask != nullptr) val += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
+      if constexpr (MASKED) val += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
       const int64_t o = b * a.o_sb + (int64_t)ti * a.o_st + qh * a.o_sh + t;
       if constexpr (OUTK == 0) ((float*)a.out)[o] = val;
       else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)val;
@@ -276,31 +213,41 @@ __global__ __launch_bounds__((GQ_CONSUMERS + GQ_PRODUCERS) * 64, 1) void k_logit
     }
   };
 
+  // the start of step i: tile i - 1 handed over and stored, tile i's stage
+  // complete for every wave, the DMA of tile i + ahead issued.  The wait
+  // leaves outstanding exactly what this wave issued after its DMA of tile i:
+  // the DMA of tiles i + 1 .. i + ahead - 1 and (p = 1) the ns logit stores
+  // of each step from i - ahead (after that step's DMA) to i - 1 that
+  // emitted (steps >= 1).  The counter retires in issue order.
+  const int ns = p == 1 ? min(gs, 4) : 0;
   for (int i = 0; i < ntl; ++i) {
+    if (p == 0 && i >= 1) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) carry[i & 1][slot][lane][v] = prev[v];
+    }
+    gq_wait_vm_n(min(ahead - 1, ntl - 1 - i) * d.cnt + ns * min(ahead, max(i - 1, 0)));
     __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS reads and writes are done
-    __builtin_amdgcn_s_barrier();
-    if (p == 1 && i > 0) {
+    asm volatile("s_barrier" ::: "memory");
+    if (i + ahead < ntl) d.issue(i + ahead);  // into the stage of tile i - 1, read before this barrier
+    if (p == 1 && i >= 1) {
       float sum[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) sum[v] = prev[v] + carry[(i - 1) & 1][slot][lane][v];
+      for (int v = 0; v < 4; ++v) sum[v] = prev[v] + carry[i & 1][slot][lane][v];
       emit(sum, tile0 + i - 1);
     }
     const char* st = ring + (i % nst) * stage;
-    XV xb[8];
+    XV xb[NK];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      if (kk < nk) xb[kk] = *(const XV*)(st + xo[kk]);
+    for (int kk = 0; kk < NK; ++kk) xb[kk] = *(const XV*)(st + xo[kk]);
     half8 T4[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) T4[g] = *(const half8*)(st + stage - 8192 + ((4 * p + g) * 64 + lane) * 16);
     // K^T of M-tiles p (k0) and p+2 (k1)
     floatx16 k0 = floatx16{}, k1 = floatx16{};
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      if (kk < nk) {
-        k0 = gq_mfma<XT>(bt[0][kk], xb[kk], k0);
-        k1 = gq_mfma<XT>(bt[1][kk], xb[kk], k1);
-      }
+    for (int kk = 0; kk < NK; ++kk) {
+      k0 = gq_mfma<XT>(bt[0][kk], xb[kk], k0);
+      k1 = gq_mfma<XT>(bt[1][kk], xb[kk], k1);
     }
     // rotate: accumulator v is dim d = 32m + 8g + 4hh + e (g = v/4, e = v%4)
     // and its partner d + 64; (a cos, a sin) of frequency 32p + 8g + 4hh + e
@@ -309,30 +256,29 @@ __global__ __launch_bounds__((GQ_CONSUMERS + GQ_PRODUCERS) * 64, 1) void k_logit
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const float c = (float)T4[v >> 2][2 * (v & 3)], s = (float)T4[v >> 2][2 * (v & 3) + 1];
-      const float lo = k0[v] * c - k1[v] * s;
-      const float hi = k1[v] * c + k0[v] * s;
-      bop[v >> 3][v & 7] = (_Float16)lo;
-      bop[2 + (v >> 3)][v & 7] = (_Float16)hi;
+      bop[v >> 3][v & 7] = (_Float16)(k0[v] * c - k1[v] * s);
+      bop[2 + (v >> 3)][v & 7] = (_Float16)(k1[v] * c + k0[v] * s);
     }
+    // two chains of two K-steps each (dims 0-63 and their partners)
     floatx16 la = mfma_f16(qa[0], bop[0], floatx16{});
+    floatx16 lb = mfma_f16(qa[2], bop[2], floatx16{});
     la = mfma_f16(qa[1], bop[1], la);
-    la = mfma_f16(qa[2], bop[2], la);
-    la = mfma_f16(qa[3], bop[3], la);
-    if (p == 0) {
+    lb = mfma_f16(qa[3], bop[3], lb);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) carry[i & 1][slot][lane][v] = la[v];
-    } else {
+    for (int v = 0; v < 4; ++v) prev[v] = la[v] + lb[v];
+  }
+  // the last tile: handed over after one more barrier
+  if (p == 0) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) prev[v] = la[v];
-    }
+    for (int v = 0; v < 4; ++v) carry[ntl & 1][slot][lane][v] = prev[v];
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();              // publishes the last tile's partials
+  asm volatile("s_barrier" ::: "memory");
   if (p == 0) return;
   {
     float sum[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) sum[v] = prev[v] + carry[(ntl - 1) & 1][slot][lane][v];
+    for (int v = 0; v < 4; ++v) sum[v] = prev[v] + carry[ntl & 1][slot][lane][v];
     emit(sum, tile0 + ntl - 1);
   }
   if constexpr (OUTK == 0) {
@@ -347,12 +293,114 @@ __global__ __launch_bounds__((GQ_CONSUMERS + GQ_PRODUCERS) * 64, 1) void k_logit
   }
 }
 
+// OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
+template <typename XT, int OUTK, bool MASKED>
+__global__ __launch_bounds__(GQ_WAVES * 64, 2) void k_logits_gqa_kernel(const KArgs a) {
+  __shared__ __attribute__((aligned(16))) char ring[GQ_RING];          // a.ws_nst stages of a.ws_stage bytes
+  __shared__ float carry[2][GQ_MAXH][64][4];                           // p = 0 partial logits, by tile parity
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int chunk = blockIdx.x, wgp = blockIdx.y, b = blockIdx.z;
+  const int S = a.S;
+  const int n_tiles = (S + TILE - 1) / TILE;
+  const int tile0 = chunk * a.tiles_per_chunk;
+  const int tile1 = min(tile0 + a.tiles_per_chunk, n_tiles);
+  if (tile0 >= tile1) return;
+  const int ntl = tile1 - tile0;
+
+  // ---- the workgroup's KV heads (items of waves 0 and 2), their ranks and
+  // chunk offsets in a stage
+  GqHeads H;
+  H.tot = 0;
+#pragma unroll
+  for (int k = 0; k < GQ_MAXH; ++k) {
+    const uint32_t itm = a.items[wgp * GQ_WAVES + 2 * k][0];
+    H.hkv[k] = 0; H.hrank[k] = 8; H.hoff[k] = 1 << 30;
+    if (!item_valid(itm)) continue;
+    H.hkv[k] = item_kv(itm);
+    H.hrank[k] = a.krank[H.hkv[k]];
+    H.hoff[k] = H.tot;
+    H.tot += 32 * (H.hrank[k] >> 3);
+  }
+  // stage: latent chunks [0, 64 * nX), the RoPE operand in the last 8 KB
+  const int nX = (H.tot + 63) / 64, stage = a.ws_stage, nst = a.ws_nst;
+  if (H.tot == 0 || nX * 1024 + 8192 > stage || nst < 2 || nst * stage > GQ_RING) return;   // uniform
+  const int ahead = nst - 1;     // stage of tile i - 1 (its reads ended at barrier i) takes tile i + ahead
+
+  // ---- this wave's DMA share
+  GqDma d;
+  {
+    const int nI = nX + 8;
+    d.cnt = 0;
+#pragma unroll
+    for (int k = 0; k < GQ_MAXK; ++k) {
+      const int m = wave + GQ_WAVES * k;
+      d.base[k] = (const char*)a.rope; d.lstep[k] = 0; d.rowp[k] = -(1 << 30); d.adv[k] = 0; d.dst[k] = 0;
+      if (m >= nI) continue;
+      ++d.cnt;
+      if (m >= nX) {
+        const int j = m - nX;
+        d.base[k] = (const char*)a.rope + (int64_t)tile0 * 8192 + (j * 64 + lane) * 16;
+        d.lstep[k] = 8192;
+        d.dst[k] = stage - 8192 + j * 1024;
+        continue;
+      }
+      int q = m * 64 + lane;
+      if (q >= H.tot) q = H.tot - 1;        // lanes past the last chunk re-read it into an unused slot
+      int hb = H.hoff[0], hr = H.hrank[0], hk = H.hkv[0];
+#pragma unroll
+      for (int j = 1; j < GQ_MAXH; ++j)
+        if (H.hoff[j] <= q) { hb = H.hoff[j]; hr = H.hrank[j]; hk = H.hkv[j]; }
+      const int n16 = hr >> 3, loc = q - hb;
+      const int row = loc / n16, cr = loc % n16;
+      const int c = (cr - gq_shift(row, n16) % n16 + n16) % n16;
+      const int pitch = a.xpitch[hk] * 2;
+      d.base[k] = (const char*)a.x + (b * a.x_sb + a.xoff[hk]) * 2 + (int64_t)c * 16 +
+                  (int64_t)(tile0 * TILE + row) * pitch;
+      d.lstep[k] = (uint32_t)(TILE * pitch);
+      d.rowp[k] = row;
+      d.adv[k] = pitch;
+      d.dst[k] = m * 1024;
+    }
+    d.ring = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)ring;
+    d.stage = stage; d.nst = nst; d.tile0 = tile0; d.S = S;
+  }
+  const int slot = wave >> 1, p = wave & 1;
+  const uint32_t itm = a.items[wgp * GQ_WAVES + wave][0];
+  if (!item_valid(itm)) {
+    // no head: this wave's DMA share and the workgroup's barriers only
+    for (int i = 0; i < min(ahead, ntl); ++i) d.issue(i);
+    for (int i = 0; i < ntl; ++i) {
+      gq_wait_vm_n(min(ahead - 1, ntl - 1 - i) * d.cnt);
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("s_barrier" ::: "memory");
+      if (i + ahead < ntl) d.issue(i + ahead);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("s_barrier" ::: "memory");
+    return;
+  }
+  const int kv = item_kv(itm);
+  const int nk = (H.hrank[slot] + 15) >> 4;
+  if (nk <= 2) gq_consume<XT, OUTK, 2, MASKED>(a, H, d, ring, carry, slot, p, kv, b, chunk, ntl, ahead);
+  else if (nk <= 4) gq_consume<XT, OUTK, 4, MASKED>(a, H, d, ring, carry, slot, p, kv, b, chunk, ntl, ahead);
+  else if (nk <= 6) gq_consume<XT, OUTK, 6, MASKED>(a, H, d, ring, carry, slot, p, kv, b, chunk, ntl, ahead);
+  else gq_consume<XT, OUTK, 8, MASKED>(a, H, d, ring, carry, slot, p, kv, b, chunk, ntl, ahead);
+}
+
+template <typename XT, int OUTK>
+static void launch_gqa_o(const KArgs& a, dim3 grid, dim3 block, hipStream_t st) {
+  if (a.mask != nullptr) hipLaunchKernelGGL((k_logits_gqa_kernel<XT, OUTK, true>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((k_logits_gqa_kernel<XT, OUTK, false>), grid, block, 0, st, a);
+}
+
 template <typename XT>
 static int launch_gqa_t(const KArgs& a, int outk, int B, hipStream_t st) {
-  dim3 grid(a.n_chunks, a.n_wg, B), block((GQ_CONSUMERS + GQ_PRODUCERS) * 64);
-  if (outk == 0) hipLaunchKernelGGL((k_logits_gqa_kernel<XT, 0>), grid, block, 0, st, a);
-  else if (outk == 1) hipLaunchKernelGGL((k_logits_gqa_kernel<XT, 1>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((k_logits_gqa_kernel<XT, 2>), grid, block, 0, st, a);
+  dim3 grid(a.n_chunks, a.n_wg, B), block(GQ_WAVES * 64);
+  if (outk == 0) launch_gqa_o<XT, 0>(a, grid, block, st);
+  else if (outk == 1) launch_gqa_o<XT, 1>(a, grid, block, st);
+  else launch_gqa_o<XT, 2>(a, grid, block, st);
   return (int)hipGetLastError();
 }
 
