@@ -72,6 +72,8 @@ __device__ inline void gq_wait_vm_n(int n) {
 // 16 * lane).  Written as inline assembly so that the compiler, which does
 // not see it write LDS, adds no waits of its own before the reads of other
 // stages; the kernel orders it with explicit vmcnt waits and barriers.
+// Each statement sets m0 itself (the compiler treats m0 as reserved and
+// ignores it as a clobber; its code for this kernel holds nothing in m0).
 __device__ inline void gq_dma(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
