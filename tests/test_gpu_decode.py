@@ -114,6 +114,20 @@ def test_decode_with_mask():
     assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
 
 
+def test_decode_with_mask_gqa():
+    # 4 query heads per KV head: the grouped-query K-logit kernel, whose masked
+    # form is a kernel of its own
+    case = make_case(2, 32, 8, 700, cfg4_ranks(), 256, seed=11)
+    mask = torch.zeros(2, 1, 1, 700, device="cuda", dtype=torch.float16)
+    mask[0, ..., :130] = torch.finfo(torch.float16).min     # left padding of sequence 0
+    mask[1, ..., 650:] = -5.0
+    _flush("[decode] GQA with mask")
+    out = _run_decode(case, mask=mask)
+    ref, _, _ = oracle_decode(case, mask=mask.float().view(2, 1, 700))
+    mx, mr = errors(out, ref)
+    assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
+
+
 def test_decode_deterministic():
     case = make_case(4, 32, 32, 3000, cfg2_ranks(), 1640, seed=4)
     a = _run_decode(case).clone()
