@@ -88,37 +88,57 @@ int validate_klayout(const starkv_klatent& k, int dtype) {
     for (int h = 0; h < k.n_kv_heads; ++h)
       if (k.pos_stride[h] < k.rank[h] || k.head_offset[h] < 0) return STARKV_ERR_SHAPE;
   } else {
-    // quantised: ranks multiples of 8, rows aligned for 8-byte (int8) / 4-byte (int4) loads
+    // quantised: any rank and any byte layout (rows that are not aligned for
+    // whole 8-byte (int8) / 4-byte (int4) chunks, or ranks that are not a
+    // multiple of 8, take the unaligned-row loads: k_quant_aligned)
     if (!k.scale) return STARKV_ERR_NULL;
     const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
     if (two && (k.split % 16 || k.split > 128)) return STARKV_ERR_SHAPE;
     if (two && k.split_format != STARKV_FMT_INT4_REF && k.split_format != STARKV_FMT_INT8_SYM) return STARKV_ERR_FORMAT;
     const int split = two ? k.split : 128;
     const bool a8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
-    const int al_a = a8 ? 8 : 4;
-    if (!al(k.data, al_a) || !al64(k.stride_b, al_a) || !al(k.scale, 2)) return STARKV_ERR_ALIGN;
+    if (!al(k.scale, 2)) return STARKV_ERR_ALIGN;
     if (k.scale_stride_b < 0 || k.scale_stride_h < 0) return STARKV_ERR_SHAPE;
     bool any_lo = false;
     for (int h = 0; h < k.n_kv_heads; ++h) {
       const int r = k.rank[h];
-      if (r % 8) return STARKV_ERR_SHAPE;
       const int ra = std::min(r, split);
-      if (k.head_offset[h] < 0 || k.pos_stride[h] < (a8 ? ra : ra / 2)) return STARKV_ERR_SHAPE;
-      if (!al64(k.head_offset[h], al_a) || !al64(k.pos_stride[h], al_a)) return STARKV_ERR_ALIGN;
+      if (k.head_offset[h] < 0 || k.pos_stride[h] < (a8 ? ra : (ra + 1) / 2)) return STARKV_ERR_SHAPE;
       any_lo |= r > split;
     }
     if (any_lo) {
       if (!k.data2 || !k.scale2 || !k.head_offset2 || !k.pos_stride2) return STARKV_ERR_NULL;
-      if (!al(k.data2, 4) || !al64(k.stride2_b, 4) || !al(k.scale2, 2)) return STARKV_ERR_ALIGN;
+      if (!al(k.scale2, 2)) return STARKV_ERR_ALIGN;
       if (k.stride2_b < 0 || k.scale2_stride_b < 0 || k.scale2_stride_h < 0) return STARKV_ERR_SHAPE;
       for (int h = 0; h < k.n_kv_heads; ++h) {
         if (k.rank[h] <= split) continue;
-        if (k.head_offset2[h] < 0 || k.pos_stride2[h] < (k.rank[h] - split) / 2) return STARKV_ERR_SHAPE;
-        if (!al64(k.head_offset2[h], 4) || !al64(k.pos_stride2[h], 4)) return STARKV_ERR_ALIGN;
+        if (k.head_offset2[h] < 0 || k.pos_stride2[h] < (k.rank[h] - split + 1) / 2) return STARKV_ERR_SHAPE;
       }
     }
   }
   return STARKV_OK;
+}
+
+// Quantised K whose rows take whole 8-byte (int8) / 4-byte (int4) chunk loads:
+// ranks multiples of 8 and every row start aligned to the chunk size.
+bool k_quant_aligned(const starkv_klatent& k) {
+  const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+  const int split = two ? k.split : 128;
+  const bool a8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
+  const int al_a = a8 ? 8 : 4;
+  if (!al(k.data, al_a) || !al64(k.stride_b, al_a)) return false;
+  bool any_lo = false;
+  for (int h = 0; h < k.n_kv_heads; ++h) {
+    if (k.rank[h] % 8) return false;
+    if (!al64(k.head_offset[h], al_a) || !al64(k.pos_stride[h], al_a)) return false;
+    any_lo |= k.rank[h] > split;
+  }
+  if (any_lo) {
+    if (!al(k.data2, 4) || !al64(k.stride2_b, 4)) return false;
+    for (int h = 0; h < k.n_kv_heads; ++h)
+      if (k.rank[h] > split && (!al64(k.head_offset2[h], 4) || !al64(k.pos_stride2[h], 4))) return false;
+  }
+  return true;
 }
 
 // Warp-specialised K-logit kernel: dense latents with 16-byte aligned rows
@@ -428,12 +448,13 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
   return STARKV_OK;
 }
 
-// Vector-load variant: B_k and q rows 8-byte aligned, and (dense) latent rows
-// 16-byte aligned with ranks a multiple of 8.  Quantised latents are always
-// read with vector loads (their alignment is validated).
+// Vector-load variant: B_k and q rows 8-byte aligned, and latent rows aligned
+// for whole-chunk loads with ranks a multiple of 8 (dense: 16-byte rows;
+// quantised: k_quant_aligned).
 bool k_fast(const starkv_klatent& k, int dtype, const void* q, int64_t q_sb, int64_t q_sh) {
   const bool dense = k.format == STARKV_FMT_DENSE;
   const int xe = esize(dtype);
+  if (!dense && !k_quant_aligned(k)) return false;
   if (dense && (!al(k.data, 16) || !al64(k.stride_b * xe, 16))) return false;
   for (int h = 0; h < k.n_kv_heads; ++h) {
     if (dense && k.rank[h] % 8) return false;
@@ -524,9 +545,12 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
 }
 
 // V latent: validate the description and fill the P.V kernel's storage
-// fields (x / x2 / scales / zero points, split); *vq = its storage kind.
-// Quantised formats need rank and split multiples of 8 and 4-byte (int4) or
-// 8-byte (int8) aligned rows: they always run the vector-load kernel.
+// fields (x / x2 / scales / zero points, split, bytes per row); *vq = its
+// storage kind.  Quantised formats take any rank and byte layout (the
+// per-token block formats need a split that is a multiple of 8, so an 8-rank
+// chunk never straddles it); pa.qfast tells whether every row is aligned for
+// whole 4-byte (int4) / 8-byte (int8) chunk loads with ranks (and the lower
+// block) a multiple of 8, else the P.V kernel reads unaligned rows.
 int validate_v(const starkv_vlatent& v, PVArgs& pa, int* vq) {
   if (!v.data) return STARKV_ERR_NULL;
   if (v.rank < 1 || v.rank > MAX_RV) return STARKV_ERR_RANK;
@@ -539,43 +563,45 @@ int validate_v(const starkv_vlatent& v, PVArgs& pa, int* vq) {
       return STARKV_OK;
     case STARKV_FMT_INT4_REF:
     case STARKV_FMT_INT8_SYM: {
-      if (v.rank % 8) return STARKV_ERR_SHAPE;
       if (!v.scale) return STARKV_ERR_NULL;
       const bool two = v.format == STARKV_FMT_INT4_REF && v.split > 0 && v.split < v.rank;
       if (two && v.split_format != STARKV_FMT_INT4_REF && v.split_format != STARKV_FMT_INT8_SYM)
         return STARKV_ERR_FORMAT;
       const int split = two ? v.split : v.rank;
       const bool a8 = two ? v.split_format == STARKV_FMT_INT8_SYM : v.format == STARKV_FMT_INT8_SYM;
-      if (split % 8) return STARKV_ERR_SHAPE;
+      if (two && split % 8) return STARKV_ERR_SHAPE;
       const int al_a = a8 ? 8 : 4;
-      if (v.stride_s < (a8 ? split : split / 2)) return STARKV_ERR_SHAPE;
-      if (!al(v.data, al_a) || !al64(v.stride_s, al_a) || !al64(v.stride_b, al_a) || !al(v.scale, 2))
-        return STARKV_ERR_ALIGN;
+      const int nb = a8 ? split : (split + 1) / 2;
+      if (v.stride_s < nb) return STARKV_ERR_SHAPE;
+      if (!al(v.scale, 2)) return STARKV_ERR_ALIGN;
       if (v.scale_stride_b < 0 || v.scale_stride_s < 0) return STARKV_ERR_SHAPE;
-      pa.split = split; pa.a_int8 = a8;
+      pa.split = split; pa.a_int8 = a8; pa.xnb = nb;
       pa.xs = v.scale; pa.xs_sb = v.scale_stride_b; pa.xs_ss = v.scale_stride_s;
+      bool fast = split % 8 == 0 && al(v.data, al_a) && al64(v.stride_s, al_a) && al64(v.stride_b, al_a);
       if (two) {
+        const int nb2 = (v.rank - split + 1) / 2;
         if (!v.data2 || !v.scale2) return STARKV_ERR_NULL;
-        if (v.stride2_s < (v.rank - split) / 2 || v.stride2_b < 0 || v.scale2_stride_b < 0 || v.scale2_stride_s < 0)
+        if (v.stride2_s < nb2 || v.stride2_b < 0 || v.scale2_stride_b < 0 || v.scale2_stride_s < 0)
           return STARKV_ERR_SHAPE;
-        if (!al(v.data2, 4) || !al64(v.stride2_s, 4) || !al64(v.stride2_b, 4) || !al(v.scale2, 2))
-          return STARKV_ERR_ALIGN;
-        pa.x2 = v.data2; pa.x2_sb = v.stride2_b; pa.x2_ss = v.stride2_s;
+        if (!al(v.scale2, 2)) return STARKV_ERR_ALIGN;
+        pa.x2 = v.data2; pa.x2_sb = v.stride2_b; pa.x2_ss = v.stride2_s; pa.x2nb = nb2;
         pa.xs2 = v.scale2; pa.xs2_sb = v.scale2_stride_b; pa.xs2_ss = v.scale2_stride_s;
+        fast = fast && (v.rank - split) % 8 == 0 && al(v.data2, 4) && al64(v.stride2_s, 4) && al64(v.stride2_b, 4);
       }
+      pa.qfast = fast;
       *vq = VQ_BLOCK;
       return STARKV_OK;
     }
     case STARKV_FMT_INT4_G64: {
-      if (v.rank % 8) return STARKV_ERR_SHAPE;
       if (!v.scale || !v.zero) return STARKV_ERR_NULL;
-      if (v.stride_s < v.rank / 2 || v.scale_stride_s < (v.rank + 63) / 64 || v.scale_stride_b < 0)
+      const int nb = (v.rank + 1) / 2;
+      if (v.stride_s < nb || v.scale_stride_s < (v.rank + 63) / 64 || v.scale_stride_b < 0)
         return STARKV_ERR_SHAPE;
-      if (!al(v.data, 4) || !al64(v.stride_s, 4) || !al64(v.stride_b, 4) || !al(v.scale, 2) || !al(v.zero, 2))
-        return STARKV_ERR_ALIGN;
+      if (!al(v.scale, 2) || !al(v.zero, 2)) return STARKV_ERR_ALIGN;
       if (v.stride_s >= V_MAX_PITCH || v.scale_stride_s * 2 >= V_MAX_PITCH) return STARKV_ERR_LIMIT;
       pa.xs = v.scale; pa.xs_sb = v.scale_stride_b; pa.xs_ss = v.scale_stride_s;
-      pa.xz = v.zero;
+      pa.xz = v.zero; pa.xnb = nb;
+      pa.qfast = v.rank % 8 == 0 && al(v.data, 4) && al64(v.stride_s, 4) && al64(v.stride_b, 4);
       *vq = VQ_G64;
       return STARKV_OK;
     }
@@ -584,7 +610,10 @@ int validate_v(const starkv_vlatent& v, PVArgs& pa, int* vq) {
   }
 }
 
-bool v_fast(const starkv_vlatent& v) {
+// the P.V kernel's aligned-row variant: dense rows 16-byte aligned with the
+// rank a multiple of 8; quantised rows as validate_v found them (pa.qfast)
+bool v_fast(const starkv_vlatent& v, const PVArgs& pa) {
+  if (v.format != STARKV_FMT_DENSE) return pa.qfast != 0;
   return al(v.data, 16) && al64(v.stride_s * 2, 16) && al64(v.stride_b * 2, 16) && v.rank % 8 == 0 &&
          v.stride_s * 2 < V_MAX_PITCH;
 }
@@ -618,12 +647,32 @@ int validate_decode(const starkv_decode_desc* d, int* gs, int* n_wg, int* k1pc, 
   return STARKV_OK;
 }
 
-// Prefill: dense (16-byte rows), int8 or reference split-format K latents;
-// dense (16-byte rows), group-64 int4 or per-token block (reference int4 with
-// an optional int8 / int4 upper block, or int8) V latents; q, U_v 16-byte
-// aligned.  Positions reconstructed: pos0 + n_tokens, padded to 64 in the
-// workspace.
-int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
+// Prefill inputs the reconstruction kernels cannot read in place -- latent
+// ranks that are not a multiple of 8, latent rows not aligned for their chunk
+// loads, or U_v rows that are not 16-byte aligned whole multiples of 8
+// columns -- are repacked into aligned copies in the workspace first
+// (RepackArgs).  The workspace holds the reconstructed K and V, then these
+// copies.
+struct PrefillPlan {
+  int64_t S = 0, S_pad = 0;
+  bool rk = false, rv = false, ru = false;          // repack the K latent, the V latent, U_v
+  int k_kind1 = 0, k_kind2 = 0, v_kind1 = 0, v_kind2 = 0;
+  int k_p1 = 0, k_p2 = 0, v_p1 = 0, v_p2 = 0, u_p = 0;   // repacked row pitches, bytes
+  size_t kvb = 0, off_k1 = 0, off_k2 = 0, off_v1 = 0, off_v2 = 0, off_u = 0, total = 0;
+};
+
+int pitch16(int64_t bytes) { return (int)round_up(std::max<int64_t>(bytes, 1), 16); }
+// bytes of n elements of a repack kind, n padded to 8
+int64_t rp_bytes(int kind, int n) {
+  const int64_t n8 = round_up(n, 8);
+  return kind == RP_HALF ? 2 * n8 : kind == RP_BYTE ? n8 : n8 / 2;
+}
+
+// Prefill: any K latent format and rank (dense, int8 or the reference split
+// format), any V latent format and rank (dense, group-64 int4 or per-token
+// blocks), q 16-byte aligned.  Positions reconstructed: pos0 + n_tokens,
+// padded to 64 in the workspace.
+int validate_prefill(const starkv_prefill_desc* d, int* gs, PrefillPlan* P) {
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->batch > 65535 || d->n_tokens < 1 || d->pos0 < 0) return STARKV_ERR_SHAPE;
   if ((int64_t)d->pos0 + d->n_tokens > MAX_S) return STARKV_ERR_LIMIT;
@@ -632,22 +681,12 @@ int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
   int st = validate_klatent(d->k, d->n_q_heads, d->dtype, gs);
   if (st) return st;
   const starkv_klatent& k = d->k;
-  for (int h = 0; h < k.n_kv_heads; ++h) {
-    if (k.rank[h] % 8) return STARKV_ERR_SHAPE;
-    if (k.format == STARKV_FMT_DENSE && (!al64(k.head_offset[h], 8) || !al64(k.pos_stride[h], 8)))
-      return STARKV_ERR_ALIGN;
-  }
-  if (k.format == STARKV_FMT_DENSE && (!al(k.data, 16) || !al64(k.stride_b, 8))) return STARKV_ERR_ALIGN;
-  PVArgs vtmp = {};
+  PVArgs vb = {};
   int vq = 0;
-  if ((st = validate_v(d->v, vtmp, &vq))) return st;
-  if (d->v.rank % 8) return STARKV_ERR_SHAPE;
-  if (vq == VQ_DENSE && (!al(d->v.data, 16) || !al64(d->v.stride_s, 8) || !al64(d->v.stride_b, 8)))
-    return STARKV_ERR_ALIGN;
+  if ((st = validate_v(d->v, vb, &vq))) return st;
   if (!d->q || !d->uv || !d->out || !d->rope_table) return STARKV_ERR_NULL;
   if ((int64_t)d->pos0 + d->n_tokens > d->rope_max_positions) return STARKV_ERR_SHAPE;
   if (d->uv_row_stride < d->v.rank) return STARKV_ERR_SHAPE;
-  if (!al(d->uv, 16) || !al64(d->uv_row_stride, 8)) return STARKV_ERR_ALIGN;
   if (d->q_stride_b < 0 || d->q_stride_h < 0 || d->q_stride_t < 0) return STARKV_ERR_SHAPE;
   if (!al(d->q, 16) || !al64(d->q_stride_b, 8) || !al64(d->q_stride_h, 8) || !al64(d->q_stride_t, 8))
     return STARKV_ERR_ALIGN;
@@ -660,12 +699,72 @@ int validate_prefill(const starkv_prefill_desc* d, int* gs, int64_t* S_pad) {
                                : round_up((int64_t)d->batch * ceil_div(S, PF_V_POS), 8) * nhp;
   const int64_t g_a = round_up((int64_t)d->batch * Hkv, 8) * *gs * ceil_div(d->n_tokens, PF_Q_POS);
   if (std::max({g_k, g_v, g_a}) > INT32_MAX) return STARKV_ERR_LIMIT;
-  *S_pad = round_up(S, 64);
-  return STARKV_OK;
-}
 
-size_t prefill_kv_bytes(const starkv_prefill_desc* d, int64_t S_pad) {
-  return a256((size_t)d->batch * d->k.n_kv_heads * S_pad * HEAD_DIM * 2);
+  PrefillPlan& p = *P;
+  p = PrefillPlan{};
+  p.S = S;
+  p.S_pad = round_up(S, 64);
+  // K latent
+  int rmax = 0;
+  for (int h = 0; h < k.n_kv_heads; ++h) rmax = std::max(rmax, k.rank[h]);
+  const int rmax8 = (int)round_up(rmax, 8);
+  if (k.format == STARKV_FMT_DENSE) {
+    p.rk = !al(k.data, 16) || !al64(k.stride_b, 8);
+    for (int h = 0; h < k.n_kv_heads; ++h)
+      p.rk |= k.rank[h] % 8 || !al64(k.head_offset[h], 8) || !al64(k.pos_stride[h], 8);
+    p.k_kind1 = RP_HALF;
+    p.k_p1 = pitch16(rp_bytes(RP_HALF, rmax8));
+  } else {
+    p.rk = !k_quant_aligned(k);
+    const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+    const bool a8 = two ? k.split_format == STARKV_FMT_INT8_SYM : k.format == STARKV_FMT_INT8_SYM;
+    const int split = two ? k.split : 128;
+    p.k_kind1 = a8 ? RP_BYTE : RP_NIB;
+    p.k_p1 = pitch16(rp_bytes(p.k_kind1, std::min(rmax8, split)));
+    if (rmax > split) {
+      p.k_kind2 = RP_NIB;
+      p.k_p2 = pitch16(rp_bytes(RP_NIB, rmax8 - split));
+    }
+  }
+  // V latent
+  const int Rv = d->v.rank;
+  if (vq == VQ_DENSE) {
+    p.rv = !(al(d->v.data, 16) && al64(d->v.stride_s, 8) && al64(d->v.stride_b, 8) && Rv % 8 == 0);
+    p.v_kind1 = RP_HALF;
+    p.v_p1 = pitch16(rp_bytes(RP_HALF, Rv));
+  } else if (vq == VQ_G64) {
+    p.rv = !vb.qfast;
+    p.v_kind1 = RP_NIB;
+    p.v_p1 = pitch16(rp_bytes(RP_NIB, Rv));
+  } else {
+    p.rv = !vb.qfast;
+    p.v_kind1 = vb.a_int8 ? RP_BYTE : RP_NIB;
+    p.v_p1 = pitch16(rp_bytes(p.v_kind1, vb.split));
+    if (Rv > vb.split) {
+      p.v_kind2 = RP_NIB;
+      p.v_p2 = pitch16(rp_bytes(RP_NIB, Rv - vb.split));
+    }
+  }
+  // U_v: 16-byte rows of whole 8-column chunks (the DMA's 16-byte pieces)
+  p.ru = !(al(d->uv, 16) && al64(d->uv_row_stride, 8) && Rv % 8 == 0);
+  p.u_p = pitch16(rp_bytes(RP_HALF, Rv));
+
+  const size_t B = d->batch;
+  p.kvb = a256((size_t)B * Hkv * p.S_pad * HEAD_DIM * 2);
+  size_t o = 2 * p.kvb;
+  if (p.rk) {
+    p.off_k1 = o; o += a256(B * Hkv * S * p.k_p1);
+    p.off_k2 = o; o += a256(B * Hkv * S * p.k_p2);
+  }
+  if (p.rv) {
+    p.off_v1 = o; o += a256(B * S * p.v_p1);
+    p.off_v2 = o; o += a256(B * S * p.v_p2);
+  }
+  if (p.ru) {
+    p.off_u = o; o += a256((size_t)Hkv * HEAD_DIM * p.u_p);
+  }
+  p.total = o;
+  return STARKV_OK;
 }
 
 }  // namespace
@@ -769,7 +868,7 @@ int starkv_pv_latent(const starkv_pv_desc* d, void* workspace, size_t workspace_
   a.part2 = (float*)((char*)workspace + a256((size_t)BQ * g.n_c2 * 32 * g.Rvp * 4));
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h;
   a.S = d->seq_len; a.H = d->n_heads;
-  return launch_pv(a, d->dtype, vq, false, v_fast(d->v), d->batch, (hipStream_t)stream);
+  return launch_pv(a, d->dtype, vq, false, v_fast(d->v, a), d->batch, (hipStream_t)stream);
 }
 
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d) {
@@ -819,7 +918,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   pa.part = (float*)(ws + L.off_part); pa.psum = (float*)(ws + L.off_psum); pa.part16 = L.part16;
   pa.S = d->seq_len; pa.H = Hq; pa.n_hg = L.n_hg; pa.Rv = d->v.rank; pa.Rvp = L.pv.Rvp;
   pa.n_cb = L.pv.n_cb; pa.n_c2 = L.pv.n_c2; pa.c2_len = L.pv.c2_len;
-  if ((st = launch_pv(pa, d->dtype, vq, true, v_fast(d->v), B, s))) return st;
+  if ((st = launch_pv(pa, d->dtype, vq, true, v_fast(d->v, pa), B, s))) return st;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
 
   UPArgs ua;
@@ -1072,22 +1171,91 @@ extern "C" {
 
 size_t starkv_prefill_workspace_bytes(const starkv_prefill_desc* d) {
   int gs = 0;
-  int64_t S_pad = 0;
-  if (validate_prefill(d, &gs, &S_pad)) return 0;
-  return 2 * prefill_kv_bytes(d, S_pad);
+  PrefillPlan P;
+  if (validate_prefill(d, &gs, &P)) return 0;
+  return P.total;
+}
+
+// Launch the repacks the plan asks for and point the kernel arguments at the
+// aligned copies (latent offsets: elements for dense, bytes for quantised).
+static int prefill_repack(const starkv_prefill_desc* d, const PrefillPlan& P, PFArgs& a, char* ws, hipStream_t s) {
+  const starkv_klatent& k = d->k;
+  const int Hkv = k.n_kv_heads, B = d->batch, S = (int)P.S;
+  int st;
+  auto set = [&](RepackArgs& r, int kind, const void* src, int64_t src_sb, int H, int S_, char* dst, int pitch) {
+    r = RepackArgs{};
+    r.kind = kind; r.src = (const uint8_t*)src; r.src_sb = src_sb; r.H = H; r.S = S_;
+    r.dst = (uint8_t*)dst; r.pitch = pitch; r.dst_sb = (int64_t)H * S_ * pitch;
+  };
+  if (P.rk) {
+    const bool dense = k.format == STARKV_FMT_DENSE;
+    const int es = dense ? 2 : 1;
+    const bool two = k.format == STARKV_FMT_INT4_REF && k.split > 0;
+    const int split = dense ? 128 : (two ? k.split : 128);
+    RepackArgs r;
+    set(r, P.k_kind1, k.data, k.stride_b * es, Hkv, S, ws + P.off_k1, P.k_p1);
+    for (int h = 0; h < Hkv; ++h) {
+      r.src_off[h] = k.head_offset[h] * es; r.src_pitch[h] = k.pos_stride[h] * es;
+      r.nel[h] = std::min(k.rank[h], split);
+    }
+    if ((st = launch_repack(r, B, s))) return st;
+    a.kx = r.dst; a.kx_sb = r.dst_sb / es;
+    for (int h = 0; h < Hkv; ++h) { a.kxoff[h] = (int64_t)h * S * P.k_p1 / es; a.kxpitch[h] = P.k_p1 / es; }
+    if (P.k_p2) {
+      set(r, RP_NIB, k.data2, k.stride2_b, Hkv, S, ws + P.off_k2, P.k_p2);
+      for (int h = 0; h < Hkv; ++h) {
+        const bool lo = k.rank[h] > split;
+        r.src_off[h] = lo ? k.head_offset2[h] : 0; r.src_pitch[h] = lo ? k.pos_stride2[h] : 0;
+        r.nel[h] = lo ? k.rank[h] - split : 0;
+      }
+      if ((st = launch_repack(r, B, s))) return st;
+      a.kx2 = r.dst; a.kx2_sb = r.dst_sb;
+      for (int h = 0; h < Hkv; ++h) { a.kxoff2[h] = (int64_t)h * S * P.k_p2; a.kxpitch2[h] = P.k_p2; }
+    }
+  }
+  if (P.rv) {
+    const starkv_vlatent& v = d->v;
+    const bool dense = v.format == STARKV_FMT_DENSE;
+    const int es = dense ? 2 : 1;
+    PVArgs vb = {};
+    int vq = 0;
+    if ((st = validate_v(v, vb, &vq))) return st;
+    RepackArgs r;
+    set(r, P.v_kind1, v.data, v.stride_b * es, 1, S, ws + P.off_v1, P.v_p1);
+    r.src_off[0] = 0; r.src_pitch[0] = v.stride_s * es;
+    r.nel[0] = vq == VQ_BLOCK ? vb.split : v.rank;
+    if ((st = launch_repack(r, B, s))) return st;
+    a.vx = r.dst; a.vx_sb = r.dst_sb / es; a.vx_ss = P.v_p1 / es;
+    if (P.v_p2) {
+      set(r, RP_NIB, v.data2, v.stride2_b, 1, S, ws + P.off_v2, P.v_p2);
+      r.src_off[0] = 0; r.src_pitch[0] = v.stride2_s;
+      r.nel[0] = v.rank - vb.split;
+      if ((st = launch_repack(r, B, s))) return st;
+      a.vx2 = r.dst; a.vx2_sb = r.dst_sb; a.vx2_ss = P.v_p2;
+    }
+  }
+  if (P.ru) {
+    RepackArgs r;
+    set(r, RP_HALF, d->uv, 0, 1, Hkv * HEAD_DIM, ws + P.off_u, P.u_p);
+    r.src_off[0] = 0; r.src_pitch[0] = d->uv_row_stride * 2;
+    r.nel[0] = d->v.rank;
+    if ((st = launch_repack(r, 1, s))) return st;
+    a.uv = r.dst; a.uv_rs = P.u_p / 2;
+  }
+  return STARKV_OK;
 }
 
 static int prefill_impl(const starkv_prefill_desc* d, void* workspace, size_t workspace_bytes, void* stream,
                         void* const* events) {
   int gs = 0, st;
-  int64_t S_pad = 0;
-  if ((st = validate_prefill(d, &gs, &S_pad))) return st;
-  const size_t kvb = prefill_kv_bytes(d, S_pad);
-  if (!workspace || workspace_bytes < 2 * kvb) return STARKV_ERR_WORKSPACE;
+  PrefillPlan P;
+  if ((st = validate_prefill(d, &gs, &P))) return st;
+  const size_t kvb = P.kvb;
+  if (!workspace || workspace_bytes < P.total) return STARKV_ERR_WORKSPACE;
   if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
   const starkv_klatent& k = d->k;
   PFArgs a = {};
-  a.S = d->pos0 + d->n_tokens; a.S_pad = (int)S_pad;
+  a.S = d->pos0 + d->n_tokens; a.S_pad = (int)P.S_pad;
   a.Hkv = k.n_kv_heads; a.Hq = d->n_q_heads; a.gs = gs; a.T = d->n_tokens; a.pos0 = d->pos0;
   a.kx = k.data; a.kx_sb = k.stride_b; a.k_i8 = k.format == STARKV_FMT_INT8_SYM;
   a.kscale = k.scale; a.ks_sb = k.scale_stride_b; a.ks_sh = k.scale_stride_h;
@@ -1128,6 +1296,7 @@ static int prefill_impl(const starkv_prefill_desc* d, void* workspace, size_t wo
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_sh = d->out_stride_h; a.o_st = d->out_stride_t;
   hipStream_t s = (hipStream_t)stream;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[0], s))) return st;
+  if ((st = prefill_repack(d, P, a, (char*)workspace, s))) return st;
   if ((st = launch_prefill(a, d->dtype, d->batch, s, events ? (hipEvent_t)events[1] : nullptr))) return st;
   if (events && (st = (int)hipEventRecord((hipEvent_t)events[2], s))) return st;
   return STARKV_OK;

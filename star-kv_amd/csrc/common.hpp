@@ -93,6 +93,8 @@ struct PVArgs {
   const void* xs2; int64_t xs2_sb, xs2_ss;         // fp16 scales of x2
   const void* xz;                                  // VQ_G64 fp16 zero points (strides of xs)
   int split, a_int8;                               // VQ_BLOCK: first rank of x2; x holds int8
+  int xnb, x2nb;                                   // quantised: bytes a row of x / x2 holds (unaligned rows)
+  int qfast;                                       // quantised rows aligned for whole-chunk loads (host-side)
   const float* logits; int64_t l_sb, l_st, l_sh;   // fused path: fp32 logits, K1's layout (o_sb, o_st, o_sh)
   const float* chunkmax; int n_chunk1;             // fused path: per-chunk maxima
   const void* p; int64_t p_sb, p_sh;               // drop-in path: probabilities (act dtype)
@@ -213,6 +215,23 @@ struct PFArgs {
   float scale_log2;                                // softmax scale * log2(e)
   void* out; int64_t o_sb, o_sh, o_st;             // (b, qh, t), act dtype
 };
+// Prefill inputs whose latent rank is not a multiple of 8, or whose rows are
+// not aligned for the reconstruction kernels' chunk loads, are first copied
+// into aligned workspace rows (prefill.hip repack_rows_kernel): row (b, h, s)
+// of nel[h] elements (16-bit values, bytes or int4 nibbles) at src + b*src_sb
+// + src_off[h] + s*src_pitch[h] (bytes) goes to dst + b*dst_sb + (h*S + s)*pitch,
+// the elements past nel[h] up to the pitch set to the kind's zero (0, 0,
+// nibble 8).
+constexpr int RP_HALF = 0, RP_BYTE = 1, RP_NIB = 2;
+struct RepackArgs {
+  const uint8_t* src; int64_t src_sb;
+  int64_t src_off[K_MAX_KV], src_pitch[K_MAX_KV];
+  int nel[K_MAX_KV];
+  uint8_t* dst; int64_t dst_sb; int pitch;         // pitch: bytes, a multiple of 16
+  int kind, H, S;
+};
+int launch_repack(const RepackArgs& a, int B, hipStream_t st);
+
 // ---------------------------------------------------------------------------
 // The e2e decoder layer's RMSNorm and SiLU-multiply (layer_ops.hip).
 // ---------------------------------------------------------------------------
@@ -335,6 +354,44 @@ __device__ inline void dequant16(uint4 r, bool k8, uint16_t s16, uint4& lo, uint
     o[k] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(kh2, pr[k]) + b2) * s);
   lo = make_uint4(o[0], o[1], o[2], o[3]);
   hi = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// ---------------------------------------------------------------------------
+// Rows of any byte alignment: quantised latents whose rank or pitch is not a
+// multiple of the vector width (the reference's bx default, 1228 V ranks over
+// a 256-rank upper block, leaves 486-byte int4 rows).  ld_row_bytes<N> reads
+// N bytes (4, 8 or 16) of a row from byte `off` on as aligned dwords joined
+// with v_alignbyte.  Every dword address is clamped to the dword holding the
+// row's last valid byte (row + nvalid - 1, nvalid >= 1), so no load touches a
+// dword without a byte of the row: it stays on the row's own pages.  Bytes
+// at or past nvalid come back unspecified; callers mask the ranks they hold.
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ inline void ld_row_bytes(const uint8_t* row, int off, int nvalid, uint32_t (&out)[N / 4]) {
+  static_assert(N == 4 || N == 8 || N == 16, "4, 8 or 16 bytes");
+  const uint64_t p = (uint64_t)row + (uint64_t)off;
+  const uint64_t last = ((uint64_t)row + (uint64_t)(nvalid - 1)) & ~(uint64_t)3;
+  const uint64_t base = p & ~(uint64_t)3;
+  const uint32_t sh = (uint32_t)p & 3u;
+  uint32_t d[N / 4 + 1];
+#pragma unroll
+  for (int i = 0; i <= N / 4; ++i) {
+    const uint64_t q = base + 4u * (uint64_t)i;
+    d[i] = *(const uint32_t*)(q < last ? q : last);
+  }
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) out[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+}
+
+// eight 16-bit values (rank order, two per dword): those at index >= nv become 0
+__device__ inline uint4 mask_h8(uint4 f, int nv) {
+  uint32_t w[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t m = (2 * k + 1 < nv) ? 0xFFFFFFFFu : (2 * k < nv) ? 0x0000FFFFu : 0u;
+    w[k] &= m;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -172,10 +172,13 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
     off2[i] = nvh >= 16 ? (16 * hh + 8) * XE : off1[i];
   }
   // quantised: each lane's 16 ranks sit in one block (split is a multiple of 16)
+  // Unaligned rows (!FAST): each lane reads its 16 ranks' bytes from any
+  // address (qnb: the bytes its block's row holds) and zeroes the ranks past
+  // the head's rank after dequantisation (qnl: ranks valid from its first).
   const uint8_t* qb[MAXI];
   const uint16_t* qs[MAXI];
   int64_t qpitch[MAXI];
-  int qoff[MAXI];
+  int qoff[MAXI], qnb[MAXI], qnl[MAXI];
   bool qk8[MAXI], q16[MAXI];
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
@@ -187,6 +190,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
     const bool inA = jl < a.ksplit;
     qk8[i] = inA && a.k_a_int8;
     q16[i] = (nvh > 0 ? nvh : nv) >= 16;
+    qnl[i] = nvh > 0 ? nvh : nv;
+    const int r = a.krank[kv], ra = min(r, a.ksplit);
+    qnb[i] = inA ? (qk8[i] ? ra : (ra + 1) / 2) : (r - a.ksplit + 1) / 2;
     qb[i] = inA ? (const uint8_t*)a.x + b * a.x_sb + a.xoff[kv] : (const uint8_t*)a.x2 + b * a.x2_sb + a.xoff2[kv];
     qpitch[i] = inA ? a.xpitch[kv] : a.xpitch2[kv];
     qoff[i] = qk8[i] ? jl : (inA ? jl / 2 : (jl - a.ksplit) / 2);
@@ -228,7 +234,18 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
       } else {
         const uint8_t* q = qb[i] + (int64_t)pos * qpitch[i] + qoff[i];
         uint4 r = make_uint4(0, 0, 0, 0);
-        if (qk8[i]) {
+        if (!FAST) {
+          const uint8_t* row = qb[i] + (int64_t)pos * qpitch[i];
+          if (qk8[i]) {
+            uint32_t w[4];
+            ld_row_bytes<16>(row, qoff[i], qnb[i], w);
+            r = make_uint4(w[0], w[1], w[2], w[3]);
+          } else {
+            uint32_t w[2];
+            ld_row_bytes<8>(row, qoff[i], qnb[i], w);
+            r.x = w[0]; r.y = w[1];
+          }
+        } else if (qk8[i]) {
           const uint2 lo = *(const uint2*)q;
           r.x = lo.x; r.y = lo.y;
           if (q16[i]) {
@@ -282,6 +299,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
       } else {
         uint4 h0, h1;
         dequant16(kb.x[i][0], qk8[i], kb.sq[i], h0, h1);
+        if (!FAST) {
+          h0 = mask_h8(h0, qnl[i]);
+          h1 = mask_h8(h1, qnl[i] - 8);
+        }
         part = dot8<_Float16>(h0, acc, 0, part);
         part = dot8<_Float16>(h1, acc, 8, part);
       }

@@ -185,8 +185,10 @@ __global__ __launch_bounds__(256, 2) void recon_kernel(const PFArgs a) {
   const int b = blk / a.rc_nb;
   const int pw = (blk - b * a.rc_nb) * RC_POS + wave * RC_WAVE_POS;
   const int S = a.S;
-  const int R = a.krank[h];                         // multiple of 8 (host-checked)
-  const int nks = (R + RC_KS - 1) / RC_KS;
+  // latent rows hold Rl = round_up(R, 8) ranks (rows of other ranks are
+  // repacked by the host into padded copies whose extra ranks are zero)
+  const int R = a.krank[h], Rl = (R + 7) & ~7;
+  const int nks = (Rl + RC_KS - 1) / RC_KS;
 
   // per N-tile latent row (clamped position) and scales
   const uint8_t* xrow[RC_NT];
@@ -206,8 +208,8 @@ __global__ __launch_bounds__(256, 2) void recon_kernel(const PFArgs a) {
     }
   }
 
-  // Ranks past R (the last step only) read a valid chunk instead (address
-  // clamped to rank R - 8): the A rows of those ranks are zero, so any finite
+  // Ranks past Rl (the last step only) read a valid chunk instead (address
+  // clamped to rank Rl - 8): the A rows of those ranks are zero, so any finite
   // value adds nothing, and no load is conditional (a conditional load would
   // zero its register first and wait for the previous load into it).
   auto load = [&](int ks, RkRaw<Q>& r) {
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(256, 2) void recon_kernel(const PFArgs a) {
     for (int nt = 0; nt < RC_NT; ++nt)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const int j = min(j0 + 8 * kk, R - 8);
+        const int j = min(j0 + 8 * kk, Rl - 8);
         if constexpr (Q == 0) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * j);
         else if constexpr (Q == 1) r.d[nt][kk] = *(const uint2*)(xrow[nt] + j);
         else r.d[nt][kk] = pf_ld_block(xrow[nt], xrow2[nt], j, a.ksplit, a.k_a8);
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void recon_kernel(const PFArgs a) {
       if constexpr (Q == 1) {
         f = pf_dq_int8(r.d[nt][kk], ksc[nt]);
       } else {
-        const int j = min(ks * RC_KS + 32 * hh + 8 * kk, R - 8);
+        const int j = min(ks * RC_KS + 32 * hh + 8 * kk, Rl - 8);
         f = pf_dq_block(r.d[nt][kk], j, a.ksplit, a.k_a8, ksc[nt], ksc2[nt]);
       }
       if constexpr (!__is_same(XT, _Float16)) f = pf_f16_to_bf16(f);
@@ -391,7 +393,7 @@ __device__ __attribute__((aligned(16))) uint4 pf_zero_line = {0u, 0u, 0u, 0u};
 // Q: 0 dense act dtype, 1 group-64 int4 (scale and zero per (b, s, group)),
 // 2 per-token blocks (the reference int4 format with an optional int8 / int4
 // upper block, or int8; one scale per (b, s) and block)
-// NARROW (group-64 only): Rv < 32, rows shorter than one 16-byte load
+// NARROW (group-64 only): round_up(Rv, 8) < 32, rows shorter than one 16-byte load
 template <typename XT, int Q, bool NARROW>
 __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[RV_STAGE];
@@ -428,8 +430,10 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
   if (blk >= a.rv_blocks) return;
   const int b = blk / a.rv_nb;
   const int pw = (blk - b * a.rv_nb) * RV_POS + RV_WAVE_POS * wave;   // this wave's first position
-  const int S = a.S, R = a.Rv;
-  const int nks = (R + 63) >> 6;
+  // latent rows hold Rl = round_up(Rv, 8) ranks (see recon_kernel); U_v
+  // columns at or past Rv are zero in LDS
+  const int S = a.S, R = a.Rv, Rl = (R + 7) & ~7;
+  const int nks = (Rl + 63) >> 6;
 
   auto stage = [&](auto ic) __attribute__((always_inline)) -> uint8_t* {
     constexpr int i = decltype(ic)::value % 4;
@@ -460,8 +464,8 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
     }
   }
 
-  // latent loads of step ks (clamped to the last step; ranks past R read the
-  // chunk at rank R - 8, which meets zero U_v chunks)
+  // latent loads of step ks (clamped to the last step; ranks past Rl read the
+  // chunk at rank Rl - 8, which meets zero U_v chunks)
   typedef RvRaw<Q> Raw;
   auto load = [&](int ks_, Raw& r) __attribute__((always_inline)) {
     const int ks = min(ks_, nks - 1);
@@ -471,7 +475,7 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
       if constexpr (Q == 2) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          r.d[nt][kk] = pf_ld_block(xrow[nt], xrow2[nt], min(j0 + 8 * kk, R - 8), a.vsplit, a.v_a8);
+          r.d[nt][kk] = pf_ld_block(xrow[nt], xrow2[nt], min(j0 + 8 * kk, Rl - 8), a.vsplit, a.v_a8);
       } else if constexpr (Q == 1) {
         // one 16-byte load per N-tile in every step (an equal instruction
         // count keeps the compiler's own wait counts exact).  Where the lane's
@@ -480,17 +484,17 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
         // past R and meet zero U_v).  Rows shorter than 16 bytes take 4-byte
         // loads (NARROW: more instructions, so the waits only wait longer).
         if constexpr (!NARROW) {
-          r.d[nt] = *(const uint4*)(xrow[nt] + min(j0, R - 32) / 2);   // shifted by tail_fix
+          r.d[nt] = *(const uint4*)(xrow[nt] + min(j0, Rl - 32) / 2);   // shifted by tail_fix
         } else {
           uint32_t w[4];
 #pragma unroll
-          for (int kk = 0; kk < 4; ++kk) w[kk] = *(const uint32_t*)(xrow[nt] + min(j0 + 8 * kk, R - 8) / 2);
+          for (int kk = 0; kk < 4; ++kk) w[kk] = *(const uint32_t*)(xrow[nt] + min(j0 + 8 * kk, Rl - 8) / 2);
           r.d[nt] = make_uint4(w[0], w[1], w[2], w[3]);
         }
         r.sz[nt] = szrow[nt][ks];
       } else {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * min(j0 + 8 * kk, R - 8));
+        for (int kk = 0; kk < 4; ++kk) r.d[nt][kk] = *(const uint4*)(xrow[nt] + 2 * min(j0 + 8 * kk, Rl - 8));
       }
     }
   };
@@ -500,7 +504,7 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
   auto tail_fix = [&](Raw& r, int ks) __attribute__((always_inline)) {
     if constexpr (Q == 1 && !NARROW) {
       const int j0 = ks * 64 + 32 * hh;
-      const int sh = (j0 - min(j0, R - 32)) >> 3;   // 0 .. 3
+      const int sh = (j0 - min(j0, Rl - 32)) >> 3;   // 0 .. 3
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const uint4 w = r.d[nt];
@@ -519,7 +523,7 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
       const auto sz = __builtin_amdgcn_permlane32_swap((uint32_t)r.sz[nt], (uint32_t)r.sz[nt], false, false);
       f = pf_dq_g64(w, (uint16_t)sz[0], (uint16_t)sz[1]);
     } else if constexpr (Q == 2) {
-      const int j = min(ks * 64 + 32 * hh + 8 * kk, R - 8);
+      const int j = min(ks * 64 + 32 * hh + 8 * kk, Rl - 8);
       f = pf_dq_block(r.d[nt][kk], j, a.vsplit, a.v_a8, vsc[nt], vsc2[nt]);
     } else {
       f = r.d[nt][kk];
@@ -600,7 +604,7 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
         // latents of ks + 1, issued just after it)
         if constexpr (Q == 0) rv_vm_wait<0>();
         else rv_vm_wait<8 + NL>();
-        if (ks + 2 == nks && (R & 63)) tail_fix(raw[(i + 1) % NST], ks + 1);
+        if (ks + 2 == nks && (Rl & 63)) tail_fix(raw[(i + 1) % NST], ks + 1);
         // stage ks + 1 complete for all waves; stage ks - 1 free.  A bare
         // barrier: each wave has waited for its own DMA above, and a fence
         // here would also wait for the refills still in flight into the
@@ -674,7 +678,7 @@ __global__ __launch_bounds__(256, 1) void recon_v_kernel(const PFArgs a) {
   __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0): no scalar loads pending into the loop
   __syncthreads();
   read_a(i0, 0, afA);
-  if (nks == 1 && (R & 63)) tail_fix(raw[0], 0);
+  if (nks == 1 && (Rl & 63)) tail_fix(raw[0], 0);
   if constexpr (Q != 0) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) bfA[nt] = frag(raw[0], 0, nt, 0);
@@ -908,6 +912,45 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row repack (see RepackArgs): one thread per 4-byte word of a destination
+// row, reading its source elements byte by byte (any alignment), so the
+// reconstruction kernels always see 16-byte aligned rows of a multiple of 8
+// ranks.  Grid (words of one head's S rows / 256, head, batch).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void repack_rows_kernel(const RepackArgs a) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int wpr = a.pitch >> 2;                      // words per row
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.S * wpr) return;
+  const int s = (int)(idx / wpr), o = (int)(idx - (int64_t)s * wpr) * 4;
+  const uint8_t* row = a.src + b * a.src_sb + a.src_off[h] + (int64_t)s * a.src_pitch[h];
+  const int n = a.nel[h];
+  uint32_t w = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int by = o + k;
+    uint32_t v;
+    if (a.kind == RP_HALF) {
+      v = (by >> 1) < n ? row[by] : 0u;
+    } else if (a.kind == RP_BYTE) {
+      v = by < n ? row[by] : 0u;
+    } else {
+      const uint32_t x = 2 * by < n ? row[by] : 0x88u;
+      v = (2 * by < n ? (x & 0xFu) : 8u) | ((2 * by + 1 < n ? (x >> 4) : 8u) << 4);
+    }
+    w |= v << (8 * k);
+  }
+  *(uint32_t*)(a.dst + b * a.dst_sb + ((int64_t)h * a.S + s) * a.pitch + o) = w;
+}
+
+int launch_repack(const RepackArgs& a, int B, hipStream_t st) {
+  const int64_t words = (int64_t)a.S * (a.pitch / 4);
+  if (words == 0) return 0;
+  hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)ceil_div(words, 256), a.H, B), dim3(256), 0, st, a);
+  return (int)hipGetLastError();
+}
+
 template <typename XT>
 static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t mid) {
   PFArgs r = a;
@@ -923,7 +966,7 @@ static int launch_prefill_t(const PFArgs& a, int B, hipStream_t st, hipEvent_t m
   r.rv_hpx = nhp >= 8 ? (int)ceil_div(nhp, 8) : 0;
   const dim3 vg((unsigned)(r.rv_hpx ? 8 * r.rv_hpx * r.rv_blocks : ceil_div(r.rv_blocks, 8) * 8 * nhp));
   if (a.v_blk) hipLaunchKernelGGL((recon_v_kernel<XT, 2, false>), vg, dim3(256), 0, st, r);
-  else if (a.v_g64 && a.Rv < 32) hipLaunchKernelGGL((recon_v_kernel<XT, 1, true>), vg, dim3(256), 0, st, r);
+  else if (a.v_g64 && ((a.Rv + 7) & ~7) < 32) hipLaunchKernelGGL((recon_v_kernel<XT, 1, true>), vg, dim3(256), 0, st, r);
   else if (a.v_g64) hipLaunchKernelGGL((recon_v_kernel<XT, 1, false>), vg, dim3(256), 0, st, r);
   else hipLaunchKernelGGL((recon_v_kernel<XT, 0, false>), vg, dim3(256), 0, st, r);
   int e = (int)hipGetLastError();

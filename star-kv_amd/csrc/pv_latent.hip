@@ -269,10 +269,27 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
         const int64_t r = min(kc * KSTEP + grow[c], rmax);
         if constexpr (VQ == VQ_BLOCK) {
           const bool lo = cok[c] && qlo[c];
-          const uint8_t* p = (lo ? xq2 + r * a.x2_ss : xq + r * a.x_ss) + (cok[c] ? qoff[c] : 0);
-          st.q[c].x = *(const uint32_t*)p;
-          st.q[c].y = *(const uint32_t*)(p + (q8[c] ? 4 : 0));
+          if (FAST) {
+            const uint8_t* p = (lo ? xq2 + r * a.x2_ss : xq + r * a.x_ss) + (cok[c] ? qoff[c] : 0);
+            st.q[c].x = *(const uint32_t*)p;
+            st.q[c].y = *(const uint32_t*)(p + (q8[c] ? 4 : 0));
+          } else {
+            // rows of any alignment and length: 8 bytes from the chunk's first
+            // byte (int4 uses the first 4); bytes past the row are unspecified
+            // and land only in output columns >= Rv, which are discarded
+            uint32_t w[2];
+            ld_row_bytes<8>(lo ? xq2 + r * a.x2_ss : xq + r * a.x_ss, cok[c] ? qoff[c] : 0, lo ? a.x2nb : a.xnb, w);
+            st.q[c] = make_uint2(w[0], w[1]);
+          }
           st.s[c] = lo ? sq2[r * a.xs2_ss] : sq[r * a.xs_ss];
+        } else if constexpr (!FAST) {
+          const uint32_t ru = (uint32_t)r, so = __umul24(ru, sp) + sco[c];
+          uint32_t w[1];
+          ld_row_bytes<4>((const uint8_t*)xrow0 + (__umul24(ru, xp)), xco[c], a.xnb, w);
+          st.q[c].x = w[0];
+          st.q[c].y = 0;
+          st.s[c] = *(const uint16_t*)(srow0 + so);
+          st.z[c] = *(const uint16_t*)(zrow0 + so);
         } else {
           const uint32_t ru = (uint32_t)r, so = __umul24(ru, sp) + sco[c];
           st.q[c].x = *(const uint32_t*)(xrow0 + (__umul24(ru, xp) + xco[c]));
@@ -527,11 +544,16 @@ int pv_tiles_per_wave(int Rvp, bool fused, int vq) {
   return 13;
 }
 
+// fast: dense rows 16-byte aligned (ranks a multiple of 8); quantised rows
+// aligned for 4-byte (int4) / 8-byte (int8) chunk loads, else the
+// unaligned-row loads
 template <typename VT, bool FUSED, int NTW>
 static void launch_pv_n(const PVArgs& a, int vq, bool fast, int B, hipStream_t st) {
   dim3 grid(a.n_cb * a.n_c2, B), block(256);
-  if (vq == VQ_BLOCK) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_BLOCK>), grid, block, 0, st, a);
-  else if (vq == VQ_G64) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_G64>), grid, block, 0, st, a);
+  if (vq == VQ_BLOCK && fast) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_BLOCK>), grid, block, 0, st, a);
+  else if (vq == VQ_BLOCK) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, false, VQ_BLOCK>), grid, block, 0, st, a);
+  else if (vq == VQ_G64 && fast) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_G64>), grid, block, 0, st, a);
+  else if (vq == VQ_G64) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, false, VQ_G64>), grid, block, 0, st, a);
   else if (fast) hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, true, VQ_DENSE>), grid, block, 0, st, a);
   else hipLaunchKernelGGL((pv_kernel<VT, NTW, FUSED, false, VQ_DENSE>), grid, block, 0, st, a);
 }
@@ -561,9 +583,9 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
   return (int)hipGetLastError();
 }
 
-// Quantised formats always take the vector-load variant (the C ABI checks the
-// alignment they need).  Fused: the P.V kernel alone (its partials are reduced
-// by the up-projection kernel); drop-in: P.V and the partial reduction.
+// fast: the aligned-row variant (the C ABI decides which rows qualify).
+// Fused: the P.V kernel alone (its partials are reduced by the up-projection
+// kernel); drop-in: P.V and the partial reduction.
 int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st) {
   if (dtype == STARKV_F16)
     return fused ? launch_pv_t<_Float16, true>(a, vq, fast, B, st) : launch_pv_t<_Float16, false>(a, vq, fast, B, st);

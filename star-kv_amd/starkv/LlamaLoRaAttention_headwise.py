@@ -52,16 +52,12 @@ def _rotate_half(x: torch.Tensor) -> torch.Tensor:
 
 
 def _prefill_layout_ok(k: torch.Tensor, v: torch.Tensor, uv: torch.Tensor) -> bool:
-    """Whether the caches meet starkv_prefill_attention's layout (dense latents:
-    ranks, strides and offsets multiples of 8 elements, 16-byte aligned data).
-    Other layouts keep the reference's torch route."""
-    def a16(t):
-        return t.data_ptr() % 16 == 0
+    """Whether starkv_prefill_attention takes the caches (dense fp16 / bf16
+    latents with contiguous last dims; any rank, stride or alignment -- the
+    library repacks what its kernels cannot read in place).  Other caches keep
+    the reference's torch route."""
     return (k.dim() == 4 and v.dim() == 3 and k.dtype == v.dtype == uv.dtype and k.dtype in (torch.float16, torch.bfloat16)
-            and k.stride(3) == 1 and v.stride(2) == 1 and uv.stride(1) == 1 and k.shape[3] % 8 == 0
-            and v.shape[2] % 8 == 0 and all(s % 8 == 0 for s in (k.stride(0), k.stride(1), k.stride(2), v.stride(0),
-                                                                   v.stride(1), uv.stride(0)))
-            and a16(k) and a16(v) and a16(uv))
+            and k.stride(3) == 1 and v.stride(2) == 1 and uv.stride(1) == 1)
 
 
 def _additive(mask: Optional[torch.Tensor], dtype: torch.dtype) -> Optional[torch.Tensor]:

@@ -109,7 +109,7 @@ class LlamaCustomAttention(nn.Module):
                                                      split=UPPER_RANKS_K)
             return kspec, VLatentSpec.int4_ref(vu_q, svu, rv, split=UPPER_RANKS_V, x2=vl_q, scale2=svl)
 
-        if query_len > 1 and mask is None and rk % 8 == 0 and rv % 8 == 0:
+        if query_len > 1 and mask is None:
             kspec, vspec = specs()
             out = prefill_attention(q, kspec, vspec, v_u.weight, rope=self.rope, pos0=S - query_len,
                                     scale=self.scaling)

@@ -59,8 +59,6 @@ class LatentCache:
             self.v_data = torch.zeros(B, C, self.Rv, dtype=dtype, device=dev)
             self.v_spec = VLatentSpec.dense(self.v_data)
             return
-        if any(r % 8 for r in self.ranks) or self.Rv % 8:
-            raise StarKVError("quantised caches need ranks that are multiples of 8")
         # scale rows padded to 8 positions: the K-logit kernel stages them in 16-byte pieces
         self.k_scale = torch.ones(B, Hkv, _round(C, 8), dtype=torch.float16, device=dev)
         if fmt == "int8_g64":
@@ -71,7 +69,7 @@ class LatentCache:
             self._k = dict(data=self.k_data, head_offset=offs, pos_stride=pitch, stride_b=self.k_data.stride(0),
                            fmt=FMT_INT8_SYM, scale=self.k_scale)
             G = (self.Rv + 63) // 64
-            self.v_data = torch.zeros(B, C, self.Rv // 2, dtype=torch.uint8, device=dev)
+            self.v_data = torch.zeros(B, C, (self.Rv + 1) // 2, dtype=torch.uint8, device=dev)
             self.v_scale = torch.ones(B, C, G, dtype=torch.float16, device=dev)
             self.v_zero = torch.zeros(B, C, G, dtype=torch.float16, device=dev)
             self.v_spec = VLatentSpec.int4_g64(self.v_data, self.v_scale, self.v_zero, self.Rv)
@@ -82,7 +80,7 @@ class LatentCache:
         up = [min(r, k_split) for r in self.ranks]
         lo = [max(r - k_split, 0) for r in self.ranks]
         pitch1 = [_round(u, 8) for u in up]
-        pitch2 = [_round(l // 2, 4) for l in lo]
+        pitch2 = [_round((l + 1) // 2, 4) for l in lo]
         self.k_data = torch.zeros(B, C * sum(pitch1), dtype=torch.int8, device=dev)
         self.k_data2 = torch.zeros(B, max(1, C * sum(pitch2)), dtype=torch.uint8, device=dev)
         self.k_scale2 = torch.ones(B, Hkv, C, dtype=torch.float16, device=dev)
@@ -95,7 +93,7 @@ class LatentCache:
         self.v_data = torch.zeros(B, C, vu, dtype=torch.int8, device=dev)
         self.v_scale = torch.ones(B, C, 1, dtype=torch.float16, device=dev)
         if self.Rv > vu:
-            self.v_data2 = torch.zeros(B, C, (self.Rv - vu) // 2, dtype=torch.uint8, device=dev)
+            self.v_data2 = torch.zeros(B, C, (self.Rv - vu + 1) // 2, dtype=torch.uint8, device=dev)
             self.v_scale2 = torch.ones(B, C, 1, dtype=torch.float16, device=dev)
             self.v_spec = VLatentSpec.int4_ref(self.v_data, self.v_scale, self.Rv, split=vu, x2=self.v_data2,
                                                scale2=self.v_scale2)

@@ -48,6 +48,22 @@ def _require_cuda(*ts):
 _WS: dict = {}
 _WS_RETIRED: list = []
 
+# Test hook: when True, every output and workspace the operators allocate is
+# filled with 0xFF bytes before the call (NaN in fp16, bf16 and fp32), so an
+# element a kernel fails to write reads as NaN rather than as a stale value
+# left in recycled memory.  Skipped inside a graph capture.
+POISON = False
+
+
+def _poison(t: torch.Tensor) -> torch.Tensor:
+    if POISON and t.is_cuda and not torch.cuda.is_current_stream_capturing():
+        t.view(torch.uint8).fill_(0xFF)
+    return t
+
+
+def _out(*shape, dtype, device) -> torch.Tensor:
+    return _poison(torch.empty(*shape, dtype=dtype, device=device))
+
 
 def _workspace(device, nbytes: int) -> torch.Tensor:
     """Per-device scratch reused across calls (ordered on one stream).
@@ -67,6 +83,7 @@ def _workspace(device, nbytes: int) -> torch.Tensor:
         ws = torch.empty(max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20), dtype=torch.uint8,
                          device=device)
         _WS[key] = ws
+    _poison(ws[:max(nbytes, 1)])
     return ws
 
 
@@ -139,7 +156,8 @@ class KLatentSpec:
                              split: Optional[int] = None) -> "KLatentSpec":
         """The quantised K cache of LlamaLoRaAttention_headwise_quant.py:107-127:
         x1 [B, H, S, split] int8 (or [B, H, S, split/2] uint8 int4 nibbles),
-        s1 [B, H, S, 1] fp16, x2 [B, H, S, (rank - split)/2] uint8 int4 nibbles,
+        s1 [B, H, S, 1] fp16, x2 [B, H, S, ceil((rank - split)/2)] uint8 int4 nibbles
+        (any rank; split a multiple of 16),
         s2 [B, H, S, 1] fp16; b = k_u^T [Hkv, rank, 128] with H = Hkv or a
         multiple of it.  With x2 None, x1 holds all ranks (int8: INT8_SYM,
         uint8 nibbles: INT4_REF)."""
@@ -152,7 +170,7 @@ class KLatentSpec:
         if x2 is None:
             if x1.dtype == torch.int8 and w1 == rank:
                 fmt = FMT_INT8_SYM
-            elif w1 * 2 == rank:
+            elif w1 == (rank + 1) // 2:
                 fmt = FMT_INT4_REF
             else:
                 raise StarKVError(f"x1 last dim {w1} matches neither int8 nor int4 storage of rank {rank}")
@@ -161,8 +179,8 @@ class KLatentSpec:
         upper = FMT_INT8_SYM if (x1.dtype == torch.int8 and w1 == split) else FMT_INT4_REF
         if upper == FMT_INT4_REF and w1 * 2 != split:
             raise StarKVError("x1 does not hold `split` ranks")
-        if x2.dim() != 4 or x2.shape[3] * 2 != rank - split or x2.stride(3) != 1:
-            raise StarKVError("x2 must be [B, H, S, (rank - split)/2]")
+        if x2.dim() != 4 or x2.shape[3] != (rank - split + 1) // 2 or x2.stride(3) != 1:
+            raise StarKVError("x2 must be [B, H, S, ceil((rank - split)/2)]")
         return cls(x1, [rank] * H, ho, ps, x1.stride(0), b, bko, bkr, FMT_INT4_REF, s1, s1.stride(0), s1.stride(1),
                    split=split, split_fmt=upper, data2=x2, head_offset2=[h * x2.stride(1) for h in range(H)],
                    pos_stride2=[x2.stride(2)] * H, stride2_b=x2.stride(0), scale2=s2,
@@ -231,7 +249,7 @@ def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = R
     B, Hq, _ = q.shape
     S = int(seq_len)
     out_dtype = out_dtype or torch.float32
-    out = torch.empty(B, Hq, S, dtype=out_dtype, device=q.device)
+    out = _out(B, Hq, S, dtype=out_dtype, device=q.device)
     table, cap = rope_table(rope, S, q.device)
     m, mdt, msb, msh = _mask_args(mask, B, S, Hq)
     keep: list = []
@@ -278,23 +296,25 @@ class VLatentSpec:
         """The reference's quantised V cache (bx_quant.py:117-166): ranks
         [0, split) in ``x1`` with one fp16 scale per token ``scale1`` [B, S, 1],
         ranks [split, rank) in ``x2`` / ``scale2``; ``x2`` holds int4 nibbles
-        [B, S, (rank - split)/2] (rank 2k in the low nibble of byte k, value
-        nibble - 8).  ``x1`` holds int4 nibbles [B, S, split/2] (the Triton
+        [B, S, ceil((rank - split)/2)] (rank 2k in the low nibble of byte k, value
+        nibble - 8).  Any rank; split a multiple of 8 (the Triton kernel needs a
+        multiple of its 64-rank block, bx_quant.py:72).  ``x1`` holds int4
+        nibbles [B, S, ceil(split/2)] (the Triton
         kernel's reading, bx_quant.py:75-86) or int8 values [B, S, split] (the
         reading of LlamaLoRaAttention_headwise_quant.py:138, 164); the last
         dimension tells which."""
         split = int(rank if split is None else split)
         if x1.dim() != 3 or scale1.dim() != 3 or x1.stride(2) != 1:
             raise StarKVError("x1 must be [B, S, bytes] and its scale [B, S, 1]")
-        if x1.shape[2] == split // 2:
-            upper = FMT_INT4_REF
-        elif x1.shape[2] == split and x1.dtype == torch.int8:
+        if x1.shape[2] == split and x1.dtype == torch.int8:
             upper = FMT_INT8_SYM
+        elif x1.shape[2] == (split + 1) // 2:
+            upper = FMT_INT4_REF
         else:
-            raise StarKVError(f"x1 last dim {x1.shape[2]} matches neither int4 ({split // 2}) nor int8 ({split}) storage")
+            raise StarKVError(f"x1 last dim {x1.shape[2]} matches neither int4 ({(split + 1) // 2}) nor int8 ({split}) storage")
         if split < rank:
-            if x2 is None or scale2 is None or x2.shape[2] != (rank - split) // 2:
-                raise StarKVError("the lower block needs x2 [B, S, (rank - split)/2] and its scales")
+            if x2 is None or scale2 is None or x2.shape[2] != (rank - split + 1) // 2:
+                raise StarKVError("the lower block needs x2 [B, S, ceil((rank - split)/2)] and its scales")
             return cls(rank, FMT_INT4_REF, x1, scale1, split, upper, x2, scale2)
         return cls(rank, FMT_INT4_REF if upper == FMT_INT4_REF else FMT_INT8_SYM, x1, scale1)
 
@@ -343,7 +363,7 @@ def pv_latent(p: torch.Tensor, xv) -> torch.Tensor:
     B, H, S = p.shape
     if v.data.shape[0] != B or v.data.shape[1] < S:
         raise StarKVError("the V latent must be [B, >=S, ...]")
-    out = torch.empty(B, H, v.rank, dtype=p.dtype, device=p.device)
+    out = _out(B, H, v.rank, dtype=p.dtype, device=p.device)
     d = PVDesc()
     d.batch, d.n_heads, d.seq_len, d.dtype = B, H, S, _dt(p)
     d.p, d.p_stride_b, d.p_stride_h = p.data_ptr(), p.stride(0), p.stride(1)
@@ -382,7 +402,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     if uv_weight.shape[0] != k.n_kv_heads * HEAD_DIM:
         raise StarKVError("uv_weight rows must be Hkv*128")
     if out is None:
-        out = torch.empty(B, Hq, HEAD_DIM, dtype=out_dtype or q.dtype, device=q.device)
+        out = _out(B, Hq, HEAD_DIM, dtype=out_dtype or q.dtype, device=q.device)
     if out.dtype not in (q.dtype, torch.float32) or out.stride(-1) != 1:
         raise StarKVError("out must be [B, Hq, 128] of q's dtype or float32")
     table, cap = rope_table(rope, S, q.device)
@@ -447,7 +467,7 @@ def prefill_attention(q: torch.Tensor, k: KLatentSpec, xv, uv_weight: torch.Tens
     if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape != (k.n_kv_heads * HEAD_DIM, v.rank):
         raise StarKVError("uv_weight must be [Hkv*128, Rv] with a contiguous last dim")
     if out is None:
-        out = torch.empty(B, Hq, T, HEAD_DIM, dtype=q.dtype, device=q.device)
+        out = _out(B, Hq, T, HEAD_DIM, dtype=q.dtype, device=q.device)
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
         raise StarKVError("out must be [B, Hq, T, 128] of q's dtype with a contiguous last dim")
     table, cap = rope_table(rope, int(pos0) + T, q.device)

@@ -7,8 +7,11 @@ Its two functions are defined by their call sites:
   (LlamaLoRaAttention_headwise_quant.py:107-117) returns
   ``(upper_q, scale_upper, lower_q, scale_lower, r4)``: ranks [0, split_r) as
   int8 with one fp16 scale per token ("Top-r ranks stored in int8", 22-25),
-  ranks [split_r, R) as packed int4 with one fp16 scale per token, and
-  ``r4 = R - split_r``.  Build-defined rounding (the reference's is unknown):
+  ranks [split_r, R) as packed int4 with one fp16 scale per token
+  (ceil(r4 / 2) bytes per token; an odd r4 leaves the last high nibble at 8,
+  the value 0), and ``r4 = R - split_r``.  Any R >= split_r is accepted (the
+  reference module splits K at 16 and V at 256 ranks; its ``bx`` check runs
+  R = 1228, a 972-rank lower block of 486-byte rows, bx_quant.py:224-248).  Build-defined rounding (the reference's is unknown):
   s = fp16(amax / 127) and q = clip(rint(x / s), -127, 127) for int8;
   s = fp16(amax / 7) and n = clip(rint(x / s), -8, 7), stored as nibble n + 8
   with rank 2k in the low nibble of byte k, for int4.  Runs on the HIP cache
@@ -29,13 +32,13 @@ __all__ = ["quantize_r_split_int8_int4_packed", "unpack_uint8_to_int4_signed"]
 def quantize_r_split_int8_int4_packed(x: torch.Tensor, split_r: int):
     """x: K latent [B, H, T, R] or V latent [B, T, R] (fp16 / bf16, on the GPU)."""
     R, U = x.shape[-1], int(split_r)
-    if not 0 < U < R or U % 16 or (R - U) % 8:
-        raise StarKVError(f"split_r {U} must be a multiple of 16 in (0, {R}) with R - split_r a multiple of 8")
+    if not 0 < U <= R or U % 16:
+        raise StarKVError(f"split_r {U} must be a multiple of 16 in (0, {R}]")
     x = x if x.stride(-1) == 1 else x.contiguous()
     dev = x.device
     lead = x.shape[:-1]
     up = torch.empty(*lead, U, dtype=torch.int8, device=dev)
-    lo = torch.empty(*lead, (R - U) // 2, dtype=torch.uint8, device=dev)
+    lo = torch.empty(*lead, (R - U + 1) // 2, dtype=torch.uint8, device=dev)
     s_up = torch.empty(*lead, 1, dtype=torch.float16, device=dev)
     s_lo = torch.empty(*lead, 1, dtype=torch.float16, device=dev)
     if x.dim() == 4:

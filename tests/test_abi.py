@@ -322,14 +322,14 @@ def test_cache_writer_validation():
     assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_NULL           # group-64 without zero points
     v.v.zero, v.v.stride_s = FAKE, 30
     assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_SHAPE          # row shorter than rank/2 bytes
-    v.v.stride_s, v.v.data = 32, FAKE + 2
+    v.v.stride_s, v.v.scale = 32, FAKE + 1                                  # fp16 scales at an odd address
     assert lib.starkv_v_append(ctypes.byref(v), None) == ERR_ALIGN
     assert lib.starkv_v_append(None, None) == ERR_NULL
     # the combined writer reports each description's own status, and a dtype mismatch
     d.k.format = L.FMT_DENSE
     assert lib.starkv_decode_append(ctypes.byref(d), ctypes.byref(v), None, None) == ERR_ALIGN
     assert lib.starkv_decode_append(None, ctypes.byref(v), None, None) == ERR_NULL
-    v.v.data = FAKE
+    v.v.scale = FAKE
     q = L.RopeApplyDesc(batch=2, n_heads=8, n_tokens=4, dtype=L.BF16, x=FAKE, stride_b=8 * 4 * 128,
                         stride_h=4 * 128, stride_t=128, rope_table=FAKE, rope_max_positions=16, pos0=10)
     assert lib.starkv_decode_append(ctypes.byref(d), ctypes.byref(v), ctypes.byref(q), None) == ERR_DTYPE
@@ -367,8 +367,8 @@ def test_prefill_workspace_holds_the_reconstructed_k_and_v():
 
 @pytest.mark.parametrize("what,code", [
     ("n_tokens0", ERR_SHAPE), ("pos0_neg", ERR_SHAPE), ("rope_short", ERR_SHAPE), ("head_dim", ERR_SHAPE),
-    ("k_format", ERR_FORMAT), ("v_format", ERR_FORMAT), ("k_split_format", ERR_FORMAT), ("k_rank_odd", ERR_SHAPE), ("v_rank_odd", ERR_SHAPE),
-    ("q_stride", ERR_ALIGN), ("q_null", ERR_NULL), ("uv_stride", ERR_ALIGN), ("gqa", ERR_SHAPE),
+    ("k_format", ERR_FORMAT), ("v_format", ERR_FORMAT), ("k_split_format", ERR_FORMAT),
+    ("q_stride", ERR_ALIGN), ("q_null", ERR_NULL), ("gqa", ERR_SHAPE),
     ("dtype", ERR_DTYPE),
 ])
 def test_prefill_rejects(what, code):
@@ -388,22 +388,68 @@ def test_prefill_rejects(what, code):
         d.v.format, d.v.scale = 77, FAKE
     elif what == "k_split_format":
         d.k.format, d.k.scale, d.k.split, d.k.split_format = L.FMT_INT4_REF, FAKE, 16, L.FMT_INT4_G64
-    elif what == "k_rank_odd":
-        d.k.rank[2] = 20
-    elif what == "v_rank_odd":
-        d.v.rank, d.uv_row_stride = 60, 60
     elif what == "q_stride":
         d.q_stride_t = 132
     elif what == "q_null":
         d.q = None
-    elif what == "uv_stride":
-        d.uv_row_stride = 68
     elif what == "gqa":
         d.n_q_heads = 6
     elif what == "dtype":
         d.dtype = L.F32
     assert L.lib().starkv_prefill_attention(ctypes.byref(d), FAKE, 1 << 30, None) == code
     assert L.lib().starkv_prefill_workspace_bytes(ctypes.byref(d)) == 0
+
+
+@pytest.mark.parametrize("what,extra", [
+    # ranks or rows the reconstruction kernels cannot read in place are
+    # repacked into aligned workspace rows after the reconstructed K and V:
+    # (kind of copy, its bytes)
+    ("k_rank_odd", 2 * 4 * 120 * 64),            # K: B x Hkv x S rows of 32 ranks (rank 20 padded) x 2 B
+    ("k_offset_odd", 2 * 4 * 120 * 64),          # K: a head offset that is not a multiple of 8 elements
+    ("v_rank_odd", 2 * 120 * 128 + 4 * 128 * 128),   # V rows of 64 ranks (60 padded) and U_v rows of 64
+    ("uv_stride", 4 * 128 * 128),                # U_v rows 68 elements apart (not 16-byte rows)
+    ("v_data_odd", 2 * 120 * 128),               # V data 2 bytes into its buffer
+])
+def test_prefill_repacks_what_it_cannot_read_in_place(what, extra):
+    keep = []
+    d = _prefill_desc(keep)
+    base = L.lib().starkv_prefill_workspace_bytes(ctypes.byref(d))
+    if what == "k_rank_odd":
+        d.k.rank[2] = 20
+    elif what == "k_offset_odd":
+        d.k.head_offset[1] += 4
+    elif what == "v_rank_odd":
+        d.v.rank, d.uv_row_stride = 60, 60
+    elif what == "uv_stride":
+        d.uv_row_stride = 68
+    elif what == "v_data_odd":
+        d.v.data = FAKE + 2
+    assert L.lib().starkv_prefill_workspace_bytes(ctypes.byref(d)) == base + extra
+
+
+def test_quantised_layouts_take_any_rank_and_alignment():
+    """The reference's bx check shape (bx_quant.py:224-248): rank 1228 over a
+    256-rank upper block, 486-byte lower rows; odd K ranks; unaligned rows."""
+    lib = L.lib()
+    v = L.VLatent(rank=1228, format=L.FMT_INT4_REF, data=FAKE, stride_b=4096 * 128, stride_s=128,
+                  scale=FAKE, scale_stride_b=4096, scale_stride_s=1, split=256, split_format=L.FMT_INT4_REF,
+                  data2=FAKE + 2, stride2_b=4096 * 486, stride2_s=486, scale2=FAKE, scale2_stride_b=4096,
+                  scale2_stride_s=1)
+    d = L.PVDesc(batch=16, n_heads=32, seq_len=4096, dtype=L.F16, p=FAKE, p_stride_b=32 * 4096, p_stride_h=4096,
+                 v=v, out=FAKE, out_stride_b=32 * 1228, out_stride_h=1228)
+    assert lib.starkv_pv_latent_workspace_bytes(ctypes.byref(d)) > 0
+    d.v.stride2_s = 485                                                     # shorter than ceil(972 / 2)
+    assert lib.starkv_pv_latent(ctypes.byref(d), FAKE, 1 << 30, None) == ERR_SHAPE
+    d.v.stride2_s, d.v.split = 486, 252                                     # split not a multiple of 8
+    assert lib.starkv_pv_latent(ctypes.byref(d), FAKE, 1 << 30, None) == ERR_SHAPE
+    keep = []
+    dd = _decode_desc(keep, ranks=[37, 60, 5, 64, 17, 50, 33, 1])
+    dd.k.format, dd.k.scale, dd.k.scale_stride_b, dd.k.scale_stride_h = L.FMT_INT8_SYM, FAKE, 8 * 1024, 1024
+    dd.k.pos_stride[0] = 37
+    dd.k.head_offset[0] = 3
+    assert lib.starkv_decode_workspace_bytes(ctypes.byref(dd)) > 0
+    dd.k.pos_stride[0] = 36                                                 # row shorter than its 37 ranks
+    assert _call(dd) == ERR_SHAPE
 
 
 def test_rope_apply_validation():

@@ -142,14 +142,17 @@ class _VProj(torch.nn.Module):
 
 
 @pytest.mark.gpu
-def test_quant_module_prefill_and_decode_match_dequantised_history():
+@pytest.mark.parametrize("Hq,Hkv,r,Rv", [(8, 2, 80, 512),
+                                         # the reference's own odd shapes: K rank 100 (16 + 84), V rank
+                                         # int(0.3 * 4096) = 1228 (256 + 972: 486-byte int4 rows)
+                                         (8, 2, 100, 1228)])
+def test_quant_module_prefill_and_decode_match_dequantised_history(Hq, Hkv, r, Rv):
     from oracle import starkv_oracle as o
     from transformers import LlamaConfig
     from transformers.cache_utils import DynamicCache
     from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
     from starkv.LlamaLoRaAttention_headwise_quant import LlamaCustomAttention
-    _flush("[quant module] Hq=8 Hkv=2 r=80 Rv=512, prefill 33 (checked) + 3 decode steps")
-    Hq, Hkv, r, Rv = 8, 2, 80, 512
+    _flush(f"[quant module] Hq={Hq} Hkv={Hkv} r={r} Rv={Rv}, prefill 33 (checked) + 3 decode steps")
     torch.manual_seed(0)
     cfg = LlamaConfig(hidden_size=Hq * HEAD, num_attention_heads=Hq, num_key_value_heads=Hkv,
                       intermediate_size=256, num_hidden_layers=1, max_position_embeddings=4096)

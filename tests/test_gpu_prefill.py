@@ -131,6 +131,15 @@ CASES = [
     ("ref4k_int8v_mha", 2, 4, [64] * 4, 264, 129, 0, torch.float16, "ref4_32", "int8"),
     ("ref4w_k_int4w_v", 1, 4, [48] * 2, 512, 257, 3, torch.bfloat16, "ref4w", "int4_whole"),
     ("ref8k_ref8v_cfg_ranks", 1, 32, [128] * 8, 1640, 64, 200, torch.float16, "ref8_16", "ref_int8:256"),
+    # ranks that are not multiples of 8 and rows of any alignment (repacked into aligned workspace
+    # rows first): dense K heads back to back, V rank 60 (U_v rows of 60 columns too), int8 K of odd
+    # ranks with group-64 V of rank 1229, the reference module's K at rank 100 over the bx default
+    # V rank 1228 (486-byte lower rows), whole-rank int4 K and V of odd ranks, int8 V of rank 77
+    ("dense_any_rank", 2, 4, [20, 37, 5, 128], 60, 150, 10, torch.float16, "dense", "dense"),
+    ("int8k_g64v_any_rank_bf16", 1, 8, [37, 100], 1229, 120, 0, torch.bfloat16, "int8", "g64"),
+    ("ref8k_r100_ref4v_r1228", 1, 8, [100, 100], 1228, 100, 20, torch.float16, "ref8_16", "ref_int4:256"),
+    ("ref4w_k_int4w_v_odd", 1, 4, [75, 75], 203, 97, 0, torch.float16, "ref4w", "int4_whole"),
+    ("int8k_int8v_odd", 2, 4, [33, 17], 77, 64, 3, torch.bfloat16, "int8", "int8"),
 ]
 
 

@@ -27,15 +27,30 @@ def _flush(msg):
     sys.stdout.flush()
 
 
-def make_quant_v(kind, B, S, R, split=256, seed=0, outliers=True):
-    """Returns (VLatentSpec on cuda, dequantised V as fp16 numpy [B, S, R], float V)."""
+def _dev_pitched(a, pad):
+    """[B, S, n] bytes on the GPU inside rows of n + pad bytes, starting one
+    byte into an allocation: rows of any alignment (a view, as a caller's
+    cache slice would be)."""
+    if not pad:
+        return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    B, S, n = a.shape
+    big = torch.zeros(B, S, n + pad + 1, dtype=torch.from_numpy(a[:0]).dtype, device="cuda")
+    v = big[..., 1:1 + n]
+    v.copy_(torch.from_numpy(np.ascontiguousarray(a)).cuda())
+    return v
+
+
+def make_quant_v(kind, B, S, R, split=256, seed=0, outliers=True, pad=0):
+    """Returns (VLatentSpec on cuda, dequantised V as fp16 numpy [B, S, R], float V).
+    pad > 0: the packed rows sit unaligned (one byte in, pitch + pad)."""
     from oracle import starkv_oracle as o
     from starkv import VLatentSpec
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((B, S, R)).astype(np.float32)
     if outliers:
         x[..., ::97] *= 10.0                                           # 1 % outlier channels
-    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    dev = lambda a: (_dev_pitched(a, pad) if a.dtype in (np.uint8, np.int8)
+                     else torch.from_numpy(np.ascontiguousarray(a)).cuda())
     if kind in ("ref_int4", "ref_int8"):
         lo_r = R - split
         if kind == "ref_int4":
@@ -65,16 +80,18 @@ def make_quant_v(kind, B, S, R, split=256, seed=0, outliers=True):
 
 KINDS = [("ref_int4", 384, 256), ("ref_int8", 1640, 256), ("int4_whole", 512, 512), ("int8", 264, 264),
          ("g64", 1640, 0), ("g64", 200, 0)]
+# ranks that are not multiples of 8 (rows of any byte length: the reference's
+# bx default R = 1228 over 256 upper ranks leaves 486-byte lower rows), and
+# aligned ranks in rows placed one byte into their buffer (pad)
+ODD_KINDS = [("ref_int4", 1228, 256, 0), ("ref_int8", 1228, 256, 0), ("ref_int4", 1227, 256, 0),
+             ("int4_whole", 203, 203, 0), ("int8", 77, 77, 0), ("g64", 203, 0, 0), ("g64", 1229, 0, 0),
+             ("ref_int4", 384, 256, 3), ("int8", 264, 264, 5), ("g64", 1640, 0, 2)]
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("kind,R,split", KINDS)
-def test_pv_dequant_bit_exact(kind, R, split, dtype):
+def _dequant_one_hot(kind, R, split, dtype, pad=0):
     from starkv import pv_latent
-    _flush(f"[dequant] {kind} R={R} split={split} {dtype}")
     B, S, H = 2, 45, 32
-    spec, deq, _ = make_quant_v(kind, B, S, R, split=split or 256, seed=R)
+    spec, deq, _ = make_quant_v(kind, B, S, R, split=split or 256, seed=R, pad=pad)
     p = torch.zeros(B, H, S, dtype=dtype, device="cuda")
     pick = [[(7 * h + 3 * b) % S for h in range(H)] for b in range(B)]
     for b in range(B):
@@ -87,6 +104,22 @@ def test_pv_dequant_bit_exact(kind, R, split, dtype):
     bad = (got.view(torch.int16) != want.view(torch.int16)).sum().item()
     _flush(f"   mismatching values: {bad} of {got.numel()}")
     assert bad == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("kind,R,split", KINDS)
+def test_pv_dequant_bit_exact(kind, R, split, dtype):
+    _flush(f"[dequant] {kind} R={R} split={split} {dtype}")
+    _dequant_one_hot(kind, R, split, dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("kind,R,split,pad", ODD_KINDS)
+def test_pv_dequant_bit_exact_any_rank(kind, R, split, pad, dtype):
+    _flush(f"[dequant any rank] {kind} R={R} split={split} pad={pad} {dtype}")
+    _dequant_one_hot(kind, R, split, dtype, pad=pad)
 
 
 @pytest.mark.gpu
@@ -153,3 +186,58 @@ def test_bx_dropin(upper):
     mx, mr = errors(out.float(), ref)
     _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
     assert mr <= 1e-3 and mx <= 2e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("upper", ["int4", "int8"])
+def test_bx_reference_check_shape(upper):
+    """The reference's own bx check (bx_quant.py:224-248, defaults 245-252):
+    B 16, 32 heads, S 4096, total rank int(0.3 * 4096) = 1228 over 256 upper
+    ranks (a 972-rank lower block: 486-byte int4 rows), fp16, P ~ N(0, 1).
+    The dequantisation is bit-exact (one-hot P over the first batches) and the
+    output meets the attention gate against the oracle in float64."""
+    from oracle import starkv_oracle as o
+    from starkv.bx_quant import bx
+    B, H, S, R, U = 16, 32, 4096, int(0.3 * 4096), 256
+    _flush(f"[bx reference shape] B={B} S={S} R={R} upper={U} ({upper})")
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((B, S, R)).astype(np.float32)
+    x[..., ::97] *= 10.0
+    if upper == "int4":
+        p1, s1 = o.quant_int4_ref(x[..., :U])
+        d1 = o.dequant_int4_ref(p1, s1, U)
+    else:
+        p1, s1 = o.quant_int8_sym(x[..., :U])
+        d1 = o.dequant_int8_sym(p1, s1)
+    p2, s2 = o.quant_int4_ref(x[..., U:])
+    assert p2.shape[-1] == 486
+    deq = np.concatenate([d1, o.dequant_int4_ref(p2, s2, R - U)], axis=-1)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    x1, x2, sc1, sc2 = dev(p1), dev(p2), dev(s1), dev(s2)
+    # one-hot P: each head of batches 0..1 picks one position -> its dequantised row
+    p = torch.zeros(B, H, S, dtype=torch.float16, device="cuda")
+    pick = [[(131 * h + 17 * b) % S for h in range(H)] for b in range(2)]
+    for b in range(2):
+        for h in range(H):
+            p[b, h, pick[b][h]] = 1.0
+    out = bx(p, x1, x2, sc1, sc2, original_rank=R, upper_rank=U)
+    torch.cuda.synchronize()
+    want = torch.from_numpy(np.stack([deq[b][pick[b]] for b in range(2)])).half()
+    got = out[:2].cpu()
+    bad = (got.view(torch.int16) != want.view(torch.int16)).sum().item()
+    _flush(f"   one-hot mismatching values: {bad} of {got.numel()}")
+    assert bad == 0
+    assert torch.count_nonzero(out[2:]).item() == 0
+    # the reference's own probabilities: N(0, 1), fp16
+    g = torch.Generator(device="cuda").manual_seed(12)
+    p = torch.randn(B, H, S, generator=g, device="cuda").half()
+    out = bx(p, x1, x2, sc1, sc2, original_rank=R, upper_rank=U)
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, R) and out.dtype == torch.float16
+    ref = p.double().cpu() @ torch.from_numpy(deq).double()
+    mx, mr = errors(out.float(), ref)
+    # P is not normalised here, so |out| reaches ~1e2: the max-abs gate of 2e-2
+    # applies per element to max(1, |ref|) (an fp16 output keeps ~5e-4 relative)
+    scaled = ((out.double().cpu() - ref).abs() / ref.abs().clamp_min(1.0)).max().item()
+    _flush(f"   max_abs={mx:.3e} scaled max_abs={scaled:.3e} mean_rel={mr:.3e}  (|ref| mean {ref.abs().mean():.2f})")
+    assert mr <= 1e-3 and scaled <= 2e-2

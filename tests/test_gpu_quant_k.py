@@ -235,3 +235,95 @@ def test_decode_int8_k_g64_v():
     bk_h = [bk_all[bko[h] // HEAD:bko[h] // HEAD + r].cpu() for h, r in enumerate(ranks)]
     ref, _, _ = o.decode_attention(q.cpu(), bk_h, deq_k, torch.from_numpy(deq_v), uv.cpu(), cos, sin)
     check_output(out, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_k_logits_int8_any_rank(dtype):
+    """int8 K of ranks that are not multiples of 8, heads back to back (rows of
+    any byte alignment; the bytes past a row are the next row's): the
+    register-streaming kernel's unaligned-row loads, with the ranks past each
+    head's rank masked."""
+    from oracle import starkv_oracle as o
+    from starkv import KLatentSpec, k_logits
+    from starkv._lib import FMT_INT8_SYM
+    ranks = [37, 100, 5, 64, 17, 128, 90, 1, 33, 71, 16, 127]
+    _flush(f"[k int8 any rank] ranks {ranks} {dtype}")
+    B, S = 2, 517
+    Hkv = len(ranks)
+    buf, scales, offs, deq = ragged_int8_k(B, S, ranks, seed=21)
+    g = torch.Generator(device="cuda").manual_seed(22)
+    q = torch.randn(B, Hkv, HEAD, generator=g, device="cuda").to(dtype)
+    bko = list(np.cumsum([0] + ranks[:-1]) * HEAD)
+    bk_all = torch.cat([torch.randn(r, HEAD, generator=g, device="cuda") / math.sqrt(r) for r in ranks]).to(dtype)
+    sc = _dev(scales)
+    spec = KLatentSpec(_dev(buf), ranks, offs, ranks, buf.shape[1], bk_all, bko, HEAD,
+                       fmt=FMT_INT8_SYM, scale=sc, scale_stride_b=sc.stride(0), scale_stride_h=sc.stride(1))
+    out = k_logits(q, spec, S, scale=0.5)
+    torch.cuda.synchronize()
+    cos, sin = _rope_cs(S)
+    bk_h = [bk_all[bko[h] // HEAD:bko[h] // HEAD + r].cpu() for h, r in enumerate(ranks)]
+    ref = o.k_logits(q.cpu(), bk_h, deq, cos, sin, scale=0.5)
+    check_logits(out, ref, 0.5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hq,Hkv,upper,lower,kind", [
+    (32, 8, 16, 84, "int8"),     # the reference module's K at rank 100 (16 int8 + 84 int4)
+    (8, 8, 16, 37, "int8"),      # odd lower block: 19-byte rows
+    (8, 4, 32, 21, "int4"),
+    (8, 8, 0, 75, "int4"),       # whole-rank int4, 38-byte rows
+])
+def test_k_logits_reference_split_any_rank(Hq, Hkv, upper, lower, kind):
+    from oracle import starkv_oracle as o
+    from starkv import KLatentSpec, k_logits
+    _flush(f"[k split any rank] Hq={Hq} Hkv={Hkv} upper={upper} lower={lower} {kind}")
+    B, S = 2, 301
+    r = upper + lower
+    if upper == 0:
+        q1, s1, _, _, deq = reference_split_k(B, Hkv, S, lower, 0, "int4", seed=23)
+    else:
+        q1, s1, q2, s2, deq = reference_split_k(B, Hkv, S, upper, lower, kind, seed=23)
+    g = torch.Generator(device="cuda").manual_seed(24)
+    q = torch.randn(B, Hq, HEAD, generator=g, device="cuda").half()
+    bk = (torch.randn(Hkv, r, HEAD, generator=g, device="cuda") / math.sqrt(r)).half()
+    if upper == 0:
+        spec = KLatentSpec.from_reference_quant(_dev(q1), _dev(s1), bk, r)
+    else:
+        spec = KLatentSpec.from_reference_quant(_dev(q1), _dev(s1), bk, r, x2=_dev(q2), s2=_dev(s2), split=upper)
+    out = k_logits(q, spec, S)
+    torch.cuda.synchronize()
+    cos, sin = _rope_cs(S)
+    ref = o.k_logits(q.cpu(), [bk[h].cpu() for h in range(Hkv)], [torch.from_numpy(deq[:, h]) for h in range(Hkv)],
+                     cos, sin)
+    check_logits(out, ref, 1.0)
+
+
+@pytest.mark.gpu
+def test_decode_any_rank_int8_k_g64_v():
+    """Fused decode over int8 K of odd ranks (unaligned rows) and group-64 V of
+    rank 1229 (615-byte rows)."""
+    from oracle import starkv_oracle as o
+    from starkv import KLatentSpec, decode_attention
+    from starkv._lib import FMT_INT8_SYM
+    from test_gpu_quant import make_quant_v
+    ranks = [37, 100, 5, 64, 17, 128, 90, 1]
+    B, S, Rv = 2, 777, 1229
+    _flush(f"[decode any rank] int8 K ranks {ranks}, g64 V Rv={Rv}")
+    Hkv = len(ranks)
+    buf, scales, offs, deq_k = ragged_int8_k(B, S, ranks, seed=25)
+    vspec, deq_v, _ = make_quant_v("g64", B, S, Rv, seed=26)
+    g = torch.Generator(device="cuda").manual_seed(27)
+    q = torch.randn(B, 4 * Hkv, HEAD, generator=g, device="cuda").half()
+    bko = list(np.cumsum([0] + ranks[:-1]) * HEAD)
+    bk_all = torch.cat([torch.randn(r, HEAD, generator=g, device="cuda") / math.sqrt(r) for r in ranks]).half()
+    uv = (torch.randn(Hkv * HEAD, Rv, generator=g, device="cuda") / math.sqrt(Rv)).half()
+    sc = _dev(scales)
+    kspec = KLatentSpec(_dev(buf), ranks, offs, ranks, buf.shape[1], bk_all, bko, HEAD,
+                        fmt=FMT_INT8_SYM, scale=sc, scale_stride_b=sc.stride(0), scale_stride_h=sc.stride(1))
+    out = decode_attention(q, kspec, vspec, uv, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    cos, sin = _rope_cs(S)
+    bk_h = [bk_all[bko[h] // HEAD:bko[h] // HEAD + r].cpu() for h, r in enumerate(ranks)]
+    ref, _, _ = o.decode_attention(q.cpu(), bk_h, deq_k, torch.from_numpy(deq_v), uv.cpu(), cos, sin)
+    check_output(out, ref)

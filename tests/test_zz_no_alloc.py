@@ -21,7 +21,7 @@ def test_noalloc_decode_matches_the_workspace_entry_point(dtype):
     assert NOALLOC_SCRATCH_BYTES == 128 << 20
     for i, case in enumerate(cases):
         print(f"[noalloc] call {i}: B={case.B} Hq={case.Hq} Hkv={case.Hkv} S={case.S} Rv={case.Rv} {dtype}", flush=True)
-        out = torch.empty(case.B, case.Hq, 128, dtype=dtype, device="cuda")
+        out = torch.full((case.B, case.Hq, 128), float("nan"), dtype=dtype, device="cuda")   # every element written
         got = decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, out=out, noalloc=True)
         want = decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope)
         torch.cuda.synchronize()
