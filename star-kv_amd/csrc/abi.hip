@@ -13,7 +13,7 @@ using namespace starkv;
 
 namespace {
 
-constexpr int MI355X_CUS = 256;     // launch geometry is planned for one MI355X
+constexpr int FULL_CHIP_CUS = 256;  // an MI355X: planning default when no device can be queried
 constexpr int K1_WG_PER_CU = 1;     // k_logits_kernel: one 8-wave (or 4-wave) workgroup per CU
 constexpr int MAX_S = 1 << 24;
 constexpr int MAX_RV = 8192;
@@ -33,6 +33,26 @@ bool al(const void* p, int n) { return ((uintptr_t)p % (uintptr_t)n) == 0; }
 bool al64(int64_t v, int n) { return v % n == 0; }
 
 size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Compute units of the current device, the unit of every launch plan below
+// (rounds of resident workgroups), read once per device.  A partitioned GPU
+// or another part reports fewer; with no device to ask (argument validation
+// on a machine without a GPU) the plan assumes a whole MI355X.
+int device_cus() {
+  constexpr int MAXD = 64;
+  static std::mutex mu;
+  static int cus[MAXD] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXD) return FULL_CHIP_CUS;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+      n = FULL_CHIP_CUS;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
 
 // Choose how many position splits minimise the modelled time of a launch of
 // `groups` independent (batch, plan) groups over `n_units` position units:
@@ -492,7 +512,7 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
   const double vbytes = vq == VQ_DENSE ? 2.0 * Rv : Rv / 2.0 + 4.0 * ceil_div(Rv, 64);
   // (below ~8K positions the launch is latency-bound and partials are cheap)
   const double frac = 32.0 * g.Rvp * 8.0 / g.n_cb / ((double)std::max(S, 8192) * (vbytes / g.n_cb + 128.0));
-  int n = choose_splits((int64_t)B * g.n_cb, MI355X_CUS * wg_per_cu, n_ks, 512, 4.0, frac);
+  int n = choose_splits((int64_t)B * g.n_cb, device_cus() * wg_per_cu, n_ks, 512, 4.0, frac);
   const int64_t max_ks = std::max<int64_t>(1, ((int64_t)1 << 31) / std::max<int64_t>(row_bytes, 1) / KSTEP);
   n = std::max<int64_t>(n, ceil_div(n_ks, max_ks));
   g.c2_len = (int)ceil_div(n_ks, n) * KSTEP;
@@ -522,14 +542,15 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   DecodeLayout L;
   L.S_pad = (int)round_up(S, 64);
   const int n_tiles = (int)ceil_div(S, TILE);
-  L.n_c1 = choose_splits((int64_t)B * n_wg, MI355X_CUS * k1pc, n_tiles, 256, 3.0, 0.0);
+  const int cus = device_cus();
+  L.n_c1 = choose_splits((int64_t)B * n_wg, cus * k1pc, n_tiles, 256, 3.0, 0.0);
   L.tiles_per_chunk = (int)ceil_div(n_tiles, L.n_c1);
   L.n_c1 = (int)ceil_div(n_tiles, L.tiles_per_chunk);
   L.n_hg = head_groups(Hq);
   L.pv = pv_geometry(B * L.n_hg, S, Rv, true, vq, v_row_bytes);
-  L.sw = up_slice_width(Hkv, Rv);
+  L.sw = up_slice_width(Hkv, Rv, cus);
   L.n_sl = (int)ceil_div(Rv, L.sw);
-  L.n_cs = up_chunk_sets(Hkv, L.n_sl, L.pv.n_c2);
+  L.n_cs = up_chunk_sets(Hkv, L.n_sl, L.pv.n_c2, cus);
   const int Rvp = L.pv.Rvp, n_c2 = L.pv.n_c2;
   const size_t BQ = (size_t)B * L.n_hg;
   size_t o = 0;
@@ -829,7 +850,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
   const int n_tiles = (int)ceil_div(d->seq_len, TILE);
-  int nc = choose_splits((int64_t)d->batch * plan.n_wg, MI355X_CUS * plan.per_cu, n_tiles, 256, 3.0, 0.0);
+  int nc = choose_splits((int64_t)d->batch * plan.n_wg, device_cus() * plan.per_cu, n_tiles, 256, 3.0, 0.0);
   a.tiles_per_chunk = (int)ceil_div(n_tiles, nc);
   a.n_chunks = (int)ceil_div(n_tiles, a.tiles_per_chunk);
   const bool fast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);

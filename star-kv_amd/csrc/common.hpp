@@ -413,8 +413,8 @@ int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ran
 // dense variants (8 and 13 tiles) take one, the others two
 constexpr int pv_wg_per_cu(int ntw, int vq) { return ntw >= 8 && vq == VQ_DENSE ? 1 : 2; }
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st);
-int up_slice_width(int n_kv, int Rv);                 // V-rank columns per up-projection workgroup
-int up_chunk_sets(int n_kv, int n_sl, int n_c2);      // chunk sets per (slice, KV head)
+int up_slice_width(int n_kv, int Rv, int cus);        // V-rank columns per up-projection workgroup
+int up_chunk_sets(int n_kv, int n_sl, int n_c2, int cus);   // chunk sets per (slice, KV head)
 int launch_fill_i32(int* p, int n, int v, hipStream_t st);
 int launch_k_append(const KAppendArgs& a, int dtype, hipStream_t st);
 int launch_v_append(const VAppendArgs& a, int dtype, hipStream_t st);

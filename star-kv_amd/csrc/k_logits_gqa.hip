@@ -73,7 +73,8 @@ __device__ inline void gq_wait_vm_n(int n) {
 // not see it write LDS, adds no waits of its own before the reads of other
 // stages; the kernel orders it with explicit vmcnt waits and barriers.
 // Each statement sets m0 itself (the compiler treats m0 as reserved and
-// ignores it as a clobber; its code for this kernel holds nothing in m0).
+// ignores it as a clobber; its code for this kernel holds nothing in m0,
+// which tests/test_gqa_m0.py checks on the compiled gfx950 assembly).
 __device__ inline void gq_dma(const void* src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
@@ -136,6 +137,20 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
   const int gs = a.gs, S = a.S, tile0 = d.tile0, stage = d.stage, nst = d.nst;
   const int r = H.hrank[slot], hb = H.hoff[slot], n16 = r >> 3;
 
+  // The q.K step runs on fp16 MFMA.  bf16 models hold keys and queries in
+  // bf16 (the reference too, abx_rope_batched.py:114-125), whose range fp16
+  // lacks.  Their queries enter scaled by 2^-8 (exact: |q| up to 1.6e7;
+  // those below 0.016 among fp16's subnormals, with an absolute error under
+  // 7.6e-6) and the logits leave scaled by 2^8.  A tile whose rotated keys
+  // could pass fp16's range (|y| <= (|k0| + |k1|) a <= 2 a max(|k0|, |k1|),
+  // a = |table cos at position 0|, the attention scaling) takes them scaled
+  // by 2^-16 (exact; up to ~4e9).  Keys are not scaled on every tile: that
+  // puts the small ones among fp16's subnormals, measured 1.6x slower.
+  constexpr bool BF = !__is_same(XT, _Float16);
+  constexpr float IN_SCALE = BF ? 0x1p-8f : 1.f;
+  constexpr float F16_SAFE = 60000.f;
+  const float wscale = a.wscale * (BF ? 0x1p8f : 1.f);
+  const float ta = fabsf((float)((const _Float16*)a.rope)[0]);
   // B_k^T operands of M-tiles p and p+2: lane l holds dim 32m + l%32, ranks
   // 16kk + 8hh + 0..7 (zero past r)
   XV bt[2][NK];
@@ -170,7 +185,10 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int dd = 32 * (kk2 >> 1) + 8 * (2 * (kk2 & 1) + (i >> 2)) + 4 * hh + (i & 3);
-        v[i] = h < gs ? (_Float16)to_f32(qrow[dd]) : (_Float16)0.f;
+        // scaled in the act dtype first (exact): converted to fp16 before
+        // the multiply, which the compiler may otherwise do, it would overflow
+        const XT qs = (XT)(to_f32(qrow[dd]) * IN_SCALE);
+        v[i] = h < gs ? (_Float16)to_f32(qs) : (_Float16)0.f;
       }
       qa[n] = v;
     }
@@ -205,7 +223,7 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
       const int h = 4 * hh + v;
       if (h >= gs || s >= S) continue;
       const int qh = kv * gs + h;
-      float val = a.wscale * sum[v];
+      float val = wscale * sum[v];
       if constexpr (MASKED) val += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
       const int64_t o = b * a.o_sb + (int64_t)ti * a.o_st + qh * a.o_sh + t;
       if constexpr (OUTK == 0) ((float*)a.out)[o] = val;
@@ -251,6 +269,20 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
       k0 = gq_mfma<XT>(bt[0][kk], xb[kk], k0);
       k1 = gq_mfma<XT>(bt[1][kk], xb[kk], k1);
     }
+    float lscale = 1.f;
+    if constexpr (BF) {
+      float m = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) m = fmaxf(m, fmaxf(fabsf(k0[v]), fabsf(k1[v])));
+      if (__builtin_amdgcn_ballot_w64(2.f * m * ta > F16_SAFE) != 0) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          k0[v] *= 0x1p-16f;
+          k1[v] *= 0x1p-16f;
+        }
+        lscale = 0x1p16f;
+      }
+    }
     // rotate: accumulator v is dim d = 32m + 8g + 4hh + e (g = v/4, e = v%4)
     // and its partner d + 64; (a cos, a sin) of frequency 32p + 8g + 4hh + e
     // are elements 2e, 2e+1 of table K-step 4p + g
@@ -267,7 +299,7 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
     la = mfma_f16(qa[1], bop[1], la);
     lb = mfma_f16(qa[3], bop[3], lb);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) prev[v] = la[v] + lb[v];
+    for (int v = 0; v < 4; ++v) prev[v] = (la[v] + lb[v]) * lscale;
   }
   // the last tile: handed over after one more barrier
   if (p == 0) {

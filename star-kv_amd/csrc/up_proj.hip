@@ -255,14 +255,14 @@ static void launch_up_t(const UPArgs& a, bool fast, hipStream_t st) {
   else launch_up_sw<WT, 32>(a, fast, grid, st);
 }
 
-// slice width: 64 columns when that still gives >= 256 workgroups, else 32
+// slice width: 64 columns when that still gives a workgroup per CU, else 32
 // (whole 128-byte lines of the partials either way)
-int up_slice_width(int n_kv, int Rv) { return (int64_t)n_kv * ceil_div(Rv, 64) >= 256 ? 64 : 32; }
+int up_slice_width(int n_kv, int Rv, int cus) { return (int64_t)n_kv * ceil_div(Rv, 64) >= cus ? 64 : 32; }
 
 // chunk sets: enough workgroups for two per CU, with at least 16 chunks each
-int up_chunk_sets(int n_kv, int n_sl, int n_c2) {
+int up_chunk_sets(int n_kv, int n_sl, int n_c2, int cus) {
   const int64_t wg = (int64_t)n_kv * n_sl;
-  return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(512, wg), n_c2 / 16));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2 * cus, wg), n_c2 / 16));
 }
 
 int launch_up_proj(const UPArgs& a, int dtype, bool fast, hipStream_t st) {

@@ -194,3 +194,31 @@ def test_rope_apply_matches_oracle(dtype, device_pos):
     err = (x.double().cpu() - ref).abs()
     ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
     assert float((err / ref.abs().clamp_min(1e-3)).max()) <= ulp or float(err.max()) <= ulp * 4, float(err.max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("latent_scale,q_scale", [(30000.0, 1.0), (1.0, 1e5), (3000.0, 3e4)],
+                         ids=["keys", "queries", "both"])
+def test_k_logits_gqa_bf16_beyond_fp16_range(latent_scale, q_scale):
+    """bf16 grouped-query K logits whose keys or queries exceed fp16's range
+    (the reference holds them in bf16, abx_rope_batched.py:114-125): the
+    grouped-query kernel's fp16 q.K step takes bf16 queries and keys scaled
+    by 2^-8 (exact) and scales the logits back, so values up to 1.6e7 stay
+    finite and the logits match the oracle relative to their own RMS
+    (max-abs 2e-2, mean-rel 1e-3)."""
+    from starkv import k_logits
+    ranks = cfg4_ranks()
+    case = make_case(1, 32, 8, 300, ranks, 512, dtype=torch.bfloat16, seed=41, latent_scale=latent_scale)
+    case.q.mul_(q_scale)
+    kmax = max(float((x.float() @ b.float()).abs().max()) for x, b in zip(case.xk_heads, case.bk_heads))
+    qmax = float(case.q.float().abs().max())
+    print(f"[k logits gqa bf16 large] max |K| before RoPE {kmax:.3e}, max |q| {qmax:.3e}", flush=True)
+    assert max(kmax, qmax) > 65504.0
+    out = k_logits(case.q, case.kspec, case.S)
+    torch.cuda.synchronize()
+    ref = oracle_logits(case)
+    assert torch.isfinite(out).all()
+    rms = float(ref.pow(2).mean().sqrt())
+    mx, mr = errors(out / rms, ref / rms)
+    print(f"   RMS {rms:.3e}: max_abs/RMS={mx:.3e} mean_rel={mr:.3e}", flush=True)
+    assert mx <= 2e-2 and mr <= 1e-3
