@@ -209,7 +209,92 @@ def build_workload(name, dev):
                "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": Hq, "kv_heads": Hkv,
                "rotated_input_copies": n_copies}
         return dict(case=case, bytes=nb, step=step, B=B, S=S, rope=rope, dtype="bf16", config=cfg)
+    if name.startswith("abx-"):
+        # the reference's abx benchmark (abx_rope_batched.py:205-250, 274-280):
+        # total rank int(0.2 * 4096) = 819 over 32 query heads in KV groups of
+        # 4 -> 8 KV heads of rank 102, fp16, theta 10000, one query per head,
+        # at a context from target_seq_lens (4096, 16384, 65536, 262144); its
+        # tensors carry no batch dimension, i.e. batch 1.  A step is one abx
+        # call (the K-logit kernel): fp16 logits [1, 32, 1, S] out.
+        from starkv.abx_rope_batched import abx
+        S = int(name.split("-", 1)[1])
+        B, Hq, Hkv = 1, 32, 8
+        r = int(4096 * 0.2) // Hkv
+        per = {"x": B * Hkv * S * r * 2, "b": Hkv * r * HEAD_DIM * 2, "a": B * Hq * HEAD_DIM * 2, "out": B * Hq * S * 2}
+        tot = sum(per.values())
+        nb = {"k_logits": tot, "pv_latent": 0, "up_proj": 0, "total": tot}
+        # rotate over input copies spanning >= 512 MB so each call streams from HBM
+        n_copies = max(1, min(1024, -(-(512 << 20) // tot)))
+        g = torch.Generator(device=dev).manual_seed(7)
+        copies = [(torch.randn(B, Hq, 1, HEAD_DIM, generator=g, device=dev).half(),
+                   (torch.randn(Hq, r, HEAD_DIM, generator=g, device=dev) / math.sqrt(r)).half(),
+                   torch.randn(B, Hkv, S, r, generator=g, device=dev).half()) for _ in range(n_copies)]
+        turn = [0]
+
+        def step(ev=None):
+            a, b, x = copies[turn[0] % n_copies]
+            turn[0] += 1
+            if ev:
+                ev[0].record()
+            abx(a, b, x, dtype=torch.float16)
+            if ev:
+                for e in ev[1:]:
+                    e.record()
+        cfg = {"workload": f"{name}: the reference's abx micro-benchmark shape (abx_rope_batched.py:274-280): "
+                           f"32 query heads in KV groups of 4, 8 KV heads of K rank 102 (total 819), fp16, "
+                           f"batch 1, context {S}; one abx call (K logits with RoPE, fp16 out)",
+               "batch": B, "seq_len": S, "k_rank_total": Hkv * r, "heads": Hq, "kv_heads": Hkv,
+               "rotated_input_copies": n_copies}
+        return dict(case=None, bytes=nb, step=step, B=B, S=S, rope=RopeConfig(), dtype="f16", config=cfg)
     raise SystemExit(f"unknown workload {name!r}")
+
+
+def graphed_attention_ms(atts, B, reps=20):
+    """The attention work of one graph-replayed decode step on its own: for
+    every layer the cache write with the query rotation (one launch) and the
+    decode attention over the whole cache capacity under the device mask --
+    the calls LatentAttention.core makes in the captured step, on the same
+    caches at the same length -- captured in one graph of their own and
+    replayed; returns ms per replay.  (Each replay rewrites the first free
+    cache position, which no real step has written yet.)"""
+    import torch
+    from starkv import decode_attention
+    from starkv.e2e import DecodeGraphState
+    a0 = atts[0]
+    dev = a0.bk.device
+    L, cap = a0.cache.length, a0.cache.cap
+    assert L < cap, "the attention-only graph writes one free cache position"
+    state = DecodeGraphState(B, cap, L, dev)
+    state.open_position()
+    g = torch.Generator(device=dev).manual_seed(11)
+    bufs = [(torch.randn(B, a.n_heads, 1, HEAD_DIM, generator=g, device=dev).half(),
+             torch.randn(B, 1, sum(a.ranks), generator=g, device=dev).half(),
+             torch.randn(B, 1, a.v_u.weight.shape[1], generator=g, device=dev).half()) for a in atts]
+
+    def attn():
+        for a, (q, k, v) in zip(atts, bufs):
+            ks, vs = a.cache.append_at(k, v, a.bk, state.pos, error_flag=state.error, q=q, rope=a.rope)
+            decode_attention(q[:, :, 0], ks, vs, a.v_u.weight, rope=a.rope, seq_len=state.capacity,
+                             scale=a.scaling, mask=state.mask)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        attn()                                        # eager once: tables and workspace in place
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        attn()
+    for _ in range(3):
+        graph.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    state.check()
+    return e0.elapsed_time(e1) / reps
 
 
 def run_e2e(args, emit=True):
@@ -218,15 +303,16 @@ def run_e2e(args, emit=True):
     the latent cache (cfg3 ranks and formats: K int8, V int4-g64), prefill 8192
     random tokens at batch 8 (starkv_prefill_attention), then greedy decode
     steps replayed from one captured HIP graph (starkv.e2e.decode_graphed).
-    A few eager steps before it time the attention kernels (HIP events) for the
-    attention share."""
+    The attention share is the attention work of one step, captured and
+    replayed as a graph of its own (graphed_attention_ms), over the timed
+    step."""
     import torch
     from _util import cfg2_ranks
     from starkv.e2e import attention_layers, build_model, decode_graphed
-    B, P, steps, n_eager = 8, 8192, args.e2e_steps, 8
+    B, P, steps = 8, 8192, args.e2e_steps
     t0 = time.perf_counter()
     model = build_model(n_layers=32, hidden=4096, heads=32, kv_heads=32, intermediate=11008, vocab=32000,
-                        ranks=cfg2_ranks(), v_rank=1640, batch=B, capacity=P + n_eager + steps + 1,
+                        ranks=cfg2_ranks(), v_rank=1640, batch=B, capacity=P + steps + 1,
                         fmt="int8_g64", seed=0)
     torch.cuda.synchronize()
     t_build = time.perf_counter() - t0
@@ -241,29 +327,17 @@ def run_e2e(args, emit=True):
         tok = out.logits[:, -1].argmax(-1, keepdim=True)
         torch.cuda.synchronize()
         t_prefill = time.perf_counter() - t0
-        # eager steps: attention kernel time per step (events around each layer's decode)
-        for a in atts:
-            a.events = []
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        t0 = time.perf_counter()
-        for t in range(n_eager):
-            pos = torch.full((B, 1), P + t, device="cuda", dtype=torch.long)
-            out = model(input_ids=tok, position_ids=pos, use_cache=False, logits_to_keep=1)
-            tok = out.logits[:, -1].argmax(-1, keepdim=True)
-        e1.record()
-        torch.cuda.synchronize()
-        eager_wall = time.perf_counter() - t0
-        attn_s = sum(x.elapsed_time(y) for a in atts for (x, y) in a.events) * 1e-3 / n_eager
-        for a in atts:
-            a.events = None
         # graph-replayed decode: the timed region
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         toks, _ = decode_graphed(model, tok, steps, keep_logits=False)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        # the same step's attention work alone, graph-replayed, at the context
+        # the decode ended on
+        attn_ms = graphed_attention_ms(atts, B)
     step_s = wall / steps
+    n_layers = len(atts)
     rec = {
         "metric": "e2e decode tok/s", "value": round(B * steps / wall, 1), "unit": "tok/s", "n_gpus": 1,
         "steps": steps, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
@@ -273,11 +347,12 @@ def run_e2e(args, emit=True):
                                "captured HIP graph",
                    "batch": B, "prompt": P, "decode_steps": steps},
         "ms_per_decode_step": round(step_s * 1e3, 3),
-        # the share is measured on the eager steps (events around each layer's
-        # decode kernels, which also count any launch gaps between them)
-        "eager_ms_per_decode_step": round(eager_wall * 1e3 / n_eager, 3),
-        "eager_attention_ms_per_decode_step": round(attn_s * 1e3, 3),
-        "eager_attention_share": round(attn_s / (eager_wall / n_eager), 4),
+        # every layer's cache write + query rotation and decode attention of
+        # one step, captured and replayed as a graph of their own (context
+        # P + steps), against the timed graph-replayed step
+        "attention_ms_per_decode_step": round(attn_ms, 3),
+        "attention_us_per_layer": round(attn_ms * 1e3 / n_layers, 1),
+        "attention_share": round(attn_ms / (step_s * 1e3), 4),
         "prefill_s": round(t_prefill, 3), "build_s": round(t_build, 1),
     }
     del model
@@ -453,6 +528,7 @@ def main():
     ap.add_argument("--workload", default="cfg2",
                     help="cfg2 (default: the metric's workload), cfg3 (B16 S32768, K int8 + V int4-g64 cache), "
                          "cfg3-long (B4 S131072, same formats), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S), "
+                         "abx-<S> (the reference's abx micro-benchmark: 8 KV heads of rank 102, groups of 4, fp16, batch 1), "
                          "e2e (32-layer model, prefill 8192, greedy decode at batch 8; prints e2e decode tok/s), "
                          "prefill (one layer's 8192-token causal prefill at batch 8 over the int8 / int4-g64 "
                          "latent cache; prints TFLOP/s against the MFMA roofline)")
@@ -619,9 +695,9 @@ def main():
         torch.cuda.empty_cache()
         e2e = run_e2e(args, emit=False)
         rec["e2e_decode_tok_s"] = e2e["value"]
-        rec["e2e"] = {k: e2e[k] for k in ("ms_per_decode_step", "eager_ms_per_decode_step",
-                                          "eager_attention_ms_per_decode_step", "eager_attention_share",
-                                          "prefill_s", "steps", "config")}
+        rec["e2e"] = {k: e2e[k] for k in ("ms_per_decode_step", "attention_ms_per_decode_step",
+                                          "attention_us_per_layer", "attention_share", "prefill_s", "steps",
+                                          "config")}
     print(json.dumps(rec), flush=True)
 
 

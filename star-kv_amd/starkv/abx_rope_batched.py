@@ -27,8 +27,11 @@ def abx(a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, dtype: torch.dtype = 
         rope: Optional[RopeConfig] = None) -> torch.Tensor:
     """Decode logits A @ RoPE(X @ B)^T without the 1/sqrt(D) scale.
 
-    a: rotated query [B, Hq, 1, 128]; b: ``k_u^T`` [Hkv, r, 128]; x: key
-    latent cache [B, Hkv, S, r] (last dim contiguous).  ``dtype`` is the
+    a: rotated query [B, Hq, 1, 128]; b: ``k_u^T`` [Hkv, r, 128], or with
+    more rows -- the reference's own check passes one per query head,
+    [Hq, r, 128] (abx_rope_batched.py:254-265) -- of which, as in the Triton
+    kernel (row q // gs, abx_rope_batched.py:81), only the first Hkv are read;
+    x: key latent cache [B, Hkv, S, r] (last dim contiguous).  ``dtype`` is the
     reference's compute-dtype switch (float16 / bfloat16 / float32); the
     kernel computes in the operands' own dtype with fp32 accumulation, so it
     only selects which inputs are accepted.  ``rope`` (an extension) selects
@@ -46,6 +49,8 @@ def abx(a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, dtype: torch.dtype = 
         raise StarKVError(f"abx: a {tuple(a.shape)} and x {tuple(x.shape)} disagree on batch or heads")
     if not (a.dtype == b.dtype == x.dtype):
         raise StarKVError(f"abx: a, b and x must share one dtype (got {a.dtype}, {b.dtype}, {x.dtype})")
-    spec = KLatentSpec.from_reference(x, b)
+    if b.shape[0] < x.shape[1]:
+        raise StarKVError(f"abx: b {tuple(b.shape)} holds fewer than the {x.shape[1]} KV heads of x")
+    spec = KLatentSpec.from_reference(x, b[:x.shape[1]])
     out = k_logits(a, spec, seq_len=x.shape[2], rope=rope or RopeConfig(), scale=1.0, out_dtype=x.dtype)
     return out.unsqueeze(2)

@@ -18,7 +18,7 @@ cache and takes positions from it.
 from __future__ import annotations
 
 import math
-from typing import List, Optional, Sequence
+from typing import Callable, List, Optional, Sequence
 
 import torch
 import torch.nn as nn
@@ -441,11 +441,14 @@ def generate_graphed(model, prompt: torch.Tensor, steps: int, keep_logits: bool 
 
 
 @torch.no_grad()
-def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = True):
+def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = True,
+                   on_step: Optional[Callable[[int], None]] = None):
     """``steps`` greedy decode steps from token ``tok`` [B, 1] at the caches'
     current length: the first step runs eagerly in graph form (which also
     warms up every table and workspace), one step is captured, and the rest
-    replay it, each step's argmax feeding the next inside the graph.  Returns
+    replay it, each step's argmax feeding the next inside the graph.
+    ``on_step(i)`` (optional) runs on the host after step i (0: the eager
+    one) has been enqueued, e.g. to read what the step wrote.  Returns
     (tokens [B, steps], logits per step or [])."""
     atts = attention_layers(model)
     B = tok.shape[0]
@@ -491,15 +494,19 @@ def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = Tru
         if keep_logits:
             logits.append(logit_buf.clone())
         toks.append(tok_buf.clone())
+        if on_step is not None:
+            on_step(0)
         if steps > 1:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 step()
-            for _ in range(steps - 1):
+            for i in range(1, steps):
                 graph.replay()
                 if keep_logits:
                     logits.append(logit_buf.clone())
                 toks.append(tok_buf.clone())
+                if on_step is not None:
+                    on_step(i)
     finally:
         for att in atts:
             att.graph = None

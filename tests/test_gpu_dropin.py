@@ -153,3 +153,39 @@ def test_attention_module_prefill_then_decode(Hq, Hkv, r, Rv, dtype):
         check_output(outs[0], ref[:, :P], "module prefill output: ")
         for i, t in enumerate(range(P, P + n_dec)):
             check_output(outs[1 + i], ref[:, t:t + 1], f"module decode t={t} output: ")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,S", [(4, 1024), (1, 262144)])
+def test_abx_reference_check_and_bench_shape(B, S):
+    """The reference's own abx shapes (abx_rope_batched.py:254-280): total
+    rank int(0.2 * 4096) = 819 over 32 query heads in KV groups of 4, i.e.
+    8 KV heads of rank 819 // 8 = 102 (not a multiple of 8), fp16; b passed
+    with one row per query head as the check does ([32, 102, 128], rows
+    q // 4 read).  B4 S1024 is the check (run_test, 254-270); B1 S262144 the
+    longest benchmark context (target_seq_lens, 280), checked on 2048 sampled
+    positions (each logit depends on its own position only)."""
+    from oracle import starkv_oracle as o
+    from starkv import RopeConfig
+    from starkv.abx_rope_batched import abx
+    Hq, gs = 32, 4
+    Hkv, r = Hq // gs, int(4096 * 0.2) // (Hq // gs)
+    assert r == 102
+    _flush(f"[abx reference shape] B={B} S={S} Hq={Hq} Hkv={Hkv} r={r} fp16")
+    g = torch.Generator(device="cuda").manual_seed(13)
+    a = torch.randn(B, Hq, 1, HEAD, generator=g, device="cuda").half()
+    b = (torch.randn(Hq, r, HEAD, generator=g, device="cuda") / math.sqrt(r)).half()
+    x = torch.randn(B, Hkv, S, r, generator=g, device="cuda").half()
+    out = abx(a, b, x, dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert out.shape == (B, Hq, 1, S) and out.dtype == torch.float16
+    rope = RopeConfig()
+    if S <= 4096:
+        pos = torch.arange(S)
+    else:
+        pos = torch.cat([torch.arange(32), torch.randperm(S - 64, generator=torch.Generator().manual_seed(1))[:1984] + 32,
+                         torch.arange(S - 32, S)]).sort().values
+    cos, sin = o.rope_cos_sin(rope.inv_freq(), pos, rope.attention_scaling)
+    ref = o.k_logits(a[:, :, 0].cpu(), [b[h].cpu() for h in range(Hkv)],
+                     [x[:, h, pos.cuda()].cpu() for h in range(Hkv)], cos, sin, scale=1.0)
+    check_logits(out[:, :, 0, pos.cuda()], ref, 1.0, "fp16 out: ")

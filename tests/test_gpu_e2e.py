@@ -157,3 +157,39 @@ def test_e2e_decode_over_exported_ragged_projections(fmt):
         toks, logits = e2e.generate(model, prompt, steps)
     assert rec.check() == 2 * (steps + 1)
     assert all(torch.isfinite(x).all() for x in logits)
+
+
+def test_e2e_graphed_decode_cfg5_layer_matches_oracle():
+    """The path the e2e tok/s times: decode steps replayed from one captured
+    graph, each attention over the whole cache capacity under the device mask
+    (the not yet written positions at -1e30), at the e2e workload's layer
+    shape (hidden 4096, MHA 32 x 128, cfg2 ranks int8 K, V rank 1640 int4
+    group-64) with capacity past the length.  Every layer's attention output
+    of every step -- the eager first step and each replay, whose recorded
+    buffers the replay rewrites -- is checked against the fp64 oracle over
+    the caches as they stand after that step."""
+    import starkv.e2e as e2e
+    L, B, P, steps = 2, 2, 200, 4
+    cap = P + steps + 5
+    _flush(f"[e2e graphed cfg5 layers] layers={L} B={B} prompt={P} steps={steps} capacity={cap}")
+    model = e2e.build_model(n_layers=L, hidden=4096, heads=32, kv_heads=32, intermediate=11008, vocab=32000,
+                            ranks=cfg2_ranks(), v_rank=1640, batch=B, capacity=cap, fmt="int8_g64", seed=7)
+    prompt = torch.randint(0, 32000, (B, P), generator=torch.Generator(device="cuda").manual_seed(8), device="cuda")
+    checked = []
+    with torch.no_grad():
+        out = model(input_ids=prompt, position_ids=torch.arange(P, device="cuda")[None].expand(B, P),
+                    use_cache=False, logits_to_keep=1)
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        with KernelRecorder(e2e) as rec:
+            def on_step(i):
+                calls = rec.calls[-L:]
+                assert len(calls) == L and all(c["kind"] == "decode" and c["S"] == cap and c["mask"] is not None
+                                               for c in calls)
+                view = KernelRecorder(e2e)
+                view.calls = calls
+                _flush(f"   step {i} ({'eager' if i == 0 else 'replay'}), position {P + i}")
+                checked.append(view.check())
+            toks, _ = e2e.decode_graphed(model, tok, steps, keep_logits=False, on_step=on_step)
+    assert toks.shape == (B, steps)
+    assert checked == [L] * steps
+    assert all(layer.self_attn.cache.length == P + steps for layer in model.model.layers)

@@ -180,20 +180,29 @@ def test_prefill_last_row_matches_decode():
 
 
 @pytest.mark.gpu
-def test_prefill_e2e_shape_sampled_rows():
-    """The e2e workload's prefill layer at full prompt length: 8192 tokens,
-    MHA 32 x 128, the cfg2 ragged K ranks (sum 1640) as int8 per (b, h, s),
-    V rank 1640 as int4 group-64, fp16, batch 2.  The whole prompt runs on the
-    GPU; sampled query rows are checked against the oracle's decode step over
-    the first t + 1 positions (a prefill row is that decode step: pinned on
-    the CPU by the oracle's chunk / last-row identities)."""
+@pytest.mark.parametrize("B,T", [(2, 8192), (1, 16384), (1, 32768)])
+def test_prefill_e2e_shape_sampled_rows(B, T):
+    """The e2e workload's prefill layer at full prompt length (8192 tokens)
+    and at the longer contexts the reference's e2e sweep reaches (latency.py:
+    353-357): MHA 32 x 128, the cfg2 ragged K ranks (sum 1640) as int8 per
+    (b, h, s), V rank 1640 as int4 group-64, fp16.  The whole prompt runs on
+    the GPU; sampled query rows are checked against the oracle's prefill of
+    that row alone (pos0 = t: the decode step over the first t + 1 positions,
+    pinned on the CPU by the oracle's chunk / last-row identities) as the
+    reference computes it for an fp16 model: cos / sin cast to fp16 (HF's
+    rotary embedding returns them in the activations' dtype) and K, V
+    materialised in fp16 (model.py:431-442), then fp64 attention.  The error
+    against fp32 cos / sin with fp64 K, V is printed beside it: those two
+    fp16 roundings, which the reference shares, put ~7e-4 mean-rel between
+    the two oracles at 16K positions (CPU emulation of the kernel's steps:
+    7e-5 from the first, 7.6e-4 from the second)."""
     from oracle import starkv_oracle as o
     from starkv import KLatentSpec, RopeConfig, prefill_attention
     from starkv._lib import FMT_INT8_SYM
     from test_gpu_quant import make_quant_v
     from test_gpu_quant_k import ragged_int8_k
     from _util import cfg2_ranks
-    B, T, Rv = 2, 8192, 1640
+    Rv = 1640
     ranks = cfg2_ranks()
     Hkv = Hq = len(ranks)
     _flush(f"[prefill e2e shape] B={B} T={T} Hq={Hq} ranks sum {sum(ranks)} int8 K, Rv={Rv} g64 V")
@@ -214,8 +223,13 @@ def test_prefill_e2e_shape_sampled_rows():
     xv = torch.from_numpy(deq_v.astype(np.float64))
     bk = [b.double().cpu() for b in bk_heads]
     uvd = uv.double().cpu()
-    for b, t in [(0, 0), (1, 1), (0, 777), (1, 4095), (0, 6000), (1, T - 1)]:
+    for b, t in [(0, 0), (B - 1, 1), (0, 777), (B - 1, 4095), (0, T // 2 + 17), (B - 1, T - 1)]:
         S = t + 1
-        ref, _, _ = o.decode_attention(q[b:b + 1, :, t].double().cpu(), bk, [x[b:b + 1, :S] for x in deq_k],
-                                       xv[b:b + 1, :S], uvd, cos.double(), sin.double())
-        check_output(out[b:b + 1, :, t], ref, f"b={b} t={t}: ")
+        qt = q[b:b + 1, :, t:t + 1].double().cpu()
+        xks = [x[b:b + 1, :S] for x in deq_k]
+        ref64 = o.prefill_attention(qt, bk, xks, xv[b:b + 1, :S], uvd, cos.double()[:S], sin.double()[:S], pos0=t)
+        mx64, mr64 = errors(out[b:b + 1, :, t], ref64[:, :, 0])
+        _flush(f"   b={b} t={t}: against fp64 K / V: max_abs={mx64:.3e} mean_rel={mr64:.3e}")
+        ref = o.prefill_attention(qt, bk, xks, xv[b:b + 1, :S], uvd, cos.half().double()[:S],
+                                  sin.half().double()[:S], pos0=t, kv_dtype=torch.float16)
+        check_output(out[b:b + 1, :, t], ref[:, :, 0], f"b={b} t={t} (fp16 cos / sin, K, V: the reference's): ")
