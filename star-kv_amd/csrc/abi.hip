@@ -463,7 +463,7 @@ int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArg
       max_chunks = std::max(max_chunks, chunks);
     }
     a.ws_stage = (int)round_up(max_chunks, 64) * 16 + 8192 + (a.ws_i8 ? 1024 : 0);
-    a.ws_nst = gqa ? std::min(6, K1_GQ_RING_BYTES / a.ws_stage) : std::min(4, K1_WS_RING_BYTES / a.ws_stage);
+    a.ws_nst = gqa ? std::min(6, K1_GQ_RING_BYTES / a.ws_stage) : std::min(4, (a.ws_i8 ? K1_WS_RING_I8_BYTES : K1_WS_RING_BYTES) / a.ws_stage);
   }
   return STARKV_OK;
 }
@@ -504,8 +504,11 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
   PVGeom g;
   g.Rvp = (int)round_up(Rv, 32);
   const int ntw = pv_tiles_per_wave(g.Rvp, fused, vq);
-  g.n_cb = (int)ceil_div(g.Rvp / 32, 4 * ntw);
-  const int wg_per_cu = pv_wg_per_cu(ntw, vq);
+  // one 8-wave workgroup for all columns (its 24-bit row offsets need
+  // every pitch below 16 MB)
+  const bool wide = pv_wide_tiles(g.Rvp, fused, vq) > 0 && row_bytes < V_MAX_PITCH;
+  g.n_cb = wide ? 1 : (int)ceil_div(g.Rvp / 32, 4 * ntw);
+  const int wg_per_cu = wide ? 1 : pv_wg_per_cu(ntw, vq);
   const int n_ks = (int)ceil_div(S, KSTEP);
   // each extra split writes and re-reads one fp32 partial of 32 x Rvp per
   // column block, against the X_v bytes and logits the split streams

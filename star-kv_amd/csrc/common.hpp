@@ -29,7 +29,8 @@ constexpr int K_MAXI = 4;          // items per wave (upper bound over kernel va
 constexpr int K_MAX_WAVES = 64;    // waves in one batch's plan
 constexpr int K_MAX_KV = 64;
 constexpr int K_MAX_QH = 64;
-constexpr int K1_WS_RING_BYTES = 163840 - 1024;   // warp-specialised K-logit LDS ring (+ 1 KB carry)
+constexpr int K1_WS_RING_BYTES = 163840 - 1024;      // warp-specialised K-logit LDS ring (+ 1 KB carry)
+constexpr int K1_WS_RING_I8_BYTES = 163840 - 1536;   // the same for int8 latents (+ 1.5 KB carry)
 
 // item word: qhead[0:8) kv[8:16) mtile[16:20) nvalid[20:26) last_of_q[26] valid[27]
 __host__ __device__ inline uint32_t item_pack(int qh, int kv, int mt, int nv, int last) {
@@ -409,6 +410,7 @@ int launch_k_logits_ws(const KArgs& a, int dtype, bool out_f32, int out_dtype, i
 int launch_k_logits_gqa(const KArgs& a, int dtype, bool out_f32, int out_dtype, int B, hipStream_t st);
 int launch_pv(const PVArgs& a, int dtype, int vq, bool fused, bool fast, int B, hipStream_t st);
 int pv_tiles_per_wave(int Rvp, bool fused, int vq);   // column tiles (of 32 ranks) per P.V wave
+int pv_wide_tiles(int Rvp, bool fused, int vq);       // > 0: the 8-wave all-columns kernel, tiles per wave
 // P.V workgroups resident per CU (the kernel's register budget): the wide
 // dense variants (8 and 13 tiles) take one, the others two
 constexpr int pv_wg_per_cu(int ntw, int vq) { return ntw >= 8 && vq == VQ_DENSE ? 1 : 2; }

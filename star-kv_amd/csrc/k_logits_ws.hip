@@ -130,6 +130,26 @@ __device__ inline void dot_piece(const uint4& u0, const uint4& u1, const floatx1
 
 #define WS_FENCE() __builtin_amdgcn_sched_barrier(0)
 
+// int8 latents: the 16 bytes of a lane with the sign bit flipped (n + 128,
+// unsigned) and the fp16 scale broadcast to both halves
+__device__ inline uint4 i8_bias(uint4 r) {
+  return make_uint4(r.x ^ 0x80808080u, r.y ^ 0x80808080u, r.z ^ 0x80808080u, r.w ^ 0x80808080u);
+}
+__device__ inline kh2 i8_scale(uint16_t s16) { return __builtin_bit_cast(kh2, (uint32_t)s16 * 0x10001u); }
+
+// piece k of an int8 dot: ranks 2k, 2k+1 of the lane's 16 (bytes 2k, 2k+1 of
+// w = i8_bias(latent)) dequantised bit-exactly, fp16(n * s) as in dequant16,
+// times accumulator rows 2k, 2k+1 into p[(2k) & 3], p[(2k+1) & 3]: pieces
+// 0..7 in order are the sums of dequant16 + dot16h
+__device__ inline void i8_piece(const uint4& w, kh2 s, const floatx16& acc, int k, float p[4]) {
+  const uint32_t u = (k >> 1) == 0 ? w.x : (k >> 1) == 1 ? w.y : (k >> 1) == 2 ? w.z : w.w;
+  const uint32_t pr = __builtin_amdgcn_perm(0x64646464u, u, (k & 1) ? 0x04030402u : 0x04010400u);
+  const kh2 b2 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  const kh2 h = (__builtin_bit_cast(kh2, pr) + b2) * s;
+  p[(2 * k) & 3] = fmaf((float)h[0], acc[2 * k], p[(2 * k) & 3]);
+  p[(2 * k + 1) & 3] = fmaf((float)h[1], acc[2 * k + 1], p[(2 * k + 1) & 3]);
+}
+
 }  // namespace
 
 // OUTK: 0 = fp32 logits + chunk maxima, 1 = fp16 logits, 2 = bf16 logits
@@ -142,8 +162,9 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
   constexpr int NCONS = ws_consumers<XI8>();
   constexpr int MAXI = XI8 ? 2 : 4;                  // items per consumer wave
   constexpr bool XB = !XI8 && !__is_same(XT, _Float16);   // bf16 latents
-  __shared__ __attribute__((aligned(16))) char ring[WS_RING];   // a.ws_nst stages of a.ws_stage bytes
-  __shared__ float carry[2][WS_BINS][32];            // straddling heads: first half's partial logits
+  constexpr int RING = XI8 ? K1_WS_RING_I8_BYTES : WS_RING;
+  __shared__ __attribute__((aligned(16))) char ring[RING];   // a.ws_nst stages of a.ws_stage bytes
+  __shared__ float carry[XI8 ? 3 : 2][WS_BINS][32];  // straddling heads: first half's partial logits
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -189,7 +210,7 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
   const int nX = (tot + 63) / 64, stage = a.ws_stage, nst = a.ws_nst;
   constexpr int SCB = XI8 ? 1024 : 0;
   const int sc_off = stage - 8192 - SCB;
-  if (tot == 0 || nX * 1024 + SCB + 8192 > stage || nst < 2 || nst * stage > WS_RING) return;   // uniform
+  if (tot == 0 || nX * 1024 + SCB + 8192 > stage || nst < 2 || nst * stage > RING) return;   // uniform
 
   if (wave >= NCONS) {
     // ================= producer =================
@@ -386,10 +407,9 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
   };
   // the first head of a receiving wave ends at its item j0
   const int j0 = item_last(it[0]) ? 0 : 1;
-  float pend = 0.f;                          // receiving wave: own partial of the previous tile
 
+  if constexpr (!XI8) {
   for (int i = 0; i < ntl; ++i) {
-    if constexpr (!XI8) {
     __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS reads are done
     __builtin_amdgcn_s_barrier();
     if (!item_valid(it[0])) continue;
@@ -442,63 +462,114 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
         emit(v, item_qh(it[j]), s, mx[j]);
       }
     }
-    } else {
-    __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS reads and writes are done
-    __builtin_amdgcn_s_barrier();
-    if (!item_valid(it[0])) continue;
-    if (recv && i > 0)
-      emit(pend + carry[(i - 1) & 1][bin][t], item_qh(it[j0]), (tile0 + i - 1) * TILE + t, mx[j0]);
-    const char* st = ring + (i % nst) * stage;
-    const int s = (tile0 + i) * TILE + t;
-    half8 T[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) T[k] = *(const half8*)(st + stage - 8192 + (k * 64 + lane) * 16);
-    // both chains every tile (an unused item has zero W rows and reads valid
-    // LDS data), interleaved so the MFMA pipe stays busy
-    uint4 x0[MAXI], x1[MAXI];
-    uint16_t sc[MAXI];
-#pragma unroll
-    for (int j = 0; j < MAXI; ++j) {
-      x0[j] = *(const uint4*)(st + xo0[j]);
-      x1[j] = XI8 ? x0[j] : *(const uint4*)(st + xo1[j]);
-      sc[j] = XI8 ? *(const uint16_t*)(st + sco[j]) : 0;
-    }
-    floatx16 acc[MAXI];
-#pragma unroll
-    for (int j = 0; j < MAXI; ++j) acc[j] = mfma_f16(wr[j][0], T[0], floatx16{});
-#pragma unroll
-    for (int k = 1; k < 8; ++k)
-#pragma unroll
-      for (int j = 0; j < MAXI; ++j) acc[j] = mfma_f16(wr[j][k], T[k], acc[j]);
-    float part = 0.f;
-#pragma unroll
-    for (int j = 0; j < MAXI; ++j) {
-      if constexpr (XI8) {
-        uint4 lo, hi;
-        dequant16(x0[j], true, sc[j], lo, hi);
-        part += dot16h(lo, hi, acc[j]);
-      } else if constexpr (__is_same(XT, _Float16)) {
-        part += dot16h(x0[j], x1[j], acc[j]);
-      } else {
-        part += dot16b(x0[j], x1[j], acc[j]);
-      }
-      if (item_last(it[j])) {
-        const float v = add_halves(part);
-        part = 0.f;
-        if (recv && j == j0) pend = v;
-        else emit(v, item_qh(it[j]), s, mx[j]);
-      }
-    }
-    if (send) {
-      const float v = add_halves(part);
-      if (hh == 0) carry[i & 1][bin][t] = v;
-    }
-      }
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();              // publishes the last tile's partials
-  if (recv && item_valid(it[0]))
-    emit(pend + carry[(ntl - 1) & 1][bin][t], item_qh(it[j0]), (tile0 + ntl - 1) * TILE + t, mx[j0]);
+  __builtin_amdgcn_s_barrier();              // the producers' extra barrier
+  } else {
+    // int8: the MFMA chains of tile i carry the dequantisation and dot
+    // products of the item before in (tile, item) order,
+    //     chain (i, 0) || pieces of (i-1, 1),   chain (i, 1) || pieces of (i, 0),
+    // so each chain's VALU work runs under the MFMA pipe of the same wave (the
+    // per-tile barrier keeps the two consumer waves of a SIMD in phase: one
+    // wave's VALU work does not hide under the other's MFMAs).  Item 1 of the
+    // last tile is finished after the loop.  Straddling heads: the sending
+    // wave writes tile k's partials during tile k+1 (after the loop for the
+    // last tile) into carry slot k % 3; the receiving wave adds them to its
+    // own part after the barrier of tile k+2 (after the final barrier for the
+    // last two tiles), holding its parts in a two-tile shift register (qn
+    // newest, qo older).  Three slots: within one barrier interval the
+    // receiver reads tile k's slot while the sender writes tile k+1's and,
+    // after the loop, tile k+2's.
+    const bool v0 = item_valid(it[0]);
+    floatx16 accp = floatx16{};              // accumulators of item (i-1, 1)
+    uint4 wp = make_uint4(0, 0, 0, 0);       // its latent bytes ^ 0x80 and scale
+    kh2 sp = kh2{};
+    float hold = 0.f;                        // item 0's part of a head that continues into item 1
+    float qn = 0.f, qo = 0.f;
+    auto fin0 = [&](float d, int s) __attribute__((always_inline)) {
+      if (item_last(it[0])) {
+        const float v = add_halves(d);
+        if (recv && j0 == 0) qn = v;
+        else emit(v, item_qh(it[0]), s, mx[0]);
+      } else {
+        hold = d;
+      }
+    };
+    auto fin1 = [&](float d, int s, int slot) __attribute__((always_inline)) {
+      if (!item_valid(it[1])) return;
+      const float v = add_halves((item_last(it[0]) ? 0.f : hold) + d);
+      if (item_last(it[1])) {
+        if (recv && j0 == 1) qn = v;
+        else emit(v, item_qh(it[1]), s, mx[1]);
+      } else if (send && hh == 0) {
+        carry[slot][bin][t] = v;
+      }
+    };
+    for (int i = 0; i < ntl; ++i) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);    // this wave's LDS reads and writes are done
+      __builtin_amdgcn_s_barrier();
+      if (!v0) continue;
+      if (recv) {
+        if (i >= 2) emit((j0 ? qn : qo) + carry[(i - 2) % 3][bin][t], item_qh(it[j0]), (tile0 + i - 2) * TILE + t, mx[j0]);
+        qo = qn;
+      }
+      const char* st = ring + (i % nst) * stage;
+      const int s = (tile0 + i) * TILE + t;
+      half8 T[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) T[k] = *(const half8*)(st + stage - 8192 + (k * 64 + lane) * 16);
+      uint4 xn[MAXI];
+      uint16_t scn[MAXI];
+#pragma unroll
+      for (int j = 0; j < MAXI; ++j) {
+        xn[j] = *(const uint4*)(st + xo0[j]);
+        scn[j] = *(const uint16_t*)(st + sco[j]);
+      }
+      // an unused item has zero W rows and reads valid LDS data; at i = 0 the
+      // pieces of chain 0 work on zeros and are discarded
+      float p[4] = {0.f, 0.f, 0.f, 0.f};
+      floatx16 acc0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc0 = mfma_f16(wr[0][k], T[k], k == 0 ? floatx16{} : acc0);
+        WS_FENCE();
+        i8_piece(wp, sp, accp, k, p);
+        asm volatile("" :: "v"(p[(2 * k) & 3]), "v"(p[(2 * k + 1) & 3]));
+        WS_FENCE();
+      }
+      if (i > 0) fin1((p[0] + p[1]) + (p[2] + p[3]), s - TILE, (i - 1) % 3);
+      const uint4 w0 = i8_bias(xn[0]);
+      const kh2 s0 = i8_scale(scn[0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[e] = 0.f;
+      floatx16 acc1;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc1 = mfma_f16(wr[1][k], T[k], k == 0 ? floatx16{} : acc1);
+        WS_FENCE();
+        i8_piece(w0, s0, acc0, k, p);
+        asm volatile("" :: "v"(p[(2 * k) & 3]), "v"(p[(2 * k + 1) & 3]));
+        WS_FENCE();
+      }
+      fin0((p[0] + p[1]) + (p[2] + p[3]), s);
+      accp = acc1;
+      wp = i8_bias(xn[1]);
+      sp = i8_scale(scn[1]);
+    }
+    if (v0) {
+      float p[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) i8_piece(wp, sp, accp, k, p);
+      if (recv && j0 == 1) qo = qn;
+      fin1((p[0] + p[1]) + (p[2] + p[3]), (tile0 + ntl - 1) * TILE + t, (ntl - 1) % 3);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();            // publishes the last two tiles' partials
+    if (recv && v0) {
+      if (ntl >= 2) emit(qo + carry[(ntl - 2) % 3][bin][t], item_qh(it[j0]), (tile0 + ntl - 2) * TILE + t, mx[j0]);
+      emit(qn + carry[(ntl - 1) % 3][bin][t], item_qh(it[j0]), (tile0 + ntl - 1) * TILE + t, mx[j0]);
+    }
+  }
   if constexpr (OUTK == 0) {
     if (a.chunkmax != nullptr) {
 #pragma unroll

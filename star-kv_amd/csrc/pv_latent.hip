@@ -42,6 +42,7 @@ namespace starkv {
 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_fp16x4;
 
 constexpr int PV_QDEPTH = 2;   // quantised latents: K-steps loaded ahead
+constexpr int PV_WDEPTH = 3;   // the all-columns kernel: register stages of its software pipeline
 
 __device__ inline uint2 lds_read_tr16(const uint16_t* p) {
   auto r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) lds_fp16x4*)(p));
@@ -72,9 +73,10 @@ __device__ inline uint32_t as_u32(h2v h) { return __builtin_bit_cast(uint32_t, h
 // the bytes are int8 (x, y), else eight int4 nibbles in x, rank 2k in the low
 // nibble of byte k.  Ranks in order (0..7), except group-64 int4: ranks
 // 0 2 4 6 1 3 5 7 (pv_g64_rank maps an LDS column back to its rank).
+// s2, z2: the fp16 scale / zero-point bits in both halves of a dword
 template <int VQ>
-__device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16) {
-  const h2v s = as_h2((uint32_t)s16 * 0x10001u);
+__device__ inline uint4 dequant8(uint2 q, bool kind8, uint32_t s2, uint32_t z2) {
+  const h2v s = as_h2(s2);
   uint32_t pr[4];
   _Float16 bias;
   if (VQ == VQ_BLOCK && kind8) {
@@ -109,7 +111,7 @@ __device__ inline uint4 dequant8(uint2 q, bool kind8, uint16_t s16, uint16_t z16
   for (int k = 0; k < 4; ++k) {
     const h2v n = as_h2(pr[k] | ebyte) + b2;                           // exact small integers
     if constexpr (VQ == VQ_G64) {
-      const h2v zz = as_h2((uint32_t)z16 * 0x10001u);
+      const h2v zz = as_h2(z2);
       o[k] = as_u32(__builtin_elementwise_fma(n, s, zz));
     } else {
       o[k] = as_u32(n * s);
@@ -355,7 +357,8 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
       } else if constexpr (VQ == VQ_DENSE) {
         *(uint4*)&sbuf[soff[c]] = st.r[c];
       } else {
-        uint4 h = dequant8<VQ>(st.q[c], q8[c], st.s[c], VQ == VQ_G64 ? st.z[VQ == VQ_G64 ? c : 0] : (uint16_t)0);
+        uint4 h = dequant8<VQ>(st.q[c], q8[c], (uint32_t)st.s[c] * 0x10001u,
+                               VQ == VQ_G64 ? (uint32_t)st.z[VQ == VQ_G64 ? c : 0] * 0x10001u : 0u);
         if constexpr (__is_same(VT, __bf16)) h = f16x8_to_bf16x8(h);
         *(uint4*)&sbuf[soff[c]] = h;
       }
@@ -482,6 +485,313 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   }
 }
 
+// Fused quantised P.V over all columns of the V latent in one workgroup.
+//
+// 8 waves split the column tiles (NTW each, Rvp <= 8 * NTW * 32), so a
+// K-step's logits and scale / zero rows are fetched once per (chunk, batch,
+// head group) instead of once per column block (blocks of one chunk run on
+// different XCDs, each fetching them through its own L2), and the K-step's
+// 32 x 16 exponentials are formed once instead of by every wave: thread
+// (eh, head en, ee) forms P[en][8 eh + ee] and writes it into a
+// double-buffered LDS A operand that every wave reads with one 16-byte load
+// (the A layout of pv_kernel: lane (n, hh) holds positions 8 hh .. 8 hh + 7 of
+// head n).  The K-step's scale / zero rows take the same route (at most two
+// 16-bit loads per thread), so the global loads of a wave are its packed
+// bytes.  Buffers of K-step ks+1 are written while K-step ks computes; one
+// barrier per K-step publishes them.  X_v slabs stay wave-private as in
+// pv_kernel (dequantised by the loading lane, read back transposed).
+template <int NTW>
+struct PVWStage {
+  uint2 q[8];          // packed bytes of the lane's 8 chunks (int4: .x)
+  float p;             // the thread's logit
+  uint16_t sz[2];      // the thread's scale / zero items
+};
+
+template <typename VT, int NTW, bool FAST, int VQ>
+__global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
+  constexpr int NWV = 8, DEPTH = PV_WDEPTH;
+  constexpr int PITCH = NTW * 32 + 8;            // elements per staged row (16-byte pad)
+  constexpr int STAGE = 16 * PITCH;              // elements per staged K-step
+  constexpr int CPR = NTW * 4;                   // 8-rank chunks per staged row
+  constexpr bool BF = __is_same(VT, __bf16);
+  constexpr int NA = BF ? 2 : 1;                 // A operand pieces (bf16: high and low parts)
+  static_assert(VQ != VQ_DENSE, "quantised latents only");
+  __shared__ __attribute__((aligned(16))) uint16_t stage[NWV][2][STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t Ash[2][NA][512];   // [buf][piece][eh][en][ee]
+  __shared__ uint32_t Ssh[2][2][16][32];         // [buf][scale | zero][row][group or block], bits in both halves
+  __shared__ float Ms[32];
+  __shared__ float Ps2[2][32];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hh = lane >> 5;
+  const int c2 = blockIdx.x, bq = blockIdx.y;
+  const int b = bq / a.n_hg, h0 = (bq - b * a.n_hg) * 32;    // batch, first head of the group
+  const int tile0 = wave * NTW;                               // first 32-column tile of this wave
+  const int nvt = max(0, min(NTW, a.Rvp / 32 - tile0));       // valid tiles (wave-uniform)
+  const int col0 = tile0 * 32;
+  const int H = a.H;
+  const int eh = tid >> 8, en = (tid >> 3) & 31, ee = tid & 7;
+
+  if (tid < 256) {
+    const int q = tid >> 3, j = tid & 7;
+    float m = -INFINITY;
+    if (h0 + q < H)
+      for (int c = j; c < a.n_chunk1; c += 8) m = fmaxf(m, a.chunkmax[((int64_t)b * H + h0 + q) * a.n_chunk1 + c]);
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    if (j == 0) Ms[q] = h0 + q < H ? m : 0.f;
+  }
+  __syncthreads();
+  const float MqL = -Ms[en] * 1.4426950408889634f;   // exp(l - M) = exp2(l * log2(e) - M * log2(e))
+  const bool eok = h0 + en < H;
+
+  const int s_begin = c2 * a.c2_len;
+  const int s_end = min(a.S, s_begin + a.c2_len);
+  const int nks = (s_end - s_begin + KSTEP - 1) / KSTEP;
+  const int rmax = s_end - 1 - s_begin;                        // last valid row of the chunk
+
+  floatx16 acc[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) acc[j] = floatx16{};
+  float psum = 0.f;
+
+  // ---- per-lane chunk map: lane (n, hh) takes the 8-rank column chunk n of
+  // the wave's slab in rows 2c + hh, c = 0..7 (NCH chunks).  One load
+  // instruction then reads 4*CPR contiguous bytes of each of two rows, and
+  // the lane's column, scale group and slab offset are the same for every
+  // chunk.  Lanes past the slab (n >= CPR) load column 0 and store into the
+  // row's pad, which is never read.
+  constexpr int NCH = 8;
+  const int c16 = min(n, CPR);
+  const int gcol = col0 + c16 * 8;
+  const bool cok = n < CPR && c16 / 4 < nvt && gcol < a.Rv;
+  const bool qlo = VQ == VQ_BLOCK && gcol >= a.split;
+  const bool q8 = VQ == VQ_BLOCK && !qlo && a.a_int8;
+  const int qoff = !cok ? 0 : qlo ? (gcol - a.split) / 2 : (q8 ? gcol : gcol / 2);
+  // scale column of the chunk in the staged rows: group-64 int4 its group,
+  // block formats its block (0 upper, 1 lower)
+  const int qsel = VQ == VQ_G64 ? min(gcol / 64, 31) : (qlo ? 1 : 0);
+  const int soff0 = hh * PITCH + c16 * 8;          // slab offset of chunk 0 (row hh)
+  const uint8_t* xq = (const uint8_t*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
+  const uint8_t* xq2 = (const uint8_t*)a.x2 + b * a.x2_sb + (int64_t)s_begin * a.x2_ss;
+  // Offsets from a stream's first row of the chunk are 32-bit, rows by a
+  // 24-bit multiply: the host takes this kernel only when every row pitch is
+  // below 16 MB, and keeps a chunk below 2 GB.  (64-bit row products cost
+  // quarter-rate multiplies per chunk and K-step.)
+  const uint32_t xp = (uint32_t)a.x_ss, xp2 = (uint32_t)a.x2_ss;
+
+  // ---- scale / zero items of a K-step: nsz per row (group-64: ng scales then
+  // ng zero points; block formats: the upper block's scale, the lower's);
+  // thread item f = row * nsz + k for f = tid, tid + 512
+  const int ng = VQ == VQ_G64 ? (a.Rv + 63) / 64 : 0;
+  const int nsz = VQ == VQ_G64 ? 2 * ng : (a.split < a.Rv ? 2 : 1);
+  int zrow[2], zsel[2], zg[2];
+  bool zok[2];
+  const uint16_t* zsrc[2];
+  uint32_t zpitch[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int f0 = tid + 512 * u;
+    zok[u] = f0 < 16 * nsz;
+    const int f = min(f0, 16 * nsz - 1);
+    zrow[u] = f / nsz;
+    const int k = f % nsz;
+    if constexpr (VQ == VQ_G64) {
+      zsel[u] = k >= ng;
+      zg[u] = k - zsel[u] * ng;
+      zsrc[u] = (const uint16_t*)(zsel[u] ? a.xz : a.xs) + b * a.xs_sb + (int64_t)s_begin * a.xs_ss + zg[u];
+      zpitch[u] = (uint32_t)a.xs_ss;
+    } else {
+      zsel[u] = 0;
+      zg[u] = k;
+      zsrc[u] = k ? (const uint16_t*)a.xs2 + b * a.xs2_sb + (int64_t)s_begin * a.xs2_ss
+                  : (const uint16_t*)a.xs + b * a.xs_sb + (int64_t)s_begin * a.xs_ss;
+      zpitch[u] = (uint32_t)(k ? a.xs2_ss : a.xs_ss);
+    }
+  }
+  const float* lrow = a.logits + b * a.l_sb + min(h0 + en, H - 1) * a.l_sh;
+
+  // Every load is issued from a clamped, in-bounds address (K-steps past the
+  // chunk re-read its last K-step, rows past s_end its last row, chunks past
+  // the slab column 0); those values meet P = 0 or discarded columns only.
+  // The logit and the scale / zero items go first: they are consumed one
+  // K-step before the packed bytes of the same stage.
+  auto load = [&](PVWStage<NTW>& st, int ks) {
+    const int kc = min(ks, nks - 1);
+    // the logits buffer holds S_pad >= round_up(s_end, 16) positions
+    const int sa = s_begin + kc * KSTEP + 8 * eh + ee;
+    st.p = lrow[__umul24((uint32_t)(sa >> 5), (uint32_t)a.l_st) + (uint32_t)(sa & 31)];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) st.sz[u] = zsrc[u][__umul24((uint32_t)min(kc * KSTEP + zrow[u], rmax), zpitch[u])];
+    const bool lo = VQ == VQ_BLOCK && cok && qlo;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const uint32_t r = (uint32_t)min(kc * KSTEP + 2 * c + hh, rmax);
+      if (FAST) {
+        // one unsigned 32-bit offset from the stream's (uniform) base
+        const uint32_t o = (lo ? __umul24(r, xp2) : __umul24(r, xp)) + (uint32_t)qoff;
+        const uint8_t* base = lo ? xq2 : xq;
+        st.q[c].x = *(const uint32_t*)(base + o);
+        st.q[c].y = (VQ == VQ_BLOCK && q8) ? *(const uint32_t*)(base + (o + 4u)) : 0u;
+      } else {
+        const uint8_t* rowp = lo ? xq2 + __umul24(r, xp2) : xq + __umul24(r, xp);
+        // rows of any alignment and length; bytes past the row land only in
+        // output columns >= Rv, which are discarded
+        if constexpr (VQ == VQ_BLOCK) {
+          uint32_t w[2];
+          ld_row_bytes<8>(rowp, qoff, lo ? a.x2nb : a.xnb, w);
+          st.q[c] = make_uint2(w[0], w[1]);
+        } else {
+          uint32_t w[1];
+          ld_row_bytes<4>(rowp, qoff, a.xnb, w);
+          st.q[c] = make_uint2(w[0], 0u);
+        }
+      }
+    }
+  };
+
+  // the exponentials of K-step ks (logits loaded with st) into Ash[ks & 1]
+  auto publish_p = [&](const PVWStage<NTW>& st, int ks) {
+    const int buf = ks & 1;
+    const int sp = s_begin + ks * KSTEP + 8 * eh + ee;
+    // computed for every thread and selected (logits past s_end are other
+    // chunks' or unwritten workspace)
+    const float ex = __builtin_amdgcn_exp2f(fmaf(st.p, 1.4426950408889634f, MqL));
+    const float pv = (eok && sp < s_end) ? ex : 0.f;
+    psum += pv;
+    if constexpr (BF) {
+      const __bf16 hi = (__bf16)pv;
+      Ash[buf][0][tid] = __builtin_bit_cast(uint16_t, hi);
+      Ash[buf][NA - 1][tid] = __builtin_bit_cast(uint16_t, (__bf16)(pv - (float)hi));
+    } else {
+      Ash[buf][0][tid] = __builtin_bit_cast(uint16_t, (_Float16)pv);
+    }
+  };
+  // the scale / zero items of K-step ks (loaded with st) into Ssh[ks & 1]
+  auto publish_sz = [&](const PVWStage<NTW>& st, int ks) {
+    const int buf = ks & 1;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (zok[u]) Ssh[buf][zsel[u]][zrow[u]][zg[u]] = (uint32_t)st.sz[u] * 0x10001u;
+  };
+  // K-step ks's packed bytes (in st) dequantised with the scales in
+  // Ssh[ks & 1] into the wave's slab ks & 1
+  auto dequant = [&](const PVWStage<NTW>& st, int ks) {
+    const int buf = ks & 1;
+    uint16_t* sbuf = &stage[wave][buf][0];
+    uint32_t s2[NCH], z2[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      s2[c] = Ssh[buf][0][2 * c + hh][qsel];
+      z2[c] = VQ == VQ_G64 ? Ssh[buf][1][2 * c + hh][qsel] : 0u;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      uint4 h = dequant8<VQ>(st.q[c], q8, s2[c], z2[c]);
+      if constexpr (BF) h = f16x8_to_bf16x8(h);
+      *(uint4*)&sbuf[soff0 + 2 * c * PITCH] = h;
+    }
+  };
+
+  // transposed-read addressing: group g = lane/16, rho = lane%16
+  const int g = lane >> 4, rho = lane & 15;
+  const int tr_off = (8 * hh + (rho >> 2)) * PITCH + 16 * (g & 1) + 4 * (rho & 3);
+
+  // the MFMAs of K-step ks: A from Ash[ks & 1], B from the slab ks & 1.
+  // Every tile of the slab is multiplied (tiles past nvt hold finite data and
+  // are never stored), so the iteration is one basic block and the compiler
+  // can interleave these MFMAs with the next K-step's dequantisation.
+  auto mfmas = [&](int ks) {
+    const int buf = ks & 1;
+    uint4 Araw[NA];
+#pragma unroll
+    for (int k = 0; k < NA; ++k) Araw[k] = *(const uint4*)&Ash[buf][k][8 * lane];
+    const uint16_t* sb = &stage[wave][buf][0] + tr_off;
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const uint2 lo = lds_read_tr16(sb + 32 * j);
+      const uint2 hi = lds_read_tr16(sb + 32 * j + 4 * PITCH);
+      const uint4 bv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      if constexpr (BF) {
+        acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, Araw[0]), __builtin_bit_cast(bf16x8, bv), acc[j]);
+        acc[j] = mfma_bf16(__builtin_bit_cast(bf16x8, Araw[NA - 1]), __builtin_bit_cast(bf16x8, bv), acc[j]);
+      } else {
+        acc[j] = mfma_f16(__builtin_bit_cast(half8, Araw[0]), __builtin_bit_cast(half8, bv), acc[j]);
+      }
+    }
+  };
+
+  // Software pipeline over K-steps, DEPTH register stages (stage k in
+  // st[k % DEPTH]).  Iteration k multiplies K-step k (its slab written by
+  // this wave in iteration k-1) while the wave dequantises K-step k+1, forms
+  // its exponentials and publishes the scale rows of K-step k+2; then it
+  // loads K-step k+1+DEPTH into the registers K-step k+1 freed and barriers.
+  // The last group runs up to DEPTH - 1 iterations past the chunk with P = 0
+  // (clamped loads, no branch in the loop body).
+  if (nks > 0) {                             // uniform: every wave takes part in the barriers
+    PVWStage<NTW> st[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(st[d], d);
+    publish_p(st[0], 0);
+    publish_sz(st[0], 0);
+    __syncthreads();
+    dequant(st[0], 0);
+    publish_sz(st[1], 1);
+    load(st[0], DEPTH);
+    __syncthreads();                         // Ssh[1] published; Ssh[0] consumed
+    for (int ks = 0; ks < nks; ks += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int k = ks + d;
+        PVWStage<NTW>& cur = st[(d + 1) % DEPTH];          // K-step k+1
+        mfmas(k);
+        dequant(cur, k + 1);
+        publish_p(cur, k + 1);
+        publish_sz(st[(d + 2) % DEPTH], k + 2);            // K-step k+2's items
+        load(cur, k + 1 + DEPTH);
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- the chunk's softmax sums per head, then its partial sums (as in
+  // pv_kernel's fused mode)
+  psum += __shfl_xor(psum, 1, 64);
+  psum += __shfl_xor(psum, 2, 64);
+  psum += __shfl_xor(psum, 4, 64);
+  if (ee == 0) Ps2[eh][en] = psum;
+  __syncthreads();
+  if (tid < 32) a.psum[((int64_t)bq * a.n_c2 + c2) * 32 + tid] = Ps2[0][tid] + Ps2[1][tid];
+  const int Rvp = a.Rvp;
+  if (a.part16) {
+    _Float16* part = (_Float16*)a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
+      const float sq = Ps2[0][q] + Ps2[1][q];
+      const float inv = sq > 0.f ? 1.0f / sq : 0.f;
+#pragma unroll
+      for (int j = 0; j < NTW; ++j)
+        if (j < nvt)
+          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = (_Float16)(acc[j][v] * inv);
+    }
+    return;
+  }
+  float* part = a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    if (j < nvt) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
+        part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = acc[j][v];
+      }
+    }
+  }
+}
+
 // Drop-in path (bx): sum of the chunk partials in fixed chunk order into the
 // act-dtype output.  Each thread sums four columns of a 32x32 output tile;
 // the partial loads are issued eight chunks at a time (32 loads in flight per
@@ -529,6 +839,15 @@ __global__ __launch_bounds__(256) void pv_reduce_kernel(const PVArgs a) {
   }
 }
 
+int pv_wide_tiles(int Rvp, bool fused, int vq) {
+  const int tiles = Rvp / 32;
+  // fused quantised latents past 32 tiles: the all-columns kernel, 8 waves
+  // of ceil(tiles / 8) tiles (B16 S32768 int4-g64, 52 tiles: two column
+  // blocks of 4 x 8 tiles fetch the logits and scale rows twice)
+  if (!fused || vq == VQ_DENSE || tiles <= 32 || tiles > 64) return 0;
+  return (tiles + 7) / 8;
+}
+
 int pv_tiles_per_wave(int Rvp, bool fused, int vq) {
   const int tiles = Rvp / 32;
   // Quantised formats: 8 tiles per wave, two workgroups per CU.  A quantised
@@ -565,10 +884,29 @@ static void launch_pv_n13(const PVArgs& a, bool fast, int B, hipStream_t st) {
   else hipLaunchKernelGGL((pv_kernel<VT, 13, true, false, VQ_DENSE>), grid, block, 0, st, a);
 }
 
+template <typename VT, int NTW>
+static void launch_pv_wide_n(const PVArgs& a, int vq, bool fast, int B, hipStream_t st) {
+  dim3 grid(a.n_c2, B), block(512);
+  if (vq == VQ_BLOCK && fast) hipLaunchKernelGGL((pv_wide_kernel<VT, NTW, true, VQ_BLOCK>), grid, block, 0, st, a);
+  else if (vq == VQ_BLOCK) hipLaunchKernelGGL((pv_wide_kernel<VT, NTW, false, VQ_BLOCK>), grid, block, 0, st, a);
+  else if (fast) hipLaunchKernelGGL((pv_wide_kernel<VT, NTW, true, VQ_G64>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((pv_wide_kernel<VT, NTW, false, VQ_G64>), grid, block, 0, st, a);
+}
+
 template <typename VT, bool FUSED>
 static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st) {
   const int ntw = pv_tiles_per_wave(a.Rvp, FUSED, vq);
   const int BQ = B * a.n_hg;
+  if constexpr (FUSED) {
+    // the host's geometry chose the all-columns kernel (one column block)
+    if (const int w = pv_wide_tiles(a.Rvp, FUSED, vq); w && a.n_cb == 1) {
+      if (w == 5) launch_pv_wide_n<VT, 5>(a, vq, fast, BQ, st);
+      else if (w == 6) launch_pv_wide_n<VT, 6>(a, vq, fast, BQ, st);
+      else if (w == 7) launch_pv_wide_n<VT, 7>(a, vq, fast, BQ, st);
+      else launch_pv_wide_n<VT, 8>(a, vq, fast, BQ, st);
+      return (int)hipGetLastError();
+    }
+  }
   if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, vq, fast, BQ, st);
   else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, vq, fast, BQ, st);
   else if constexpr (FUSED) launch_pv_n13<VT>(a, fast, BQ, st);

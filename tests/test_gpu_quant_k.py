@@ -58,12 +58,14 @@ def ragged_int8_k(B, S, ranks, seed=0):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_k_logits_int8_ragged(dtype):
+@pytest.mark.parametrize("B,S", [(2, 700),
+                                 (1, 31), (1, 64),      # one and two tiles: the pipelined int8 loop's edges
+                                 (1, 4099), (4, 2100)])  # chunks of many tiles, partial last tile
+def test_k_logits_int8_ragged(dtype, B, S):
     from oracle import starkv_oracle as o
     from starkv import KLatentSpec, k_logits
     from starkv._lib import FMT_INT8_SYM
-    _flush(f"[k int8 ragged] {dtype}")
-    B, S = 2, 700
+    _flush(f"[k int8 ragged] {dtype} B={B} S={S}")
     ranks = cfg2_ranks()
     Hkv = len(ranks)
     buf, scales, offs, deq = ragged_int8_k(B, S, ranks, seed=1)
