@@ -124,6 +124,11 @@ __device__ inline uint4 dequant8(uint2 q, bool kind8, uint32_t s2, uint32_t z2) 
 // column n (within a 32-column tile)
 __device__ inline int pv_g64_rank(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
 
+// a normalised fp16 partial: a convex combination of V rows, within fp16
+// range except where a bf16 model rounded a value near the fp16 limit up
+// (at most 65536): clamped there
+__device__ inline _Float16 part16_value(float x) { return (_Float16)fminf(fmaxf(x, -65504.f), 65504.f); }
+
 __device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
   const uint32_t w[4] = {h.x, h.y, h.z, h.w};
   uint32_t o[4];
@@ -134,6 +139,27 @@ __device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
     o[k] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// the maximum of one head's K1 chunk maxima cm[0, n) over c = j, j+8, ...:
+// eight independent loads in flight per step (a load-then-max loop would wait
+// out one memory latency per chunk: 32 of them at 256 chunks)
+__device__ inline float chunk_max_part(const float* cm, int n, int j) {
+  float m[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) m[u] = -INFINITY;
+  int c = j;
+  for (; c + 56 < n; c += 64) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = cm[c + 8 * u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m[u] = fmaxf(m[u], v[u]);
+  }
+  for (; c < n; c += 8) m[0] = fmaxf(m[0], cm[c]);
+#pragma unroll
+  for (int u = 1; u < 8; ++u) m[0] = fmaxf(m[0], m[u]);
+  return m[0];
 }
 
 template <typename VT, int NTW, bool FUSED, bool FAST, int VQ>
@@ -168,8 +194,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
   if constexpr (FUSED) {
     const int q = tid >> 3, j = tid & 7;
     float m = -INFINITY;
-    if (q < H)
-      for (int c = j; c < a.n_chunk1; c += 8) m = fmaxf(m, a.chunkmax[((int64_t)b * H + h0 + q) * a.n_chunk1 + c]);
+    if (h0 + q < H) m = chunk_max_part(a.chunkmax + ((int64_t)b * H + h0 + q) * a.n_chunk1, a.n_chunk1, j);
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
@@ -468,7 +493,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
 #pragma unroll
       for (int j = 0; j < NTW; ++j)
         if (j < nvt)
-          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = (_Float16)(acc[j][v] * inv);
+          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = part16_value(acc[j][v] * inv);
     }
     return;
   }
@@ -536,8 +561,7 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
   if (tid < 256) {
     const int q = tid >> 3, j = tid & 7;
     float m = -INFINITY;
-    if (h0 + q < H)
-      for (int c = j; c < a.n_chunk1; c += 8) m = fmaxf(m, a.chunkmax[((int64_t)b * H + h0 + q) * a.n_chunk1 + c]);
+    if (h0 + q < H) m = chunk_max_part(a.chunkmax + ((int64_t)b * H + h0 + q) * a.n_chunk1, a.n_chunk1, j);
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
@@ -775,7 +799,7 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
 #pragma unroll
       for (int j = 0; j < NTW; ++j)
         if (j < nvt)
-          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = (_Float16)(acc[j][v] * inv);
+          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = part16_value(acc[j][v] * inv);
     }
     return;
   }
