@@ -534,10 +534,9 @@ struct DecodeLayout {
   size_t off_logits, off_cmax, off_part, off_psum, off_ypart, total;
 };
 
-// f16: fp16 model.  Short P.V chunks (<= 512 positions) of an fp16 model or
-// of a quantised V latent keep their partials in fp16, each divided by its
-// chunk's softmax sum (a convex combination of V rows: bounded by max |V|,
-// which fp16 holds there): there the partials are a large
+// f16: fp16 model.  Short P.V chunks (<= 512 positions) then keep their
+// partials in fp16, each divided by its chunk's softmax sum (a convex
+// combination of V rows: bounded by max |V|): there the partials are a large
 // share of the P.V traffic (at 272 positions about as many bytes as the
 // int4 V latent) and halving them pays for the per-chunk rescale in the
 // up-projection; with long chunks it does not (measured).
@@ -560,9 +559,7 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
-  // quantised V in a bf16 model: dequantised values are fp16 (the kernels
-  // clamp the bf16 rounding of a value near the fp16 limit to +-65504)
-  const bool part16 = (f16 || vq != VQ_DENSE) && L.pv.c2_len <= 512;
+  const bool part16 = f16 && L.pv.c2_len <= 512;
   L.part16 = part16;
   L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * (part16 ? 2 : 4));
   L.off_psum = o; o = a256(o + BQ * n_c2 * 32 * 4);

@@ -124,11 +124,6 @@ __device__ inline uint4 dequant8(uint2 q, bool kind8, uint32_t s2, uint32_t z2) 
 // column n (within a 32-column tile)
 __device__ inline int pv_g64_rank(int n) { return (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1); }
 
-// a normalised fp16 partial: a convex combination of V rows, within fp16
-// range except where a bf16 model rounded a value near the fp16 limit up
-// (at most 65536): clamped there
-__device__ inline _Float16 part16_value(float x) { return (_Float16)fminf(fmaxf(x, -65504.f), 65504.f); }
-
 __device__ inline uint4 f16x8_to_bf16x8(uint4 h) {
   const uint32_t w[4] = {h.x, h.y, h.z, h.w};
   uint32_t o[4];
@@ -493,7 +488,7 @@ __global__ __launch_bounds__(256, pv_wg_per_cu(NTW, VQ)) void pv_kernel(const PV
 #pragma unroll
       for (int j = 0; j < NTW; ++j)
         if (j < nvt)
-          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = part16_value(acc[j][v] * inv);
+          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = (_Float16)(acc[j][v] * inv);
     }
     return;
   }
@@ -799,7 +794,7 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
 #pragma unroll
       for (int j = 0; j < NTW; ++j)
         if (j < nvt)
-          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = part16_value(acc[j][v] * inv);
+          part[(int64_t)q * Rvp + col0 + 32 * j + (VQ == VQ_G64 ? pv_g64_rank(n) : n)] = (_Float16)(acc[j][v] * inv);
     }
     return;
   }
