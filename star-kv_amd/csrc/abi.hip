@@ -165,7 +165,9 @@ bool k_quant_aligned(const starkv_klatent& k) {
 // (ranks a multiple of 8), or int8 latents with one scale per (b, h, s) whose
 // rows start on 16-byte boundaries (pitch a multiple of 16 bytes, so the 16-byte
 // DMA pieces never straddle rows); q and B_k are read element-wise there.
-bool k_ws(const starkv_klatent& k, int dtype, int S) {
+// padded: dense rows hold round_up(r, 8) elements, zero past r (the K-logit
+// entry's repacked copy), so a rank need not be a multiple of 8.
+bool k_ws(const starkv_klatent& k, int dtype, int S, bool padded = false) {
   const bool i8 = k.format == STARKV_FMT_INT8_SYM;
   if (k.format != STARKV_FMT_DENSE && !i8) return false;
   const int xe = i8 ? 1 : esize(dtype);
@@ -177,7 +179,7 @@ bool k_ws(const starkv_klatent& k, int dtype, int S) {
              k.scale_stride_h < round_up(S, 8)))
     return false;
   for (int h = 0; h < k.n_kv_heads; ++h) {
-    if (k.rank[h] % 8) return false;
+    if (k.rank[h] % 8 && !(padded && !i8)) return false;
     if (!al64(k.head_offset[h] * xe, 16) || !al64(k.pos_stride[h] * xe, 16)) return false;
     if ((int64_t)TILE * k.pos_stride[h] * xe >= ((int64_t)1 << 31)) return false;   // 32-bit per-tile DMA step
   }
@@ -186,7 +188,7 @@ bool k_ws(const starkv_klatent& k, int dtype, int S) {
 
 // 16-byte LDS chunks of one 32-position tile row of a head in that kernel
 int ws_row_chunks(const starkv_klatent& k, int h) {
-  return k.format == STARKV_FMT_INT8_SYM ? (int)ceil_div(k.rank[h], 16) : k.rank[h] / 8;
+  return (int)ceil_div(k.rank[h], k.format == STARKV_FMT_INT8_SYM ? 16 : 8);
 }
 
 // First-fit decreasing of heads hs (u[h] units each) into at most nb bins of
@@ -301,8 +303,9 @@ static bool ws_balance(const starkv_klatent& k, int Hq, int unit, int nw, int ca
 // (first fit decreasing, whole heads per wave; 4 once any head has rank > 64)
 // and deal the waves round-robin over workgroups of 8 waves (2-item waves) or
 // 4 waves (4-item waves).
-int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArgs& a, KPlan& plan) {
-  const bool ws = k_ws(k, dtype, S);
+int build_k_plan(const starkv_klatent& k, int Hq, int gs, int dtype, int S, KArgs& a, KPlan& plan,
+                 bool padded = false) {
+  const bool ws = k_ws(k, dtype, S, padded);
   const int unit = 32;                        // ranks per item
   struct QH { int qh, kv, ni; };              // ni: items of the head
   std::vector<QH> heads;
@@ -828,10 +831,38 @@ int starkv_rope_build(const float* inv_freq_host, float attention_scaling, int m
   return launch_rope_table(f, max_positions, attention_scaling, table, (hipStream_t)stream);
 }
 
-size_t starkv_k_logits_workspace_bytes(const starkv_klogits_desc*) { return 0; }
+// Dense K whose rows the warp-specialised and grouped-query K-logit kernels
+// cannot stream (a rank not a multiple of 8, or rows not 16-byte aligned: the
+// reference abx benchmark's 102 ranks per KV head, abx_rope_batched.py:274-280,
+// leaves 204-byte rows) is first copied into the workspace as rows of
+// round_up(r, 8) elements, zero past r, one 16-byte pitch for all heads
+// ([B][Hkv][S][pitch]); the kernels then read that copy.
+struct KRepack {
+  bool on = false;
+  int pitch = 0;              // bytes
+  size_t bytes = 0;
+};
+
+KRepack k_repack_plan(const starkv_klatent& k, int dtype, int B, int S) {
+  KRepack r;
+  if (k.format != STARKV_FMT_DENSE || k_ws(k, dtype, S)) return r;
+  int rmax = 8;
+  for (int h = 0; h < k.n_kv_heads; ++h) rmax = std::max(rmax, k.rank[h]);
+  r.pitch = (int)round_up((int64_t)round_up(rmax, 8) * esize(dtype), 16);
+  if ((int64_t)TILE * r.pitch >= ((int64_t)1 << 31)) return r;
+  r.bytes = a256((size_t)B * k.n_kv_heads * S * r.pitch);
+  r.on = true;
+  return r;
+}
+
+size_t starkv_k_logits_workspace_bytes(const starkv_klogits_desc* d) {
+  int gs = 0;
+  if (!d || d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S || validate_klatent(d->k, d->n_q_heads, d->dtype, &gs))
+    return 0;
+  return k_repack_plan(d->k, d->dtype, d->batch, d->seq_len).bytes;
+}
 
 int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace; (void)workspace_bytes;
   if (!d) return STARKV_ERR_NULL;
   if (d->batch < 1 || d->seq_len < 1 || d->seq_len > MAX_S || d->head_dim != HEAD_DIM) return STARKV_ERR_SHAPE;
   int gs = 0, st;
@@ -840,11 +871,37 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   if (d->seq_len > d->rope_max_positions) return STARKV_ERR_SHAPE;
   if (d->out_dtype != STARKV_F32 && d->out_dtype != STARKV_F16 && d->out_dtype != STARKV_BF16) return STARKV_ERR_DTYPE;
   if ((st = check_mask(d->mask, d->mask_dtype))) return st;
+  const KRepack rp = k_repack_plan(d->k, d->dtype, d->batch, d->seq_len);
+  starkv_klatent k = d->k;
+  int64_t rp_hoff[K_MAX_KV], rp_pstr[K_MAX_KV];   // the repacked copy's head offsets and row pitches
+  if (rp.on) {
+    if (!workspace || workspace_bytes < rp.bytes) return STARKV_ERR_WORKSPACE;
+    if (!al(workspace, 256)) return STARKV_ERR_ALIGN;
+    const int H = k.n_kv_heads, S = d->seq_len, xe = esize(d->dtype);
+    RepackArgs ra = {};
+    ra.src = (const uint8_t*)k.data; ra.src_sb = k.stride_b * xe;
+    for (int h = 0; h < H; ++h) {
+      ra.src_off[h] = k.head_offset[h] * xe;
+      ra.src_pitch[h] = k.pos_stride[h] * xe;
+      ra.nel[h] = k.rank[h];
+    }
+    ra.dst = (uint8_t*)workspace; ra.dst_sb = (int64_t)H * S * rp.pitch; ra.pitch = rp.pitch;
+    ra.kind = RP_HALF; ra.H = H; ra.S = S;
+    if ((st = launch_repack(ra, d->batch, (hipStream_t)stream))) return st;
+    k.data = workspace;
+    k.stride_b = (int64_t)H * S * rp.pitch / xe;
+    for (int h = 0; h < H; ++h) {
+      rp_hoff[h] = (int64_t)h * S * rp.pitch / xe;
+      rp_pstr[h] = rp.pitch / xe;
+    }
+    k.head_offset = rp_hoff;
+    k.pos_stride = rp_pstr;
+  }
   KArgs a;
   KPlan plan;
-  if ((st = build_k_plan(d->k, d->n_q_heads, gs, d->dtype, d->seq_len, a, plan))) return st;
+  if ((st = build_k_plan(k, d->n_q_heads, gs, d->dtype, d->seq_len, a, plan, rp.on))) return st;
   a.q = d->q; a.q_sb = d->q_stride_b; a.q_sh = d->q_stride_h;
-  a.x = d->k.data; a.x_sb = d->k.stride_b;
+  a.x = k.data; a.x_sb = k.stride_b;
   a.xscale = d->k.scale; a.xs_sb = d->k.scale_stride_b; a.xs_sh = d->k.scale_stride_h;
   a.bk = d->k.bk; a.bk_rs = d->k.bk_row_stride;
   a.rope = (const uint4*)d->rope_table;
@@ -856,8 +913,8 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   int nc = choose_splits((int64_t)d->batch * plan.n_wg, device_cus() * plan.per_cu, n_tiles, 256, 3.0, 0.0);
   a.tiles_per_chunk = (int)ceil_div(n_tiles, nc);
   a.n_chunks = (int)ceil_div(n_tiles, a.tiles_per_chunk);
-  const bool fast = k_fast(d->k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
-  return launch_k_logits(a, d->dtype, d->k.format, d->out_dtype == STARKV_F32, d->out_dtype, fast, d->batch, (hipStream_t)stream);
+  const bool fast = k_fast(k, d->dtype, d->q, d->q_stride_b, d->q_stride_h);
+  return launch_k_logits(a, d->dtype, k.format, d->out_dtype == STARKV_F32, d->out_dtype, fast, d->batch, (hipStream_t)stream);
 }
 
 size_t starkv_pv_latent_workspace_bytes(const starkv_pv_desc* d) {

@@ -135,7 +135,7 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
   typedef typename GqVec<XT>::T XV;
   const int lane = threadIdx.x & 63, t = lane & 31, hh = lane >> 5;
   const int gs = a.gs, S = a.S, tile0 = d.tile0, stage = d.stage, nst = d.nst;
-  const int r = H.hrank[slot], hb = H.hoff[slot], n16 = r >> 3;
+  const int r = H.hrank[slot], hb = H.hoff[slot], n16 = (r + 7) >> 3;   // chunks of a row (padded rows past r)
 
   // The q.K step runs on fp16 MFMA.  bf16 models hold keys and queries in
   // bf16 (the reference too, abx_rope_batched.py:114-125), whose range fp16
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(GQ_WAVES * 64, 2) void k_logits_gqa_kernel(const KA
     H.hkv[k] = item_kv(itm);
     H.hrank[k] = a.krank[H.hkv[k]];
     H.hoff[k] = H.tot;
-    H.tot += 32 * (H.hrank[k] >> 3);
+    H.tot += 32 * ((H.hrank[k] + 7) >> 3);
   }
   // stage: latent chunks [0, 64 * nX), the RoPE operand in the last 8 KB
   const int nX = (H.tot + 63) / 64, stage = a.ws_stage, nst = a.ws_nst;
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(GQ_WAVES * 64, 2) void k_logits_gqa_kernel(const KA
 #pragma unroll
       for (int j = 1; j < GQ_MAXH; ++j)
         if (H.hoff[j] <= q) { hb = H.hoff[j]; hr = H.hrank[j]; hk = H.hkv[j]; }
-      const int n16 = hr >> 3, loc = q - hb;
+      const int n16 = (hr + 7) >> 3, loc = q - hb;
       const int row = loc / n16, cr = loc % n16;
       const int c = (cr - gq_shift(row, n16) % n16 + n16) % n16;
       const int pitch = a.xpitch[hk] * 2;

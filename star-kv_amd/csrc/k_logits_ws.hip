@@ -68,8 +68,9 @@ __device__ inline int ws_shift(int row, int n16) {
   return row / (8 / g);
 }
 
-// 16-byte chunks of one staged row: fp16/bf16 2r bytes, int8 r bytes rounded up
-template <bool XI8> __device__ inline int ws_n16(int r) { return XI8 ? (r + 15) >> 4 : r >> 3; }
+// 16-byte chunks of one staged row: fp16/bf16 2r bytes, int8 r bytes, each
+// rounded up (rows are padded to 16 bytes past the rank)
+template <bool XI8> __device__ inline int ws_n16(int r) { return XI8 ? (r + 15) >> 4 : (r + 7) >> 3; }
 
 // s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31]
 template <int N> __device__ inline void wait_vm() {

@@ -159,7 +159,6 @@ constexpr int RC_NT = RC_WAVE_POS / 32;          // N-tiles per wave
 constexpr int RC_POS = 4 * RC_WAVE_POS;          // positions per workgroup
 static_assert(RC_POS == PF_K_POS, "host grid sizing");
 constexpr int RC_KS = 64;                        // ranks per K-step
-constexpr int UV_PITCH = 72;                     // halves per staged U_v row (64 ranks + 8), V kernel
 constexpr int BK_PITCH = 136;                    // halves per staged B_k row (128 dims + 8)
 constexpr int C_PITCH = 136;                     // halves per epilogue row
 constexpr int RC_LDS = 4 * RC_WAVE_POS * C_PITCH;
@@ -913,19 +912,15 @@ __global__ __launch_bounds__(FA_WAVES * 64, 1) void fa_causal_kernel(const PFArg
 }
 
 // ---------------------------------------------------------------------------
-// Row repack (see RepackArgs): one thread per 4-byte word of a destination
-// row, reading its source elements byte by byte (any alignment), so the
-// reconstruction kernels always see 16-byte aligned rows of a multiple of 8
-// ranks.  Grid (words of one head's S rows / 256, head, batch).
+// Row repack (see RepackArgs): one thread per 16-byte piece of a destination
+// row (pitches are multiples of 16), so the reconstruction and K-logit kernels
+// always see 16-byte aligned rows of a multiple of 8 ranks.  A piece of
+// 16-bit elements whose source is 4-byte aligned and wholly inside the row is
+// read as four words; any other piece byte by byte (any alignment, zero /
+// nibble-8 fill past the row).  Grid (pieces of one head's S rows / 256,
+// head, batch).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void repack_rows_kernel(const RepackArgs a) {
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int wpr = a.pitch >> 2;                      // words per row
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)a.S * wpr) return;
-  const int s = (int)(idx / wpr), o = (int)(idx - (int64_t)s * wpr) * 4;
-  const uint8_t* row = a.src + b * a.src_sb + a.src_off[h] + (int64_t)s * a.src_pitch[h];
-  const int n = a.nel[h];
+__device__ inline uint32_t repack_word(const RepackArgs& a, const uint8_t* row, int n, int o) {
   uint32_t w = 0;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -941,13 +936,33 @@ __global__ __launch_bounds__(256) void repack_rows_kernel(const RepackArgs a) {
     }
     w |= v << (8 * k);
   }
-  *(uint32_t*)(a.dst + b * a.dst_sb + ((int64_t)h * a.S + s) * a.pitch + o) = w;
+  return w;
+}
+
+__global__ __launch_bounds__(256) void repack_rows_kernel(const RepackArgs a) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int ppr = a.pitch >> 4;                      // 16-byte pieces per row
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.S * ppr) return;
+  const int s = (int)(idx / ppr), o = (int)(idx - (int64_t)s * ppr) * 16;
+  const uint8_t* row = a.src + b * a.src_sb + a.src_off[h] + (int64_t)s * a.src_pitch[h];
+  const int n = a.nel[h];
+  uint32_t w[4];
+  if (a.kind == RP_HALF && o + 16 <= 2 * n && ((uintptr_t)(row + o) & 3) == 0) {
+    const uint32_t* p = (const uint32_t*)(row + o);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = p[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = repack_word(a, row, n, o + 4 * k);
+  }
+  *(uint4*)(a.dst + b * a.dst_sb + ((int64_t)h * a.S + s) * a.pitch + o) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 int launch_repack(const RepackArgs& a, int B, hipStream_t st) {
-  const int64_t words = (int64_t)a.S * (a.pitch / 4);
-  if (words == 0) return 0;
-  hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)ceil_div(words, 256), a.H, B), dim3(256), 0, st, a);
+  const int64_t pieces = (int64_t)a.S * (a.pitch / 16);
+  if (pieces == 0) return 0;
+  hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)ceil_div(pieces, 256), a.H, B), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 

@@ -263,7 +263,11 @@ def k_logits(q: torch.Tensor, k: KLatentSpec, seq_len: int, rope: RopeConfig = R
     d.mask = m.data_ptr() if m is not None else None
     d.mask_dtype, d.mask_stride_b, d.mask_stride_h = mdt, msb, msh
     d.out, d.out_dtype, d.out_stride_b, d.out_stride_h = out.data_ptr(), _dt(out), out.stride(0), out.stride(1)
-    check(_lib.lib().starkv_k_logits(ctypes.byref(d), None, 0, _stream(q.device)), "starkv_k_logits")
+    L = _lib.lib()
+    nb = L.starkv_k_logits_workspace_bytes(ctypes.byref(d))
+    ws = _workspace(q.device, nb) if nb else None
+    check(L.starkv_k_logits(ctypes.byref(d), ctypes.c_void_p(ws.data_ptr()) if ws is not None else None,
+                            ws.numel() if ws is not None else 0, _stream(q.device)), "starkv_k_logits")
     return out
 
 

@@ -281,6 +281,28 @@ def test_k_logits_validation():
     assert lib.starkv_k_logits(None, None, 0, None) == ERR_NULL
 
 
+def test_k_logits_repack_workspace():
+    """Dense K whose rows the streaming K-logit kernels cannot read (rank 102,
+    the reference abx benchmark's: 204-byte rows) asks for a workspace that
+    holds a padded copy ([B][Hkv][S][208 bytes]) and refuses to run without it;
+    ranks that are multiples of 8 on aligned rows need none."""
+    lib = L.lib()
+    keep = []
+    k = _klatent([102] * 8, keep)
+    keep.append(L.i64_array([102] * 8))
+    k.pos_stride = keep[-1]
+    d = L.KLogitsDesc(batch=2, n_q_heads=32, head_dim=128, seq_len=64, dtype=L.F16, q=FAKE,
+                      q_stride_b=32 * 128, q_stride_h=128, k=k, rope_table=FAKE, rope_max_positions=64,
+                      scale=1.0, out=FAKE, out_dtype=L.F16, out_stride_b=32 * 64, out_stride_h=64)
+    need = lib.starkv_k_logits_workspace_bytes(ctypes.byref(d))
+    assert need >= 2 * 8 * 64 * 208
+    assert lib.starkv_k_logits(ctypes.byref(d), None, 0, None) == ERR_WORKSPACE
+    assert lib.starkv_k_logits(ctypes.byref(d), FAKE, need - 1, None) == ERR_WORKSPACE
+    assert lib.starkv_k_logits(ctypes.byref(d), FAKE + 16, need, None) == ERR_ALIGN
+    d.k = _klatent([104] * 8, keep)
+    assert lib.starkv_k_logits_workspace_bytes(ctypes.byref(d)) == 0
+
+
 def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(L, "_lib", None)
     monkeypatch.setattr(L, "LIB_PATH", os.path.join(ROOT, "no-such-dir", "libstarkv.so"))
