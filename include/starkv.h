@@ -110,8 +110,13 @@ int starkv_rope_apply(const starkv_rope_apply_desc* d, void* stream);
  * B_k (k_u^T, model.py:455) row j of head h lives at
  * bk + bk_head_offset[h] + j*bk_row_stride, 128 contiguous elements.
  *
- * Quantised K (offsets and strides of data/data2 in bytes; ranks multiples
- * of 8; every value dequantised to fp16 before use, as the reference's
+ * Any rank 1..128 and any row layout in every format.  Dense rows that the
+ * streaming K-logit kernels cannot read (a rank that is not a multiple of 8,
+ * or rows not 16-byte aligned) are copied by starkv_k_logits into its
+ * workspace first; quantised rows of any byte alignment are read as aligned
+ * words joined in registers.
+ * Quantised K (offsets and strides of data/data2 in bytes; every value
+ * dequantised to fp16 before use, as the reference's
  * dequantise-then-multiply path does, LlamaLoRaAttention_headwise_quant.py:
  * 137-144):
  *   INT8_SYM  all ranks int8 in data, x = q * s, fp16 scale per (b,h,s) at
@@ -161,6 +166,11 @@ typedef struct {
  * q + b*q_stride_b + q*q_stride_h + d.  out: out_dtype (act dtype or F32),
  * element (b,q,s) at out + b*out_stride_b + q*out_stride_h + s.
  * Position s uses the angle of position s (the Triton kernel's semantics).
+ * Workspace: starkv_k_logits_workspace_bytes is 0 when the K rows can be
+ * streamed in place (dense: ranks multiples of 8 on 16-byte aligned rows;
+ * int8 or the split format: always), else the size of a padded copy of the
+ * dense K latent ([B][Hkv][S] rows of round_up(r, 8) elements, 16-byte pitch)
+ * that the call writes before the logits.
  * ------------------------------------------------------------------- */
 typedef struct {
   int batch, n_q_heads, head_dim, seq_len;
@@ -179,10 +189,12 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
 /* ---------------------------------------------------------------------
  * V-latent description.  Dense: element (b, s, j) at
  * data + b*stride_b + s*stride_s + j (reference cache [B, S, Rv],
- * LlamaLoRaAttention_headwise.py:96-102).  Quantised formats (rank and split
- * multiples of 8; strides of data/data2 in bytes, of scales in fp16
- * elements; every value dequantised to fp16 exactly as the reference kernel
- * does, then rounded to bf16 for bf16 activations):
+ * LlamaLoRaAttention_headwise.py:96-102).  Quantised formats (any rank and
+ * any byte alignment of rows -- the reference bx default, rank 1228 over a
+ * 256-rank upper block, leaves 486-byte lower rows -- with the two-block
+ * INT4_REF split a multiple of 8; strides of data/data2 in bytes, of scales
+ * in fp16 elements; every value dequantised to fp16 exactly as the reference
+ * kernel does, then rounded to bf16 for bf16 activations):
  *   INT4_REF (bx_quant.py:117-166 x1/x2): with 0 < split < rank, ranks
  *     [0, split) in data ((b,s,byte) at data + b*stride_b + s*stride_s +
  *     byte) with the fp16 per-token scale (b,s) at scale + b*scale_stride_b +
@@ -347,18 +359,19 @@ int starkv_decode_append(const starkv_k_append_desc* k, const starkv_v_append_de
  * starkv_v_append).  q: rotated queries, act dtype, element (b,q,t,d) at
  * q + b*q_stride_b + q*q_stride_h + t*q_stride_t + d (16-byte aligned, strides
  * multiples of 8).  out likewise with out_stride_*, act dtype.
- * K latent: STARKV_FMT_DENSE (ranks, offsets and pitches multiples of 8,
- * data 16-byte aligned), STARKV_FMT_INT8_SYM or STARKV_FMT_INT4_REF (the
- * reference module's split cache, either upper-block format; ranks multiples
- * of 8); V latent: STARKV_FMT_DENSE (rank and strides multiples of 8, data
- * 16-byte aligned), STARKV_FMT_INT4_G64, STARKV_FMT_INT8_SYM or
- * STARKV_FMT_INT4_REF (with or without its upper block; rank a multiple of
- * 8); each under the same layout rules as in decode.  uv: 16-byte aligned,
- * row stride a multiple of 8.  Quantised latents are dequantised bit-exactly
- * as in decode.  The workspace holds the reconstructed K and V
- * (2 x batch x Hkv x round_up(pos0 + n_tokens, 64) x 128 fp16 elements, for
- * either act dtype: bf16 activations attend in fp16, exact for |values| up to
- * 65504, with 8x finer rounding of K and V than bf16 storage).
+ * K latent: STARKV_FMT_DENSE, STARKV_FMT_INT8_SYM or STARKV_FMT_INT4_REF (the
+ * reference module's split cache, either upper-block format); V latent:
+ * STARKV_FMT_DENSE, STARKV_FMT_INT4_G64, STARKV_FMT_INT8_SYM or
+ * STARKV_FMT_INT4_REF (with or without its upper block); any rank and row
+ * layout: latents (and a U_v) that the reconstruction kernels cannot read in
+ * place -- ranks or pitches that are not multiples of 8, rows not aligned --
+ * are first repacked into aligned rows of a multiple of 8 ranks in the
+ * workspace (zero past the rank; nibble 8 for int4).  Quantised latents are
+ * dequantised bit-exactly as in decode.  The workspace holds the
+ * reconstructed K and V (2 x batch x Hkv x round_up(pos0 + n_tokens, 64) x
+ * 128 fp16 elements, for either act dtype: bf16 activations attend in fp16,
+ * exact for |values| up to 65504, with 8x finer rounding of K and V than
+ * bf16 storage) and any repacked copies.
  * ------------------------------------------------------------------- */
 typedef struct {
   int batch, n_q_heads, head_dim, n_tokens, pos0;
