@@ -538,7 +538,12 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
   static_assert(VQ != VQ_DENSE, "quantised latents only");
   __shared__ __attribute__((aligned(16))) uint16_t stage[NWV][2][STAGE];
   __shared__ __attribute__((aligned(16))) uint16_t Ash[2][NA][512];   // [buf][piece][eh][en][ee]
-  __shared__ uint32_t Ssh[2][2][16][32];         // [buf][scale | zero][row][group or block], bits in both halves
+  // scale / zero rows of a K-step, bits in both halves of a word: per
+  // (group or block g, row parity hh) a 20-word block holding (scale, zero) of
+  // rows hh, hh + 2, ..., hh + 14 -- the rows of a lane's chunks -- so a lane
+  // reads its 16 words with four 16-byte loads (the 4 pad words keep the
+  // groups of a half-wave on distinct banks)
+  __shared__ __attribute__((aligned(16))) uint32_t Ssh[2][64 * 20];
   __shared__ float Ms[32];
   __shared__ float Ps2[2][32];
 
@@ -693,18 +698,24 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
     const int buf = ks & 1;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
-      if (zok[u]) Ssh[buf][zsel[u]][zrow[u]][zg[u]] = (uint32_t)st.sz[u] * 0x10001u;
+      if (zok[u]) Ssh[buf][(2 * zg[u] + (zrow[u] & 1)) * 20 + (zrow[u] >> 1) * 2 + zsel[u]] = (uint32_t)st.sz[u] * 0x10001u;
   };
-  // K-step ks's packed bytes (in st) dequantised with the scales in
-  // Ssh[ks & 1] into the wave's slab ks & 1
-  auto dequant = [&](const PVWStage<NTW>& st, int ks) {
+  // the (scale, zero) words of this lane's chunks of K-step ks, from Ssh[ks & 1]
+  auto read_scales = [&](int ks, uint4 (&sz)[4]) {
+    const uint32_t* p = &Ssh[ks & 1][(2 * qsel + hh) * 20];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sz[k] = *(const uint4*)(p + 4 * k);
+  };
+  // K-step ks's packed bytes (in st) dequantised with its scale words into
+  // the wave's slab ks & 1
+  auto dequant = [&](const PVWStage<NTW>& st, int ks, const uint4 (&sz)[4]) {
     const int buf = ks & 1;
     uint16_t* sbuf = &stage[wave][buf][0];
     uint32_t s2[NCH], z2[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      s2[c] = Ssh[buf][0][2 * c + hh][qsel];
-      z2[c] = VQ == VQ_G64 ? Ssh[buf][1][2 * c + hh][qsel] : 0u;
+      s2[c] = (c & 1) ? sz[c >> 1].z : sz[c >> 1].x;
+      z2[c] = VQ == VQ_G64 ? ((c & 1) ? sz[c >> 1].w : sz[c >> 1].y) : 0u;
     }
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -756,7 +767,11 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
     publish_p(st[0], 0);
     publish_sz(st[0], 0);
     __syncthreads();
-    dequant(st[0], 0);
+    {
+      uint4 sz[4];
+      read_scales(0, sz);
+      dequant(st[0], 0, sz);
+    }
     publish_sz(st[1], 1);
     load(st[0], DEPTH);
     __syncthreads();                         // Ssh[1] published; Ssh[0] consumed
@@ -765,8 +780,10 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
       for (int d = 0; d < DEPTH; ++d) {
         const int k = ks + d;
         PVWStage<NTW>& cur = st[(d + 1) % DEPTH];          // K-step k+1
+        uint4 sz[4];
+        read_scales(k + 1, sz);                            // first: the dequantisation waits for them
         mfmas(k);
-        dequant(cur, k + 1);
+        dequant(cur, k + 1, sz);
         publish_p(cur, k + 1);
         publish_sz(st[(d + 2) % DEPTH], k + 2);            // K-step k+2's items
         load(cur, k + 1 + DEPTH);
