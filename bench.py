@@ -136,9 +136,14 @@ def build_workload(name, dev):
                "batch": B, "seq_len": S, "k_rank_total": sum(ranks), "v_rank": Rv, "heads": H}
         return dict(case=case, bytes=algorithmic_bytes(case), step=step, B=B, S=S, rope=rope, dtype="f16", config=cfg)
 
-    if name in ("cfg3", "cfg3-long"):
+    if name in ("cfg3", "cfg3-long", "cfg3-e2e", "cfg3-e2e-mask"):
         ranks = cfg2_ranks()
-        B, S = (16, 32768) if name == "cfg3" else (4, 131072)
+        # cfg3-e2e: the e2e harness's attention shape (B8, prompt 8192 + 256
+        # decode steps + 1 of cache capacity)
+        # cfg3-e2e-mask: the same under the harness's additive device mask
+        # ([B, 1, S] fp32, -1e30 on the positions not yet written)
+        B, S = {"cfg3": (16, 32768), "cfg3-long": (4, 131072), "cfg3-e2e": (8, 8449),
+                "cfg3-e2e-mask": (8, 8449)}[name]
         H, Rv, rmax = len(ranks), 1640, max(ranks)
         g = torch.Generator(device=dev).manual_seed(0)
         k_new = torch.randn(B, H, S, rmax, generator=g, device=dev, dtype=torch.float16)
@@ -154,9 +159,13 @@ def build_workload(name, dev):
         torch.cuda.empty_cache()
         rope = RopeConfig()
         out = torch.empty(B, H, HEAD_DIM, dtype=torch.float16, device=dev)
+        mask = None
+        if name == "cfg3-e2e-mask":
+            mask = torch.zeros(B, 1, S, dtype=torch.float32, device=dev)
+            mask[:, :, S - 128:] = -1e30
 
         def step(ev=None):
-            decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=S, out=out, events=ev)
+            decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=S, out=out, events=ev, mask=mask)
         G = (Rv + 63) // 64
         xk = B * S * sum(ranks) + B * H * S * 2                  # int8 + fp16 scale per (b, h, s)
         xv = B * S * Rv // 2 + B * S * G * 4                     # packed int4 + fp16 scale and zero per group
@@ -527,7 +536,7 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=100)
     ap.add_argument("--workload", default="cfg2",
                     help="cfg2 (default: the metric's workload), cfg3 (B16 S32768, K int8 + V int4-g64 cache), "
-                         "cfg3-long (B4 S131072, same formats), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S), "
+                         "cfg3-long (B4 S131072, same formats), cfg3-e2e (B8 S8449, the e2e attention shape), cfg4-<S> (llama3 GQA bf16 B1, V int4-g64, context S), "
                          "abx-<S> (the reference's abx micro-benchmark: 8 KV heads of rank 102, groups of 4, fp16, batch 1), "
                          "e2e (32-layer model, prefill 8192, greedy decode at batch 8; prints e2e decode tok/s), "
                          "prefill (one layer's 8192-token causal prefill at batch 8 over the int8 / int4-g64 "
