@@ -24,6 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ._lib import StarKVError
 from .cache import LatentCache
 from .ops import GEMM_ADD, GEMM_SILU_MUL, SKINNY_MAX_ROWS, decode_attention, prefill_attention, skinny_linear
 from .rope import RopeConfig
@@ -253,6 +254,11 @@ def _fused_decoder_forward(self, hidden_states: torch.Tensor, attention_mask=Non
         return type(self).forward(self, hidden_states, attention_mask=attention_mask, position_ids=position_ids,
                                   past_key_values=past_key_values, use_cache=use_cache,
                                   position_embeddings=position_embeddings, **kwargs)
+    _refresh_layer_(self)
+    if _recording_hidden_states():
+        # HF keeps each layer's output (and the embedding) as the hidden
+        # states it returns: update a copy, not the tensor it recorded
+        hidden_states = hidden_states.clone()
     B, T, Hd = hidden_states.shape
     eps_in, eps_post = self.input_layernorm.variance_epsilon, self.post_attention_layernorm.variance_epsilon
     if B * T <= SKINNY_MAX_ROWS and getattr(self.mlp, "gate_up_packed", None) is not None:
@@ -302,6 +308,10 @@ def _fused_norm_forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
 def _fused_lm_head_forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
     """nn.Linear forward of the output projection on ``starkv_skinny_gemm``
     (packed weight) for decode batches, torch's GEMM otherwise."""
+    if _signature((self.weight,)) != getattr(self, "_starkv_sig", None):
+        _no_capture("the output projection's weight")
+        self.packed = _pack_head(self)
+        self._starkv_sig = _signature((self.weight,))
     rows = hidden_states.numel() // hidden_states.shape[-1]
     if rows <= SKINNY_MAX_ROWS and getattr(self, "packed", None) is not None:
         return skinny_linear(hidden_states.contiguous(), self.packed)
@@ -312,6 +322,78 @@ def _packable(w: torch.Tensor) -> bool:
     return w.dim() == 2 and w.shape[0] % 32 == 0 and w.shape[1] % 64 == 0
 
 
+def _recording_hidden_states() -> bool:
+    """True while HF collects every decoder layer's output
+    (``output_hidden_states=True``: transformers' output-capturing hooks,
+    active through a context variable); True as well when that mechanism is
+    not found (another transformers version), so no recorded tensor is ever
+    updated in place."""
+    try:
+        from transformers.utils.output_capturing import _active_collector
+    except ImportError:
+        return True
+    col = _active_collector.get()
+    return col is not None and "hidden_states" in col
+
+
+def _signature(ts) -> tuple:
+    """Identity and in-place version of each tensor: it changes when a weight
+    is replaced or written (``load_state_dict``, ``load_projections``)."""
+    return tuple((t.data_ptr(), t._version) for t in ts)
+
+
+def _layer_sources(layer) -> tuple:
+    att, mlp = layer.self_attn, layer.mlp
+    return (att.q_proj.weight, att.k_vs.weight, att.v_vs.weight, layer.input_layernorm.weight, att.o_proj.weight,
+            mlp.gate_proj.weight, mlp.up_proj.weight, layer.post_attention_layernorm.weight, mlp.down_proj.weight)
+
+
+def _no_capture(what: str) -> None:
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise StarKVError(f"{what} changed since its packed copy was made: run one step eagerly (which repacks) "
+                          "before capturing a graph")
+
+
+def _fuse_layer_(layer) -> None:
+    """Merge and pack one decoder layer's weights (see ``fuse_layers_``) and
+    record the signature of the weights they were made from."""
+    from .ops import pack_weight
+    att = layer.self_attn
+    att.merge_projections_()
+    mlp = layer.mlp
+    with torch.no_grad():
+        w = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).contiguous()
+    mlp.register_buffer("gate_up_weight", w, persistent=False)
+    n = mlp.gate_proj.weight.shape[0]
+    mlp.gate_proj.weight = nn.Parameter(w[:n], requires_grad=False)
+    mlp.up_proj.weight = nn.Parameter(w[n:], requires_grad=False)
+    mlp.gate_up_packed = None
+    # qkv rows need 16 (tiles), the others 32 (gate/up halves), k 64
+    if (att.qkv_weight.shape[0] % 16 == 0 and att.qkv_weight.shape[1] % 64 == 0
+            and all(_packable(t) for t in (att.o_proj.weight, w, mlp.down_proj.weight))):
+        with torch.no_grad():
+            att.qkv_packed = pack_weight(att.qkv_weight, layer.input_layernorm.weight)
+            att.o_packed = pack_weight(att.o_proj.weight)
+            mlp.gate_up_packed = pack_weight(w, layer.post_attention_layernorm.weight)
+            mlp.down_packed = pack_weight(mlp.down_proj.weight)
+    layer._starkv_sig = _signature(_layer_sources(layer))
+
+
+def _refresh_layer_(layer) -> None:
+    """Re-merge and repack a layer whose weights changed after
+    ``fuse_layers_`` (the merged and packed copies would otherwise keep the
+    old values); refused inside a graph capture."""
+    if _signature(_layer_sources(layer)) != getattr(layer, "_starkv_sig", None):
+        _no_capture("a decoder layer's weight")
+        _fuse_layer_(layer)
+
+
+def _pack_head(head):
+    from .ops import pack_weight
+    with torch.no_grad():
+        return pack_weight(head.weight)
+
+
 def fuse_layers_(model) -> None:
     """Run every decoder layer of ``model`` (and the final norm) through
     ``_fused_decoder_forward``: q / k / v latent projections and the MLP's
@@ -320,35 +402,20 @@ def fuse_layers_(model) -> None:
     activation on the library's kernels.  For decode batches each layer's
     four projections also get a packed copy for ``starkv_skinny_gemm``
     (``pack_weight``), the input and post-attention RMSNorm weights folded
-    into the q/k/v and gate/up copies."""
+    into the q/k/v and gate/up copies.  Each layer (and the output
+    projection) records the version of the weights its copies come from and
+    rebuilds them when a weight has been replaced or written since
+    (``load_state_dict``, ``load_projections``)."""
     import types
-    from .ops import pack_weight
     for layer in model.model.layers:
-        att = layer.self_attn
-        att.merge_projections_()
-        mlp = layer.mlp
-        with torch.no_grad():
-            w = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).contiguous()
-        mlp.register_buffer("gate_up_weight", w, persistent=False)
-        n = mlp.gate_proj.weight.shape[0]
-        mlp.gate_proj.weight = nn.Parameter(w[:n], requires_grad=False)
-        mlp.up_proj.weight = nn.Parameter(w[n:], requires_grad=False)
-        mlp.gate_up_packed = None
-        # qkv rows need 16 (tiles), the others 32 (gate/up halves), k 64
-        if (att.qkv_weight.shape[0] % 16 == 0 and att.qkv_weight.shape[1] % 64 == 0
-                and all(_packable(t) for t in (att.o_proj.weight, w, mlp.down_proj.weight))):
-            with torch.no_grad():
-                att.qkv_packed = pack_weight(att.qkv_weight, layer.input_layernorm.weight)
-                att.o_packed = pack_weight(att.o_proj.weight)
-                mlp.gate_up_packed = pack_weight(w, layer.post_attention_layernorm.weight)
-                mlp.down_packed = pack_weight(mlp.down_proj.weight)
+        _fuse_layer_(layer)
         layer.forward = types.MethodType(_fused_decoder_forward, layer)
     model.model.norm.forward = types.MethodType(_fused_norm_forward, model.model.norm)
     head = model.lm_head
     head.packed = None
     if _packable(head.weight) and head.bias is None:
-        with torch.no_grad():
-            head.packed = pack_weight(head.weight)
+        head.packed = _pack_head(head)
+        head._starkv_sig = _signature((head.weight,))
         head.forward = types.MethodType(_fused_lm_head_forward, head)
 
 

@@ -14,7 +14,7 @@ import sys
 import pytest
 import torch
 
-from _util import KernelRecorder, cfg2_ranks
+from _util import KernelRecorder, cfg2_ranks, errors
 
 pytestmark = pytest.mark.gpu
 
@@ -85,6 +85,60 @@ def test_e2e_graph_replay_matches_eager(fmt):
     _compare_logits(logits, ref_logits, tol=1e-3)
     assert torch.equal(toks, ref_toks)
     assert all(layer.self_attn.cache.length == P + steps for layer in model.model.layers)
+
+
+@pytest.mark.gpu
+def test_fused_layers_follow_loaded_weights():
+    """fuse_layers_ packs decode copies of each layer's weights (norms folded
+    in) and of the output projection; weights loaded afterwards
+    (load_state_dict, written in place) must reach them: a model built with
+    one seed that loads another seed's state decodes like a model built with
+    that seed."""
+    from starkv.e2e import build_model, generate
+    _flush("[e2e] fused layers after load_state_dict")
+    B, P, steps = 2, 24, 4
+    kw = dict(n_layers=2, hidden=1024, heads=8, kv_heads=2, intermediate=2048, vocab=1000, ranks=[48, 96],
+              v_rank=256, batch=B, capacity=P + steps + 3, fmt="int8_g64")
+    prompt = torch.randint(0, 1000, (B, P), generator=torch.Generator(device="cuda").manual_seed(8), device="cuda")
+    want = build_model(seed=5, **kw)
+    toks, logits = generate(want, prompt, steps)
+    model = build_model(seed=4, **kw)
+    model.load_state_dict(want.state_dict())
+    got_toks, got = generate(model, prompt, steps, forced=toks[:, :steps])
+    torch.cuda.synchronize()
+    _compare_logits(got, logits, tol=1e-3)
+    assert torch.equal(got_toks, toks)
+
+
+@pytest.mark.gpu
+def test_fused_layers_keep_recorded_hidden_states():
+    """The fused decoder layer updates the residual stream in place; with
+    output_hidden_states=True HF keeps every layer's output, so those must
+    survive the layers after them: each recorded hidden state matches the
+    reference path's (HF's own layers over the same latent attention)."""
+    from starkv.e2e import attention_layers, build_model
+    _flush("[e2e] output_hidden_states through the fused layers")
+    B, P = 2, 24
+    kw = dict(n_layers=3, hidden=1024, heads=8, kv_heads=2, intermediate=2048, vocab=1000, ranks=[48, 96],
+              v_rank=256, batch=B, capacity=P + 4, fmt="int8_g64", seed=6)
+    prompt = torch.randint(0, 1000, (B, P), generator=torch.Generator(device="cuda").manual_seed(9), device="cuda")
+    pos = torch.arange(P, device="cuda")[None].expand(B, P)
+    outs = []
+    for reference in (False, True):
+        model = build_model(**kw)
+        for att in attention_layers(model):
+            att.reference = reference
+        model.model.norm.starkv_reference = reference
+        with torch.no_grad():
+            outs.append(model(input_ids=prompt, position_ids=pos, use_cache=False, output_hidden_states=True))
+    torch.cuda.synchronize()
+    got, ref = outs[0].hidden_states, outs[1].hidden_states
+    assert len(got) == len(ref) == kw["n_layers"] + 1
+    for i, (g, r) in enumerate(zip(got, ref)):
+        mx, mr = errors(g.float(), r.float())
+        _flush(f"   hidden state {i}: max_abs={mx:.3e} mean_rel={mr:.3e}")
+        assert mr <= 1e-2, (i, mr)
+    assert not torch.equal(got[1], got[-1])
 
 
 def test_e2e_graph_state_reports_a_skipped_row():
