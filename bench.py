@@ -261,7 +261,8 @@ def build_workload(name, dev):
 def graphed_attention_ms(atts, B, reps=20):
     """The attention work of one graph-replayed decode step on its own: for
     every layer the cache write with the query rotation (one launch) and the
-    decode attention over the whole cache capacity under the device mask --
+    decode attention over the whole cache capacity, positions past the
+    device-held write position at -1e30 --
     the calls LatentAttention.core makes in the captured step, on the same
     caches at the same length -- captured in one graph of their own and
     replayed; returns ms per replay.  (Each replay rewrites the first free
@@ -274,7 +275,6 @@ def graphed_attention_ms(atts, B, reps=20):
     L, cap = a0.cache.length, a0.cache.cap
     assert L < cap, "the attention-only graph writes one free cache position"
     state = DecodeGraphState(B, cap, L, dev)
-    state.open_position()
     g = torch.Generator(device=dev).manual_seed(11)
     bufs = [(torch.randn(B, a.n_heads, 1, HEAD_DIM, generator=g, device=dev).half(),
              torch.randn(B, 1, sum(a.ranks), generator=g, device=dev).half(),
@@ -284,7 +284,7 @@ def graphed_attention_ms(atts, B, reps=20):
         for a, (q, k, v) in zip(atts, bufs):
             ks, vs = a.cache.append_at(k, v, a.bk, state.pos, error_flag=state.error, q=q, rope=a.rope)
             decode_attention(q[:, :, 0], ks, vs, a.v_u.weight, rope=a.rope, seq_len=state.capacity,
-                             scale=a.scaling, mask=state.mask)
+                             scale=a.scaling, last_pos=state.pos)
 
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))

@@ -24,7 +24,7 @@ extern "C" {
 
 /* Bumped on every change of a struct layout or of an entry point's meaning;
  * the Python binding refuses a library of another version. */
-#define STARKV_ABI_VERSION 4
+#define STARKV_ABI_VERSION 5
 
 /* element types */
 enum {
@@ -262,6 +262,11 @@ typedef struct {
   float scale;
   const void* mask; int mask_dtype; int64_t mask_stride_b, mask_stride_h;   /* optional */
   void* out; int out_dtype; int64_t out_stride_b, out_stride_h;
+  /* optional: a device int; positions after *last_pos_device take the logit
+   * -1e30, as an additive mask of -1e30 would give them (a context length
+   * kept on the device, for steps replayed from one captured graph; no
+   * counterpart in the reference, whose eager decode passes the length) */
+  const int* last_pos_device;
 } starkv_decode_desc;
 
 size_t starkv_decode_workspace_bytes(const starkv_decode_desc* d);

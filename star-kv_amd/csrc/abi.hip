@@ -906,6 +906,7 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.bk = d->k.bk; a.bk_rs = d->k.bk_row_stride;
   a.rope = (const uint4*)d->rope_table;
   a.mask = d->mask; a.m_sb = d->mask_stride_b; a.m_sh = d->mask_stride_h; a.mask_dtype = d->mask_dtype;
+  a.last_pos = nullptr;
   a.out = d->out; a.o_sb = d->out_stride_b; a.o_st = TILE; a.o_sh = d->out_stride_h;   // rows
   a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
@@ -981,6 +982,7 @@ static int decode_impl(const starkv_decode_desc* d, void* workspace, size_t work
   ka.bk = d->k.bk; ka.bk_rs = d->k.bk_row_stride;
   ka.rope = (const uint4*)d->rope_table;
   ka.mask = d->mask; ka.m_sb = d->mask_stride_b; ka.m_sh = d->mask_stride_h; ka.mask_dtype = d->mask_dtype;
+  ka.last_pos = d->last_pos_device;
   // logits in 32-position tiles of all heads: a tile's 4 KB is written together
   // by the workgroups of one chunk and read contiguously by P.V
   ka.out = ws + L.off_logits; ka.o_sb = (int64_t)Hq * L.S_pad; ka.o_st = (int64_t)Hq * TILE; ka.o_sh = TILE;

@@ -54,6 +54,7 @@ struct KArgs {
   const void* bk; int64_t bk_rs;
   const uint4* rope;                               // RoPE operand table [tile][8][64] x 16 B
   const void* mask; int64_t m_sb, m_sh; int mask_dtype;
+  const int* last_pos;                             // optional (device): positions past it take -1e30
   // logit (b, q, s) at out + b*o_sb + (s / 32)*o_st + q*o_sh + s % 32: rows
   // (o_st = 32) or 32-position tiles of all heads (o_sh = 32, o_st = Hq*32)
   void* out; int64_t o_sb, o_st, o_sh;

@@ -25,6 +25,8 @@
 // has rank > 64, packed on the host so ragged head-wise ranks are balanced.
 // A wave streams its latent rows two tiles ahead in registers; the MFMA
 // result of each item is consumed before the next item's MFMAs.
+#include <climits>
+
 #include "common.hpp"
 
 namespace starkv {
@@ -280,6 +282,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
       for (int p = 0; p < TPT; ++p) Ts[slot][j][tid + p * NT] = ts.v[j][p];
   };
 
+  // positions past a device-held last position take -1e30 (read once)
+  const int lastp = a.last_pos != nullptr ? *a.last_pos : INT_MAX;
   auto compute = [&](const KBuf<XFMT, MAXI>& kb, int tile, int slot, int j) __attribute__((always_inline)) {
     const int s = tile * TILE + t;
     const bool store = tile < tile1 && s < S;
@@ -312,6 +316,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
         const int qh = item_qh(it[i]);
         if (store) {
           if (a.mask != nullptr) tot += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
+          if (s > lastp) tot = -1e30f;
           const int64_t o = b * a.o_sb + (int64_t)(s >> 5) * a.o_st + qh * a.o_sh + (s & 31);
           if constexpr (OUTK == 0) ((float*)a.out)[o] = tot;
           else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)tot;

@@ -35,6 +35,8 @@
 // rotation -> q.K MFMAs).  The p = 0 wave hands its partial logits of a
 // tile to the p = 1 wave through LDS one tile later; the p = 1 wave adds
 // its own and stores.
+#include <climits>
+
 #include "common.hpp"
 
 namespace starkv {
@@ -212,6 +214,8 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
   for (int v = 0; v < 4; ++v) mx[v] = -INFINITY;
   float prev[4] = {0.f, 0.f, 0.f, 0.f};      // this wave's partial logits of the tile before the current one
 
+  // positions past a device-held last position take -1e30 (read once)
+  const int lastp = a.last_pos != nullptr ? *a.last_pos : INT_MAX;
   // epilogue of tile `ti` (absolute tile index): scale, mask, store, maxima
   // (one store instruction per v < min(gs, 4): lane t = 0 of lane half 0
   // always stores, so none is skipped; the DMA waits count them)
@@ -225,6 +229,7 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
       const int qh = kv * gs + h;
       float val = wscale * sum[v];
       if constexpr (MASKED) val += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
+      if (s > lastp) val = -1e30f;
       const int64_t o = b * a.o_sb + (int64_t)ti * a.o_st + qh * a.o_sh + t;
       if constexpr (OUTK == 0) ((float*)a.out)[o] = val;
       else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)val;

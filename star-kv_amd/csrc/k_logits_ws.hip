@@ -40,6 +40,8 @@
 // workgroup barriers, the producers issue the DMA of tile i+nst-1 into the
 // stage consumed at tile i-1, and the consumers compute tile i.  One extra
 // barrier after the last tile publishes the last straddle partials.
+#include <climits>
+
 #include "common.hpp"
 
 namespace starkv {
@@ -393,10 +395,13 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) mx[i] = -INFINITY;
 
+  // positions past a device-held last position take -1e30 (read once)
+  const int lastp = a.last_pos != nullptr ? *a.last_pos : INT_MAX;
   // logit epilogue of one head at position s: mask, store, running maximum
   auto emit = [&](float v, int qh, int s, float& m) __attribute__((always_inline)) {
     if (s < S) {
       if (a.mask != nullptr) v += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
+      if (s > lastp) v = -1e30f;
       if (hh == 0) {                         // both halves hold the sum; one stores
         const int64_t o = b * a.o_sb + (int64_t)(s >> 5) * a.o_st + qh * a.o_sh + (s & 31);
         if constexpr (OUTK == 0) ((float*)a.out)[o] = v;

@@ -97,6 +97,7 @@ class DecodeDesc(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("mask", ctypes.c_void_p), ("mask_dtype", ctypes.c_int), ("mask_stride_b", ctypes.c_int64), ("mask_stride_h", ctypes.c_int64),
         ("out", ctypes.c_void_p), ("out_dtype", ctypes.c_int), ("out_stride_b", ctypes.c_int64), ("out_stride_h", ctypes.c_int64),
+        ("last_pos_device", ctypes.c_void_p),
     ]
 
 
@@ -197,7 +198,7 @@ EXPORTS = (
     "starkv_rms_norm", "starkv_silu_mul", "starkv_skinny_gemm",
 )
 
-ABI_VERSION = 4          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
+ABI_VERSION = 5          # STARKV_ABI_VERSION of include/starkv.h that these structs mirror
 NOALLOC_SCRATCH_BYTES = 128 << 20   # STARKV_NOALLOC_SCRATCH_BYTES
 
 _lib = None

@@ -41,17 +41,15 @@ def _rotate_half(x: torch.Tensor) -> torch.Tensor:
 
 
 class DecodeGraphState:
-    """Device-side decode position and mask shared by every layer of a decode
-    step captured once in a CUDA/HIP graph.  Each replay writes the new latents
-    at ``pos`` and attends over the whole cache capacity, the positions not
-    yet written masked off by an additive -1e30; ``open_position`` and
-    ``advance`` run inside the graph."""
+    """Device-side decode position shared by every layer of a decode step
+    captured once in a CUDA/HIP graph.  Each replay writes the new latents at
+    ``pos`` and attends over the whole cache capacity; the decode kernels read
+    ``pos`` and give the positions after it (not yet written) the logit
+    -1e30.  ``advance`` runs inside the graph."""
 
     def __init__(self, batch: int, capacity: int, length: int, device):
         self.capacity = int(capacity)
         self.pos = torch.tensor([length], dtype=torch.int32, device=device)
-        self.mask = torch.full((batch, 1, self.capacity), -1e30, dtype=torch.float32, device=device)
-        self.mask[:, :, :length] = 0.0
         # set by the RoPE and cache-writer kernels when a replay's position
         # falls outside the capacity (they skip those rows)
         self.error = torch.zeros(1, dtype=torch.int32, device=device)
@@ -61,9 +59,6 @@ class DecodeGraphState:
         if int(self.error.item()) != 0:
             from ._lib import StarKVError
             raise StarKVError("a graph-replayed decode step ran past the latent cache's capacity")
-
-    def open_position(self):
-        self.mask.index_fill_(2, self.pos.long(), 0.0)
 
     def advance(self):
         self.pos.add_(1)
@@ -213,7 +208,7 @@ class LatentAttention(nn.Module):
             kspec, vspec = self.cache.append_at(k_new, v_new, self.bk, self.graph.pos, error_flag=self.graph.error,
                                                 q=q, rope=self.rope)
             o = decode_attention(q[:, :, 0], kspec, vspec, self.v_u.weight, rope=self.rope,
-                                 seq_len=self.graph.capacity, scale=self.scaling, mask=self.graph.mask)
+                                 seq_len=self.graph.capacity, scale=self.scaling, last_pos=self.graph.pos)
             return o.unsqueeze(1).reshape(B, T, self.n_heads * HEAD_DIM)
         if self.reference:
             kspec, vspec, S = self.cache.append(k_new, v_new, self.bk)
@@ -539,7 +534,6 @@ def decode_graphed(model, tok: torch.Tensor, steps: int, keep_logits: bool = Tru
         # per-forward position, mask and rotary bookkeeping: the latent
         # attentions take their positions from the graph state
         nonlocal logit_buf
-        state.open_position()
         h = model.model.embed_tokens(tok_buf)
         for layer in model.model.layers:
             h = layer(h, attention_mask=None, position_ids=pos_buf, position_embeddings=None)

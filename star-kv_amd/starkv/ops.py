@@ -385,20 +385,27 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
                      rope: RopeConfig = RopeConfig(), seq_len: Optional[int] = None,
                      mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                      out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
-                     events: Optional[Sequence] = None, noalloc: bool = False) -> torch.Tensor:
+                     events: Optional[Sequence] = None, noalloc: bool = False,
+                     last_pos: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused decode attention core (model.py:450-487): [B, Hq, 128] in q's dtype
     (or float32 with out_dtype=torch.float32).  ``events``: four
     torch.cuda.Event recorded around the three kernels (timing).
     ``noalloc``: run starkv_decode_attention_noalloc, whose workspace is the
     library's own device array (no workspace allocation; with ``out`` given
     the call allocates nothing at all).
+    ``last_pos``: an int32 device tensor whose first element is read by the
+    kernels: positions after it take the logit -1e30, as an additive -1e30
+    mask would give them (a context length kept on the device for graph
+    replay; the caller keeps it alive while the call or a captured graph runs).
 
     q: rotated query [B, Hq, 128]; k: key-latent spec; xv: V latent [B, S, Rv]
     (dense tensor) or a VLatentSpec; uv_weight: v_proj.U.weight [Hkv*128, Rv];
     seq_len defaults to the V latent's position count."""
     q = _q3(q)
     v = _vspec(xv)
-    _require_cuda(q, uv_weight, mask, *k.tensors, *v.tensors)
+    _require_cuda(q, uv_weight, mask, last_pos, *k.tensors, *v.tensors)
+    if last_pos is not None and (last_pos.dtype != torch.int32 or last_pos.numel() < 1):
+        raise StarKVError("last_pos must be an int32 device tensor with at least one element")
     B, Hq, _ = q.shape
     S = int(seq_len if seq_len is not None else v.data.shape[1])
     if uv_weight.dim() != 2 or uv_weight.stride(1) != 1 or uv_weight.shape[1] != v.rank:
@@ -425,6 +432,7 @@ def decode_attention(q: torch.Tensor, k: KLatentSpec, xv: torch.Tensor, uv_weigh
     d.mask_dtype, d.mask_stride_b, d.mask_stride_h = mdt, msb, msh
     d.out, d.out_stride_b, d.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
     d.out_dtype = F32 if out.dtype == torch.float32 else 0
+    d.last_pos_device = last_pos.data_ptr() if last_pos is not None else None
     L = _lib.lib()
     if noalloc:
         if events is not None:

@@ -44,7 +44,7 @@ def test_version_and_status_strings():
     header_version = int(m.group(1))
     # the library, the header and the ctypes mirrors must agree: a struct
     # layout change bumps all three together
-    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 4
+    assert lib.starkv_abi_version() == header_version == L.ABI_VERSION == 5
     for code in (OK, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_RANK, ERR_WORKSPACE, ERR_LIMIT, ERR_FORMAT):
         s = lib.starkv_status_string(code).decode()
         assert s and s != "unknown error"
@@ -66,7 +66,7 @@ int main(void) {
   S(starkv_pv_desc) F(starkv_pv_desc, p) F(starkv_pv_desc, v) F(starkv_pv_desc, out_stride_h)
   S(starkv_decode_desc) F(starkv_decode_desc, k) F(starkv_decode_desc, v) F(starkv_decode_desc, uv)
   F(starkv_decode_desc, rope_table) F(starkv_decode_desc, scale) F(starkv_decode_desc, mask) F(starkv_decode_desc, out_dtype)
-  F(starkv_decode_desc, out_stride_h)
+  F(starkv_decode_desc, out_stride_h) F(starkv_decode_desc, last_pos_device)
   S(starkv_k_append_desc) F(starkv_k_append_desc, k) F(starkv_k_append_desc, src_head_offset)
   F(starkv_k_append_desc, pos0_device) F(starkv_k_append_desc, error_flag)
   S(starkv_v_append_desc) F(starkv_v_append_desc, v) F(starkv_v_append_desc, pos0_device)

@@ -14,6 +14,7 @@ pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
 MEAN_REL = 1e-3
+HEAD_DIM_T = 128
 
 
 def _flush(msg):
@@ -222,3 +223,68 @@ def test_k_logits_gqa_bf16_beyond_fp16_range(latent_scale, q_scale):
     mx, mr = errors(out / rms, ref / rms)
     print(f"   RMS {rms:.3e}: max_abs/RMS={mx:.3e} mean_rel={mr:.3e}", flush=True)
     assert mx <= 2e-2 and mr <= 1e-3
+
+
+LAST_POS_CASES = [
+    # name, B, Hq, Hkv, S, ranks, Rv, layout: each K-logit kernel family
+    ("mha_ws_dense", 2, 32, 32, 700, None, 256, "ragged"),
+    ("gqa4_dense", 2, 32, 8, 700, [32, 128, 32, 80, 32, 64, 80, 64], 256, "ragged"),
+    ("unaligned_r_streaming", 2, 32, 32, 129, [20] * 32, 50, "reference"),
+]
+
+
+@pytest.mark.parametrize("name,B,Hq,Hkv,S,ranks,Rv,layout", LAST_POS_CASES, ids=[c[0] for c in LAST_POS_CASES])
+def test_decode_last_pos_matches_additive_mask(name, B, Hq, Hkv, S, ranks, Rv, layout):
+    """A device-held last position (positions after it at -1e30) gives the
+    outputs of the additive -1e30 mask over the same positions, and both
+    match the oracle."""
+    from starkv import RopeConfig, decode_attention
+    ranks = ranks or cfg2_ranks()
+    _flush(f"[decode last_pos] {name}")
+    case = make_case(B, Hq, Hkv, S, ranks, Rv, seed=21, layout=layout)
+    last = S - 1 - S // 5
+    mask = torch.zeros(B, 1, S, device="cuda", dtype=torch.float32)
+    mask[..., last + 1:] = -1e30
+    lp = torch.tensor([last], dtype=torch.int32, device="cuda")
+    rope = RopeConfig()
+    a = decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, last_pos=lp)
+    m = decode_attention(case.q, case.kspec, case.xv, case.uv, rope=rope, mask=mask)
+    ref, _, _ = oracle_decode(case, mask=mask.double().cpu())
+    mx, mr = errors(a, m.float())
+    _flush(f"   last_pos vs mask: max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mx <= 1e-3 and mr <= 1e-5, (mx, mr)
+    mx, mr = errors(a, ref)
+    _flush(f"   last_pos vs oracle: max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mx <= MAX_ABS and mr <= MEAN_REL, (mx, mr)
+
+
+def test_decode_last_pos_int8_k_cache():
+    """The same over the int8-K / int4-g64-V cache the e2e harness decodes
+    from: the warp-specialised int8 K-logit kernel takes its pipelined loop
+    under last_pos and its mask loop under the additive mask."""
+    from starkv import RopeConfig, decode_attention
+    from starkv.cache import LatentCache
+    _flush("[decode last_pos] int8 K cache")
+    ranks, B, S, Rv = cfg2_ranks(), 2, 1500, 1640
+    H, rmax = len(ranks), max(ranks)
+    g = torch.Generator(device="cuda").manual_seed(22)
+    k_new = torch.randn(B, H, S, rmax, generator=g, device="cuda").half()
+    v_new = torch.randn(B, S, Rv, generator=g, device="cuda").half()
+    bk = (torch.randn(H, rmax, HEAD_DIM_T, generator=g, device="cuda") / math.sqrt(rmax)).half()
+    uv = (torch.randn(H * HEAD_DIM_T, Rv, generator=g, device="cuda") / math.sqrt(Rv)).half()
+    q = torch.randn(B, H, HEAD_DIM_T, generator=g, device="cuda").half()
+    cache = LatentCache(B, ranks, Rv, S + 7, torch.float16, "cuda", fmt="int8_g64")
+    kspec, vspec, _ = cache.append(k_new, v_new, bk)
+    cap = S + 7
+    last = S - 1
+    mask = torch.zeros(B, 1, cap, device="cuda", dtype=torch.float32)
+    mask[..., last + 1:] = -1e30
+    lp = torch.tensor([last], dtype=torch.int32, device="cuda")
+    rope = RopeConfig()
+    a = decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=cap, last_pos=lp)
+    m = decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=cap, mask=mask)
+    e = decode_attention(q, kspec, vspec, uv, rope=rope, seq_len=S)
+    for nm, other in (("mask", m), ("length", e)):
+        mx, mr = errors(a, other.float())
+        _flush(f"   last_pos vs {nm}: max_abs={mx:.3e} mean_rel={mr:.3e}")
+        assert mx <= 2e-3 and mr <= 1e-4, (nm, mx, mr)

@@ -215,8 +215,8 @@ def test_e2e_decode_over_exported_ragged_projections(fmt):
 
 def test_e2e_graphed_decode_cfg5_layer_matches_oracle():
     """The path the e2e tok/s times: decode steps replayed from one captured
-    graph, each attention over the whole cache capacity under the device mask
-    (the not yet written positions at -1e30), at the e2e workload's layer
+    graph, each attention over the whole cache capacity with the positions
+    after the device-held write position at -1e30, at the e2e workload's layer
     shape (hidden 4096, MHA 32 x 128, cfg2 ranks int8 K, V rank 1640 int4
     group-64) with capacity past the length.  Every layer's attention output
     of every step -- the eager first step and each replay, whose recorded
@@ -237,7 +237,7 @@ def test_e2e_graphed_decode_cfg5_layer_matches_oracle():
         with KernelRecorder(e2e) as rec:
             def on_step(i):
                 calls = rec.calls[-L:]
-                assert len(calls) == L and all(c["kind"] == "decode" and c["S"] == cap and c["mask"] is not None
+                assert len(calls) == L and all(c["kind"] == "decode" and c["S"] == cap and int(c["last_pos"].reshape(-1)[0]) == P + i
                                                for c in calls)
                 view = KernelRecorder(e2e)
                 view.calls = calls
