@@ -522,6 +522,8 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
   const int64_t max_ks = std::max<int64_t>(1, ((int64_t)1 << 31) / std::max<int64_t>(row_bytes, 1) / KSTEP);
   n = std::max<int64_t>(n, ceil_div(n_ks, max_ks));
   g.c2_len = (int)ceil_div(n_ks, n) * KSTEP;
+  // the all-columns kernels take whole 32-position steps (a chunk still below 2 GB)
+  if (wide) g.c2_len = (int)std::min<int64_t>(round_up(g.c2_len, 2 * KSTEP), std::max<int64_t>(2 * KSTEP, max_ks * KSTEP / (2 * KSTEP) * (2 * KSTEP)));
   g.n_c2 = (int)ceil_div(S, g.c2_len);
   g.n_grp = g.n_c2 > PV_RG ? (int)ceil_div(g.n_c2, PV_RG) : 0;
   return g;

@@ -828,6 +828,329 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
   }
 }
 
+// Fused group-64 int4 P.V over all columns, with the V latent staged raw.
+//
+// As pv_wide_kernel (8 waves over all column tiles of one position chunk,
+// each K-step's exponentials formed once and shared through LDS), but the
+// packed rows go to LDS as they are and are dequantised after a transposed
+// read, so LDS carries 1 byte per latent element instead of 4 (the fp16
+// value written and read back):
+// * a K-step is 32 positions; the workgroup copies their rows (ranks padded
+//   to whole 64-rank groups, LDS row pitch PB = 8 * odd bytes) into a ring of
+//   four stages with buffer_load_dword ... lds, one descriptor per K-step
+//   whose range ends at the chunk's last row, so the copy needs no registers
+//   and no address arithmetic per K-step;
+// * wave w owns whole groups (two 32-column tiles each, the groups shared out
+//   so that the two waves of a SIMD hold 14 or fewer tiles at Rv 1640) and
+//   reads a tile with one ds_read_b64_tr_b4, the gfx950 transposed 4-bit
+//   read: within a 16-lane group, lane j receives nibble j of the 8 bytes
+//   each of the 16 lanes addresses (element i from lane i).  Lane (n, hh)
+//   addresses row 16 hh + n % 16, ranks 16 (n / 16) .. +15 of the tile, so it
+//   receives column n at rows 16 hh + 0..15: the B operands of two 32x32x16
+//   MFMAs (rows 16 hh + 0..7, then 16 hh + 8..15);
+// * the nibbles are dequantised there to the exact fp16(n * s + z) of the
+//   other kernels: masked into bytes (the even rows' nibbles, then the odd
+//   rows'), two bytes at a time go through v_cvt_scalef32_pk_f16_fp8 with
+//   scale 512 -- a byte n <= 15 read as fp8 e4m3 is exactly n / 512 (n < 8
+//   subnormal, 8..15 normal), so each pair becomes the exact fp16 pair (n_a,
+//   n_b) -- and one packed FMA applies the pair's scales and zero points,
+//   rounding once.  The pairs come out as rows 0 2 4 6 1 3 5 7 of each 8, the
+//   K order of the MFMA, which the A operand (P) and the staged scale / zero
+//   pairs follow.
+// Logits and scale / zero items go through registers two K-steps ahead and
+// are published (exponentials, transposed scale pairs) one K-step ahead;
+// one barrier per K-step.
+constexpr int PVN_KS = 32;                       // positions per K-step
+constexpr int PVN_NGW = 4;                       // 64-rank groups per wave (Rvp <= 2048)
+constexpr int PVN_NJ = 17;                       // copy instructions per wave and K-step
+constexpr int PVN_STAGE = PVN_NJ * 8 * 256;      // bytes of one raw stage: 32 rows of <= 1032 bytes, padded
+
+__device__ inline uint2 lds_read_tr4(const uint8_t* p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const v2i r = __builtin_amdgcn_ds_read_tr4_b64_v2i32((__attribute__((address_space(3))) v2i*)(p));
+  return make_uint2((uint32_t)r.x, (uint32_t)r.y);
+}
+
+// the LDS row pitch of the raw stage for ngp 64-rank groups: whole groups
+// plus 8 bytes, an odd multiple of 8, so the 16 rows of one transposed read
+// fall on distinct banks
+__host__ __device__ constexpr int pvn_pitch(int ngp) { return 32 * ngp + 8; }
+
+template <typename VT>
+__global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
+  constexpr bool BF = __is_same(VT, __bf16);
+  constexpr int NA = BF ? 2 : 1;
+  typedef __attribute__((address_space(3))) void lds_void;
+  // four raw stages, separate arrays so that the compiler sees a stage's
+  // reads apart from the copies in flight into the others
+  __shared__ __attribute__((aligned(16))) uint8_t V0[PVN_STAGE], V1[PVN_STAGE], V2[PVN_STAGE], V3[PVN_STAGE];
+  // A operands: [buf][piece][mfma m][lane * 8 + e], e the K order 0 2 4 6 1 3 5 7
+  __shared__ __attribute__((aligned(16))) uint16_t Ash[2 * NA * 1024];
+  // scale / zero pairs per (buf, group, row half hh): 16 words, word
+  // 8 m + 4 z + k holding the scales (z = 0) or zero points (z = 1) of the
+  // two rows of pair k of MFMA m (rows 16 hh + 8 m + {0,2}, {4,6}, {1,3}, {5,7})
+  __shared__ __attribute__((aligned(16))) uint16_t Ssh[2 * 32 * 2 * 32];
+  __shared__ float Ms[32];
+  __shared__ float Ps[32];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hh = lane >> 5;
+  const int c2 = blockIdx.x, bq = blockIdx.y;
+  const int b = bq / a.n_hg, h0 = (bq - b * a.n_hg) * 32;
+  const int H = a.H;
+
+  if (tid < 256) {
+    const int q = tid >> 3, j = tid & 7;
+    float m = -INFINITY;
+    if (h0 + q < H) m = chunk_max_part(a.chunkmax + ((int64_t)b * H + h0 + q) * a.n_chunk1, a.n_chunk1, j);
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    if (j == 0) Ms[q] = h0 + q < H ? m : 0.f;
+  }
+  __syncthreads();
+
+  const int s_begin = c2 * a.c2_len;
+  const int s_end = min(a.S, s_begin + a.c2_len);
+  const int len = s_end - s_begin;
+  const int nks = (len + PVN_KS - 1) / PVN_KS;
+  const int ngp = (a.Rvp + 63) / 64;             // 64-rank groups (the last may be half a group)
+  const int PB = pvn_pitch(ngp);
+  const int ndw = a.Rv / 8;                      // dwords of a packed row (Rv a multiple of 8)
+
+  // ---- this wave's groups: ngp / 8 each, one more for the first ngp % 8
+  // waves (waves w and w + 4 share a SIMD)
+  const int gbase = ngp / 8, grem = ngp % 8;
+  const int ngw = gbase + (wave < grem ? 1 : 0);
+  const int g0 = wave * gbase + min(wave, grem);
+  const int ntile = a.Rvp / 32;
+
+  // ---- copy plan: a stage is 32 rows of PB bytes plus padding to whole
+  // 2 KB (PVN_NJ instructions of 256 bytes per wave); instruction m = wave +
+  // 8 j writes stage bytes [256 m, 256 m + 256), lane i's dword D = 64 m + i
+  // being row D / (PB / 4), dword D % (PB / 4) of the row (pad dwords re-read
+  // the row's last dword).  A K-step's descriptor ends at its last row, so
+  // rows past the chunk and the slots past row 31 read zeros (out of range:
+  // no memory access) -- every wave issues the same PVN_NJ copies.
+  const int PBd = PB / 4;
+  uint32_t voff[PVN_NJ];
+#pragma unroll
+  for (int j = 0; j < PVN_NJ; ++j) {
+    const int D = 64 * (wave + 8 * j) + lane;
+    const int r = D / PBd;
+    voff[j] = (uint32_t)r * (uint32_t)a.x_ss + 4u * (uint32_t)min(D - r * PBd, ndw - 1);
+  }
+  const uint8_t* xq = (const uint8_t*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
+  const uint32_t xp = (uint32_t)a.x_ss;
+  auto copy = [&](uint8_t* st, int ks) {
+    const int rows = max(0, min(PVN_KS, len - ks * PVN_KS));
+    // (uniform; readfirstlane keeps the descriptor in scalar registers)
+    const uint64_t base = (uint64_t)(xq + (int64_t)min(ks, nks - 1) * PVN_KS * a.x_ss);
+    const uint64_t bu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)bu, (short)0, __builtin_amdgcn_readfirstlane((int)((uint32_t)rows * xp)), 0x00020000);
+#pragma unroll
+    for (int j = 0; j < PVN_NJ; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st + 256 * (wave + 8 * j)), 4, voff[j], 0, 0, 0);
+  };
+
+  // ---- logits: thread (head eh, pair ej) takes positions 2 ej, 2 ej + 1
+  const int eh = tid >> 4, ej = tid & 15;
+  const bool hok = h0 + eh < H;
+  const float MqL = -Ms[eh] * 1.4426950408889634f;
+  // uniform bases with 32-bit lane offsets (the loads take the scalar-base form)
+  const char* lbase = (const char*)(a.logits + b * a.l_sb + (int64_t)h0 * a.l_sh);
+  const uint32_t loff = 4u * (uint32_t)(min(eh, H - 1 - h0) * (int)a.l_sh + 2 * ej);
+  const uint32_t lst = 4u * (uint32_t)a.l_st;    // bytes per logit tile (32 positions of every head)
+  const int tile_s0 = s_begin >> 5;              // c2_len is a multiple of 32
+  // Ash slots (fp16 units, without buf / piece) of the thread's two positions
+  int aslot[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int p = 2 * ej + u, q = p & 15, q8 = q & 7;
+    aslot[u] = (q >> 3) * 512 + (eh + 32 * (p >> 4)) * 8 + (q8 >> 1) + 4 * (q8 & 1);
+  }
+  // ---- scale / zero items: slot u (0, 1) of the thread is item f = tid +
+  // 512 u of [row][g] (32 x ng items), whose scale and zero point it loads
+  const int ng = (a.Rv + 63) / 64;
+  const char* sbase = (const char*)a.xs + 2 * (b * a.xs_sb + (int64_t)s_begin * a.xs_ss);
+  const char* zbase = (const char*)a.xz + 2 * (b * a.xs_sb + (int64_t)s_begin * a.xs_ss);
+  const uint32_t zp = 2u * (uint32_t)a.xs_ss;
+  int zrg[2], zdst[2];                           // row * 64 + g; the scale's u16 index within a buffer (-1: none)
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int f0 = tid + 512 * u;
+    const int f = min(f0, 32 * ng - 1);
+    const int row = f / ng, g = f - row * ng;
+    zrg[u] = row * 64 + g;
+    const int q = row & 15, q8 = q & 7;
+    const int word = 8 * (q >> 3) + 2 * (q8 & 1) + (q8 >> 2);     // the zero point: word + 4
+    zdst[u] = f0 < 32 * ng ? ((g * 2 + (row >> 4)) * 16 + word) * 2 + ((q8 >> 1) & 1) : -1;
+  }
+
+  struct Regs { float2 l; uint16_t z[4]; };      // z: scales of slots 0, 1, zero points of slots 0, 1
+  auto load = [&](Regs& R, int ks) {
+    const int kc = min(ks, nks - 1);
+    R.l = *(const float2*)(lbase + ((uint32_t)(tile_s0 + kc) * lst + loff));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t o = (uint32_t)min(kc * PVN_KS + (zrg[u] >> 6), len - 1) * zp + 2u * (uint32_t)(zrg[u] & 63);
+      R.z[u] = *(const uint16_t*)(sbase + o);
+      R.z[2 + u] = *(const uint16_t*)(zbase + o);
+    }
+  };
+  float psum = 0.f;
+  auto publish = [&](const Regs& R, int ks) {
+    const int buf = ks & 1;
+    uint16_t* ab = &Ash[buf * NA * 1024];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float lv = u ? R.l.y : R.l.x;
+      const float ex = __builtin_amdgcn_exp2f(fmaf(lv, 1.4426950408889634f, MqL));
+      const float pv = (hok && ks * PVN_KS + 2 * ej + u < len) ? ex : 0.f;
+      psum += pv;
+      if constexpr (BF) {
+        const __bf16 hi = (__bf16)pv;
+        ab[aslot[u]] = __builtin_bit_cast(uint16_t, hi);
+        ab[1024 + aslot[u]] = __builtin_bit_cast(uint16_t, (__bf16)(pv - (float)hi));
+      } else {
+        ab[aslot[u]] = __builtin_bit_cast(uint16_t, (_Float16)pv);
+      }
+    }
+    uint16_t* sd = &Ssh[buf * 2048];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (zdst[u] >= 0) {
+        sd[zdst[u]] = R.z[u];
+        sd[zdst[u] + 8] = R.z[2 + u];
+      }
+  };
+
+  floatx16 acc[2 * PVN_NGW];
+#pragma unroll
+  for (int j = 0; j < 2 * PVN_NGW; ++j) acc[j] = floatx16{};
+
+  // transposed-read address of the lane within a stage (tile 0)
+  const int tr_off = (16 * hh + (lane & 15)) * PB + 8 * ((lane >> 4) & 1);
+
+  auto compute = [&](const uint8_t* st, int ks) {
+    const int buf = ks & 1;
+    uint4 A[2][NA];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int p = 0; p < NA; ++p) A[m][p] = *(const uint4*)&Ash[(buf * NA + p) * 1024 + m * 512 + 8 * lane];
+    const uint8_t* sb = st + tr_off;
+#pragma unroll
+    for (int gi = 0; gi < PVN_NGW; ++gi) {
+      if (gi < ngw) {
+        const int g = g0 + gi;
+        const uint4* sp = (const uint4*)&Ssh[((buf * 32 + g) * 2 + hh) * 32];
+        const uint4 S0 = sp[0], Z0 = sp[1], S1 = sp[2], Z1 = sp[3];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint2 w = lds_read_tr4(sb + 32 * g + 16 * t);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            const uint32_t wm = m ? w.y : w.x;
+            const uint4 S = m ? S1 : S0, Z = m ? Z1 : Z0;
+            const uint32_t lo = wm & 0x0F0F0F0Fu, hi = (wm >> 4) & 0x0F0F0F0Fu;
+            const h2v nv[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false),
+                               __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true),
+                               __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false),
+                               __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true)};
+            const uint32_t sk[4] = {S.x, S.y, S.z, S.w}, zk[4] = {Z.x, Z.y, Z.z, Z.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              o[k] = as_u32(__builtin_elementwise_fma(nv[k], as_h2(sk[k]), as_h2(zk[k])));
+            uint4 bv = make_uint4(o[0], o[1], o[2], o[3]);
+            if constexpr (BF) {
+              bv = f16x8_to_bf16x8(bv);
+              acc[2 * gi + t] = mfma_bf16(__builtin_bit_cast(bf16x8, A[m][0]), __builtin_bit_cast(bf16x8, bv), acc[2 * gi + t]);
+              acc[2 * gi + t] = mfma_bf16(__builtin_bit_cast(bf16x8, A[m][NA - 1]), __builtin_bit_cast(bf16x8, bv), acc[2 * gi + t]);
+            } else {
+              acc[2 * gi + t] = mfma_f16(__builtin_bit_cast(half8, A[m][0]), __builtin_bit_cast(half8, bv), acc[2 * gi + t]);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  // ---- software pipeline: copies three K-steps ahead (stage k % 4),
+  // register loads two ahead (set k & 1), publication one ahead.  Iteration
+  // k: barrier (stage k and the A / scale buffers k & 1 visible; stage k - 1
+  // and buffers (k + 1) & 1 free), load k + 2, copy k + 3, compute k, wait for
+  // the loads of k + 1 (issued before the copies of k + 2 and k + 3 and the
+  // loads of k + 2, and after the copy of k + 1), publish k + 1.  The loop is
+  // unrolled by the four stages.
+  uint8_t* const VS[4] = {V0, V1, V2, V3};
+  if (nks > 0) {                                 // uniform
+    Regs R[2];
+    copy(V0, 0);
+    copy(V1, 1);
+    copy(V2, 2);
+    load(R[0], 0);
+    load(R[1], 1);
+    __builtin_amdgcn_s_waitcnt(0);               // vmcnt(0) expcnt(0) lgkmcnt(0)
+    publish(R[0], 0);
+    for (int ks = 0; ks < nks; ks += 4) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int k = ks + d;
+        if (d > 0 && k >= nks) break;            // uniform
+        __builtin_amdgcn_s_waitcnt(0xC07F);      // this wave's LDS accesses are done
+        __builtin_amdgcn_s_barrier();
+        load(R[d & 1], k + 2);
+        copy(VS[(d + 3) & 3], k + 3);
+        compute(VS[d], k);
+        constexpr int VM = 2 * PVN_NJ + 5;       // 5: the register loads of one K-step
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (VM & 15) | ((VM >> 4) << 14));
+        publish(R[(d & 1) ^ 1], k + 1);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);               // no copy may land after the wave ends
+  }
+
+  // ---- softmax sums per head (the 16 threads of a head are one wave's lanes)
+  psum += __shfl_xor(psum, 1, 64);
+  psum += __shfl_xor(psum, 2, 64);
+  psum += __shfl_xor(psum, 4, 64);
+  psum += __shfl_xor(psum, 8, 64);
+  if (ej == 0) Ps[eh] = psum;
+  __syncthreads();
+  if (tid < 32) a.psum[((int64_t)bq * a.n_c2 + c2) * 32 + tid] = Ps[tid];
+  const int Rvp = a.Rvp;
+#pragma unroll
+  for (int gi = 0; gi < PVN_NGW; ++gi) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int T = 2 * (g0 + gi) + t;
+      if (gi >= ngw || T >= ntile) continue;
+      const int col = 32 * T + n;
+      if (a.part16) {
+        _Float16* part = (_Float16*)a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
+          const float sq = Ps[q];
+          part[(int64_t)q * Rvp + col] = (_Float16)(acc[2 * gi + t][v] * (sq > 0.f ? 1.0f / sq : 0.f));
+        }
+      } else {
+        float* part = a.part + (((int64_t)bq * a.n_c2 + c2) * 32) * Rvp;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int q = 8 * (v >> 2) + 4 * hh + (v & 3);
+          part[(int64_t)q * Rvp + col] = acc[2 * gi + t][v];
+        }
+      }
+    }
+  }
+}
+
 // Drop-in path (bx): sum of the chunk partials in fixed chunk order into the
 // act-dtype output.  Each thread sums four columns of a 32x32 output tile;
 // the partial loads are issued eight chunks at a time (32 loads in flight per
@@ -936,6 +1259,10 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
   if constexpr (FUSED) {
     // the host's geometry chose the all-columns kernel (one column block)
     if (const int w = pv_wide_tiles(a.Rvp, FUSED, vq); w && a.n_cb == 1) {
+      if (vq == VQ_G64 && fast) {
+        hipLaunchKernelGGL((pv_nib_kernel<VT>), dim3(a.n_c2, BQ), dim3(512), 0, st, a);
+        return (int)hipGetLastError();
+      }
       if (w == 5) launch_pv_wide_n<VT, 5>(a, vq, fast, BQ, st);
       else if (w == 6) launch_pv_wide_n<VT, 6>(a, vq, fast, BQ, st);
       else if (w == 7) launch_pv_wide_n<VT, 7>(a, vq, fast, BQ, st);

@@ -160,6 +160,74 @@ def test_decode_with_quantised_v(kind, R, split):
     assert mr <= 1e-3 and mx <= 2e-2
 
 
+# Group-64 V of 33..64 column tiles with aligned rows takes the all-columns
+# raw-nibble P.V kernel: both activation dtypes, an odd tile count, a half
+# last group with two head groups, the largest rank, a long context (many
+# splits), contexts that are not multiples of its 32-position step.
+G64_WIDE = [("bf16_1640", torch.bfloat16, 1640, 32, 777), ("f16_1056_odd_tiles", torch.float16, 1056, 32, 650),
+            ("f16_1096_half_group_h64", torch.float16, 1096, 64, 1500), ("f16_2048", torch.float16, 2048, 32, 333),
+            ("bf16_1288_long", torch.bfloat16, 1288, 32, 6001)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,dtype,R,H,S", G64_WIDE, ids=[c[0] for c in G64_WIDE])
+def test_decode_g64_all_columns(name, dtype, R, H, S):
+    from oracle import starkv_oracle as o
+    from starkv import RopeConfig, decode_attention
+    from _util import make_case
+    _flush(f"[decode g64 all columns] {name}: R={R} H={H} S={S} {dtype}")
+    B = 2
+    case = make_case(B, H, H, S, [32, 48, 64, 16] * (H // 4), R, dtype=dtype, seed=R + S)
+    spec, deq, _ = make_quant_v("g64", B, S, R, seed=S)
+    out = decode_attention(case.q, case.kspec, spec, case.uv, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rope = RopeConfig()
+    cos, sin = o.rope_cos_sin(rope.inv_freq(), torch.arange(S), rope.attention_scaling)
+    v = torch.from_numpy(deq)
+    if dtype == torch.bfloat16:
+        v = v.to(torch.bfloat16)                     # the P.V operand, as torch_bx's .to(b.dtype)
+    ref, _, _ = o.decode_attention(case.q.cpu(), [b.cpu() for b in case.bk_heads], [x.cpu() for x in case.xk_heads],
+                                   v, case.uv.cpu(), cos, sin)
+    mx, mr = errors(out, ref)
+    _flush(f"   max_abs={mx:.3e} mean_rel={mr:.3e}")
+    assert mr <= 1e-3 and mx <= 2e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("R,S", [(1640, 700), (200, 300)])
+def test_decode_g64_dequant_bit_exact(R, S, dtype):
+    """The fused decode's dequantisation, exactly: a mask that leaves one
+    position per (batch, head) makes P one-hot (exp(0) = 1, sum 1), and a
+    one-hot U_v picks 128 V ranks per head, so every fp32 output is one
+    dequantised value fp16(n * s + z) (bf16 models: rounded once more to
+    bf16), bit for bit.  R = 1640 runs the all-columns raw-nibble P.V kernel,
+    R = 200 the column-block kernel."""
+    from starkv import decode_attention
+    from _util import make_case
+    _flush(f"[decode g64 bit-exact] R={R} S={S} {dtype}")
+    B, H = 2, 32
+    case = make_case(B, H, H, S, [32, 48, 64, 16] * 8, R, dtype=dtype, seed=R)
+    spec, deq, _ = make_quant_v("g64", B, S, R, seed=R + 1)
+    pick = [[(37 * h + 11 * b + 5) % S for h in range(H)] for b in range(B)]
+    mask = torch.full((B, H, S), -1e30, dtype=torch.float32, device="cuda")
+    for b in range(B):
+        for h in range(H):
+            mask[b, h, pick[b][h]] = 0.0
+    sel = torch.tensor([[(97 * h + 13 * d) % R for d in range(HEAD)] for h in range(H)])
+    uv = torch.zeros(H * HEAD, R, dtype=dtype)
+    uv[torch.arange(H * HEAD), sel.reshape(-1)] = 1.0
+    out = decode_attention(case.q, case.kspec, spec, uv.cuda(), mask=mask, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    v = torch.from_numpy(deq)
+    if dtype == torch.bfloat16:
+        v = v.to(torch.bfloat16)
+    want = torch.stack([torch.stack([v[b, pick[b][h]][sel[h]] for h in range(H)]) for b in range(B)]).float()
+    bad = (out.cpu() != want).sum().item()
+    _flush(f"   mismatching values: {bad} of {want.numel()}")
+    assert bad == 0
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("upper", ["int4", "int8"])
 def test_bx_dropin(upper):
