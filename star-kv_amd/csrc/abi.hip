@@ -913,6 +913,9 @@ int starkv_k_logits(const starkv_klogits_desc* d, void* workspace, size_t worksp
   a.chunkmax = nullptr;
   a.S = d->seq_len; a.Hq = d->n_q_heads; a.wscale = d->scale;
   const int n_tiles = (int)ceil_div(d->seq_len, TILE);
+  // the K-logit kernels address one batch's logits with 32-bit element offsets
+  if ((int64_t)(d->n_q_heads - 1) * d->out_stride_h + (int64_t)n_tiles * TILE >= ((int64_t)1 << 32))
+    return STARKV_ERR_LIMIT;
   int nc = choose_splits((int64_t)d->batch * plan.n_wg, device_cus() * plan.per_cu, n_tiles, 256, 3.0, 0.0);
   a.tiles_per_chunk = (int)ceil_div(n_tiles, nc);
   a.n_chunks = (int)ceil_div(n_tiles, a.tiles_per_chunk);

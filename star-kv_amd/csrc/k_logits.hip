@@ -284,6 +284,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
 
   // positions past a device-held last position take -1e30 (read once)
   const int lastp = a.last_pos != nullptr ? *a.last_pos : INT_MAX;
+  // this batch's logits: a uniform base and 32-bit element offsets (kept
+  // below 2^32 by the host)
+  char* const obase = (char*)a.out + b * a.o_sb * (OUTK == 0 ? 4 : 2);
+  const uint32_t ost = (uint32_t)a.o_st, osh = (uint32_t)a.o_sh;
   auto compute = [&](const KBuf<XFMT, MAXI>& kb, int tile, int slot, int j) __attribute__((always_inline)) {
     const int s = tile * TILE + t;
     const bool store = tile < tile1 && s < S;
@@ -317,10 +321,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_logits_kernel(const KArgs a) {
         if (store) {
           if (a.mask != nullptr) tot += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
           if (s > lastp) tot = -1e30f;
-          const int64_t o = b * a.o_sb + (int64_t)(s >> 5) * a.o_st + qh * a.o_sh + (s & 31);
-          if constexpr (OUTK == 0) ((float*)a.out)[o] = tot;
-          else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)tot;
-          else ((__bf16*)a.out)[o] = (__bf16)tot;
+          const uint32_t o = (uint32_t)(s >> 5) * ost + (uint32_t)qh * osh + (uint32_t)(s & 31);
+          if constexpr (OUTK == 0) ((float*)obase)[o] = tot;
+          else if constexpr (OUTK == 1) ((_Float16*)obase)[o] = (_Float16)tot;
+          else ((__bf16*)obase)[o] = (__bf16)tot;
           mx[i] = fmaxf(mx[i], tot);
         }
       }

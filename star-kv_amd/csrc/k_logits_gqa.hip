@@ -219,6 +219,10 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
   // epilogue of tile `ti` (absolute tile index): scale, mask, store, maxima
   // (one store instruction per v < min(gs, 4): lane t = 0 of lane half 0
   // always stores, so none is skipped; the DMA waits count them)
+  // this batch's logits: a uniform base and 32-bit element offsets (kept
+  // below 2^32 by the host)
+  char* const obase = (char*)a.out + b * a.o_sb * (OUTK == 0 ? 4 : 2);
+  const uint32_t ost = (uint32_t)a.o_st, osh = (uint32_t)a.o_sh;
   auto emit = [&](const float* sum, int ti) __attribute__((always_inline)) {
     const int s = ti * TILE + t;
 #pragma unroll
@@ -230,10 +234,10 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
       float val = wscale * sum[v];
       if constexpr (MASKED) val += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
       if (s > lastp) val = -1e30f;
-      const int64_t o = b * a.o_sb + (int64_t)ti * a.o_st + qh * a.o_sh + t;
-      if constexpr (OUTK == 0) ((float*)a.out)[o] = val;
-      else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)val;
-      else ((__bf16*)a.out)[o] = (__bf16)val;
+      const uint32_t o = (uint32_t)ti * ost + (uint32_t)qh * osh + (uint32_t)t;
+      if constexpr (OUTK == 0) ((float*)obase)[o] = val;
+      else if constexpr (OUTK == 1) ((_Float16*)obase)[o] = (_Float16)val;
+      else ((__bf16*)obase)[o] = (__bf16)val;
       mx[v] = fmaxf(mx[v], val);
     }
   };

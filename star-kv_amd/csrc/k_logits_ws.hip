@@ -398,15 +398,20 @@ __global__ __launch_bounds__((ws_consumers<XI8>() + WS_PRODUCERS) * 64, 1) void 
   // positions past a device-held last position take -1e30 (read once)
   const int lastp = a.last_pos != nullptr ? *a.last_pos : INT_MAX;
   // logit epilogue of one head at position s: mask, store, running maximum
+  // this batch's logits: a uniform base and 32-bit element offsets (the host
+  // keeps a batch's offsets below 2^32; a 64-bit per-lane address held
+  // across the tile loop had cost the int8 kernel a spill)
+  char* const obase = (char*)a.out + b * a.o_sb * (OUTK == 0 ? 4 : 2);
+  const uint32_t ost = (uint32_t)a.o_st, osh = (uint32_t)a.o_sh;
   auto emit = [&](float v, int qh, int s, float& m) __attribute__((always_inline)) {
     if (s < S) {
       if (a.mask != nullptr) v += load_elem_f32(a.mask, a.mask_dtype, b * a.m_sb + qh * a.m_sh + s);
       if (s > lastp) v = -1e30f;
       if (hh == 0) {                         // both halves hold the sum; one stores
-        const int64_t o = b * a.o_sb + (int64_t)(s >> 5) * a.o_st + qh * a.o_sh + (s & 31);
-        if constexpr (OUTK == 0) ((float*)a.out)[o] = v;
-        else if constexpr (OUTK == 1) ((_Float16*)a.out)[o] = (_Float16)v;
-        else ((__bf16*)a.out)[o] = (__bf16)v;
+        const uint32_t o = (uint32_t)(s >> 5) * ost + (uint32_t)qh * osh + (uint32_t)(s & 31);
+        if constexpr (OUTK == 0) ((float*)obase)[o] = v;
+        else if constexpr (OUTK == 1) ((_Float16*)obase)[o] = (_Float16)v;
+        else ((__bf16*)obase)[o] = (__bf16)v;
       }
       m = fmaxf(m, v);
     }
