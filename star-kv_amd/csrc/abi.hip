@@ -510,8 +510,10 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
   // one 8-wave workgroup for all columns (its 24-bit row offsets need
   // every pitch below 16 MB)
   const bool wide = pv_wide_tiles(g.Rvp, fused, vq) > 0 && row_bytes < V_MAX_PITCH;
+  // fused group-64 V of up to 16 tiles: the 4-wave raw-nibble kernel, three per CU
+  const bool nib4 = fused && vq == VQ_G64 && g.Rvp <= 512;
   g.n_cb = wide ? 1 : (int)ceil_div(g.Rvp / 32, 4 * ntw);
-  const int wg_per_cu = wide ? 1 : pv_wg_per_cu(ntw, vq);
+  const int wg_per_cu = wide ? 1 : nib4 ? 3 : pv_wg_per_cu(ntw, vq);
   const int n_ks = (int)ceil_div(S, KSTEP);
   // each extra split writes and re-reads one fp32 partial of 32 x Rvp per
   // column block, against the X_v bytes and logits the split streams
@@ -522,8 +524,9 @@ PVGeom pv_geometry(int B, int S, int Rv, bool fused, int vq, int64_t row_bytes) 
   const int64_t max_ks = std::max<int64_t>(1, ((int64_t)1 << 31) / std::max<int64_t>(row_bytes, 1) / KSTEP);
   n = std::max<int64_t>(n, ceil_div(n_ks, max_ks));
   g.c2_len = (int)ceil_div(n_ks, n) * KSTEP;
-  // the all-columns kernels take whole 32-position steps (a chunk still below 2 GB)
-  if (wide) g.c2_len = (int)std::min<int64_t>(round_up(g.c2_len, 2 * KSTEP), std::max<int64_t>(2 * KSTEP, max_ks * KSTEP / (2 * KSTEP) * (2 * KSTEP)));
+  // the all-columns and raw-nibble kernels take whole 32-position steps (a
+  // chunk still below 2 GB)
+  if (wide || nib4) g.c2_len = (int)std::min<int64_t>(round_up(g.c2_len, 2 * KSTEP), std::max<int64_t>(2 * KSTEP, max_ks * KSTEP / (2 * KSTEP) * (2 * KSTEP)));
   g.n_c2 = (int)ceil_div(S, g.c2_len);
   g.n_grp = g.n_c2 > PV_RG ? (int)ceil_div(g.n_c2, PV_RG) : 0;
   return g;

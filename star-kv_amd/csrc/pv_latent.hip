@@ -861,9 +861,6 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
 // are published (exponentials, transposed scale pairs) one K-step ahead;
 // one barrier per K-step.
 constexpr int PVN_KS = 32;                       // positions per K-step
-constexpr int PVN_NGW = 4;                       // 64-rank groups per wave (Rvp <= 2048)
-constexpr int PVN_NJ = 17;                       // copy instructions per wave and K-step
-constexpr int PVN_STAGE = PVN_NJ * 8 * 256;      // bytes of one raw stage: 32 rows of <= 1032 bytes, padded
 
 __device__ inline uint2 lds_read_tr4(const uint8_t* p) {
   typedef int v2i __attribute__((ext_vector_type(2)));
@@ -876,20 +873,37 @@ __device__ inline uint2 lds_read_tr4(const uint8_t* p) {
 // fall on distinct banks
 __host__ __device__ constexpr int pvn_pitch(int ngp) { return 32 * ngp + 8; }
 
-template <typename VT>
-__global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
+// Workgroup shapes: NWV waves of up to NGW groups each -- 8 x 4 for 33..64
+// column tiles (one workgroup per CU), 4 x 2 for up to 16 tiles (three per
+// CU).  NJ copy instructions per wave and K-step fill a stage of 32 rows
+// (padded to whole instructions); a thread forms PPT exponentials and loads
+// ZS scale items per K-step.
+template <int NWV, int NGW> struct PVNGeom {
+  static constexpr int GMAX = NWV * NGW;
+  static constexpr int NJ = (32 * pvn_pitch(GMAX) + 256 * NWV - 1) / (256 * NWV);
+  static constexpr int STAGE = NJ * NWV * 256;
+  static constexpr int PPT = 1024 / (64 * NWV);
+  static constexpr int TPH = 32 / PPT;             // threads per head
+  static constexpr int ZS = (32 * GMAX + 64 * NWV - 1) / (64 * NWV);
+  static constexpr int WGS = NWV == 8 ? 1 : 3;     // workgroups per CU (LDS)
+};
+
+template <typename VT, int NWV, int NGW>
+__global__ __launch_bounds__(NWV * 64, (PVNGeom<NWV, NGW>::WGS)) void pv_nib_kernel(const PVArgs a) {
+  typedef PVNGeom<NWV, NGW> G;
   constexpr bool BF = __is_same(VT, __bf16);
   constexpr int NA = BF ? 2 : 1;
+  constexpr int NJ = G::NJ, PPT = G::PPT, TPH = G::TPH, ZS = G::ZS, GMAX = G::GMAX;
   typedef __attribute__((address_space(3))) void lds_void;
   // four raw stages, separate arrays so that the compiler sees a stage's
   // reads apart from the copies in flight into the others
-  __shared__ __attribute__((aligned(16))) uint8_t V0[PVN_STAGE], V1[PVN_STAGE], V2[PVN_STAGE], V3[PVN_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t V0[G::STAGE], V1[G::STAGE], V2[G::STAGE], V3[G::STAGE];
   // A operands: [buf][piece][mfma m][lane * 8 + e], e the K order 0 2 4 6 1 3 5 7
   __shared__ __attribute__((aligned(16))) uint16_t Ash[2 * NA * 1024];
   // scale / zero pairs per (buf, group, row half hh): 16 words, word
   // 8 m + 4 z + k holding the scales (z = 0) or zero points (z = 1) of the
   // two rows of pair k of MFMA m (rows 16 hh + 8 m + {0,2}, {4,6}, {1,3}, {5,7})
-  __shared__ __attribute__((aligned(16))) uint16_t Ssh[2 * 32 * 2 * 32];
+  __shared__ __attribute__((aligned(16))) uint16_t Ssh[2 * GMAX * 2 * 32];
   __shared__ float Ms[32];
   __shared__ float Ps[32];
 
@@ -919,25 +933,25 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
   const int PB = pvn_pitch(ngp);
   const int ndw = a.Rv / 8;                      // dwords of a packed row (Rv a multiple of 8)
 
-  // ---- this wave's groups: ngp / 8 each, one more for the first ngp % 8
-  // waves (waves w and w + 4 share a SIMD)
-  const int gbase = ngp / 8, grem = ngp % 8;
+  // ---- this wave's groups: ngp / NWV each, one more for the first
+  // ngp % NWV waves (with 8 waves, waves w and w + 4 share a SIMD)
+  const int gbase = ngp / NWV, grem = ngp % NWV;
   const int ngw = gbase + (wave < grem ? 1 : 0);
   const int g0 = wave * gbase + min(wave, grem);
   const int ntile = a.Rvp / 32;
 
   // ---- copy plan: a stage is 32 rows of PB bytes plus padding to whole
-  // 2 KB (PVN_NJ instructions of 256 bytes per wave); instruction m = wave +
-  // 8 j writes stage bytes [256 m, 256 m + 256), lane i's dword D = 64 m + i
+  // instructions (NJ of 256 bytes per wave); instruction m = wave + NWV j
+  // writes stage bytes [256 m, 256 m + 256), lane i's dword D = 64 m + i
   // being row D / (PB / 4), dword D % (PB / 4) of the row (pad dwords re-read
   // the row's last dword).  A K-step's descriptor ends at its last row, so
   // rows past the chunk and the slots past row 31 read zeros (out of range:
-  // no memory access) -- every wave issues the same PVN_NJ copies.
+  // no memory access) -- every wave issues the same NJ copies.
   const int PBd = PB / 4;
-  uint32_t voff[PVN_NJ];
+  uint32_t voff[NJ];
 #pragma unroll
-  for (int j = 0; j < PVN_NJ; ++j) {
-    const int D = 64 * (wave + 8 * j) + lane;
+  for (int j = 0; j < NJ; ++j) {
+    const int D = 64 * (wave + NWV * j) + lane;
     const int r = D / PBd;
     voff[j] = (uint32_t)r * (uint32_t)a.x_ss + 4u * (uint32_t)min(D - r * PBd, ndw - 1);
   }
@@ -952,36 +966,36 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)bu, (short)0, __builtin_amdgcn_readfirstlane((int)((uint32_t)rows * xp)), 0x00020000);
 #pragma unroll
-    for (int j = 0; j < PVN_NJ; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st + 256 * (wave + 8 * j)), 4, voff[j], 0, 0, 0);
+    for (int j = 0; j < NJ; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st + 256 * (wave + NWV * j)), 4, voff[j], 0, 0, 0);
   };
 
-  // ---- logits: thread (head eh, pair ej) takes positions 2 ej, 2 ej + 1
-  const int eh = tid >> 4, ej = tid & 15;
+  // ---- logits: thread (head eh, ej) takes positions PPT ej .. PPT ej + PPT - 1
+  const int eh = tid / TPH, ej = tid % TPH;
   const bool hok = h0 + eh < H;
   const float MqL = -Ms[eh] * 1.4426950408889634f;
   // uniform bases with 32-bit lane offsets (the loads take the scalar-base form)
   const char* lbase = (const char*)(a.logits + b * a.l_sb + (int64_t)h0 * a.l_sh);
-  const uint32_t loff = 4u * (uint32_t)(min(eh, H - 1 - h0) * (int)a.l_sh + 2 * ej);
+  const uint32_t loff = 4u * (uint32_t)(min(eh, H - 1 - h0) * (int)a.l_sh + PPT * ej);
   const uint32_t lst = 4u * (uint32_t)a.l_st;    // bytes per logit tile (32 positions of every head)
   const int tile_s0 = s_begin >> 5;              // c2_len is a multiple of 32
-  // Ash slots (fp16 units, without buf / piece) of the thread's two positions
-  int aslot[2];
+  // Ash slots (fp16 units, without buf / piece) of the thread's positions
+  int aslot[PPT];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int p = 2 * ej + u, q = p & 15, q8 = q & 7;
+  for (int u = 0; u < PPT; ++u) {
+    const int p = PPT * ej + u, q = p & 15, q8 = q & 7;
     aslot[u] = (q >> 3) * 512 + (eh + 32 * (p >> 4)) * 8 + (q8 >> 1) + 4 * (q8 & 1);
   }
-  // ---- scale / zero items: slot u (0, 1) of the thread is item f = tid +
-  // 512 u of [row][g] (32 x ng items), whose scale and zero point it loads
+  // ---- scale / zero items: slot u < ZS of the thread is item f = tid +
+  // 64 NWV u of [row][g] (32 x ng items), whose scale and zero point it loads
   const int ng = (a.Rv + 63) / 64;
   const char* sbase = (const char*)a.xs + 2 * (b * a.xs_sb + (int64_t)s_begin * a.xs_ss);
   const char* zbase = (const char*)a.xz + 2 * (b * a.xs_sb + (int64_t)s_begin * a.xs_ss);
   const uint32_t zp = 2u * (uint32_t)a.xs_ss;
-  int zrg[2], zdst[2];                           // row * 64 + g; the scale's u16 index within a buffer (-1: none)
+  int zrg[ZS], zdst[ZS];                         // row * 64 + g; the scale's u16 index within a buffer (-1: none)
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int f0 = tid + 512 * u;
+  for (int u = 0; u < ZS; ++u) {
+    const int f0 = tid + 64 * NWV * u;
     const int f = min(f0, 32 * ng - 1);
     const int row = f / ng, g = f - row * ng;
     zrg[u] = row * 64 + g;
@@ -990,15 +1004,16 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
     zdst[u] = f0 < 32 * ng ? ((g * 2 + (row >> 4)) * 16 + word) * 2 + ((q8 >> 1) & 1) : -1;
   }
 
-  struct Regs { float2 l; uint16_t z[4]; };      // z: scales of slots 0, 1, zero points of slots 0, 1
+  typedef float lvec __attribute__((ext_vector_type(PPT)));
+  struct Regs { lvec l; uint16_t z[2 * ZS]; };   // z: the slots' scales, then their zero points
   auto load = [&](Regs& R, int ks) {
     const int kc = min(ks, nks - 1);
-    R.l = *(const float2*)(lbase + ((uint32_t)(tile_s0 + kc) * lst + loff));
+    R.l = *(const lvec*)(lbase + ((uint32_t)(tile_s0 + kc) * lst + loff));
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < ZS; ++u) {
       const uint32_t o = (uint32_t)min(kc * PVN_KS + (zrg[u] >> 6), len - 1) * zp + 2u * (uint32_t)(zrg[u] & 63);
       R.z[u] = *(const uint16_t*)(sbase + o);
-      R.z[2 + u] = *(const uint16_t*)(zbase + o);
+      R.z[ZS + u] = *(const uint16_t*)(zbase + o);
     }
   };
   float psum = 0.f;
@@ -1006,10 +1021,9 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
     const int buf = ks & 1;
     uint16_t* ab = &Ash[buf * NA * 1024];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float lv = u ? R.l.y : R.l.x;
-      const float ex = __builtin_amdgcn_exp2f(fmaf(lv, 1.4426950408889634f, MqL));
-      const float pv = (hok && ks * PVN_KS + 2 * ej + u < len) ? ex : 0.f;
+    for (int u = 0; u < PPT; ++u) {
+      const float ex = __builtin_amdgcn_exp2f(fmaf(R.l[u], 1.4426950408889634f, MqL));
+      const float pv = (hok && ks * PVN_KS + PPT * ej + u < len) ? ex : 0.f;
       psum += pv;
       if constexpr (BF) {
         const __bf16 hi = (__bf16)pv;
@@ -1019,18 +1033,18 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
         ab[aslot[u]] = __builtin_bit_cast(uint16_t, (_Float16)pv);
       }
     }
-    uint16_t* sd = &Ssh[buf * 2048];
+    uint16_t* sd = &Ssh[buf * GMAX * 64];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < ZS; ++u)
       if (zdst[u] >= 0) {
         sd[zdst[u]] = R.z[u];
-        sd[zdst[u] + 8] = R.z[2 + u];
+        sd[zdst[u] + 8] = R.z[ZS + u];
       }
   };
 
-  floatx16 acc[2 * PVN_NGW];
+  floatx16 acc[2 * NGW];
 #pragma unroll
-  for (int j = 0; j < 2 * PVN_NGW; ++j) acc[j] = floatx16{};
+  for (int j = 0; j < 2 * NGW; ++j) acc[j] = floatx16{};
 
   // transposed-read address of the lane within a stage (tile 0)
   const int tr_off = (16 * hh + (lane & 15)) * PB + 8 * ((lane >> 4) & 1);
@@ -1044,10 +1058,10 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
       for (int p = 0; p < NA; ++p) A[m][p] = *(const uint4*)&Ash[(buf * NA + p) * 1024 + m * 512 + 8 * lane];
     const uint8_t* sb = st + tr_off;
 #pragma unroll
-    for (int gi = 0; gi < PVN_NGW; ++gi) {
+    for (int gi = 0; gi < NGW; ++gi) {
       if (gi < ngw) {
         const int g = g0 + gi;
-        const uint4* sp = (const uint4*)&Ssh[((buf * 32 + g) * 2 + hh) * 32];
+        const uint4* sp = (const uint4*)&Ssh[((buf * GMAX + g) * 2 + hh) * 32];
         const uint4 S0 = sp[0], Z0 = sp[1], S1 = sp[2], Z1 = sp[3];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -1107,7 +1121,7 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
         load(R[d & 1], k + 2);
         copy(VS[(d + 3) & 3], k + 3);
         compute(VS[d], k);
-        constexpr int VM = 2 * PVN_NJ + 5;       // 5: the register loads of one K-step
+        constexpr int VM = 2 * NJ + 1 + 2 * ZS;  // 1 + 2 ZS: the register loads of one K-step
         __builtin_amdgcn_s_waitcnt(0x0F70 | (VM & 15) | ((VM >> 4) << 14));
         publish(R[(d & 1) ^ 1], k + 1);
       }
@@ -1115,17 +1129,15 @@ __global__ __launch_bounds__(512, 1) void pv_nib_kernel(const PVArgs a) {
     __builtin_amdgcn_s_waitcnt(0);               // no copy may land after the wave ends
   }
 
-  // ---- softmax sums per head (the 16 threads of a head are one wave's lanes)
-  psum += __shfl_xor(psum, 1, 64);
-  psum += __shfl_xor(psum, 2, 64);
-  psum += __shfl_xor(psum, 4, 64);
-  psum += __shfl_xor(psum, 8, 64);
+  // ---- softmax sums per head (the TPH threads of a head are one wave's lanes)
+#pragma unroll
+  for (int d = 1; d < TPH; d *= 2) psum += __shfl_xor(psum, d, 64);
   if (ej == 0) Ps[eh] = psum;
   __syncthreads();
   if (tid < 32) a.psum[((int64_t)bq * a.n_c2 + c2) * 32 + tid] = Ps[tid];
   const int Rvp = a.Rvp;
 #pragma unroll
-  for (int gi = 0; gi < PVN_NGW; ++gi) {
+  for (int gi = 0; gi < NGW; ++gi) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int T = 2 * (g0 + gi) + t;
@@ -1260,7 +1272,7 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
     // the host's geometry chose the all-columns kernel (one column block)
     if (const int w = pv_wide_tiles(a.Rvp, FUSED, vq); w && a.n_cb == 1) {
       if (vq == VQ_G64 && fast) {
-        hipLaunchKernelGGL((pv_nib_kernel<VT>), dim3(a.n_c2, BQ), dim3(512), 0, st, a);
+        hipLaunchKernelGGL((pv_nib_kernel<VT, 8, 4>), dim3(a.n_c2, BQ), dim3(512), 0, st, a);
         return (int)hipGetLastError();
       }
       if (w == 5) launch_pv_wide_n<VT, 5>(a, vq, fast, BQ, st);
@@ -1269,6 +1281,11 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
       else launch_pv_wide_n<VT, 8>(a, vq, fast, BQ, st);
       return (int)hipGetLastError();
     }
+  }
+  if (FUSED && vq == VQ_G64 && fast && a.Rvp <= 512) {
+    // group-64 V of up to 16 tiles: the raw-nibble kernel, 4 waves of up to two groups
+    hipLaunchKernelGGL((pv_nib_kernel<VT, 4, 2>), dim3(a.n_c2, BQ), dim3(256), 0, st, a);
+    return (int)hipGetLastError();
   }
   if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, vq, fast, BQ, st);
   else if (ntw == 8) launch_pv_n<VT, FUSED, 8>(a, vq, fast, BQ, st);
