@@ -160,13 +160,17 @@ def test_decode_with_quantised_v(kind, R, split):
     assert mr <= 1e-3 and mx <= 2e-2
 
 
-# Group-64 V of 33..64 column tiles with aligned rows takes the all-columns
-# raw-nibble P.V kernel: both activation dtypes, an odd tile count, a half
-# last group with two head groups, the largest rank, a long context (many
-# splits), contexts that are not multiples of its 32-position step.
+# Group-64 V with aligned rows takes the raw-nibble P.V kernel (8 waves over
+# 33..64 column tiles, 4 waves up to 16 tiles): both activation dtypes, an odd
+# tile count, a half last group with two head groups, the largest rank, long
+# contexts (many splits), contexts that are not multiples of its 32-position
+# step, one partial step.
 G64_WIDE = [("bf16_1640", torch.bfloat16, 1640, 32, 777), ("f16_1056_odd_tiles", torch.float16, 1056, 32, 650),
             ("f16_1096_half_group_h64", torch.float16, 1096, 64, 1500), ("f16_2048", torch.float16, 2048, 32, 333),
-            ("bf16_1288_long", torch.bfloat16, 1288, 32, 6001)]
+            ("bf16_1288_long", torch.bfloat16, 1288, 32, 6001), ("f16_1640_s5", torch.float16, 1640, 32, 5),
+            # up to 16 tiles: the 4-wave shape (one or two groups per wave)
+            ("bf16_512_s33", torch.bfloat16, 512, 32, 33), ("f16_480_h64", torch.float16, 480, 64, 2100),
+            ("bf16_136_long", torch.bfloat16, 136, 32, 9000)]
 
 
 @pytest.mark.gpu
