@@ -870,27 +870,31 @@ __device__ inline uint2 lds_read_tr4(const uint8_t* p) {
 
 // the LDS row pitch of the raw stage for ngp 64-rank groups: whole groups
 // plus 8 bytes, an odd multiple of 8, so the 16 rows of one transposed read
-// fall on distinct banks
-__host__ __device__ constexpr int pvn_pitch(int ngp) { return 32 * ngp + 8; }
+// fall on distinct banks; with 16-byte copies (D16) whole groups plus 16
+// bytes, an odd multiple of 16 (distinct banks over 256 bytes)
+__host__ __device__ constexpr int pvn_pitch(int ngp, bool d16 = false) { return 32 * ngp + (d16 ? 16 : 8); }
 
 // Workgroup shapes: NWV waves of up to NGW groups each -- 8 x 4 for 33..64
 // column tiles (one workgroup per CU), 4 x 2 for up to 16 tiles (three per
-// CU).  NJ copy instructions per wave and K-step fill a stage of 32 rows
-// (padded to whole instructions); a thread forms PPT exponentials and loads
-// ZS scale items per K-step.
-template <int NWV, int NGW> struct PVNGeom {
+// CU).  NJ copy instructions per wave and K-step (CB bytes per lane: 4, or 16
+// for 16-byte aligned rows of whole 16-byte chunks, D16, at most 31 groups)
+// fill a stage of 32 rows (padded to whole instructions); a thread forms PPT
+// exponentials and loads ZS scale items per K-step.
+template <int NWV, int NGW, bool D16 = false> struct PVNGeom {
   static constexpr int GMAX = NWV * NGW;
-  static constexpr int NJ = (32 * pvn_pitch(GMAX) + 256 * NWV - 1) / (256 * NWV);
-  static constexpr int STAGE = NJ * NWV * 256;
+  static constexpr int CB = D16 ? 16 : 4;
+  static constexpr int NJ = (32 * pvn_pitch(D16 ? GMAX - 1 : GMAX, D16) + 64 * CB * NWV - 1) / (64 * CB * NWV);
+  static constexpr int STAGE = NJ * NWV * 64 * CB;
   static constexpr int PPT = 1024 / (64 * NWV);
   static constexpr int TPH = 32 / PPT;             // threads per head
   static constexpr int ZS = (32 * GMAX + 64 * NWV - 1) / (64 * NWV);
   static constexpr int WGS = NWV == 8 ? 1 : 3;     // workgroups per CU (LDS)
 };
 
-template <typename VT, int NWV, int NGW>
-__global__ __launch_bounds__(NWV * 64, (PVNGeom<NWV, NGW>::WGS)) void pv_nib_kernel(const PVArgs a) {
-  typedef PVNGeom<NWV, NGW> G;
+template <typename VT, int NWV, int NGW, bool D16>
+__global__ __launch_bounds__(NWV * 64, (PVNGeom<NWV, NGW, D16>::WGS)) void pv_nib_kernel(const PVArgs a) {
+  typedef PVNGeom<NWV, NGW, D16> G;
+  constexpr int CB = G::CB;
   constexpr bool BF = __is_same(VT, __bf16);
   constexpr int NA = BF ? 2 : 1;
   constexpr int NJ = G::NJ, PPT = G::PPT, TPH = G::TPH, ZS = G::ZS, GMAX = G::GMAX;
@@ -930,8 +934,10 @@ __global__ __launch_bounds__(NWV * 64, (PVNGeom<NWV, NGW>::WGS)) void pv_nib_ker
   const int len = s_end - s_begin;
   const int nks = (len + PVN_KS - 1) / PVN_KS;
   const int ngp = (a.Rvp + 63) / 64;             // 64-rank groups (the last may be half a group)
-  const int PB = pvn_pitch(ngp);
-  const int ndw = a.Rv / 8;                      // dwords of a packed row (Rv a multiple of 8)
+  const int PB = pvn_pitch(ngp, D16);
+  // CB-byte pieces of a packed row (Rv a multiple of 8; D16: the host checked
+  // that the row pitch holds whole 16-byte pieces)
+  const int ndw = (a.Rv / 2 + CB - 1) / CB;
 
   // ---- this wave's groups: ngp / NWV each, one more for the first
   // ngp % NWV waves (with 8 waves, waves w and w + 4 share a SIMD)
@@ -941,19 +947,19 @@ __global__ __launch_bounds__(NWV * 64, (PVNGeom<NWV, NGW>::WGS)) void pv_nib_ker
   const int ntile = a.Rvp / 32;
 
   // ---- copy plan: a stage is 32 rows of PB bytes plus padding to whole
-  // instructions (NJ of 256 bytes per wave); instruction m = wave + NWV j
-  // writes stage bytes [256 m, 256 m + 256), lane i's dword D = 64 m + i
-  // being row D / (PB / 4), dword D % (PB / 4) of the row (pad dwords re-read
-  // the row's last dword).  A K-step's descriptor ends at its last row, so
-  // rows past the chunk and the slots past row 31 read zeros (out of range:
-  // no memory access) -- every wave issues the same NJ copies.
-  const int PBd = PB / 4;
+  // instructions (NJ of 64 CB bytes per wave); instruction m = wave + NWV j
+  // writes stage bytes [64 CB m, 64 CB (m + 1)), lane i's piece D = 64 m + i
+  // being row D / (PB / CB), piece D % (PB / CB) of the row (pad pieces
+  // re-read the row's last piece).  A K-step's descriptor ends at its last
+  // row, so rows past the chunk and the slots past row 31 read zeros (out of
+  // range: no memory access) -- every wave issues the same NJ copies.
+  const int PBd = PB / CB;
   uint32_t voff[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int D = 64 * (wave + NWV * j) + lane;
     const int r = D / PBd;
-    voff[j] = (uint32_t)r * (uint32_t)a.x_ss + 4u * (uint32_t)min(D - r * PBd, ndw - 1);
+    voff[j] = (uint32_t)r * (uint32_t)a.x_ss + (uint32_t)CB * (uint32_t)min(D - r * PBd, ndw - 1);
   }
   const uint8_t* xq = (const uint8_t*)a.x + b * a.x_sb + (int64_t)s_begin * a.x_ss;
   const uint32_t xp = (uint32_t)a.x_ss;
@@ -965,9 +971,13 @@ __global__ __launch_bounds__(NWV * 64, (PVNGeom<NWV, NGW>::WGS)) void pv_nib_ker
                         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)bu, (short)0, __builtin_amdgcn_readfirstlane((int)((uint32_t)rows * xp)), 0x00020000);
+    // (the device pass only: the host pass rejects the 16-byte form, a gfx950
+    // feature, and would then drop this instantiation's launch stub)
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st + 256 * (wave + NWV * j)), 4, voff[j], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st + 64 * CB * (wave + NWV * j)), CB, voff[j], 0, 0, 0);
+#endif
   };
 
   // ---- logits: thread (head eh, ej) takes positions PPT ej .. PPT ej + PPT - 1
@@ -1272,7 +1282,11 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
     // the host's geometry chose the all-columns kernel (one column block)
     if (const int w = pv_wide_tiles(a.Rvp, FUSED, vq); w && a.n_cb == 1) {
       if (vq == VQ_G64 && fast) {
-        hipLaunchKernelGGL((pv_nib_kernel<VT, 8, 4>), dim3(a.n_c2, BQ), dim3(512), 0, st, a);
+        // rows of whole, aligned 16-byte pieces (the latent cache pads them): 16-byte copies
+        const bool d16 = ((uintptr_t)a.x & 15) == 0 && a.x_ss % 16 == 0 && a.x_sb % 16 == 0 &&
+                         a.x_ss >= 16 * ((a.Rv + 31) / 32) && a.Rvp <= 31 * 64;
+        if (d16) hipLaunchKernelGGL((pv_nib_kernel<VT, 8, 4, true>), dim3(a.n_c2, BQ), dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((pv_nib_kernel<VT, 8, 4, false>), dim3(a.n_c2, BQ), dim3(512), 0, st, a);
         return (int)hipGetLastError();
       }
       if (w == 5) launch_pv_wide_n<VT, 5>(a, vq, fast, BQ, st);
@@ -1284,7 +1298,7 @@ static int launch_pv_t(const PVArgs& a, int vq, bool fast, int B, hipStream_t st
   }
   if (FUSED && vq == VQ_G64 && fast && a.Rvp <= 512) {
     // group-64 V of up to 16 tiles: the raw-nibble kernel, 4 waves of up to two groups
-    hipLaunchKernelGGL((pv_nib_kernel<VT, 4, 2>), dim3(a.n_c2, BQ), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pv_nib_kernel<VT, 4, 2, false>), dim3(a.n_c2, BQ), dim3(256), 0, st, a);
     return (int)hipGetLastError();
   }
   if (ntw == 4) launch_pv_n<VT, FUSED, 4>(a, vq, fast, BQ, st);

@@ -69,7 +69,10 @@ class LatentCache:
             self._k = dict(data=self.k_data, head_offset=offs, pos_stride=pitch, stride_b=self.k_data.stride(0),
                            fmt=FMT_INT8_SYM, scale=self.k_scale)
             G = (self.Rv + 63) // 64
-            self.v_data = torch.zeros(B, C, (self.Rv + 1) // 2, dtype=torch.uint8, device=dev)
+            # rows padded to 16 bytes: the P.V kernel copies them in 16-byte pieces
+            nb = (self.Rv + 1) // 2
+            self._v_rows = torch.zeros(B, C, _round(nb, 16), dtype=torch.uint8, device=dev)
+            self.v_data = self._v_rows[..., :nb]
             self.v_scale = torch.ones(B, C, G, dtype=torch.float16, device=dev)
             self.v_zero = torch.zeros(B, C, G, dtype=torch.float16, device=dev)
             self.v_spec = VLatentSpec.int4_g64(self.v_data, self.v_scale, self.v_zero, self.Rv)

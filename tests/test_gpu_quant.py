@@ -164,10 +164,12 @@ def test_decode_with_quantised_v(kind, R, split):
 # 33..64 column tiles, 4 waves up to 16 tiles): both activation dtypes, an odd
 # tile count, a half last group with two head groups, the largest rank, long
 # contexts (many splits), contexts that are not multiples of its 32-position
-# step, one partial step.
+# step, one partial step, and rows that take its 16-byte copies.
 G64_WIDE = [("bf16_1640", torch.bfloat16, 1640, 32, 777), ("f16_1056_odd_tiles", torch.float16, 1056, 32, 650),
             ("f16_1096_half_group_h64", torch.float16, 1096, 64, 1500), ("f16_2048", torch.float16, 2048, 32, 333),
             ("bf16_1288_long", torch.bfloat16, 1288, 32, 6001), ("f16_1640_s5", torch.float16, 1640, 32, 5),
+            # rows of whole 16-byte pieces (640 and 528 bytes): 16-byte copies
+            ("bf16_1280_d16", torch.bfloat16, 1280, 32, 1111),
             # up to 16 tiles: the 4-wave shape (one or two groups per wave)
             ("bf16_512_s33", torch.bfloat16, 512, 32, 33), ("f16_480_h64", torch.float16, 480, 64, 2100),
             ("bf16_136_long", torch.bfloat16, 136, 32, 9000)]
