@@ -830,16 +830,18 @@ __global__ __launch_bounds__(512, 1) void pv_wide_kernel(const PVArgs a) {
 
 // Fused group-64 int4 P.V over all columns, with the V latent staged raw.
 //
-// As pv_wide_kernel (8 waves over all column tiles of one position chunk,
-// each K-step's exponentials formed once and shared through LDS), but the
-// packed rows go to LDS as they are and are dequantised after a transposed
-// read, so LDS carries 1 byte per latent element instead of 4 (the fp16
-// value written and read back):
+// As pv_wide_kernel (one workgroup over all column tiles of one position
+// chunk, each K-step's exponentials formed once and shared through LDS), but
+// the packed rows go to LDS as they are and are dequantised after a
+// transposed read, so LDS carries 1 byte per latent element instead of 4
+// (the fp16 value written and read back).  8 waves serve 33..64 column tiles,
+// 4 waves up to 16.
 // * a K-step is 32 positions; the workgroup copies their rows (ranks padded
-//   to whole 64-rank groups, LDS row pitch PB = 8 * odd bytes) into a ring of
-//   four stages with buffer_load_dword ... lds, one descriptor per K-step
-//   whose range ends at the chunk's last row, so the copy needs no registers
-//   and no address arithmetic per K-step;
+//   to whole 64-rank groups) into a ring of four LDS stages with
+//   buffer_load_dword ... lds, or buffer_load_dwordx4 ... lds for rows of
+//   whole aligned 16-byte pieces, one descriptor per K-step whose range ends
+//   at the chunk's last row, so the copy needs no registers and no address
+//   arithmetic per K-step;
 // * wave w owns whole groups (two 32-column tiles each, the groups shared out
 //   so that the two waves of a SIMD hold 14 or fewer tiles at Rv 1640) and
 //   reads a tile with one ds_read_b64_tr_b4, the gfx950 transposed 4-bit
