@@ -547,7 +547,9 @@ struct DecodeLayout {
 // combination of V rows: bounded by max |V|): there the partials are a large
 // share of the P.V traffic (at 272 positions about as many bytes as the
 // int4 V latent) and halving them pays for the per-chunk rescale in the
-// up-projection; with long chunks it does not (measured).
+// up-projection.  With long chunks the time comes out even (measured); group-64
+// V keeps them in fp16 there too, halving the partials' share of its traffic
+// (55 of 613 MB at B16 S32768), dense V in fp32.
 DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int k1pc, int vq, int64_t v_row_bytes,
                            bool f16) {
   DecodeLayout L;
@@ -567,7 +569,7 @@ DecodeLayout decode_layout(int B, int Hq, int Hkv, int S, int Rv, int n_wg, int 
   size_t o = 0;
   L.off_logits = o; o = a256(o + (size_t)B * Hq * L.S_pad * 4);
   L.off_cmax = o; o = a256(o + (size_t)B * Hq * L.n_c1 * 4);
-  const bool part16 = f16 && L.pv.c2_len <= 512;
+  const bool part16 = f16 && (L.pv.c2_len <= 512 || vq == VQ_G64);
   L.part16 = part16;
   L.off_part = o; o = a256(o + BQ * n_c2 * 32 * Rvp * (part16 ? 2 : 4));
   L.off_psum = o; o = a256(o + BQ * n_c2 * 32 * 4);
