@@ -172,6 +172,7 @@ G64_WIDE = [("bf16_1640", torch.bfloat16, 1640, 32, 777), ("f16_1056_odd_tiles",
             ("bf16_1280_d16", torch.bfloat16, 1280, 32, 1111),
             # up to 16 tiles: the 4-wave shape (one or two groups per wave)
             ("bf16_512_s33", torch.bfloat16, 512, 32, 33), ("f16_480_h64", torch.float16, 480, 64, 2100),
+            ("f16_256_s1", torch.float16, 256, 32, 1),
             ("bf16_136_long", torch.bfloat16, 136, 32, 9000)]
 
 
