@@ -102,10 +102,19 @@ struct GqDma {
   uint32_t ring;               // LDS byte address of the ring
   int stage, nst, tile0, S;
 
-  // tile tile0 + i into stage i % nst; rows past S re-read row S - 1
+  // tile tile0 + i into stage i % nst; rows past S re-read row S - 1 (only
+  // the last tile has any: the others take one address add per instruction)
   __device__ inline void issue(int i) const {
     const int tl = tile0 + i;
     const uint32_t lb = ring + (uint32_t)((i % nst) * stage);
+    if ((tl + 1) * TILE <= S) {
+#pragma unroll
+      for (int k = 0; k < GQ_MAXK; ++k) {
+        if (k >= cnt) break;
+        gq_dma(base[k] + (uint64_t)(uint32_t)i * lstep[k], lb + (uint32_t)dst[k]);
+      }
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < GQ_MAXK; ++k) {
       if (k >= cnt) break;
@@ -143,16 +152,16 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
   // bf16 (the reference too, abx_rope_batched.py:114-125), whose range fp16
   // lacks.  Their queries enter scaled by 2^-8 (exact: |q| up to 1.6e7;
   // those below 0.016 among fp16's subnormals, with an absolute error under
-  // 7.6e-6) and the logits leave scaled by 2^8.  A tile whose rotated keys
-  // could pass fp16's range (|y| <= (|k0| + |k1|) a <= 2 a max(|k0|, |k1|),
-  // a = |table cos at position 0|, the attention scaling) takes them scaled
-  // by 2^-16 (exact; up to ~4e9).  Keys are not scaled on every tile: that
-  // puts the small ones among fp16's subnormals, measured 1.6x slower.
+  // 7.6e-6) and the logits leave scaled by 2^8.  A tile one of whose rotated
+  // keys passed fp16's range (found from its logits: inf or NaN) runs again
+  // with its keys scaled by 2^-16 (exact; up to ~4e9).  Keys are not scaled on
+  // every tile: that puts the small ones among fp16's subnormals, measured
+  // 1.6x slower; checking the rotated keys' range before the conversion cost
+  // ~50 VALU instructions per tile and wave.
   constexpr bool BF = !__is_same(XT, _Float16);
   constexpr float IN_SCALE = BF ? 0x1p-8f : 1.f;
-  constexpr float F16_SAFE = 60000.f;
+  constexpr float F32_FINITE = 3.4028235e38f;         // largest finite float
   const float wscale = a.wscale * (BF ? 0x1p8f : 1.f);
-  const float ta = fabsf((float)((const _Float16*)a.rope)[0]);
   // B_k^T operands of M-tiles p and p+2: lane l holds dim 32m + l%32, ranks
   // 16kk + 8hh + 0..7 (zero past r)
   XV bt[2][NK];
@@ -265,50 +274,64 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
       emit(sum, tile0 + i - 1);
     }
     const char* st = ring + (i % nst) * stage;
-    XV xb[NK];
+    // the tile's group logits (rows v < 4 of this lane's column), keys
+    // scaled by ks before their rotation
+    auto tile_logits = [&](float ks, float sum[4]) __attribute__((always_inline)) {
+      XV xb[NK];
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) xb[kk] = *(const XV*)(st + xo[kk]);
-    half8 T4[4];
+      for (int kk = 0; kk < NK; ++kk) xb[kk] = *(const XV*)(st + xo[kk]);
+      half8 T4[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) T4[g] = *(const half8*)(st + stage - 8192 + ((4 * p + g) * 64 + lane) * 16);
-    // K^T of M-tiles p (k0) and p+2 (k1)
-    floatx16 k0 = floatx16{}, k1 = floatx16{};
+      for (int g = 0; g < 4; ++g) T4[g] = *(const half8*)(st + stage - 8192 + ((4 * p + g) * 64 + lane) * 16);
+      // K^T of M-tiles p (k0) and p+2 (k1)
+      floatx16 k0 = floatx16{}, k1 = floatx16{};
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) {
-      k0 = gq_mfma<XT>(bt[0][kk], xb[kk], k0);
-      k1 = gq_mfma<XT>(bt[1][kk], xb[kk], k1);
-    }
-    float lscale = 1.f;
-    if constexpr (BF) {
-      float m = 0.f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) m = fmaxf(m, fmaxf(fabsf(k0[v]), fabsf(k1[v])));
-      if (__builtin_amdgcn_ballot_w64(2.f * m * ta > F16_SAFE) != 0) {
+      for (int kk = 0; kk < NK; ++kk) {
+        k0 = gq_mfma<XT>(bt[0][kk], xb[kk], k0);
+        k1 = gq_mfma<XT>(bt[1][kk], xb[kk], k1);
+      }
+      if (ks != 1.f) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          k0[v] *= 0x1p-16f;
-          k1[v] *= 0x1p-16f;
+          k0[v] *= ks;
+          k1[v] *= ks;
         }
-        lscale = 0x1p16f;
+      }
+      // rotate: accumulator v is dim d = 32m + 8g + 4hh + e (g = v/4, e = v%4)
+      // and its partner d + 64; (a cos, a sin) of frequency 32p + 8g + 4hh + e
+      // are elements 2e, 2e+1 of table K-step 4p + g
+      half8 bop[4];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float c = (float)T4[v >> 2][2 * (v & 3)], s = (float)T4[v >> 2][2 * (v & 3) + 1];
+        bop[v >> 3][v & 7] = (_Float16)(k0[v] * c - k1[v] * s);
+        bop[2 + (v >> 3)][v & 7] = (_Float16)(k1[v] * c + k0[v] * s);
+      }
+      // two chains of two K-steps each (dims 0-63 and their partners)
+      floatx16 la = mfma_f16(qa[0], bop[0], floatx16{});
+      floatx16 lb = mfma_f16(qa[2], bop[2], floatx16{});
+      la = mfma_f16(qa[1], bop[1], la);
+      lb = mfma_f16(qa[3], bop[3], lb);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sum[v] = la[v] + lb[v];
+    };
+    float sum[4];
+    tile_logits(1.f, sum);
+    if constexpr (BF) {
+      // a rotated key past fp16's range became inf, which makes every logit
+      // of its position inf or NaN (a zero query row gives 0 * inf = NaN):
+      // then the wave runs the tile again with its keys scaled by 2^-16
+      const float chk = (sum[0] + sum[1]) + (sum[2] + sum[3]);
+      if (__builtin_amdgcn_ballot_w64(!(fabsf(chk) <= F32_FINITE)) != 0) {
+        // (operands read from LDS again rather than kept in registers)
+        asm volatile("" ::: "memory");
+        tile_logits(0x1p-16f, sum);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sum[v] *= 0x1p16f;
       }
     }
-    // rotate: accumulator v is dim d = 32m + 8g + 4hh + e (g = v/4, e = v%4)
-    // and its partner d + 64; (a cos, a sin) of frequency 32p + 8g + 4hh + e
-    // are elements 2e, 2e+1 of table K-step 4p + g
-    half8 bop[4];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float c = (float)T4[v >> 2][2 * (v & 3)], s = (float)T4[v >> 2][2 * (v & 3) + 1];
-      bop[v >> 3][v & 7] = (_Float16)(k0[v] * c - k1[v] * s);
-      bop[2 + (v >> 3)][v & 7] = (_Float16)(k1[v] * c + k0[v] * s);
-    }
-    // two chains of two K-steps each (dims 0-63 and their partners)
-    floatx16 la = mfma_f16(qa[0], bop[0], floatx16{});
-    floatx16 lb = mfma_f16(qa[2], bop[2], floatx16{});
-    la = mfma_f16(qa[1], bop[1], la);
-    lb = mfma_f16(qa[3], bop[3], lb);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) prev[v] = (la[v] + lb[v]) * lscale;
+    for (int v = 0; v < 4; ++v) prev[v] = sum[v];
   }
   // the last tile: handed over after one more barrier
   if (p == 0) {
