@@ -303,9 +303,13 @@ __device__ __attribute__((always_inline)) inline void gq_consume(const KArgs& a,
       half8 bop[4];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float c = (float)T4[v >> 2][2 * (v & 3)], s = (float)T4[v >> 2][2 * (v & 3) + 1];
-        bop[v >> 3][v & 7] = (_Float16)(k0[v] * c - k1[v] * s);
-        bop[2 + (v >> 3)][v & 7] = (_Float16)(k1[v] * c + k0[v] * s);
+        // every product takes the table's fp16 (cos, sin) as it is (mixed-
+        // precision FMAs, no conversions): k1 s and k0 s rounded to fp32, then
+        // k0 c - k1 s and k1 c + k0 s rounded to fp16
+        const _Float16 c = T4[v >> 2][2 * (v & 3)], s = T4[v >> 2][2 * (v & 3) + 1];
+        const float t1 = __builtin_fmaf(k1[v], (float)s, 0.f), t2 = __builtin_fmaf(k0[v], (float)s, 0.f);
+        bop[v >> 3][v & 7] = (_Float16)__builtin_fmaf(k0[v], (float)c, -t1);
+        bop[2 + (v >> 3)][v & 7] = (_Float16)__builtin_fmaf(k1[v], (float)c, t2);
       }
       // two chains of two K-steps each (dims 0-63 and their partners)
       floatx16 la = mfma_f16(qa[0], bop[0], floatx16{});
