@@ -959,10 +959,65 @@ __global__ __launch_bounds__(256) void repack_rows_kernel(const RepackArgs a) {
   *(uint4*)(a.dst + b * a.dst_sb + ((int64_t)h * a.S + s) * a.pitch + o) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// 16-bit rows of at most RPB_MAXP source bytes each, a block of RPB_ROWS rows
+// per workgroup: the block's source bytes (from its first row's first element
+// to its last row's last element: the gaps between rows, none past the last
+// row) are read with 16-byte loads where they are 16-byte aligned and bytewise
+// at the two ends, staged in LDS at their address modulo 16, and written out
+// as whole 16-byte pieces of the padded rows.  Rows of 2n bytes at any 4-byte
+// alignment (rank 102: 204-byte rows) then take one 16-byte load per 16
+// bytes instead of four 4-byte loads and a bytewise tail per row.
+constexpr int RPB_ROWS = 64, RPB_MAXP = 512;
+__global__ __launch_bounds__(256) void repack_block_kernel(const RepackArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t blk[RPB_ROWS * RPB_MAXP + 32];
+  const int h = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int s0 = blockIdx.x * RPB_ROWS, nr = min(RPB_ROWS, a.S - s0);
+  const int n = a.nel[h];
+  const int64_t P = a.src_pitch[h];
+  const uint8_t* A = a.src + b * a.src_sb + a.src_off[h] + (int64_t)s0 * P;
+  const int64_t T = (int64_t)(nr - 1) * P + 2 * n;                 // bytes of the block
+  const int lead = (int)((uintptr_t)A & 15);
+  const uint8_t* A0 = A - lead;
+  const int64_t first = lead ? 16 : 0;                               // first whole aligned piece (offset from A0)
+  const int64_t last = (lead + T) & ~(int64_t)15;                    // end of the last whole piece
+  for (int64_t o = first + 16 * (int64_t)tid; o < last; o += 16 * 256)
+    *(uint4*)(blk + o) = *(const uint4*)(A0 + o);
+  // the partial pieces at both ends, bytewise
+  if (tid < 16) {
+    const int64_t o = lead + tid;                                    // head: [lead, min(16, lead + T))
+    if (lead && o < 16 && o < lead + T) blk[o] = A0[o];
+  } else if (tid < 32) {
+    const int64_t o = last + (tid - 16);                             // tail: [last, lead + T)
+    if (o >= first && o < lead + T) blk[o] = A0[o];
+  }
+  __syncthreads();
+  const int ppr = a.pitch >> 4;
+  uint8_t* dst = a.dst + b * a.dst_sb + ((int64_t)h * a.S + s0) * a.pitch;
+  for (int i = tid; i < nr * ppr; i += 256) {
+    const int r = i / ppr, o = (i - r * ppr) * 16;
+    const int64_t so = lead + (int64_t)r * P + o;                    // the piece's first byte in blk
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = (o >> 1) + 2 * k;                                // first element of the word
+      const uint32_t lo = e < n ? *(const uint16_t*)(blk + so + 4 * k) : 0u;
+      const uint32_t hi = e + 1 < n ? *(const uint16_t*)(blk + so + 4 * k + 2) : 0u;
+      w[k] = lo | (hi << 16);
+    }
+    *(uint4*)(dst + (int64_t)r * a.pitch + o) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 int launch_repack(const RepackArgs& a, int B, hipStream_t st) {
   const int64_t pieces = (int64_t)a.S * (a.pitch / 16);
   if (pieces == 0) return 0;
-  hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)ceil_div(pieces, 256), a.H, B), dim3(256), 0, st, a);
+  bool blockwise = a.kind == RP_HALF;
+  for (int h = 0; h < a.H && blockwise; ++h)
+    blockwise = a.src_pitch[h] % 2 == 0 && a.src_pitch[h] >= 2 * a.nel[h] && a.src_pitch[h] <= RPB_MAXP;
+  if (blockwise)
+    hipLaunchKernelGGL(repack_block_kernel, dim3((unsigned)ceil_div(a.S, RPB_ROWS), a.H, B), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(repack_rows_kernel, dim3((unsigned)ceil_div(pieces, 256), a.H, B), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 

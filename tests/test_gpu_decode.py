@@ -69,6 +69,9 @@ CASES = [
     ("mha_hq40", 2, 40, 40, 700, [96, 56, 48, 32, 16, 88, 56, 48] * 5, 1280, torch.float16, "ragged"),
     ("gqa_hq64_bf16", 1, 64, 8, 900, [32, 128, 32, 80, 32, 64, 80, 64], 512, torch.bfloat16, "ragged"),
     ("mha_hq64_s33", 2, 64, 64, 33, [16, 32] * 32, 200, torch.float16, "ragged"),
+    # odd ranks (rows 2-byte aligned, repacked in 64-row blocks), GQA 4, and a
+    # context that ends inside a block
+    ("gqa4_odd_ranks", 2, 32, 8, 1000, [102, 37, 13, 70, 102, 5, 99, 128], 512, torch.float16, "ragged"),
 ]
 
 
